@@ -1,0 +1,123 @@
+/*
+ * mamba_hip_scan.h -- C ABI of the MI355X (gfx950) fused diagonal selective scan.
+ *
+ * The recurrence (mamba_metal/scan.py:13-15 in the reference):
+ *
+ *     dA[t,d,n] = exp(-dt[t,d] * Aneg[d,n])
+ *     h[t,d,n]  = dA[t,d,n] * h[t-1,d,n] + dt[t,d] * B[t,n] * x[t,d]      h[-1] = 0
+ *     y[t,d]    = sum_n C[t,n] * h[t,d,n]
+ *
+ * Every pointer is a DEVICE pointer to contiguous row-major float32:
+ *     x, dt, y, dy, dx, ddt : (batch, seqlen, d_inner)
+ *     B, C, dB, dC          : (batch, seqlen, d_state)
+ *     aneg, daneg           : (d_inner, d_state)          (Aneg > 0, e.g. softplus(A))
+ *     ckpt                  : (batch, ceil(seqlen/chunk), d_inner, d_state),
+ *                             h at the END of every chunk of `chunk` steps
+ *     h_last, dh_last       : (batch, d_inner, d_state)   (h at t = seqlen-1)
+ *
+ * All pointers must be 16-byte aligned (torch allocations are). The caller
+ * owns every buffer, as the reference's autograd Function allocates every
+ * output (scan.py:373-375 and :401-405). Work is enqueued asynchronously on
+ * `stream` (a hipStream_t; NULL = the legacy default stream). Functions return 0
+ * or an MHS_E* code; mhs_last_error() gives a message for the calling thread.
+ * Entry points may be called concurrently from several threads / streams: no
+ * buffer is shared between calls.
+ */
+#ifndef MAMBA_HIP_SCAN_H
+#define MAMBA_HIP_SCAN_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define MHS_OK 0
+#define MHS_EINVAL 1   /* bad argument: null pointer, size, d_state unsupported */
+#define MHS_EHIP 2     /* a HIP runtime call or kernel launch failed */
+
+/* Largest supported d_state. Supported: any d_state in [1, 16], even values up
+ * to 32, multiples of 4 up to MHS_MAX_DSTATE. The reference's Metal kernels
+ * require d_state % 4 == 0 (scan.py:274-276). */
+#define MHS_MAX_DSTATE 64
+
+/* Library version, (major << 16) | (minor << 8) | patch. */
+int mhs_version(void);
+
+/* Message describing the last failure on the calling thread ("" if none). */
+const char* mhs_last_error(void);
+
+/* Number of checkpoint slots the forward writes: ceil(seqlen / chunk). */
+int64_t mhs_num_chunks(int64_t seqlen, int64_t chunk);
+
+/* The largest checkpoint stride the backward walks without first recomputing
+ * finer checkpoints (its register window); 0 if d_state is unsupported.
+ * Any chunk >= 1 is correct; strides above this cost one extra forward pass
+ * inside mhs_scan_bwd_f32. No counterpart in the reference (its stride is the
+ * module constant SSM_CHUNK, mamba_metal/scan.py:58). */
+int64_t mhs_preferred_chunk(int64_t d_state);
+
+/* Tuning knob, process-wide: force the number of state lanes each wave
+ * carries per channel (1, 2 or 4; 0 restores the automatic choice). Ignored
+ * for a d_state it does not divide. No counterpart in the reference (its
+ * Metal kernels keep all d_state lanes in one thread, scan.py:67-69). */
+int mhs_set_variant(int state_lanes_per_wave);
+
+/*
+ * Forward scan. Replaces the reference's `lib.ssm_fwd(x, dt, Aneg, Bm, Cm, y,
+ * ckpt, Bt, T, D, Kc)` launch (mamba_metal/scan.py:78-127, launched at :377-378).
+ *
+ *   y      : written (may be NULL: then only ckpt / h_last are produced)
+ *   ckpt   : written if non-NULL; checkpoint stride `chunk` (>= 1)
+ *   h_last : written if non-NULL (the state after the last step; the reference
+ *            returns ckpt[:, -1] for this, scan.py:381-387)
+ */
+int mhs_scan_fwd_f32(const float* x, const float* dt, const float* aneg,
+                     const float* B, const float* C,
+                     float* y, float* ckpt, float* h_last,
+                     int64_t batch, int64_t seqlen, int64_t d_inner, int64_t d_state,
+                     int64_t chunk, void* stream);
+
+/* Bytes of device workspace mhs_scan_bwd_f32 needs for this shape. */
+size_t mhs_scan_bwd_workspace_bytes(int64_t batch, int64_t seqlen, int64_t d_inner,
+                                    int64_t d_state, int64_t chunk);
+
+/*
+ * Backward scan. Replaces the reference's `lib.ssm_bwd(x, dt, Aneg, Bm, Cm, dy,
+ * dx, ddt, dAneg, dBm, dCm, ckpt, scratch, Bt, T, D, Kc)` launch
+ * (mamba_metal/scan.py:132-261, launched at :408-410).
+ *
+ *   ckpt     : the forward's checkpoints for the same `chunk`
+ *   dh_last  : gradient of the returned final state, or NULL (= zero; the
+ *              reference drops it, scan.py:390-393)
+ *   dx, ddt, daneg, dB, dC : fully written (no pre-zeroing needed). dB, dC and
+ *              daneg are sums over channels / (batch, time); they are reduced
+ *              through the workspace in a fixed order, so results are
+ *              bit-for-bit reproducible run to run.
+ *   workspace: >= mhs_scan_bwd_workspace_bytes(...) bytes of device memory,
+ *              256-byte aligned; its contents on entry do not matter.
+ */
+int mhs_scan_bwd_f32(const float* x, const float* dt, const float* aneg,
+                     const float* B, const float* C, const float* dy,
+                     const float* dh_last, const float* ckpt,
+                     float* dx, float* ddt, float* daneg, float* dB, float* dC,
+                     void* workspace, size_t workspace_bytes,
+                     int64_t batch, int64_t seqlen, int64_t d_inner, int64_t d_state,
+                     int64_t chunk, void* stream);
+
+/*
+ * One recurrent decode step, in place on h. Replaces the pure-torch step of
+ * the reference's MambaBlock.forward (mamba_metal/model.py:234-241):
+ *     h <- h * exp(-dt * Aneg) + dt * B * x ;  y = sum_n C * h
+ *   x, dt, y : (batch, d_inner)    B, C : (batch, d_state)    h : (batch, d_inner, d_state)
+ */
+int mhs_scan_step_f32(float* h, const float* x, const float* dt, const float* aneg,
+                      const float* B, const float* C, float* y,
+                      int64_t batch, int64_t d_inner, int64_t d_state, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* MAMBA_HIP_SCAN_H */

@@ -1,0 +1,12 @@
+"""MI355X-native fused selective scan for Mamba (gfx950 HIP kernels).
+
+Same public surface as the reference package ``mamba_metal``
+(mamba_metal/__init__.py:2-7), plus the HIP-specific names.
+"""
+from .model import MambaConfig, TinyMamba
+from .scan import (SSM_CHUNK, SelectiveScanHIP, selective_scan, selective_scan_hip,
+                   selective_scan_metal, selective_scan_ref, selective_state_step)
+
+__all__ = ["MambaConfig", "TinyMamba", "SSM_CHUNK", "SelectiveScanHIP", "selective_scan",
+           "selective_scan_hip", "selective_scan_metal", "selective_scan_ref",
+           "selective_state_step"]

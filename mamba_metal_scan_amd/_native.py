@@ -1,0 +1,183 @@
+"""ctypes binding of the gfx950 scan library and the torch custom ops over it.
+
+The shared library (``libmamba_hip_scan.so``, built in place by ``build.py``)
+exports the C ABI of ``include/mamba_hip_scan.h``. It links only the HIP
+runtime and is loaded after ``torch``: the dynamic loader then resolves its
+``libamdhip64.so.7`` to the copy torch already mapped, so the kernels run in
+torch's HIP context and on torch's streams.
+
+The ops registered here are the product path. There is no CPU or torch
+fallback behind them: if the library is absent they raise.
+"""
+from __future__ import annotations
+
+import ctypes
+import threading
+from pathlib import Path
+from typing import Optional
+
+import torch
+
+LIB_PATH = Path(__file__).resolve().with_name("libmamba_hip_scan.so")
+
+# Every symbol the C header declares (checked by the CPU test suite).
+EXPORTED_SYMBOLS = (
+    "mhs_version", "mhs_last_error", "mhs_num_chunks", "mhs_preferred_chunk",
+    "mhs_set_variant", "mhs_scan_fwd_f32", "mhs_scan_bwd_workspace_bytes",
+    "mhs_scan_bwd_f32", "mhs_scan_step_f32",
+)
+
+_lib: Optional[ctypes.CDLL] = None
+_lock = threading.Lock()
+
+_P = ctypes.c_void_p
+_I64 = ctypes.c_int64
+
+
+class HipScanError(RuntimeError):
+    """A call into the HIP scan library failed."""
+
+
+def library() -> ctypes.CDLL:
+    """Load (once) and return the HIP scan library; raises if it is not built."""
+    global _lib
+    if _lib is not None:
+        return _lib
+    with _lock:
+        if _lib is None:
+            if not LIB_PATH.exists():
+                raise HipScanError(
+                    f"the HIP scan library is not built ({LIB_PATH} is missing); "
+                    "run `python -m mamba_metal_scan_amd.build` or __graft_entry__.build()")
+            lib = ctypes.CDLL(str(LIB_PATH))
+            lib.mhs_version.restype = ctypes.c_int
+            lib.mhs_version.argtypes = []
+            lib.mhs_last_error.restype = ctypes.c_char_p
+            lib.mhs_last_error.argtypes = []
+            lib.mhs_num_chunks.restype = _I64
+            lib.mhs_num_chunks.argtypes = [_I64, _I64]
+            lib.mhs_preferred_chunk.restype = _I64
+            lib.mhs_preferred_chunk.argtypes = [_I64]
+            lib.mhs_set_variant.restype = ctypes.c_int
+            lib.mhs_set_variant.argtypes = [ctypes.c_int]
+            lib.mhs_scan_fwd_f32.restype = ctypes.c_int
+            lib.mhs_scan_fwd_f32.argtypes = [_P] * 8 + [_I64] * 5 + [_P]
+            lib.mhs_scan_bwd_workspace_bytes.restype = ctypes.c_size_t
+            lib.mhs_scan_bwd_workspace_bytes.argtypes = [_I64] * 5
+            lib.mhs_scan_bwd_f32.restype = ctypes.c_int
+            lib.mhs_scan_bwd_f32.argtypes = [_P] * 14 + [ctypes.c_size_t] + [_I64] * 5 + [_P]
+            lib.mhs_scan_step_f32.restype = ctypes.c_int
+            lib.mhs_scan_step_f32.argtypes = [_P] * 7 + [_I64] * 3 + [_P]
+            _lib = lib
+    return _lib
+
+
+def _check(rc: int, what: str) -> None:
+    if rc != 0:
+        msg = library().mhs_last_error().decode(errors="replace")
+        raise HipScanError(f"{what} failed (code {rc}): {msg}")
+
+
+def _ptr(t: Optional[torch.Tensor]):
+    return None if t is None else ctypes.c_void_p(t.data_ptr())
+
+
+def _stream(dev: torch.device) -> ctypes.c_void_p:
+    return ctypes.c_void_p(torch.cuda.current_stream(dev).cuda_stream)
+
+
+def num_chunks(seqlen: int, chunk: int) -> int:
+    return (seqlen + chunk - 1) // chunk
+
+
+def preferred_chunk(d_state: int) -> int:
+    """Largest checkpoint stride the backward kernel walks without recomputing."""
+    return int(library().mhs_preferred_chunk(d_state))
+
+
+def set_variant(state_lanes_per_wave: int) -> None:
+    """Force 1, 2 or 4 state lanes per wave (0 = automatic), process-wide."""
+    _check(library().mhs_set_variant(int(state_lanes_per_wave)), "mhs_set_variant")
+
+
+# --------------------------------------------------------------- custom ops
+
+@torch.library.custom_op("mamba_hip::scan_fwd", mutates_args=())
+def scan_fwd(x: torch.Tensor, dt: torch.Tensor, aneg: torch.Tensor, b_in: torch.Tensor,
+             c_in: torch.Tensor, chunk: int, with_ckpt: bool
+             ) -> tuple[torch.Tensor, torch.Tensor, torch.Tensor]:
+    """y (B,T,D), ckpt (B,ceil(T/chunk),D,N) or an empty tensor, h_last (B,D,N)."""
+    bt, t_len, d = x.shape
+    n = aneg.shape[1]
+    y = torch.empty_like(x)
+    ckpt = (x.new_empty((bt, num_chunks(t_len, chunk), d, n)) if with_ckpt
+            else x.new_empty((0,)))
+    h_last = x.new_empty((bt, d, n))
+    with torch.cuda.device(x.device):
+        rc = library().mhs_scan_fwd_f32(
+            _ptr(x), _ptr(dt), _ptr(aneg), _ptr(b_in), _ptr(c_in), _ptr(y),
+            _ptr(ckpt) if with_ckpt else None, _ptr(h_last),
+            bt, t_len, d, n, chunk, _stream(x.device))
+    _check(rc, "mhs_scan_fwd_f32")
+    return y, ckpt, h_last
+
+
+@scan_fwd.register_fake
+def _scan_fwd_fake(x, dt, aneg, b_in, c_in, chunk, with_ckpt):
+    bt, t_len, d = x.shape
+    n = aneg.shape[1]
+    ckpt = (x.new_empty((bt, num_chunks(t_len, chunk), d, n)) if with_ckpt
+            else x.new_empty((0,)))
+    return torch.empty_like(x), ckpt, x.new_empty((bt, d, n))
+
+
+@torch.library.custom_op("mamba_hip::scan_bwd", mutates_args=())
+def scan_bwd(x: torch.Tensor, dt: torch.Tensor, aneg: torch.Tensor, b_in: torch.Tensor,
+             c_in: torch.Tensor, dy: torch.Tensor, dh_last: Optional[torch.Tensor],
+             ckpt: torch.Tensor, chunk: int
+             ) -> tuple[torch.Tensor, torch.Tensor, torch.Tensor, torch.Tensor, torch.Tensor]:
+    """(dx, ddt, dAneg, dB, dC) for the forward that produced `ckpt`."""
+    bt, t_len, d = x.shape
+    n = aneg.shape[1]
+    lib = library()
+    dx = torch.empty_like(x)
+    ddt = torch.empty_like(dt)
+    daneg = torch.empty_like(aneg)
+    db = torch.empty_like(b_in)
+    dc = torch.empty_like(c_in)
+    ws_bytes = int(lib.mhs_scan_bwd_workspace_bytes(bt, t_len, d, n, chunk))
+    if ws_bytes == 0:
+        raise HipScanError(f"no backward workspace size for shape {(bt, t_len, d, n)} chunk {chunk}")
+    ws = torch.empty(ws_bytes, dtype=torch.uint8, device=x.device)
+    with torch.cuda.device(x.device):
+        rc = lib.mhs_scan_bwd_f32(
+            _ptr(x), _ptr(dt), _ptr(aneg), _ptr(b_in), _ptr(c_in), _ptr(dy),
+            _ptr(dh_last), _ptr(ckpt), _ptr(dx), _ptr(ddt), _ptr(daneg), _ptr(db), _ptr(dc),
+            _ptr(ws), ws_bytes, bt, t_len, d, n, chunk, _stream(x.device))
+    _check(rc, "mhs_scan_bwd_f32")
+    return dx, ddt, daneg, db, dc
+
+
+@scan_bwd.register_fake
+def _scan_bwd_fake(x, dt, aneg, b_in, c_in, dy, dh_last, ckpt, chunk):
+    return (torch.empty_like(x), torch.empty_like(dt), torch.empty_like(aneg),
+            torch.empty_like(b_in), torch.empty_like(c_in))
+
+
+@torch.library.custom_op("mamba_hip::scan_step", mutates_args=("h",))
+def scan_step(h: torch.Tensor, x: torch.Tensor, dt: torch.Tensor, aneg: torch.Tensor,
+              b_in: torch.Tensor, c_in: torch.Tensor) -> torch.Tensor:
+    """One decode step in place on h (B,D,N); returns y (B,D)."""
+    bt, d, n = h.shape
+    y = x.new_empty((bt, d))
+    with torch.cuda.device(h.device):
+        rc = library().mhs_scan_step_f32(
+            _ptr(h), _ptr(x), _ptr(dt), _ptr(aneg), _ptr(b_in), _ptr(c_in), _ptr(y),
+            bt, d, n, _stream(h.device))
+    _check(rc, "mhs_scan_step_f32")
+    return y
+
+
+@scan_step.register_fake
+def _scan_step_fake(h, x, dt, aneg, b_in, c_in):
+    return x.new_empty((h.shape[0], h.shape[1]))

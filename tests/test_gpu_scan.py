@@ -1,0 +1,226 @@
+"""Parity of the gfx950 scan kernels with the float64 oracle and the fp32 torch
+reference (the reference's gates, tests/test_scan.py:86-230, on a ROCm GPU).
+
+Bar: per tensor, max|got - ref| / max|ref| <= 1e-4 against the float64 oracle
+(oracle/scan_oracle.c); the reference-style allclose(atol=1e-4, rtol=1e-3)
+against selective_scan_ref in fp32 on the same device.
+"""
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import torch
+
+from helpers import ATOL, RTOL, TOL, assert_close, rel_err, to_np
+from mamba_metal_scan_amd import _native, selective_scan, selective_scan_hip, selective_scan_ref
+from oracle import oracle
+
+pytestmark = pytest.mark.gpu
+
+DEV = "cuda"
+
+# (B, T, D, N): the reference's kernel shapes (tests/test_scan.py:86-95), the
+# CPU-runnable configuration (2x128x64x16) and edge shapes of the training
+# configuration (T not a multiple of the window, D not a multiple of 64,
+# T = 1, batch 1, d_state 8).
+REF_SHAPES = [(2, 64, 32, 16), (1, 100, 17, 16), (4, 63, 128, 16), (1, 1, 16, 16),
+              (2, 130, 40, 8), (3, 512, 856, 16)]
+EDGE_SHAPES = [(2, 128, 64, 16), (2, 1000, 64, 16), (2, 96, 1000, 16), (1, 1, 1536, 16),
+               (1, 512, 1536, 16), (4, 512, 256, 8), (2, 33, 70, 4), (2, 40, 64, 12),
+               (1, 20, 64, 5), (2, 48, 96, 32), (1, 24, 128, 64)]
+
+
+def _to_dev(arrs):
+    return [torch.from_numpy(a).to(DEV) for a in arrs]
+
+
+def _run_hip(inp, dy, chunk=None, dh_last=None):
+    """HIP forward + backward via autograd: (y, h_last, grads)."""
+    leaves = [t.clone().requires_grad_(True) for t in inp]
+    kw = {} if chunk is None else {"chunk": chunk}
+    y, h_last = selective_scan_hip(*leaves, return_state=True, **kw)
+    outs, gouts = [y], [dy]
+    if dh_last is not None:
+        outs.append(h_last)
+        gouts.append(dh_last)
+    grads = torch.autograd.grad(outs, leaves, grad_outputs=gouts)
+    torch.cuda.synchronize()
+    return y.detach(), h_last.detach(), grads
+
+
+@pytest.mark.parametrize("shape", REF_SHAPES + EDGE_SHAPES)
+def test_forward_and_gradients_match_the_oracle(shape):
+    bt, t_len, d, n = shape
+    print(f"[case] oracle parity {shape}", flush=True)
+    arrs = oracle.make_inputs(bt, t_len, d, n, seed=1000 + d, style="bench")
+    rng = np.random.default_rng(7)
+    dy = rng.standard_normal((bt, t_len, d), dtype=np.float32)
+    y_ref, _, h_ref = oracle.scan_fwd(*arrs)
+    grads_ref = oracle.scan_bwd(*arrs, dy)
+
+    y, h_last, grads = _run_hip(_to_dev(arrs), torch.from_numpy(dy).to(DEV))
+    assert y.shape == (bt, t_len, d) and y.dtype == torch.float32
+    assert_close("y", y, y_ref)
+    assert_close("h_last", h_last, h_ref)
+    for name, g, r in zip(("dx", "ddt", "dAneg", "dB", "dC"), grads, grads_ref):
+        assert g.shape == r.shape, name
+        assert_close(name, g, r)
+
+
+@pytest.mark.parametrize("shape", REF_SHAPES)
+def test_matches_torch_reference_in_fp32(shape):
+    """The reference's own gate: kernel vs selective_scan_ref on the device."""
+    bt, t_len, d, n = shape
+    print(f"[case] torch-ref parity {shape}", flush=True)
+    arrs = oracle.make_inputs(bt, t_len, d, n, seed=1337 + d, style="ref")
+    inp = _to_dev(arrs)
+    dy = torch.from_numpy(np.random.default_rng(3).standard_normal(
+        (bt, t_len, d), dtype=np.float32)).to(DEV)
+    y, _, g_hip = _run_hip(inp, dy)
+    leaves = [t.clone().requires_grad_(True) for t in inp]
+    ref = selective_scan_ref(*leaves)
+    g_ref = torch.autograd.grad(ref, leaves, grad_outputs=dy)
+    assert torch.allclose(y, ref, atol=ATOL, rtol=RTOL), rel_err(y, ref)
+    assert_close("y", y, ref)
+    for name, g, r in zip(("dx", "ddt", "dAneg", "dB", "dC"), g_hip, g_ref):
+        assert torch.allclose(g, r, atol=ATOL, rtol=RTOL), \
+            f"{name}: max delta {(g - r).abs().max().item():.3e} scale {r.abs().max().item():.3e}"
+        assert_close(name, g, r)
+
+
+def test_state_gradient_flows():
+    """dh_last (gradient of the returned state) reaches every input."""
+    bt, t_len, d, n = 2, 77, 96, 16
+    print("[case] dh_last", flush=True)
+    arrs = oracle.make_inputs(bt, t_len, d, n, seed=5, style="bench")
+    rng = np.random.default_rng(11)
+    dy = rng.standard_normal((bt, t_len, d), dtype=np.float32)
+    dh = rng.standard_normal((bt, d, n), dtype=np.float32)
+    grads_ref = oracle.scan_bwd(*arrs, dy, dh)
+    _, _, grads = _run_hip(_to_dev(arrs), torch.from_numpy(dy).to(DEV),
+                           dh_last=torch.from_numpy(dh).to(DEV))
+    for name, g, r in zip(("dx", "ddt", "dAneg", "dB", "dC"), grads, grads_ref):
+        assert_close(name, g, r)
+
+
+@pytest.mark.parametrize("chunk", [1, 7, 16, 64, 511, 512])
+def test_checkpoint_stride_is_not_a_result(chunk):
+    """Strides 1, 7, 64, 511, 512 (tests/test_scan.py:213-221) -- fwd and bwd."""
+    bt, t_len, d, n = 2, 512, 96, 16
+    print(f"[case] chunk {chunk}", flush=True)
+    arrs = oracle.make_inputs(bt, t_len, d, n, seed=1337 + 5, style="ref")
+    dy = np.random.default_rng(9).standard_normal((bt, t_len, d), dtype=np.float32)
+    y_ref, ck_ref, h_ref = oracle.scan_fwd(*arrs, chunk=chunk)
+    grads_ref = oracle.scan_bwd(*arrs, dy)
+    inp = _to_dev(arrs)
+    y, h_last, grads = _run_hip(inp, torch.from_numpy(dy).to(DEV), chunk=chunk)
+    assert_close("y", y, y_ref)
+    assert_close("h_last", h_last, h_ref)
+    for name, g, r in zip(("dx", "ddt", "dAneg", "dB", "dC"), grads, grads_ref):
+        assert_close(name, g, r)
+    # The checkpoints themselves: h at the end of every chunk.
+    _, ckpt, _ = torch.ops.mamba_hip.scan_fwd(*inp, chunk, True)
+    assert ckpt.shape == ck_ref.shape
+    assert_close("ckpt", ckpt, ck_ref)
+
+
+def test_returned_state_is_the_recurrence_state():
+    arrs = oracle.make_inputs(1, 100, 16, 16, seed=1337 + 7, style="ref")
+    inp = _to_dev(arrs)
+    _, state = selective_scan_hip(*inp, return_state=True)
+    _, ref_state = selective_scan_ref(*inp, return_state=True)
+    assert state.shape == ref_state.shape
+    assert torch.allclose(state, ref_state, atol=ATOL, rtol=RTOL)
+
+
+def test_training_shape_fwd_bwd_matches_the_oracle():
+    """Batch 16 x T 512 x d_inner 1536 x d_state 16 against the float64 oracle."""
+    bt, t_len, d, n = 16, 512, 1536, 16
+    print("[case] 16x512x1536x16", flush=True)
+    arrs = oracle.make_inputs(bt, t_len, d, n, seed=2024, style="bench")
+    dy = np.random.default_rng(1).standard_normal((bt, t_len, d), dtype=np.float32)
+    y_ref, _, h_ref = oracle.scan_fwd(*arrs)
+    grads_ref = oracle.scan_bwd(*arrs, dy)
+    y, h_last, grads = _run_hip(_to_dev(arrs), torch.from_numpy(dy).to(DEV))
+    errs = {"y": assert_close("y", y, y_ref), "h_last": assert_close("h_last", h_last, h_ref)}
+    for name, g, r in zip(("dx", "ddt", "dAneg", "dB", "dC"), grads, grads_ref):
+        errs[name] = assert_close(name, g, r)
+    print("[errors vs fp64]", {k: f"{v:.2e}" for k, v in errs.items()}, flush=True)
+
+
+def test_backward_is_bitwise_deterministic():
+    arrs = oracle.make_inputs(4, 200, 300, 16, seed=77, style="bench")
+    inp = _to_dev(arrs)
+    dy = torch.randn(4, 200, 300, device=DEV, generator=torch.Generator(DEV).manual_seed(0))
+    g1 = _run_hip(inp, dy)[2]
+    g2 = _run_hip(inp, dy)[2]
+    for a, b in zip(g1, g2):
+        assert torch.equal(a, b)
+
+
+@pytest.mark.parametrize("npl", [1, 2, 4])
+def test_every_state_split_agrees(npl):
+    """Forcing 1, 2 or 4 state lanes per wave gives the same results."""
+    bt, t_len, d, n = 2, 100, 130, 16
+    print(f"[case] npl {npl}", flush=True)
+    arrs = oracle.make_inputs(bt, t_len, d, n, seed=31, style="bench")
+    dy = np.random.default_rng(2).standard_normal((bt, t_len, d), dtype=np.float32)
+    y_ref, _, _ = oracle.scan_fwd(*arrs)
+    grads_ref = oracle.scan_bwd(*arrs, dy)
+    try:
+        _native.set_variant(npl)
+        y, _, grads = _run_hip(_to_dev(arrs), torch.from_numpy(dy).to(DEV))
+    finally:
+        _native.set_variant(0)
+    assert_close("y", y, y_ref)
+    for name, g, r in zip(("dx", "ddt", "dAneg", "dB", "dC"), grads, grads_ref):
+        assert_close(name, g, r)
+
+
+def test_gradients_match_finite_differences():
+    """Central differences of the kernel's own forward (tests/test_scan.py:133-161)."""
+    bt, t_len, d, n = 1, 24, 12, 8
+    arrs = oracle.make_inputs(bt, t_len, d, n, seed=1337 + 11, style="ref")
+    inp = _to_dev(arrs)
+    dy = torch.from_numpy(np.random.default_rng(4).standard_normal(
+        (bt, t_len, d), dtype=np.float32)).to(DEV)
+    _, _, grads = _run_hip(inp, dy)
+
+    def f(i, j, v):
+        p = [t.clone() for t in inp]
+        p[i].view(-1)[j] = v
+        return (selective_scan_hip(*p).double() * dy.double()).sum().item()
+
+    rng = np.random.default_rng(1337)
+    worst = 0.0
+    for i, t in enumerate(inp):
+        flat = t.reshape(-1)
+        for j in rng.permutation(flat.numel())[:6].tolist():
+            v = flat[j].item()
+            h = 1e-2 * max(1.0, abs(v))
+            num = (f(i, j, v + h) - f(i, j, v - h)) / (2 * h)
+            ana = grads[i].reshape(-1)[j].item()
+            worst = max(worst, abs(num - ana) / max(1.0, abs(num), abs(ana)))
+    assert worst < 0.05, f"finite-difference mismatch {worst:.3f}"
+
+
+def test_dispatch_on_device():
+    arrs = oracle.make_inputs(1, 8, 16, 4, seed=1, style="ref")
+    inp = _to_dev(arrs)
+    y = selective_scan(*inp, impl="auto")
+    assert y is not None and y.is_cuda
+    y2 = selective_scan(*inp, impl="metal")
+    assert torch.equal(y, y2)
+    with pytest.raises(RuntimeError, match="fp32"):
+        selective_scan(*[t.double() for t in inp], impl="hip")
+    with pytest.raises(RuntimeError, match="ROCm device"):
+        selective_scan(inp[0], inp[1], inp[2].cpu(), inp[3], inp[4], impl="hip")
+
+
+def test_empty_sequence():
+    x = torch.zeros(2, 0, 8, device=DEV)
+    aneg = torch.ones(8, 4, device=DEV)
+    b = torch.zeros(2, 0, 4, device=DEV)
+    y, h = selective_scan_hip(x, x, aneg, b, b, return_state=True)
+    assert y.shape == (2, 0, 8) and h.shape == (2, 8, 4)
+    assert torch.count_nonzero(h) == 0
