@@ -1,0 +1,219 @@
+#!/usr/bin/env python3
+"""Benchmark of the MI355X selective scan (one JSON line on stdout).
+
+Default workload: the fused selective scan, forward + backward, at the Mamba
+training shape batch 16 x T 512 x d_inner 1536 x d_state 16, fp32. One step is
+one forward + backward of the scan over one batch of synthetic inputs already
+resident in HBM (x, B, C, dy ~ N(0,1); dt = softplus(N(-4,1)); Aneg[d,n] = n+1),
+through the public autograd path (selective_scan_hip + backward).
+
+Reported:
+  value          whole-job tokens/s (batch*T per step / step time)
+  ms_per_step    ms per fwd+bwd step (wall clock, synchronized)
+  roofline       the dominant kernel launch (the backward: bwd kernel + its
+                 fixed-order reduction), timed live with HIP events on the
+                 launch stream: algorithmic bytes / average duration vs 8 TB/s
+  cpu_baseline   selective_scan(impl="torch") fwd+bwd on the host CPU, same
+                 inputs, all threads of the process's CPU share
+
+Other workloads (--workload): "train" (80M TinyMamba train step), "longt"
+(4 x 16384 x 2048 x 16 fwd+bwd, checkpoint-stride sweep), "infer" (prefill
+32 x 2048 x 4096 x 16 + recurrent decode steps).
+
+Only one GPU is used: --gpus N > 1 exits with a message.
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import time
+from pathlib import Path
+
+ROOT = Path(__file__).resolve().parent
+sys.path.insert(0, str(ROOT))
+
+METRIC = ("fwd+bwd scan ms & % HBM roofline (16x512x1536x16 fp32); 80M train tok/s")
+HBM_PEAK_GBS = 8000.0
+
+
+def scan_bytes(bt: int, t_len: int, d: int, n: int) -> dict:
+    """Algorithmic (compulsory fp32) bytes: fwd reads x, dt, B, C, Aneg and writes
+    y; bwd reads x, dt, dy, B, C, Aneg and writes dx, ddt, dB, dC, dAneg."""
+    e, s, a = bt * t_len * d, bt * t_len * n, d * n
+    return {"fwd": 4 * (3 * e + 2 * s + a), "bwd": 4 * (5 * e + 4 * s + 2 * a),
+            "fwd_bwd": 4 * (8 * e + 6 * s + 3 * a)}
+
+
+def cpu_threads() -> int:
+    try:
+        n = len(os.sched_getaffinity(0))
+    except AttributeError:
+        n = os.cpu_count() or 1
+    return max(1, min(n, 16))
+
+
+def make_inputs(bt, t_len, d, n, seed=2024):
+    """Seeded synthetic scan inputs drawn on the CPU (torch generator)."""
+    import torch
+    g = torch.Generator().manual_seed(seed)
+    x = torch.randn(bt, t_len, d, generator=g)
+    dt = torch.nn.functional.softplus(torch.randn(bt, t_len, d, generator=g) - 4.0)
+    aneg = torch.arange(1, n + 1, dtype=torch.float32).repeat(d, 1)
+    b_in = torch.randn(bt, t_len, n, generator=g)
+    c_in = torch.randn(bt, t_len, n, generator=g)
+    dy = torch.randn(bt, t_len, d, generator=g)
+    return x, dt, aneg, b_in, c_in, dy
+
+
+def time_events(fn, reps: int) -> float:
+    """Average GPU duration (ms) of fn() over reps, HIP events on the current stream."""
+    import torch
+    start = [torch.cuda.Event(enable_timing=True) for _ in range(reps)]
+    stop = [torch.cuda.Event(enable_timing=True) for _ in range(reps)]
+    for i in range(reps):
+        start[i].record()
+        fn()
+        stop[i].record()
+    torch.cuda.synchronize()
+    return sum(s.elapsed_time(e) for s, e in zip(start, stop)) / reps
+
+
+def cpu_baseline_scan(bt, t_len, d, n) -> dict:
+    """selective_scan(impl='torch') fwd+bwd on the CPU, full workload, one rep."""
+    import torch
+    from mamba_metal_scan_amd import selective_scan
+    threads = cpu_threads()
+    torch.set_num_threads(threads)
+    x, dt, aneg, b_in, c_in, dy = make_inputs(bt, t_len, d, n)
+    leaves = [t.clone().requires_grad_(True) for t in (x, dt, aneg, b_in, c_in)]
+    try:
+        t0 = time.perf_counter()
+        y = selective_scan(*leaves, impl="torch")
+        y.backward(dy)
+        el = time.perf_counter() - t0
+    except (RuntimeError, MemoryError) as exc:   # e.g. out of host memory
+        return {"value": None, "unit": "tokens/s", "cores": threads, "kind": "port",
+                "sample": f"selective_scan(impl='torch') fwd+bwd {bt}x{t_len}x{d}x{n}: "
+                          f"failed ({type(exc).__name__})"}
+    cpu_model = ""
+    try:
+        for line in open("/proc/cpuinfo"):
+            if line.startswith("model name"):
+                cpu_model = line.split(":", 1)[1].strip()
+                break
+    except OSError:
+        pass
+    return {"value": bt * t_len / el, "unit": "tokens/s", "cores": threads, "kind": "port",
+            "ms_per_step": el * 1e3, "cpu": cpu_model,
+            "sample": f"selective_scan(impl='torch') fwd+bwd, full {bt}x{t_len}x{d}x{n} "
+                      f"workload, 1 rep, torch CPU threads={threads}"}
+
+
+def bench_scan(args) -> dict:
+    import torch
+    from mamba_metal_scan_amd import _native, selective_scan_hip
+    bt, t_len, d, n = args.batch, args.seqlen, args.d_inner, args.d_state
+    chunk = args.chunk
+    dev = torch.device("cuda", 0)
+    x, dt, aneg, b_in, c_in, dy = (t.to(dev) for t in make_inputs(bt, t_len, d, n))
+    leaves = [t.clone().requires_grad_(True) for t in (x, dt, aneg, b_in, c_in)]
+
+    def step():
+        for t in leaves:
+            t.grad = None
+        y = selective_scan_hip(*leaves, chunk=chunk)
+        y.backward(dy)
+
+    for _ in range(args.warmup):
+        step()
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(args.steps):
+        step()
+    torch.cuda.synchronize()
+    elapsed = time.perf_counter() - t0
+    ms = elapsed * 1e3 / args.steps
+
+    # Per-launch timing of the forward and backward ops on the launch stream.
+    xc, dtc, ac, bc, cc = (t.detach() for t in leaves)
+    _, ckpt, _ = torch.ops.mamba_hip.scan_fwd(xc, dtc, ac, bc, cc, chunk, True)
+    reps = max(args.steps, 10)
+    fwd_ms = time_events(lambda: torch.ops.mamba_hip.scan_fwd(xc, dtc, ac, bc, cc, chunk, True),
+                         reps)
+    bwd_ms = time_events(lambda: torch.ops.mamba_hip.scan_bwd(xc, dtc, ac, bc, cc, dy, None,
+                                                              ckpt, chunk), reps)
+    nbytes = scan_bytes(bt, t_len, d, n)
+    bwd_gbs = nbytes["bwd"] / (bwd_ms * 1e-3) / 1e9
+    fwd_gbs = nbytes["fwd"] / (fwd_ms * 1e-3) / 1e9
+    pair_gbs = nbytes["fwd_bwd"] / ((fwd_ms + bwd_ms) * 1e-3) / 1e9
+    traffic = None
+    tfile = ROOT / "profiles" / "scan_bwd_16x512x1536x16_traffic.json"
+    if tfile.exists() and chunk == 16 and (bt, t_len, d, n) == (16, 512, 1536, 16):
+        try:
+            traffic = json.loads(tfile.read_text()).get("hbm_bytes_per_launch")
+        except (OSError, ValueError):
+            traffic = None
+    out = {
+        "metric": METRIC,
+        "value": bt * t_len / (ms * 1e-3),
+        "unit": "tokens/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": ms,
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "f32",
+        "data": "synthetic (x,B,C,dy~N(0,1); dt=softplus(N(-4,1)); Aneg[d,n]=n+1)",
+        "config": {"workload": f"selective_scan fwd+bwd {bt}x{t_len}x{d}x{n}",
+                   "batch": bt, "seqlen": t_len, "d_inner": d, "d_state": n, "chunk": chunk,
+                   "parallelism": "single GPU"},
+        "roofline": {"bound": "hbm", "achieved": bwd_gbs, "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": bwd_gbs / HBM_PEAK_GBS, "traffic": traffic,
+                     "kernel": "scan backward launch (bwd_kernel + bwd_reduce_kernel)",
+                     "avg_ms": bwd_ms, "algorithmic_bytes": nbytes["bwd"]},
+        "scan_fwd": {"avg_ms": fwd_ms, "achieved_GBs": fwd_gbs,
+                     "algorithmic_bytes": nbytes["fwd"]},
+        "scan_fwd_bwd": {"avg_ms": fwd_ms + bwd_ms, "achieved_GBs": pair_gbs,
+                         "frac": pair_gbs / HBM_PEAK_GBS,
+                         "algorithmic_bytes": nbytes["fwd_bwd"]},
+        "library_version": hex(_native.library().mhs_version()),
+    }
+    if not args.no_cpu_baseline:
+        out["cpu_baseline"] = cpu_baseline_scan(bt, t_len, d, n)
+    return out
+
+
+def main() -> int:
+    ap = argparse.ArgumentParser(description=__doc__,
+                                 formatter_class=argparse.RawDescriptionHelpFormatter)
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=50)
+    ap.add_argument("--warmup", type=int, default=10)
+    ap.add_argument("--workload", default="scan", choices=["scan"])
+    ap.add_argument("--batch", type=int, default=16)
+    ap.add_argument("--seqlen", type=int, default=512)
+    ap.add_argument("--d-inner", dest="d_inner", type=int, default=1536)
+    ap.add_argument("--d-state", dest="d_state", type=int, default=16)
+    ap.add_argument("--chunk", type=int, default=16)
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    args = ap.parse_args()
+
+    if args.gpus != 1:
+        print(f"bench.py measures one GPU: this build runs on a single MI355X and has no "
+              f"multi-GPU path (asked for --gpus {args.gpus}).", file=sys.stderr)
+        return 2
+    import torch
+    if not torch.cuda.is_available():
+        print("bench.py needs a ROCm GPU (torch.cuda.is_available() is False)", file=sys.stderr)
+        return 1
+    out = bench_scan(args)
+    print(json.dumps(out), flush=True)
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())
