@@ -37,9 +37,10 @@ extern "C" {
 #define MHS_EINVAL 1   /* bad argument: null pointer, size, d_state unsupported */
 #define MHS_EHIP 2     /* a HIP runtime call or kernel launch failed */
 
-/* Largest supported d_state. Supported: any d_state in [1, 16], even values up
- * to 32, multiples of 4 up to MHS_MAX_DSTATE. The reference's Metal kernels
- * require d_state % 4 == 0 (scan.py:274-276). */
+/* Largest supported d_state; every d_state in [1, MHS_MAX_DSTATE] is supported
+ * (padded internally with zero states). The reference's Metal kernels
+ * require d_state % 4 == 0 (scan.py:274-276). Also required: d_inner <= 2^24
+ * and d_inner * d_state * 4 < 2^31. */
 #define MHS_MAX_DSTATE 64
 
 /* Library version, (major << 16) | (minor << 8) | patch. */
@@ -58,11 +59,12 @@ int64_t mhs_num_chunks(int64_t seqlen, int64_t chunk);
  * module constant SSM_CHUNK, mamba_metal/scan.py:58). */
 int64_t mhs_preferred_chunk(int64_t d_state);
 
-/* Tuning knob, process-wide: force the number of state lanes each wave
- * carries per channel (1, 2 or 4; 0 restores the automatic choice). Ignored
- * for a d_state it does not divide. No counterpart in the reference (its
- * Metal kernels keep all d_state lanes in one thread, scan.py:67-69). */
-int mhs_set_variant(int state_lanes_per_wave);
+/* Tuning knob, process-wide: force the number of d_state entries each GPU
+ * lane carries per channel (2 or 4; 0 restores the automatic choice: 2 up to
+ * d_state 32, 4 above). With 2, d_state above 32 becomes unsupported. No
+ * counterpart in the reference (its Metal kernels keep all d_state entries of
+ * a channel in one thread, scan.py:67-69). */
+int mhs_set_variant(int states_per_lane);
 
 /*
  * Forward scan. Replaces the reference's `lib.ssm_fwd(x, dt, Aneg, Bm, Cm, y,

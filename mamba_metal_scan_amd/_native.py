@@ -95,9 +95,9 @@ def preferred_chunk(d_state: int) -> int:
     return int(library().mhs_preferred_chunk(d_state))
 
 
-def set_variant(state_lanes_per_wave: int) -> None:
-    """Force 1, 2 or 4 state lanes per wave (0 = automatic), process-wide."""
-    _check(library().mhs_set_variant(int(state_lanes_per_wave)), "mhs_set_variant")
+def set_variant(states_per_lane: int) -> None:
+    """Force 2 or 4 states per lane (0 = automatic), process-wide."""
+    _check(library().mhs_set_variant(int(states_per_lane)), "mhs_set_variant")
 
 
 # --------------------------------------------------------------- custom ops

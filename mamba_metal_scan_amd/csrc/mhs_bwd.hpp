@@ -9,28 +9,44 @@
 //   dAneg  = -sum_{b,t} dt_t G_tn hm_tn
 //   dB_tn  = sum_d G_tdn dt_td x_td          dC_tn = sum_d dy_td h_tdn
 //
-// MI355X mapping. Same block decomposition as the forward (64 channels x one
-// batch row per block, G waves x NPL states). Chunks of K <= KI steps are
-// walked last to first. For each chunk the block stages x, dt, dy and B, C in
-// LDS (prefetched one chunk ahead), every lane recomputes its chunk of h and
-// dA from the checkpoint into VGPRs (hs[KI][NPL], da[KI][NPL]; nothing goes to
-// global scratch), then walks the chunk backwards carrying G in VGPRs across
-// chunk boundaries. It uses hm = dA * h_{t-1} from the recomputed chunk, so it
-// never subtracts h_t - b_t.
-//   dx / ddt: the per-wave partial sums over the wave's NPL states are
-//             combined across the G waves through LDS, written once.
-//   dAneg:    accumulated per lane over the whole walk (no cross-lane traffic),
-//             written once per (b, d, n) to a workspace slot.
-//   dB / dC:  sums over the 64 channels of the block. Each wave writes its
-//             per-lane G (weight dt*x) and h (weight dy) rows to LDS and
-//             reduces RROWS rows at a time: LPR = 64/RROWS lanes per row, each
-//             doing RROWS fused multiply-adds over its slice of channels,
-//             then a DPP tree over the LPR lanes. The per-block sums go to a
-//             workspace slot; bwd_reduce_kernel adds the blocks in a fixed
-//             order, so the result does not depend on scheduling.
+// MI355X mapping. Same block decomposition as the forward (32 channels x one
+// batch row per block; lane = (wave, half, channel), NPL states per lane,
+// d_state padded with zero states to NP = 2*G*NPL). Chunks of K <= 16 steps
+// are walked last to first. Each chunk takes two phases and two barriers:
+//   recompute: every lane rebuilds its chunk of dA and h from the checkpoint
+//     into VGPRs (da[16][NPL], hs[16][NPL]; nothing goes to global scratch):
+//     all dA and inputs b = B*dt*x first (independent), then the short chain
+//     h = dA*h + b. In the same straight-line code the waves also finish the
+//     previous (later-in-time) chunk (dx, ddt, dB/dC block sums), store the
+//     staged inputs of the next chunk into the other LDS buffer and issue the
+//     global loads of the chunk after that. All global accesses are
+//     bounds-checked buffer accesses whose resources end at the chunk's last
+//     step, so chunk and tensor edges need no branches.
+//   reverse: walks the chunk backwards carrying G in VGPRs across chunk
+//     boundaries, with hm = dA * h_{t-1} from the recomputed chunk (no
+//     h_t - b_t cancellation).
+// Steps k >= len of a chunk (K < 16, or the tail of the sequence) see zero
+// inputs: dA = 1 and b = 0 there, so they are identity steps for h and G, add
+// zero to every accumulated gradient, and their outputs are not written.
+//   dx / ddt: per lane s1 = sum G*B, s2 = sum Aneg*G*hm over its NPL states.
+//             The two half-waves (same channels, different states) are added
+//             with one v_permlane32_swap (lanes 0-31 keep s1, 32-63 s2); the
+//             per-wave values go to LDS and, in the next chunk's recompute
+//             phase, are summed over the G waves in a fixed order and written
+//             once, coalesced.
+//   dAneg:    accumulated per lane over the whole walk, written once per
+//             (b, d, n) to a workspace slot.
+//   dB / dC:  sums over the block's 32 channels. Each wave writes its
+//             per-lane G rows (weight dt*x) and h rows (weight dy) for two
+//             steps to LDS and reduces them: each lane does RR fused
+//             multiply-adds over a slice of channels (128-bit reads), then a
+//             DPP tree over the L lanes of the slice. The block sums are
+//             copied to a workspace slot; bwd_reduce_kernel adds the blocks in
+//             a fixed order, so the backward is bit-for-bit reproducible.
 #pragma once
 
 #include "mhs_common.hpp"
+#include "mhs_fwd.hpp"
 
 namespace mhs {
 
@@ -48,255 +64,287 @@ struct BwdArgs {
   float* wsB;            // (nblk, batch, T, N)
   float* wsC;            // (nblk, batch, T, N)
   float* wsA;            // (batch, D, N)
-  int batch, T, D, K, nchunk;
-  int vec4;              // x, dt, dy 16-byte aligned and D % 4 == 0
+  int batch, T, D, N, K, nchunk;
 };
 
-__host__ __device__ constexpr int bwd_lds_floats(int KI, int G, int NPL, int RROWS) {
-  return KI * 64 * 3                        // x, dt, dy tiles
-         + 2 * KI * G * NPL                 // B, C tiles
-         + G * KI * 64 * 2                  // per-wave (s1, s2) partials
-         + G * RROWS * 64                   // per-wave reduction rows
-         + G * (RROWS / (2 * NPL)) * 2 * 64;  // per-wave reduction weights
+constexpr int kRowStride = 68;   // reduction row pitch (64 lanes + 4: conflict-free reads)
+constexpr int kSB = 2;           // steps per reduction batch
+
+// One staging buffer (the kernel keeps two) and the single-buffered rest.
+__host__ __device__ constexpr int bwd_buf_floats(int G, int NPL) {
+  return 3 * kCH * kSteps               // dt, dy, dt*x (channel-major)
+         + 2 * kSteps * kCH             // dt*x, dy (step-major weights)
+         + 2 * kSteps * 2 * G * NPL;    // B, C tiles
+}
+__host__ __device__ constexpr int bwd_lds_floats(int G, int NPL) {
+  return 2 * bwd_buf_floats(G, NPL)
+         + G * 64 * kSteps                       // (s1, s2) per wave
+         + 2 * kSteps * 2 * G * NPL              // dB, dC block sums of a chunk
+         + G * (2 * NPL * kSB) * kRowStride;     // reduction rows
 }
 
-template <int NPL, int KI, int MAXG, int PER, int PERS, int RROWS>
-__global__ void __launch_bounds__(64 * MAXG)
+template <int NPL, int G, int MINW>
+__global__ void __launch_bounds__(64 * G, MINW)
 bwd_kernel(BwdArgs a) {
+  constexpr int NT = 64 * G;
+  constexpr int NP = 2 * G * NPL;
+  constexpr int BUF = bwd_buf_floats(G, NPL);
+  constexpr int PER = (kCH * kQuads + NT - 1) / NT;
+  constexpr int PERS = (kSteps * NP + NT - 1) / NT;
+  constexpr int FT = (kSteps / 2 * kCH + NT - 1) / NT;      // dx/ddt tasks per thread
+  constexpr int FK = kSteps * NP / NT;                      // dB (or dC) copies per thread
   constexpr int RPS = 2 * NPL;          // reduction rows per time step
-  constexpr int SB = RROWS / RPS;       // time steps per reduction batch
-  constexpr int LPR = 64 / RROWS;       // lanes per reduced row
-  static_assert(RROWS % RPS == 0 && 64 % RROWS == 0 && KI % SB == 0, "bad reduction shape");
-  static_assert(RROWS % 4 == 0, "rows are read as float4");
+  constexpr int RR = RPS * kSB;         // rows per reduction batch (= partials per lane)
+  constexpr int L = 64 / (RR * 2);      // lanes per half-row
+  static_assert(NPL == 2 || NPL == 4, "two or four states per lane");
+  static_assert(RR % 4 == 0 && 64 % (RR * 2) == 0 && L >= 1 && L <= 16, "bad reduction shape");
+  static_assert(FK * NT == kSteps * NP, "dB/dC copy-out must tile the block");
 
   extern __shared__ float lds[];
-  const int G = blockDim.x >> 6;
-  const int N = G * NPL;
+  const int N = a.N;
   const int tid = threadIdx.x;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int lane = tid & 63;
+  const int hh = lane >> 5;
+  const int c = lane & 31;
+  const int q = wave * 2 + hh;
+  const int n0 = q * NPL;
   const int b = blockIdx.y;
-  const int d0 = blockIdx.x * 64;
-  const int d = d0 + lane;
+  const int d0 = blockIdx.x * kCH;
+  const int d = d0 + c;
   const bool act = d < a.D;
-  const int n0 = wave * NPL;
   const int T = a.T, D = a.D, K = a.K;
+  const int nvalid = N - n0;
+  const int nch = a.nchunk;
 
-  float* tX = lds;
-  float* tD = tX + KI * 64;
-  float* tY = tD + KI * 64;
-  float* tB = tY + KI * 64;
-  float* tC = tB + KI * N;
-  float2* tS = reinterpret_cast<float2*>(tC + KI * N);
-  const float* wB = tB + wave * KI * NPL;  // this wave's [KI][NPL] slice
-  const float* wC = tC + wave * KI * NPL;
-  float* tR = reinterpret_cast<float*>(tS + G * KI * 64) + wave * RROWS * 64;
-  float* tW = reinterpret_cast<float*>(tS + G * KI * 64) + G * RROWS * 64 + wave * SB * 2 * 64;
+  float* tS = lds + 2 * BUF;                          // [G][64][16]
+  float* tDBC = tS + G * 64 * kSteps;                 // [2][16][NP]
+  float* tR = tDBC + 2 * kSteps * NP + wave * RR * kRowStride;
+  // Staging buffer j: dt, dy, dt*x (channel-major), dt*x, dy (step-major), B, C.
+  constexpr int oDY = kCH * kSteps, oDTX = 2 * kCH * kSteps, oWDTX = 3 * kCH * kSteps,
+                oWDY = 4 * kCH * kSteps, oB = 5 * kCH * kSteps, oC = oB + kSteps * NP;
 
+  const size_t slice = (size_t)D * N;
+  const unsigned slice_bytes = 4u * (unsigned)slice;
+  const unsigned st_lane = act ? 4u * ((unsigned)d * (unsigned)N + (unsigned)n0) : kOOB;
   float an[NPL], a2[NPL], g[NPL], acc[NPL], dan[NPL];
 #pragma unroll
   for (int j = 0; j < NPL; ++j) {
-    an[j] = act ? a.aneg[(size_t)d * N + n0 + j] : 0.f;
+    an[j] = (act && j < nvalid) ? a.aneg[(size_t)d * N + n0 + j] : 0.f;
     a2[j] = -an[j] * kLog2e;
-    g[j] = (a.dh_last != nullptr && act) ? a.dh_last[((size_t)b * D + d) * N + n0 + j] : 0.f;
     acc[j] = 0.f;
     dan[j] = 1.f;
   }
+  const float* dhl = a.dh_last != nullptr ? a.dh_last + (size_t)b * slice : a.aneg;
+  load_states<NPL>(g, GBuf(dhl, a.dh_last != nullptr ? slice_bytes : 0u), st_lane, nvalid);
 
   const size_t row0 = (size_t)b * T;
-  const float* xb = a.x + row0 * D + d0;
-  const float* db = a.dt + row0 * D + d0;
-  const float* yb = a.dy + row0 * D + d0;
-  const float* Bb = a.B + row0 * N;
-  const float* Cb = a.C + row0 * N;
-  const float* ckb = a.ckpt + (size_t)b * a.nchunk * D * N + (size_t)d * N + n0;
-
-  const TileLoader<KI, PER> tl(tid, blockDim.x);
-  const RowLoader<PERS, KI, NPL> rl(tid, blockDim.x, N);
+  const QuadLoader<kCH, PER> ql(tid, NT, D, d0);
+  const RowLoader<PERS, NPL> rl(tid, NT, N, NP);
   float4 px[PER], pd[PER], py[PER];
   float pb[PERS], pc[PERS], ph[NPL];
 
-  // Prefetch the last chunk.
-  {
-    const int c = a.nchunk - 1;
-    const int t0 = c * K;
-    const int len = min(K, T - t0);
-    const size_t off = (size_t)t0;
-    tl.load(px, xb + off * D, len, D, d0, a.vec4);
-    tl.load(pd, db + off * D, len, D, d0, a.vec4);
-    tl.load(py, yb + off * D, len, D, d0, a.vec4);
-    rl.load(pb, Bb + off * N, len, N);
-    rl.load(pc, Cb + off * N, len, N);
+  // Chunk ci (any integer): first step and length (0 outside the sequence).
+  auto chunk_t0 = [&](int ci) { return min(max(ci, 0) * K, T - 1); };
+  auto chunk_len = [&](int ci) { return ci < 0 ? 0 : max(0, min(K, T - ci * K)); };
+  // Resource over one chunk of a (batch, T, D) tensor from channel d0 on.
+  auto chunk_buf = [&](const float* base, int ci) {
+    const int len = chunk_len(ci);
+    return GBuf(base + (row0 + chunk_t0(ci)) * D + d0, len > 0 ? 4u * (unsigned)(len * D - d0) : 0u);
+  };
+  auto load_sub = [&](int ci) {           // global -> staging registers
+    const int len = chunk_len(ci);
+    const GBuf gs_b(a.B + (row0 + chunk_t0(ci)) * N, 4u * (unsigned)(len * N));
+    const GBuf gs_c(a.C + (row0 + chunk_t0(ci)) * N, 4u * (unsigned)(len * N));
+    ql.load(px, chunk_buf(a.x, ci), D);
+    ql.load(pd, chunk_buf(a.dt, ci), D);
+    ql.load(py, chunk_buf(a.dy, ci), D);
+    rl.load(pb, gs_b);
+    rl.load(pc, gs_c);
+  };
+  // h at the start of chunk ci: checkpoint ci-1, or 0 for the first chunk.
+  auto load_h0 = [&](int ci) {
+    load_states<NPL>(ph, GBuf(a.ckpt + ((size_t)b * nch + max(ci - 1, 0)) * slice,
+                              ci > 0 ? slice_bytes : 0u), st_lane, nvalid);
+  };
+  auto store_sub = [&](int j) {           // staging registers -> buffer j
+    float* s0 = lds + j * BUF;
+    ql.store_cm(s0, pd);
+    ql.store_cm(s0 + oDY, py);
+    ql.store_cm_product(s0 + oDTX, pd, px);
+    ql.store_sm_product(s0 + oWDTX, pd, px);
+    ql.store_sm(s0 + oWDY, py);
+    rl.store(s0 + oB, pb);
+    rl.store(s0 + oC, pc);
+  };
+  // dx, ddt and the dB, dC block sums of chunk ci, from tS and tDBC (which
+  // hold them until the next reverse phase). x and dt come from global memory
+  // (L2): the chunk's staging buffer is being refilled at the same time.
+  auto finalize = [&](int ci) {
+    const GBuf gx = chunk_buf(a.x, ci), gdt = chunk_buf(a.dt, ci);
+    const GBuf gdx = chunk_buf(a.dx, ci), gddt = chunk_buf(a.ddt, ci);
 #pragma unroll
-    for (int j = 0; j < NPL; ++j) ph[j] = 0.f;
-    if (c > 0 && act) load_vec<NPL>(ph, ckb + (size_t)(c - 1) * D * N);
-  }
-
-  for (int c = a.nchunk - 1; c >= 0; --c) {
-    const int t0 = c * K;
-    const int len = min(K, T - t0);
-    float hc[NPL];
+    for (int f = 0; f < FT; ++f) {
+      const int task0 = tid + f * NT;
+      const bool ok = task0 < kSteps / 2 * kCH;
+      const int task = ok ? task0 : 0;
+      const int cc = task % kCH, k = 2 * (task / kCH);
+      const unsigned o0 = (ok && d0 + cc < D) ? 4u * ((unsigned)k * (unsigned)D + cc) : kOOB;
+      const unsigned o1 = o0 == kOOB ? kOOB : o0 + 4u * (unsigned)D;
+      const float x0 = gx.ld(o0), x1 = gx.ld(o1), t0v = gdt.ld(o0), t1v = gdt.ld(o1);
+      float s1a = 0.f, s1b = 0.f, s2a = 0.f, s2b = 0.f;
 #pragma unroll
-    for (int j = 0; j < NPL; ++j) hc[j] = ph[j];
-    tl.store(tX, px);
-    tl.store(tD, pd);
-    tl.store(tY, py);
-    rl.store(tB, pb);
-    rl.store(tC, pc);
-    if (c > 0) {
-      const size_t off = (size_t)(t0 - K);
-      tl.load(px, xb + off * D, K, D, d0, a.vec4);
-      tl.load(pd, db + off * D, K, D, d0, a.vec4);
-      tl.load(py, yb + off * D, K, D, d0, a.vec4);
-      rl.load(pb, Bb + off * N, K, N);
-      rl.load(pc, Cb + off * N, K, N);
-#pragma unroll
-      for (int j = 0; j < NPL; ++j) ph[j] = 0.f;
-      if (c > 1 && act) load_vec<NPL>(ph, ckb + (size_t)(c - 2) * D * N);
+      for (int w = 0; w < G; ++w) {
+        const float2 v1 = lds2(tS + w * 64 * kSteps + cm_elem(cc, k));
+        const float2 v2 = lds2(tS + w * 64 * kSteps + cm_elem(kCH + cc, k));
+        s1a += v1.x; s1b += v1.y;
+        s2a += v2.x; s2b += v2.y;
+      }
+      gdx.st(t0v * s1a, o0);
+      gdx.st(t1v * s1b, o1);
+      gddt.st(__builtin_fmaf(x0, s1a, -s2a), o0);
+      gddt.st(__builtin_fmaf(x1, s1b, -s2b), o1);
     }
-    __syncthreads();
-
-    // Recompute the chunk's h and dA in registers. Steps k >= len of a short
-    // chunk see zero-filled tiles (dt = x = dy = B = C = 0): dA = 1 and b = 0
-    // there, so they are exact identity steps for h and for G, contribute
-    // zero to every accumulated gradient, and their outputs are not written.
-    // That keeps this loop free of per-step branches.
-    float hs[KI][NPL], da[KI][NPL];
-    {
-      float dtv = tD[lane], xv = tX[lane], Bv[NPL];
-      load_vec<NPL>(Bv, wB);
+    const int len = chunk_len(ci);
+    const size_t wrow = ((size_t)blockIdx.x * a.batch + b) * T + chunk_t0(ci);
+    const unsigned sbytes = 4u * (unsigned)(len * N);
+    const GBuf gwb(a.wsB + wrow * N, sbytes), gwc(a.wsC + wrow * N, sbytes);
 #pragma unroll
-      for (int k = 0; k < KI; ++k) {
-        float dtn = 0.f, xn = 0.f, Bn[NPL];
-        if (k + 1 < KI) {
-          dtn = tD[(k + 1) * 64 + lane];
-          xn = tX[(k + 1) * 64 + lane];
-          load_vec<NPL>(Bn, wB + (k + 1) * NPL);
-        }
-        const float dtx = dtv * xv;
+    for (int f = 0; f < FK; ++f) {
+      const int r = tid + f * NT;                 // (k, n) of the tile, n fastest
+      const int k = r / NP, n = r % NP;
+      const unsigned o = n < N ? 4u * (unsigned)(k * N + n) : kOOB;
+      gwb.st(tDBC[r], o);
+      gwc.st(tDBC[kSteps * NP + r], o);
+    }
+  };
+
+  // Prologue: the last chunk staged in LDS buffer 0, the one before it in
+  // the staging registers.
+  load_sub(nch - 1);
+  load_h0(nch - 1);
+  store_sub(0);
+  float hc[NPL];                          // h at the start of the current chunk
+#pragma unroll
+  for (int j = 0; j < NPL; ++j) hc[j] = ph[j];
+  load_sub(nch - 2);
+  load_h0(nch - 2);
+  __syncthreads();
+
+  for (int i = 0; i < nch; ++i) {
+    const int ci = nch - 1 - i;
+    const float* s0 = lds + (i & 1) * BUF;
+    const float* gB = s0 + oB + q * kSteps * NPL;
+    const float* gC = s0 + oC + q * kSteps * NPL;
+
+    // ---- recompute phase, with the pipeline work of the neighbouring chunks
+    float da[kSteps][NPL], hs[kSteps][NPL];
+#pragma unroll
+    for (int m = 0; m < kQuads; ++m) {
+      float dts[4], dtxs[4], Bq[4][NPL];
+      f4_to(dts, lds4(s0 + cm_quad(c, m)));
+      f4_to(dtxs, lds4(s0 + oDTX + cm_quad(c, m)));
+      load_quad_rows<NPL>(Bq, gB, m);
+#pragma unroll
+      for (int s = 0; s < 4; ++s)
 #pragma unroll
         for (int j = 0; j < NPL; ++j) {
-          da[k][j] = exp2_hw(dtv * a2[j]);
-          hs[k][j] = __builtin_fmaf(da[k][j], k == 0 ? hc[j] : hs[k - 1][j], Bv[j] * dtx);
+          da[4 * m + s][j] = exp2_hw(dts[s] * a2[j]);
+          hs[4 * m + s][j] = Bq[s][j] * dtxs[s];      // b_k, turned into h_k below
         }
-        step_fence();
-        if (k + 1 < KI) {
-          dtv = dtn;
-          xv = xn;
-#pragma unroll
-          for (int j = 0; j < NPL; ++j) Bv[j] = Bn[j];
-        }
-      }
+      if (m == 0) finalize(ci + 1);        // no-op stores past the sequence end
+      if (m == 1) store_sub((i + 1) & 1);  // chunk ci-1 (unused when ci == 0)
+      if (m == 2) load_sub(ci - 2);        // loads nothing when ci < 2
+      step_fence();
     }
-
-    // Reverse walk.
-    lds_reload_point();
-    float dtv = tD[(KI - 1) * 64 + lane], xv = tX[(KI - 1) * 64 + lane];
-    float dyv = tY[(KI - 1) * 64 + lane];
-    float Bv[NPL], Cv[NPL];
-    load_vec<NPL>(Bv, wB + (KI - 1) * NPL);
-    load_vec<NPL>(Cv, wC + (KI - 1) * NPL);
 #pragma unroll
-    for (int k = KI - 1; k >= 0; --k) {
-      const int slot = k % SB;
-      float dtn = 0.f, xn = 0.f, dyn = 0.f, Bn[NPL], Cn[NPL];
-      if (k > 0) {
-        dtn = tD[(k - 1) * 64 + lane];
-        xn = tX[(k - 1) * 64 + lane];
-        dyn = tY[(k - 1) * 64 + lane];
-        load_vec<NPL>(Bn, wB + (k - 1) * NPL);
-        load_vec<NPL>(Cn, wC + (k - 1) * NPL);
-      }
-      {
-        const float dtx = dtv * xv;
+    for (int k = 0; k < kSteps; ++k)
+#pragma unroll
+      for (int j = 0; j < NPL; ++j)
+        hs[k][j] = __builtin_fmaf(da[k][j], k == 0 ? hc[j] : hs[k - 1][j], hs[k][j]);
+    __syncthreads();   // finalize(ci+1) is done with tS / tDBC
+
+    // ---- reverse phase
+#pragma unroll
+    for (int m = kQuads - 1; m >= 0; --m) {
+      float dts[4], dys[4], Bq[4][NPL], Cq[4][NPL], s1q[4], s2q[4];
+      f4_to(dts, lds4(s0 + cm_quad(c, m)));
+      f4_to(dys, lds4(s0 + oDY + cm_quad(c, m)));
+      load_quad_rows<NPL>(Bq, gB, m);
+      load_quad_rows<NPL>(Cq, gC, m);
+#pragma unroll
+      for (int s = 3; s >= 0; --s) {
+        const int k = 4 * m + s;
+        const int slot = k % kSB;
         float s1 = 0.f, s2 = 0.f;
 #pragma unroll
         for (int j = 0; j < NPL; ++j) {
-          const float gj = __builtin_fmaf(dan[j], g[j], dyv * Cv[j]);
+          const float gj = __builtin_fmaf(dan[j], g[j], dys[s] * Cq[s][j]);
           const float hm = da[k][j] * (k == 0 ? hc[j] : hs[k - 1][j]);
-          s1 = __builtin_fmaf(gj, Bv[j], s1);
-          const float q = gj * hm;
-          s2 = __builtin_fmaf(an[j], q, s2);
-          acc[j] = __builtin_fmaf(dtv, q, acc[j]);
+          s1 = __builtin_fmaf(gj, Bq[s][j], s1);
+          const float qv = gj * hm;
+          s2 = __builtin_fmaf(an[j], qv, s2);
+          acc[j] = __builtin_fmaf(dts[s], qv, acc[j]);
           g[j] = gj;
           dan[j] = da[k][j];
         }
-        tS[(wave * KI + k) * 64 + lane] = make_float2(s1, s2);
+        s1q[s] = s1;
+        s2q[s] = s2;
 #pragma unroll
         for (int j = 0; j < NPL; ++j) {
-          tR[(slot * RPS + j) * 64 + lane] = g[j];
-          tR[(slot * RPS + NPL + j) * 64 + lane] = hs[k][j];
+          tR[(slot * RPS + j) * kRowStride + lane] = g[j];
+          tR[(slot * RPS + NPL + j) * kRowStride + lane] = hs[k][j];
         }
-        tW[(slot * 2 + 0) * 64 + lane] = dtx;
-        tW[(slot * 2 + 1) * 64 + lane] = dyv;
-      }
-      if (slot == 0) {
-        // Rows for steps k .. k+SB-1 are in place; rows of steps >= len are
-        // identity-step rows and are not written out.
-        wave_lds_sync();
-        const int r = lane / LPR;
-        const int seg = lane % LPR;
-        const int slot_r = r / RPS;
-        const int kind = (r % RPS) / NPL;
-        const int j = r % NPL;
-        const float* rr = tR + r * 64 + seg * RROWS;
-        const float* ww = tW + (slot_r * 2 + kind) * 64 + seg * RROWS;
-        float sum = 0.f;
+        if (slot == 0) {
+          // Rows of steps k, k+1 are in place (this wave's own LDS writes,
+          // executed in order). Lane slice: row r of half h2, RR channels.
+          const int hr = lane / L;
+          const int seg = lane % L;
+          const int r = hr >> 1;
+          const int h2 = hr & 1;
+          const int slot_r = r / RPS;
+          const int kind = (r % RPS) / NPL;
+          const int j = r % NPL;
+          const int kr = k + slot_r;
+          const float* rr = tR + r * kRowStride + h2 * kCH + seg * RR;
+          const float* ww = s0 + (kind ? oWDY : oWDTX) + kr * kCH + seg * RR;
+          float sum = 0.f;
 #pragma unroll
-        for (int i = 0; i < RROWS; i += 4) {
-          const float4 v = *reinterpret_cast<const float4*>(rr + i);
-          const float4 w = *reinterpret_cast<const float4*>(ww + i);
-          sum = __builtin_fmaf(v.x, w.x, sum);
-          sum = __builtin_fmaf(v.y, w.y, sum);
-          sum = __builtin_fmaf(v.z, w.z, sum);
-          sum = __builtin_fmaf(v.w, w.w, sum);
+          for (int e = 0; e < RR; e += 4) {
+            const float4 v = lds4(rr + e);
+            const float4 w = lds4(ww + e);
+            sum = __builtin_fmaf(v.x, w.x, sum);
+            sum = __builtin_fmaf(v.y, w.y, sum);
+            sum = __builtin_fmaf(v.z, w.z, sum);
+            sum = __builtin_fmaf(v.w, w.w, sum);
+          }
+          sum = group_sum<L>(sum);
+          // All L lanes of the slice hold the sum and store the same value.
+          tDBC[(kind * kSteps + kr) * NP + (wave * 2 + h2) * NPL + j] = sum;
         }
-        sum = group_sum<LPR>(sum);
-        const int kk = k + slot_r;
-        if (seg == 0 && kk < len) {
-          float* dst = kind ? a.wsC : a.wsB;
-          dst[(((size_t)blockIdx.x * a.batch + b) * T + t0 + kk) * N + n0 + j] = sum;
-        }
-        wave_lds_sync();
       }
+      // Add the two half-waves: lanes 0-31 end with s1, lanes 32-63 with s2.
+      float o[4];
+#pragma unroll
+      for (int s = 0; s < 4; ++s) {
+        const auto sw = __builtin_amdgcn_permlane32_swap(__float_as_uint(s1q[s]),
+                                                        __float_as_uint(s2q[s]), false, false);
+        o[s] = __uint_as_float(sw[0]) + __uint_as_float(sw[1]);
+      }
+      sts4(tS + wave * 64 * kSteps + cm_quad(lane, m), make_float4(o[0], o[1], o[2], o[3]));
       step_fence();
-      if (k > 0) {
-        dtv = dtn;
-        xv = xn;
-        dyv = dyn;
-#pragma unroll
-        for (int j = 0; j < NPL; ++j) {
-          Bv[j] = Bn[j];
-          Cv[j] = Cn[j];
-        }
-      }
     }
-    __syncthreads();
-
-    // dx, ddt for this chunk: wave w finalizes steps k with k % G == w.
-    float* dxb = a.dx + (row0 + t0) * D + d;
-    float* ddtb = a.ddt + (row0 + t0) * D + d;
-    for (int k = wave; k < len; k += G) {
-      float s1 = 0.f, s2 = 0.f;
-      for (int w = 0; w < G; ++w) {
-        const float2 v = tS[(w * KI + k) * 64 + lane];
-        s1 += v.x;
-        s2 += v.y;
-      }
-      if (act) {
-        dxb[(size_t)k * D] = tD[k * 64 + lane] * s1;
-        ddtb[(size_t)k * D] = __builtin_fmaf(tX[k * 64 + lane], s1, -s2);
-      }
-    }
-    __syncthreads();
-  }
-
-  if (act) {
-    float out[NPL];
 #pragma unroll
-    for (int j = 0; j < NPL; ++j) out[j] = -acc[j];
-    store_vec<NPL>(a.wsA + ((size_t)b * D + d) * N + n0, out);
+    for (int j = 0; j < NPL; ++j) hc[j] = ph[j];   // h at the start of chunk ci-1
+    load_h0(ci - 2);
+    __syncthreads();   // tS / tDBC complete; chunk ci-1 staged
   }
+  finalize(0);
+
+  float out[NPL];
+#pragma unroll
+  for (int j = 0; j < NPL; ++j) out[j] = -acc[j];
+  store_states<NPL>(GBuf(a.wsA + (size_t)b * slice, slice_bytes), st_lane, nvalid, out);
 }
 
 // dB, dC: sum the per-block partials over the nblk channel blocks;

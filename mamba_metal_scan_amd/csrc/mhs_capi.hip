@@ -39,18 +39,19 @@ int check_launch(const char* what) {
 
 bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
 
-// Forced state-lanes-per-wave (0 = automatic); see mhs_set_variant.
+// Forced states per lane (0 = automatic); see mhs_set_variant.
 std::atomic<int> g_npl_override{0};
 
 using FwdFn = void (*)(mhs::FwdArgs);
 using BwdFn = void (*)(mhs::BwdArgs);
 
-constexpr int kFwdKI = 16;
-constexpr int kRows = 16;
+constexpr int kKI = mhs::kSteps;           // backward register window (steps)
+constexpr int kMaxLdsBytes = 160 * 1024;   // gfx950 LDS per workgroup
+constexpr int kMaxG = 8;                   // waves per block
 
 struct Plan {
-  int npl = 0;      // state lanes per wave
-  int G = 0;        // waves per block (= N / npl)
+  int npl = 0;      // states per lane
+  int G = 0;        // waves per block (d_state padded to 2*G*npl)
   FwdFn fwd = nullptr;
   int fwd_lds = 0;  // bytes
   BwdFn bwd = nullptr;
@@ -58,76 +59,54 @@ struct Plan {
   int bwd_lds = 0;  // bytes
 };
 
-template <int NPL, int PER>
-FwdFn fwd_fn() { return &mhs::fwd_kernel<NPL, kFwdKI, 16, PER, 1>; }
-
-constexpr int kMaxLdsBytes = 160 * 1024;   // gfx950 LDS per workgroup
-
-// Backward instantiations per state-lanes-per-wave, in order of preference:
-// the larger register window (KI = 16) for up to 8 waves per block, a
-// narrower one (KI = 8) for up to 16 waves. PER: tile float4s per thread.
-struct BwdCand {
-  int ki, maxg, rows;
-  BwdFn narrow;   // for blocks of fewer than 4 waves
-  BwdFn wide;     // for blocks of 4 or more waves
-};
+// Kernel instantiations: NPL in {2, 4}, G in 1..8 (d_state up to 64).
+// MINW is the waves-per-SIMD target the register budget is sized for: 3 for
+// two states per lane (<= 168 VGPRs: at batch 16 x d_inner 1536 x d_state 16
+// the grid is exactly 3 waves per SIMD), 2 for four (<= 256 VGPRs).
+template <int NPL, int G>
+void fill(Plan& p) {
+  constexpr int MINW = NPL == 2 ? 3 : 2;
+  p.fwd = &mhs::fwd_kernel<NPL, G, MINW>;
+  p.bwd = &mhs::bwd_kernel<NPL, G, MINW>;
+  p.fwd_lds = mhs::fwd_lds_floats(G, NPL) * 4;
+  p.bwd_lds = mhs::bwd_lds_floats(G, NPL) * 4;
+}
 
 template <int NPL>
-void bwd_cands(const BwdCand*& c, int& n) {
-  static const BwdCand t[] = {
-      {16, 8, kRows, &mhs::bwd_kernel<NPL, 16, 8, 4, 1, kRows>,
-       &mhs::bwd_kernel<NPL, 16, 8, 1, 1, kRows>},
-      {8, 16, (NPL == 4 ? 16 : 8), &mhs::bwd_kernel<NPL, 8, 16, 2, 1, (NPL == 4 ? 16 : 8)>,
-       &mhs::bwd_kernel<NPL, 8, 16, 1, 1, (NPL == 4 ? 16 : 8)>},
-  };
-  c = t;
-  n = 2;
+bool fill_g(int G, Plan& p) {
+  switch (G) {
+    case 1: fill<NPL, 1>(p); break;
+    case 2: fill<NPL, 2>(p); break;
+    case 3: fill<NPL, 3>(p); break;
+    case 4: fill<NPL, 4>(p); break;
+    case 5: fill<NPL, 5>(p); break;
+    case 6: fill<NPL, 6>(p); break;
+    case 7: fill<NPL, 7>(p); break;
+    case 8: fill<NPL, 8>(p); break;
+    default: return false;
+  }
+  return true;
 }
 
 bool plan_for(int N, int npl, Plan& p) {
-  if (N % npl != 0) return false;
-  const int G = N / npl;
-  if (G < 1 || G > 16) return false;
-  const bool narrow = G < 4;   // tile loads need more than one float4 per thread
-  FwdFn fwd = nullptr;
-  const BwdCand* cands = nullptr;
-  int nc = 0;
-  switch (npl) {
-    case 4: fwd = narrow ? fwd_fn<4, 4>() : fwd_fn<4, 1>(); bwd_cands<4>(cands, nc); break;
-    case 2: fwd = narrow ? fwd_fn<2, 4>() : fwd_fn<2, 1>(); bwd_cands<2>(cands, nc); break;
-    case 1: fwd = narrow ? fwd_fn<1, 4>() : fwd_fn<1, 1>(); bwd_cands<1>(cands, nc); break;
-    default: return false;
-  }
-  const int fwd_lds = mhs::fwd_lds_floats(kFwdKI, G, npl) * 4;
-  if (fwd_lds > kMaxLdsBytes) return false;
-  for (int i = 0; i < nc; ++i) {
-    const BwdCand& c = cands[i];
-    const int lds = mhs::bwd_lds_floats(c.ki, G, npl, c.rows) * 4;
-    if (G > c.maxg || lds > kMaxLdsBytes) continue;
-    if (narrow && c.ki * 16 > 64 * G * (c.ki == 16 ? 4 : 2)) continue;
-    p.npl = npl;
-    p.G = G;
-    p.fwd = fwd;
-    p.fwd_lds = fwd_lds;
-    p.bwd = narrow ? c.narrow : c.wide;
-    p.bwd_ki = c.ki;
-    p.bwd_lds = lds;
-    return true;
-  }
-  return false;
+  const int G = (N + 2 * npl - 1) / (2 * npl);
+  if (G < 1 || G > kMaxG) return false;
+  const bool ok = npl == 2 ? fill_g<2>(G, p) : npl == 4 ? fill_g<4>(G, p) : false;
+  if (!ok) return false;
+  p.npl = npl;
+  p.G = G;
+  p.bwd_ki = kKI;
+  return p.fwd_lds <= kMaxLdsBytes && p.bwd_lds <= kMaxLdsBytes;
 }
 
 // Resolve the kernel variant for d_state N. Returns false if unsupported.
 bool make_plan(int N, Plan& p) {
   if (N < 1 || N > MHS_MAX_DSTATE) return false;
   const int forced = g_npl_override.load(std::memory_order_relaxed);
-  if (forced != 0 && plan_for(N, forced, p)) return true;
-  // Automatic: the most state lanes per wave that still gives >= 4 waves.
-  if (N % 4 == 0 && N / 4 >= 4 && plan_for(N, 4, p)) return true;
-  if (N % 2 == 0 && N / 2 >= 4 && plan_for(N, 2, p)) return true;
-  if (plan_for(N, 1, p)) return true;
-  if (N % 2 == 0 && plan_for(N, 2, p)) return true;
-  return N % 4 == 0 && plan_for(N, 4, p);
+  if (forced != 0) return plan_for(N, forced, p);
+  // Automatic: two states per lane up to d_state 32 (more, thinner blocks),
+  // four beyond.
+  return plan_for(N, N <= 32 ? 2 : 4, p);
 }
 
 // Dynamic-LDS opt-in, once per kernel function.
@@ -155,10 +134,14 @@ int check_shape(int64_t batch, int64_t seqlen, int64_t d_inner, int64_t d_state,
                 (long long)batch, (long long)seqlen, (long long)d_inner, (long long)d_state);
   if (chunk < 1) return fail(MHS_EINVAL, "chunk must be >= 1, got %lld", (long long)chunk);
   if (batch > 65535) return fail(MHS_EINVAL, "batch %lld exceeds 65535", (long long)batch);
-  if (seqlen > (1LL << 30) || d_inner > (1LL << 30))
-    return fail(MHS_EINVAL, "seqlen / d_inner too large");
+  if (seqlen > (1LL << 30)) return fail(MHS_EINVAL, "seqlen %lld too large", (long long)seqlen);
   if (d_state > MHS_MAX_DSTATE)
     return fail(MHS_EINVAL, "d_state %lld unsupported (max %d)", (long long)d_state, MHS_MAX_DSTATE);
+  // Buffer resources address at most 2 GiB: one (d_inner, d_state) state
+  // slice and 16 steps of one (T, d_inner) row must fit.
+  if (d_inner > (1LL << 24) || d_inner * d_state * 4 >= (1LL << 31))
+    return fail(MHS_EINVAL, "d_inner %lld x d_state %lld too large", (long long)d_inner,
+                (long long)d_state);
   return MHS_OK;
 }
 
@@ -170,7 +153,7 @@ struct WsLayout {
 
 WsLayout ws_layout(int64_t batch, int64_t T, int64_t D, int64_t N, int64_t chunk, int bwd_ki) {
   WsLayout w;
-  const size_t nblk = (size_t)((D + 63) / 64);
+  const size_t nblk = (size_t)((D + mhs::kCH - 1) / mhs::kCH);
   const size_t S = (size_t)batch * T * N;
   size_t off = 0;
   w.partB = off;
@@ -188,7 +171,7 @@ WsLayout ws_layout(int64_t batch, int64_t T, int64_t D, int64_t N, int64_t chunk
 int launch_fwd(const Plan& p, const mhs::FwdArgs& a, int batch, hipStream_t s) {
   int rc = ensure_lds(reinterpret_cast<const void*>(p.fwd), p.fwd_lds);
   if (rc) return rc;
-  const dim3 grid((unsigned)((a.D + 63) / 64), (unsigned)batch);
+  const dim3 grid((unsigned)((a.D + mhs::kCH - 1) / mhs::kCH), (unsigned)batch);
   hipLaunchKernelGGL(p.fwd, grid, dim3(64 * p.G), p.fwd_lds, s, a);
   return check_launch("forward scan kernel");
 }
@@ -207,8 +190,8 @@ int64_t mhs_num_chunks(int64_t seqlen, int64_t chunk) {
 }
 
 int mhs_set_variant(int npl) {
-  if (npl != 0 && npl != 1 && npl != 2 && npl != 4)
-    return fail(MHS_EINVAL, "state lanes per wave must be 0 (auto), 1, 2 or 4; got %d", npl);
+  if (npl != 0 && npl != 2 && npl != 4)
+    return fail(MHS_EINVAL, "states per lane must be 0 (auto), 2 or 4; got %d", npl);
   g_npl_override.store(npl, std::memory_order_relaxed);
   return MHS_OK;
 }
@@ -235,10 +218,9 @@ int mhs_scan_fwd_f32(const float* x, const float* dt, const float* aneg, const f
   mhs::FwdArgs a;
   a.x = x; a.dt = dt; a.aneg = aneg; a.B = B; a.C = C;
   a.y = y; a.ckpt = ckpt; a.h_last = h_last;
-  a.T = (int)seqlen; a.D = (int)d_inner;
+  a.T = (int)seqlen; a.D = (int)d_inner; a.N = (int)d_state;
   a.K = (int)std::min<int64_t>(chunk, seqlen);
   a.nchunk = (int)mhs_num_chunks(seqlen, chunk);
-  a.vec4 = (d_inner % 4 == 0) ? 1 : 0;
   return launch_fwd(p, a, (int)batch, static_cast<hipStream_t>(stream));
 }
 
@@ -268,6 +250,7 @@ int mhs_scan_bwd_f32(const float* x, const float* dt, const float* aneg, const f
     return fail(MHS_EINVAL, "workspace must be 256-byte aligned");
   Plan p;
   if (!make_plan((int)d_state, p)) return fail(MHS_EINVAL, "d_state %lld unsupported", (long long)d_state);
+  const int ch = mhs::kCH;
   const WsLayout w = ws_layout(batch, seqlen, d_inner, d_state, chunk, p.bwd_ki);
   if (workspace_bytes < w.total)
     return fail(MHS_EINVAL, "workspace too small: %zu < %zu bytes", workspace_bytes, w.total);
@@ -286,9 +269,8 @@ int mhs_scan_bwd_f32(const float* x, const float* dt, const float* aneg, const f
     f.y = nullptr;
     f.ckpt = reinterpret_cast<float*>(ws + w.fine);
     f.h_last = nullptr;
-    f.T = T; f.D = D; f.K = p.bwd_ki;
+    f.T = T; f.D = D; f.N = N; f.K = p.bwd_ki;
     f.nchunk = (int)mhs_num_chunks(T, p.bwd_ki);
-    f.vec4 = (D % 4 == 0) ? 1 : 0;
     rc = launch_fwd(p, f, (int)batch, s);
     if (rc) return rc;
     ck = f.ckpt;
@@ -302,12 +284,11 @@ int mhs_scan_bwd_f32(const float* x, const float* dt, const float* aneg, const f
   a.wsB = reinterpret_cast<float*>(ws + w.partB);
   a.wsC = reinterpret_cast<float*>(ws + w.partC);
   a.wsA = reinterpret_cast<float*>(ws + w.partA);
-  a.batch = (int)batch; a.T = T; a.D = D; a.K = Kb;
+  a.batch = (int)batch; a.T = T; a.D = D; a.N = N; a.K = Kb;
   a.nchunk = (int)mhs_num_chunks(T, Kb);
-  a.vec4 = (D % 4 == 0) ? 1 : 0;
   rc = ensure_lds(reinterpret_cast<const void*>(p.bwd), p.bwd_lds);
   if (rc) return rc;
-  const dim3 grid((unsigned)((D + 63) / 64), (unsigned)batch);
+  const dim3 grid((unsigned)((D + ch - 1) / ch), (unsigned)batch);
   hipLaunchKernelGGL(p.bwd, grid, dim3(64 * p.G), p.bwd_lds, s, a);
   rc = check_launch("backward scan kernel");
   if (rc) return rc;
@@ -317,7 +298,7 @@ int mhs_scan_bwd_f32(const float* x, const float* dt, const float* aneg, const f
   const long long total = S + A;
   const int blocks = (int)std::min<long long>((total + 255) / 256, 4096);
   hipLaunchKernelGGL(mhs::bwd_reduce_kernel, dim3(blocks), dim3(256), 0, s, a.wsB, a.wsC, a.wsA,
-                     dB, dC, daneg, (D + 63) / 64, (int)batch, S, A);
+                     dB, dC, daneg, (D + ch - 1) / ch, (int)batch, S, A);
   return check_launch("backward reduction kernel");
 }
 

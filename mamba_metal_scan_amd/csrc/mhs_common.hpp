@@ -5,11 +5,12 @@
 //   aneg                  : (D, N)             ckpt         : (batch, nchunk, D, N)
 //
 // Work decomposition used by the forward and backward kernels: one workgroup
-// owns one batch row b and a block of 64 consecutive channels d; its G waves
-// split the N state lanes into G groups of NPL (wave w owns n in
-// [w*NPL, (w+1)*NPL)). Every lane therefore carries NPL independent
-// recurrences in VGPRs, B/C are wave-uniform within a group, and x / dt / dy
-// rows are shared by the whole workgroup through LDS.
+// owns one batch row b and a block of CH consecutive channels d. The N states
+// are split into NQ groups of NPL; each wave holds NH = 64/CH groups (NH = 2:
+// lanes 0-31 and 32-63 carry the same 32 channels for two different groups),
+// so a block has G = NQ/NH waves. Every lane carries NPL independent
+// recurrences in VGPRs for the whole sequence; x / dt / dy and B / C are
+// staged per block in LDS and shared by its waves.
 #pragma once
 
 #include <hip/hip_runtime.h>
@@ -91,76 +92,186 @@ __device__ __forceinline__ void store_vec(float* p, const float (&v)[NPL]) {
   }
 }
 
-// Cooperative staging of one chunk of a (batch, T, D) tensor into a
-// [KI][64] LDS tile: the workgroup's 64 channels for KI time steps. The tile
-// is KI*16 float4 quads; thread tid moves quads tid, tid+nthreads, ... (at
-// most PER of them, PER*nthreads >= KI*16 is checked on the host). Rows at or
-// beyond `len` and channels at or beyond D are zero-filled.
-template <int KI, int PER>
-struct TileLoader {
-  int tid, nthreads;
-  __device__ __forceinline__ TileLoader(int tid_, int nthreads_) : tid(tid_), nthreads(nthreads_) {}
+// ---------------------------------------------------------------- LDS tiles
+//
+// Time is processed in sub-chunks of 16 steps ("quads" of 4 steps). Per-lane
+// operands live in channel-major tiles: row c holds the 16 steps of channel
+// c, so a lane reads 4 consecutive steps with one 128-bit LDS read (gfx950
+// moves ~2x the bytes per clock with ds_read_b128 than with b32/b64). The
+// quad index inside a row is rotated by c/4 ("quad swizzle") so that the 16
+// lanes of one 128-bit read phase hit 16 different 4-bank groups.
+constexpr int kSteps = 16;   // steps per sub-chunk
+constexpr int kQuads = 4;    // quads per sub-chunk
 
-  // base points at element (b, t0, d0) of the tensor; row stride D.
-  // vec4: base is 16-byte aligned and D % 4 == 0.
-  __device__ __forceinline__ void load(float4 (&v)[PER], const float* base, int len, int D,
-                                       int d0, bool vec4) const {
+__device__ __forceinline__ int cm_quad(int row, int m) {
+  return row * kSteps + ((((m + (row >> 2)) & 3)) << 2);
+}
+__device__ __forceinline__ int cm_elem(int row, int k) { return cm_quad(row, k >> 2) + (k & 3); }
+
+__device__ __forceinline__ float4 lds4(const float* p) { return *reinterpret_cast<const float4*>(p); }
+__device__ __forceinline__ float2 lds2(const float* p) { return *reinterpret_cast<const float2*>(p); }
+
+// ------------------------------------------------------------- buffer I/O
+//
+// Global memory is accessed through raw buffer resources: an access whose
+// byte offset is at or beyond the resource's size returns 0 (loads) or is
+// dropped (stores) by the hardware. Edges (steps past T, channels past
+// d_inner, padded states) therefore need no branches: their offsets are set
+// to kOOB, and the hot loops stay single basic blocks.
+constexpr unsigned kOOB = 0x80000000u;   // resources are < 2 GiB (checked on the host)
+
+struct GBuf {
+  __amdgpu_buffer_rsrc_t r;
+  __device__ __forceinline__ GBuf(const float* base, unsigned bytes)
+      : r(__builtin_amdgcn_make_buffer_rsrc(const_cast<float*>(base), 0, (int)bytes, 0x00020000)) {}
+  // The b32 builtins move raw 32-bit words (unsigned int): bit-cast, never convert.
+  __device__ __forceinline__ float ld(unsigned byte_off) const {
+    return __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(r, byte_off, 0, 0));
+  }
+  __device__ __forceinline__ void st(float v, unsigned byte_off) const {
+    __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(v), r, byte_off, 0, 0);
+  }
+};
+
+// NPL consecutive states of one lane at byte offset `off` (kOOB: none);
+// states at or beyond `nvalid` are padding and are not stored.
+template <int NPL>
+__device__ __forceinline__ void store_states(const GBuf& g, unsigned off, int nvalid,
+                                             const float (&v)[NPL]) {
+#pragma unroll
+  for (int j = 0; j < NPL; ++j) g.st(v[j], (off != kOOB && j < nvalid) ? off + 4u * j : kOOB);
+}
+template <int NPL>
+__device__ __forceinline__ void load_states(float (&v)[NPL], const GBuf& g, unsigned off,
+                                            int nvalid) {
+#pragma unroll
+  for (int j = 0; j < NPL; ++j) v[j] = g.ld((off != kOOB && j < nvalid) ? off + 4u * j : kOOB);
+}
+
+__device__ __forceinline__ void sts4(float* p, float4 v) { *reinterpret_cast<float4*>(p) = v; }
+
+// Staging of one sub-chunk of a (batch, T, D) tensor for the block's CH
+// channels: task (c, quad m) holds steps 4m..4m+3 of channel d0+c. Tasks are
+// numbered c-fastest so that each load instruction reads consecutive
+// channels. Thread tid owns tasks tid, tid+nthreads, ... (PER of them; tasks
+// beyond TASKS and channels beyond d_inner load zeros).
+template <int CH, int PER>
+struct QuadLoader {
+  static constexpr int TASKS = CH * kQuads;
+  int tid, nthreads;
+  unsigned toff[PER];   // byte offset of step 4m of channel c from the sub-chunk base, or kOOB
+  __device__ __forceinline__ QuadLoader(int tid_, int nthreads_, int D, int d0)
+      : tid(tid_), nthreads(nthreads_) {
 #pragma unroll
     for (int i = 0; i < PER; ++i) {
       const int e = tid + i * nthreads;
-      const int k = e >> 4, q = e & 15;
-      v[i] = make_float4(0.f, 0.f, 0.f, 0.f);
-      if (e < KI * 16 && k < len) {
-        const int dq = d0 + 4 * q;
-        const float* p = base + (size_t)k * D + 4 * q;
-        if (vec4 && dq + 3 < D) {
-          v[i] = *reinterpret_cast<const float4*>(p);
-        } else {
-          if (dq + 0 < D) v[i].x = p[0];
-          if (dq + 1 < D) v[i].y = p[1];
-          if (dq + 2 < D) v[i].z = p[2];
-          if (dq + 3 < D) v[i].w = p[3];
-        }
-      }
+      const int c = e % CH, m = e / CH;
+      toff[i] = (e < TASKS && d0 + c < D) ? 4u * ((unsigned)(4 * m) * (unsigned)D + (unsigned)c)
+                                          : kOOB;
     }
   }
-  __device__ __forceinline__ void store(float* tile, const float4 (&v)[PER]) const {
+  __device__ __forceinline__ bool valid(int i) const { return tid + i * nthreads < TASKS; }
+  __device__ __forceinline__ int chan(int i) const { return (tid + i * nthreads) % CH; }
+  __device__ __forceinline__ int quad(int i) const { return (tid + i * nthreads) / CH; }
+  // g covers (b, t0.., d0..) up to the end of the batch row (steps past T
+  // are out of range).
+  __device__ __forceinline__ void load(float4 (&v)[PER], const GBuf& g, int D) const {
+    const unsigned rs = 4u * (unsigned)D;
 #pragma unroll
     for (int i = 0; i < PER; ++i) {
-      const int e = tid + i * nthreads;
-      if (e < KI * 16) *reinterpret_cast<float4*>(tile + 4 * e) = v[i];
+      const unsigned o = toff[i];
+      const bool ok = o != kOOB;
+      v[i].x = g.ld(o);
+      v[i].y = g.ld(ok ? o + rs : kOOB);
+      v[i].z = g.ld(ok ? o + 2 * rs : kOOB);
+      v[i].w = g.ld(ok ? o + 3 * rs : kOOB);
+    }
+  }
+  // Channel-major swizzled tile [CH][16].
+  __device__ __forceinline__ void store_cm(float* tile, const float4 (&v)[PER]) const {
+#pragma unroll
+    for (int i = 0; i < PER; ++i)
+      if (valid(i)) sts4(tile + cm_quad(chan(i), quad(i)), v[i]);
+  }
+  __device__ __forceinline__ void store_cm_product(float* tile, const float4 (&a)[PER],
+                                                   const float4 (&b)[PER]) const {
+#pragma unroll
+    for (int i = 0; i < PER; ++i)
+      if (valid(i))
+        sts4(tile + cm_quad(chan(i), quad(i)),
+             make_float4(a[i].x * b[i].x, a[i].y * b[i].y, a[i].z * b[i].z, a[i].w * b[i].w));
+  }
+  // Step-major tile [16][CH] (consecutive channels contiguous).
+  __device__ __forceinline__ void store_sm(float* tile, const float4 (&v)[PER]) const {
+#pragma unroll
+    for (int i = 0; i < PER; ++i) {
+      if (!valid(i)) continue;
+      float* p = tile + 4 * quad(i) * CH + chan(i);
+      p[0] = v[i].x;
+      p[CH] = v[i].y;
+      p[2 * CH] = v[i].z;
+      p[3 * CH] = v[i].w;
+    }
+  }
+  __device__ __forceinline__ void store_sm_product(float* tile, const float4 (&a)[PER],
+                                                   const float4 (&b)[PER]) const {
+#pragma unroll
+    for (int i = 0; i < PER; ++i) {
+      if (!valid(i)) continue;
+      float* p = tile + 4 * quad(i) * CH + chan(i);
+      p[0] = a[i].x * b[i].x;
+      p[CH] = a[i].y * b[i].y;
+      p[2 * CH] = a[i].z * b[i].z;
+      p[3 * CH] = a[i].w * b[i].w;
     }
   }
 };
 
-// Cooperative staging of KI rows of a (batch, T, N) tensor (B or C) into an
-// LDS tile laid out wave-major, [G][KI][NPL]: wave w reads its NPL states of
-// step k at w*KI*NPL + k*NPL, a compile-time offset from a per-wave base.
-// Thread tid moves elements e = tid, tid+nthreads, ... (at most PERS of them)
-// of the row-major global block; rows at or beyond `len` are zero-filled.
-template <int PERS, int KI, int NPL>
+// Staging of 16 rows of a (batch, T, N) tensor (B or C) into an LDS tile of
+// NP >= N (padded) states laid out per state group, [NP/NPL][16][NPL]: group
+// q reads NPL states of 4 steps as NPL float4s at q*16*NPL + 4*m*NPL.
+// Thread tid moves tile elements tid, tid+nthreads, ... (PERS of them);
+// padded states and steps past T are zero.
+template <int PERS, int NPL>
 struct RowLoader {
-  int src[PERS];  // element index in the global [KI][N] block, or -1
-  int dst[PERS];  // its slot in the wave-major tile
-  __device__ __forceinline__ RowLoader(int tid, int nthreads, int N) {
+  unsigned src[PERS];  // byte offset in the sub-chunk's global [16][N] block, or kOOB
+  int dst[PERS];       // slot in the tile, or -1
+  __device__ __forceinline__ RowLoader(int tid, int nthreads, int N, int NP) {
 #pragma unroll
     for (int i = 0; i < PERS; ++i) {
-      const int e = tid + i * nthreads;
-      const int k = e / N, n = e % N;
-      src[i] = e < KI * N ? e : -1;
-      dst[i] = (n / NPL) * (KI * NPL) + k * NPL + (n % NPL);
+      const int e = tid + i * nthreads;       // tile element (k, n), n fastest
+      const int k = e / NP, n = e % NP;
+      const bool in_tile = e < kSteps * NP;
+      src[i] = (in_tile && n < N) ? 4u * (unsigned)(k * N + n) : kOOB;
+      dst[i] = in_tile ? (n / NPL) * (kSteps * NPL) + k * NPL + (n % NPL) : -1;
     }
   }
-  // base points at (b, t0, 0).
-  __device__ __forceinline__ void load(float (&v)[PERS], const float* base, int len, int N) const {
+  __device__ __forceinline__ void load(float (&v)[PERS], const GBuf& g) const {
 #pragma unroll
-    for (int i = 0; i < PERS; ++i) v[i] = (src[i] >= 0 && src[i] < len * N) ? base[src[i]] : 0.f;
+    for (int i = 0; i < PERS; ++i) v[i] = g.ld(src[i]);
   }
   __device__ __forceinline__ void store(float* tile, const float (&v)[PERS]) const {
 #pragma unroll
     for (int i = 0; i < PERS; ++i)
-      if (src[i] >= 0) tile[dst[i]] = v[i];
+      if (dst[i] >= 0) tile[dst[i]] = v[i];
   }
 };
+
+// NPL states x 4 steps of a group's B or C tile: v[s][j] = tile[(4m+s)*NPL + j].
+template <int NPL>
+__device__ __forceinline__ void load_quad_rows(float (&v)[4][NPL], const float* g, int m) {
+  const float* p = g + 4 * m * NPL;
+#pragma unroll
+  for (int i = 0; i < NPL; ++i) {
+    const float4 t = lds4(p + 4 * i);
+    const float tv[4] = {t.x, t.y, t.z, t.w};
+#pragma unroll
+    for (int e = 0; e < 4; ++e) v[(4 * i + e) / NPL][(4 * i + e) % NPL] = tv[e];
+  }
+}
+
+__device__ __forceinline__ void f4_to(float (&v)[4], float4 t) {
+  v[0] = t.x; v[1] = t.y; v[2] = t.z; v[3] = t.w;
+}
 
 }  // namespace mhs

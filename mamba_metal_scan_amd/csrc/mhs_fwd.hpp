@@ -1,19 +1,31 @@
 // Forward selective scan for gfx950.
 //
-// Follows the math of the reference's ssm_fwd (mamba_metal/scan.py:78-127):
+// Math of the reference's ssm_fwd (mamba_metal/scan.py:78-127):
 //   da = exp(-dt * Aneg); h = da * h + B * (dt * x); y = sum_n C * h;
 //   h is written to ckpt at the end of every chunk of K steps (and at T-1).
 //
 // MI355X mapping (not the reference's one-thread-per-channel layout):
-//   grid (ceil(D/64), batch), block 64*G. Wave w of the block owns state lanes
-//   n in [w*NPL, w*NPL+NPL) of the block's 64 channels, so the N-vector of one
-//   channel is spread over G waves (filling 256 CUs at batch 16 x D 1.5k) and
-//   each lane keeps NPL recurrences in VGPRs for the whole sequence.
-//   Time advances in sub-chunks of KI steps. Per sub-chunk the block stages
-//   x, dt (KI x 64) and B, C (KI x N) in LDS with one coalesced float4 per
-//   thread, prefetched one sub-chunk ahead in VGPRs. The per-wave partial sums
-//   of y (over the wave's NPL states) are combined across the G waves through
-//   LDS and written once, coalesced along d.
+//   grid (ceil(D/32), batch), block 64*G. Lane (wave w, half hh, channel c)
+//   owns channel d = blockIdx.x*32 + c and the NPL states n in [q*NPL,
+//   q*NPL+NPL), q = 2w + hh: the d_state vector of a channel is spread over
+//   2G lane groups (d_state padded with zero states to NP = 2*G*NPL), each
+//   lane keeping NPL recurrences in VGPRs for the whole sequence. At batch 16
+//   x d_inner 1536 x d_state 16 (NPL 2, G 4) that is 768 blocks of 4 waves:
+//   3 blocks per CU and 3 waves per SIMD.
+//
+//   Time advances in sub-chunks of 16 steps, as a software pipeline with one
+//   barrier per sub-chunk. While sub-chunk i is computed, the same waves, in
+//   the same straight-line code (all global accesses are bounds-checked
+//   buffer accesses, so there are no branches), also
+//     - sum the y partials of sub-chunk i-1 over the 2G lane groups in a
+//       fixed order and store y, coalesced along d;
+//     - store the staged inputs of sub-chunk i+1 into the other LDS buffer
+//       (dt and dt*x as channel-major tiles, B and C per lane group);
+//     - issue the global loads of sub-chunk i+2 into the staging registers.
+//   A lane reads its operands four steps at a time with 128-bit LDS reads,
+//   computes the four dA = exp2(dt * -Aneg*log2e) and inputs first
+//   (independent), then runs the four dependent h = fma(dA, h, u) steps and
+//   the C.h sums, and writes its y partials of the quad as one float4.
 #pragma once
 
 #include "mhs_common.hpp"
@@ -29,143 +41,189 @@ struct FwdArgs {
   float* y;        // may be null: then no y traffic at all
   float* ckpt;     // may be null
   float* h_last;   // may be null
-  int T, D, K, nchunk;
-  int vec4;        // x, dt 16-byte aligned and D % 4 == 0
+  int T, D, N, K, nchunk;
 };
 
-// LDS floats used by fwd_kernel for G waves.
-__host__ __device__ constexpr int fwd_lds_floats(int KI, int G, int NPL) {
-  return KI * 64 * 2          // x, dt tiles
-         + 2 * KI * G * NPL   // B, C tiles
-         + G * KI * 64;       // per-wave y partials
+constexpr int kCH = 32;   // channels per block
+
+// One pipeline buffer (the kernel keeps two).
+__host__ __device__ constexpr int fwd_buf_floats(int G, int NPL) {
+  return 2 * kCH * kSteps               // dt, dt*x tiles (channel-major)
+         + 2 * kSteps * 2 * G * NPL     // B, C tiles
+         + G * 64 * kSteps;             // per-lane y partials
+}
+__host__ __device__ constexpr int fwd_lds_floats(int G, int NPL) {
+  return 2 * fwd_buf_floats(G, NPL);
 }
 
-template <int NPL, int KI, int MAXG, int PER, int PERS>
-__global__ void __launch_bounds__(64 * MAXG)
+template <int NPL, int G, int MINW>
+__global__ void __launch_bounds__(64 * G, MINW)
 fwd_kernel(FwdArgs a) {
+  constexpr int NT = 64 * G;                    // threads
+  constexpr int NP = 2 * G * NPL;               // padded states
+  constexpr int BUF = fwd_buf_floats(G, NPL);
+  constexpr int PER = (kCH * kQuads + NT - 1) / NT;
+  constexpr int PERS = (kSteps * NP + NT - 1) / NT;
+  constexpr int FT = (kSteps / 2 * kCH + NT - 1) / NT;   // y tasks per thread
   extern __shared__ float lds[];
-  const int G = blockDim.x >> 6;
-  const int N = G * NPL;
+  const int N = a.N;
   const int tid = threadIdx.x;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int lane = tid & 63;
+  const int hh = lane >> 5;
+  const int c = lane & 31;
+  const int q = wave * 2 + hh;
+  const int n0 = q * NPL;
   const int b = blockIdx.y;
-  const int d0 = blockIdx.x * 64;
-  const int d = d0 + lane;
+  const int d0 = blockIdx.x * kCH;
+  const int d = d0 + c;
   const bool act = d < a.D;
-  const int n0 = wave * NPL;
   const int T = a.T, D = a.D;
-
-  float* tX = lds;
-  float* tD = tX + KI * 64;
-  float* tB = tD + KI * 64;
-  float* tC = tB + KI * N;
-  float* tY = tC + KI * N;
-  const float* wB = tB + wave * KI * NPL;  // this wave's [KI][NPL] slice
-  const float* wC = tC + wave * KI * NPL;
+  const int nsub = (T + kSteps - 1) / kSteps;
 
   float a2[NPL], h[NPL];
 #pragma unroll
   for (int j = 0; j < NPL; ++j) {
-    a2[j] = act ? -a.aneg[(size_t)d * N + n0 + j] * kLog2e : 0.f;
+    a2[j] = (act && n0 + j < N) ? -a.aneg[(size_t)d * N + n0 + j] * kLog2e : 0.f;
     h[j] = 0.f;
   }
 
   const size_t row0 = (size_t)b * T;
-  const float* xb = a.x + row0 * D + d0;
-  const float* db = a.dt + row0 * D + d0;
-  const float* Bb = a.B + row0 * N;
-  const float* Cb = a.C + row0 * N;
-
-  const TileLoader<KI, PER> tl(tid, blockDim.x);
-  const RowLoader<PERS, KI, NPL> rl(tid, blockDim.x, N);
+  const QuadLoader<kCH, PER> ql(tid, NT, D, d0);
+  const RowLoader<PERS, NPL> rl(tid, NT, N, NP);
   float4 px[PER], pd[PER];
   float pb[PERS], pc[PERS];
-  {
-    const int len = min(KI, T);
-    tl.load(px, xb, len, D, d0, a.vec4);
-    tl.load(pd, db, len, D, d0, a.vec4);
-    rl.load(pb, Bb, len, N);
-    rl.load(pc, Cb, len, N);
-  }
-
-  int next_ck = min(a.K, T);
-  int ck = 0;
-  for (int t0 = 0; t0 < T; t0 += KI) {
-    const int len = min(KI, T - t0);
-    tl.store(tX, px);
-    tl.store(tD, pd);
-    rl.store(tB, pb);
-    rl.store(tC, pc);
-    if (t0 + KI < T) {
-      const int nlen = min(KI, T - t0 - KI);
-      const size_t off = (size_t)(t0 + KI);
-      tl.load(px, xb + off * D, nlen, D, d0, a.vec4);
-      tl.load(pd, db + off * D, nlen, D, d0, a.vec4);
-      rl.load(pb, Bb + off * N, nlen, N);
-      rl.load(pc, Cb + off * N, nlen, N);
-    }
-    __syncthreads();
-
-    // Steps k >= len of the last sub-chunk see zero-filled tiles: dA = 1 and
-    // b = 0 there, so h passes through unchanged and nothing is written.
-    float dtv = tD[lane], xv = tX[lane];
-    float Bv[NPL], Cv[NPL];
-    load_vec<NPL>(Bv, wB);
-    load_vec<NPL>(Cv, wC);
+  // Sub-chunk i (any i >= 0): first step and length (0 past the sequence).
+  auto sub_t0 = [&](int i) { return min(max(i, 0) * kSteps, T - 1); };
+  auto sub_len = [&](int i) { return i < 0 ? 0 : max(0, min(kSteps, T - i * kSteps)); };
+  // Resource over one sub-chunk of a (batch, T, D) tensor from channel d0 on.
+  auto sub_buf = [&](const float* base, int i) {
+    const int len = sub_len(i);
+    return GBuf(base + (row0 + sub_t0(i)) * D + d0, len > 0 ? 4u * (unsigned)(len * D - d0) : 0u);
+  };
+  auto load_sub = [&](int i) {            // global -> staging registers
+    const unsigned sbytes = 4u * (unsigned)(sub_len(i) * N);
+    ql.load(px, sub_buf(a.x, i), D);
+    ql.load(pd, sub_buf(a.dt, i), D);
+    rl.load(pb, GBuf(a.B + (row0 + sub_t0(i)) * N, sbytes));
+    rl.load(pc, GBuf(a.C + (row0 + sub_t0(i)) * N, sbytes));
+  };
+  auto store_sub = [&](int i) {           // staging registers -> LDS buffer i&1
+    float* buf = lds + (i & 1) * BUF;
+    ql.store_cm(buf, pd);
+    ql.store_cm_product(buf + kCH * kSteps, pd, px);
+    rl.store(buf + 2 * kCH * kSteps, pb);
+    rl.store(buf + 2 * kCH * kSteps + kSteps * NP, pc);
+  };
+  // y of sub-chunk i: task (step pair kp, channel cc) sums the partials of
+  // its two steps over the 2G lane groups in a fixed order.
+  auto finalize_y = [&](int i) {
+    const float* yp = lds + (i & 1) * BUF + 2 * kCH * kSteps + 2 * kSteps * NP;
+    const GBuf yo = sub_buf(a.y != nullptr ? a.y : a.x, a.y != nullptr ? i : -1);
 #pragma unroll
-    for (int k = 0; k < KI; ++k) {
-      // Operands of step k+1, read while step k computes.
-      float dtn = 0.f, xn = 0.f, Bn[NPL], Cn[NPL];
-      if (k + 1 < KI) {
-        dtn = tD[(k + 1) * 64 + lane];
-        xn = tX[(k + 1) * 64 + lane];
-        load_vec<NPL>(Bn, wB + (k + 1) * NPL);
-        load_vec<NPL>(Cn, wC + (k + 1) * NPL);
-      }
-      const float bx = dtv * xv;
-      float acc = 0.f;
+    for (int f = 0; f < FT; ++f) {
+      const int task0 = tid + f * NT;
+      const bool ok = task0 < kSteps / 2 * kCH;
+      const int task = ok ? task0 : 0;
+      const int cc = task % kCH, k = 2 * (task / kCH);
+      float s0 = 0.f, s1 = 0.f;
 #pragma unroll
-      for (int j = 0; j < NPL; ++j) {
-        const float da = exp2_hw(dtv * a2[j]);
-        h[j] = __builtin_fmaf(da, h[j], Bv[j] * bx);
-        acc = __builtin_fmaf(Cv[j], h[j], acc);
-      }
-      // Written immediately (not kept for after the loop), so the y FMAs stay
-      // inside the step and the compiler cannot keep KI steps of h live.
-      if (a.y != nullptr) tY[(wave * KI + k) * 64 + lane] = acc;
-      if (t0 + k + 1 == next_ck) {
-        if (a.ckpt != nullptr && act)
-          store_vec<NPL>(a.ckpt + (((size_t)b * a.nchunk + ck) * D + d) * N + n0, h);
-        ++ck;
-        next_ck = min(next_ck + a.K, T);
-      }
-      step_fence();
-      if (k + 1 < KI) {
-        dtv = dtn;
-        xv = xn;
+      for (int w = 0; w < G; ++w) {
 #pragma unroll
-        for (int j = 0; j < NPL; ++j) {
-          Bv[j] = Bn[j];
-          Cv[j] = Cn[j];
+        for (int h2 = 0; h2 < 2; ++h2) {
+          const float2 v = lds2(yp + w * 64 * kSteps + cm_elem(h2 * kCH + cc, k));
+          s0 += v.x;
+          s1 += v.y;
         }
       }
+      const unsigned o = (ok && d0 + cc < D) ? 4u * ((unsigned)k * (unsigned)D + cc) : kOOB;
+      yo.st(s0, o);
+      yo.st(s1, o == kOOB ? kOOB : o + 4u * (unsigned)D);
     }
+  };
 
-    if (a.y != nullptr) {
-      __syncthreads();
-      float* yb = a.y + (row0 + t0) * D + d;
-      for (int k = wave; k < len; k += G) {
-        float s = 0.f;
-        for (int g = 0; g < G; ++g) s += tY[(g * KI + k) * 64 + lane];
-        if (act) yb[(size_t)k * D] = s;
+  // Prologue: sub-chunk 0 in LDS, sub-chunk 1 in the staging registers.
+  load_sub(0);
+  store_sub(0);
+  load_sub(1);
+  __syncthreads();
+
+  // Checkpoints / final state: bounds-checked stores of the lane's states
+  // (padded states and channels past d_inner are dropped). Each store gets a
+  // resource over one (D, N) slice.
+  const size_t ck_stride = (size_t)D * N;
+  const unsigned slice_bytes = 4u * (unsigned)ck_stride;
+  const unsigned ck_lane = act ? 4u * ((unsigned)d * (unsigned)N + (unsigned)n0) : kOOB;
+  const int nvalid = N - n0;
+  int next_ck = min(a.K, T);
+  int ck = 0;
+  for (int i = 0; i < nsub; ++i) {
+    const int t0 = i * kSteps;
+    const float* buf = lds + (i & 1) * BUF;
+    const float* cDT = buf;
+    const float* cBX = buf + kCH * kSteps;
+    const float* gB = buf + 2 * kCH * kSteps + q * kSteps * NPL;
+    const float* gC = buf + 2 * kCH * kSteps + kSteps * NP + q * kSteps * NPL;
+    float* myY = lds + (i & 1) * BUF + 2 * kCH * kSteps + 2 * kSteps * NP + wave * 64 * kSteps;
+
+    // Steps past T in the last sub-chunk see zero inputs: dA = 1 and u = 0
+    // there, so h passes through unchanged and nothing is stored.
+#pragma unroll
+    for (int m = 0; m < kQuads; ++m) {
+      float dts[4], bxs[4], Bq[4][NPL], Cq[4][NPL];
+      f4_to(dts, lds4(cDT + cm_quad(c, m)));
+      f4_to(bxs, lds4(cBX + cm_quad(c, m)));
+      load_quad_rows<NPL>(Bq, gB, m);
+      load_quad_rows<NPL>(Cq, gC, m);
+      float da[4][NPL], u[4][NPL];
+#pragma unroll
+      for (int s = 0; s < 4; ++s)
+#pragma unroll
+        for (int j = 0; j < NPL; ++j) {
+          da[s][j] = exp2_hw(dts[s] * a2[j]);
+          u[s][j] = Bq[s][j] * bxs[s];
+        }
+      float yq[4], hq[4][NPL];
+#pragma unroll
+      for (int s = 0; s < 4; ++s) {
+        float acc = 0.f;
+#pragma unroll
+        for (int j = 0; j < NPL; ++j) {
+          h[j] = __builtin_fmaf(da[s][j], h[j], u[s][j]);
+          acc = __builtin_fmaf(Cq[s][j], h[j], acc);
+          hq[s][j] = h[j];
+        }
+        yq[s] = acc;
       }
+      sts4(myY + cm_quad(lane, m), make_float4(yq[0], yq[1], yq[2], yq[3]));
+
+      // Pipeline work for the neighbouring sub-chunks, in this quad's
+      // scheduling region. Unconditional: past either end of the sequence the
+      // resources are empty (loads return 0, stores are dropped) and the LDS
+      // buffer written is not read again.
+      if (m == 0) finalize_y(i - 1);
+      if (m == 1) store_sub(i + 1);
+      if (m == 2) load_sub(i + 2);
+
+      // Checkpoints inside this quad.
+#pragma unroll
+      for (int s = 0; s < 4; ++s) {
+        if (t0 + 4 * m + s + 1 == next_ck) {
+          if (a.ckpt != nullptr)
+            store_states<NPL>(GBuf(a.ckpt + ((size_t)b * a.nchunk + ck) * ck_stride, slice_bytes),
+                              ck_lane, nvalid, hq[s]);
+          ++ck;
+          next_ck = min(next_ck + a.K, T);
+        }
+      }
+      step_fence();
     }
     __syncthreads();
   }
+  finalize_y(nsub - 1);
 
-  if (a.h_last != nullptr && act)
-    store_vec<NPL>(a.h_last + ((size_t)b * D + d) * N + n0, h);
+  if (a.h_last != nullptr)
+    store_states<NPL>(GBuf(a.h_last + (size_t)b * ck_stride, slice_bytes), ck_lane, nvalid, h);
 }
 
 }  // namespace mhs

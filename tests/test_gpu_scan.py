@@ -27,7 +27,8 @@ REF_SHAPES = [(2, 64, 32, 16), (1, 100, 17, 16), (4, 63, 128, 16), (1, 1, 16, 16
               (2, 130, 40, 8), (3, 512, 856, 16)]
 EDGE_SHAPES = [(2, 128, 64, 16), (2, 1000, 64, 16), (2, 96, 1000, 16), (1, 1, 1536, 16),
                (1, 512, 1536, 16), (4, 512, 256, 8), (2, 33, 70, 4), (2, 40, 64, 12),
-               (1, 20, 64, 5), (2, 48, 96, 32), (1, 24, 128, 64)]
+               (1, 20, 64, 5), (2, 48, 96, 32), (1, 24, 128, 64), (2, 37, 96, 40),
+               (1, 50, 33, 1)]
 
 
 def _to_dev(arrs):
@@ -158,11 +159,12 @@ def test_backward_is_bitwise_deterministic():
         assert torch.equal(a, b)
 
 
-@pytest.mark.parametrize("npl", [1, 2, 4])
-def test_every_state_split_agrees(npl):
-    """Forcing 1, 2 or 4 state lanes per wave gives the same results."""
-    bt, t_len, d, n = 2, 100, 130, 16
-    print(f"[case] npl {npl}", flush=True)
+@pytest.mark.parametrize("npl,n", [(2, 16), (4, 16), (2, 7), (4, 7), (4, 24), (2, 32)])
+def test_every_state_split_agrees(npl, n):
+    """Forcing 2 or 4 states per lane (other block shapes, other padding of
+    d_state) gives the same results."""
+    bt, t_len, d = 2, 100, 130
+    print(f"[case] npl {npl} d_state {n}", flush=True)
     arrs = oracle.make_inputs(bt, t_len, d, n, seed=31, style="bench")
     dy = np.random.default_rng(2).standard_normal((bt, t_len, d), dtype=np.float32)
     y_ref, _, _ = oracle.scan_fwd(*arrs)
