@@ -30,7 +30,7 @@ Differences from the reference, by design:
 * ``chunk`` (the checkpoint stride) defaults to ``SSM_CHUNK = 16``, the
   backward kernel's register window on gfx950; any ``chunk >= 1`` gives the
   same results.
-* d_state needs not be a multiple of 4 (see ``include/mamba_hip_scan.h``).
+* d_state is any value in 1..64 (the reference needs a multiple of 4).
 * dB, dC and dAneg are reduced in a fixed order: the backward is bit-for-bit
   reproducible.
 """
@@ -106,9 +106,8 @@ def _validate(x, dt, aneg, b_in, c_in, chunk) -> None:
     if not isinstance(chunk, int) or chunk < 1:
         raise ValueError(f"chunk (the checkpoint stride) must be a positive int; got {chunk!r}")
     if n > 0 and _native.preferred_chunk(n) == 0:
-        raise ValueError(f"d_state {n} is not supported by the HIP scan (supported: 1..16, "
-                         f"even up to 32, multiples of 4 up to 64; scan_impl='torch' takes "
-                         f"any size)")
+        raise ValueError(f"d_state {n} is not supported by the HIP scan (supported: 1..64; "
+                         f"scan_impl='torch' takes any size)")
 
 
 class SelectiveScanHIP(torch.autograd.Function):
@@ -162,8 +161,17 @@ def selective_scan_hip(x: torch.Tensor, dt: torch.Tensor, aneg: torch.Tensor,
     return SelectiveScanHIP.apply(x, dt, aneg, b_in, c_in, chunk, return_state)
 
 
-# Drop-in spelling for code written against the reference.
-selective_scan_metal = selective_scan_hip
+def selective_scan_metal(x: torch.Tensor, dt: torch.Tensor, aneg: torch.Tensor,
+                         b_in: torch.Tensor, c_in: torch.Tensor,
+                         chunk: int = SSM_CHUNK, dblock: Optional[int] = None,
+                         return_state: bool = False):
+    """Drop-in spelling of the reference's selective_scan_metal (scan.py:414-421).
+
+    ``dblock`` (channels per Metal threadgroup there) is accepted for call
+    compatibility and ignored: the gfx950 launch shape is chosen by the library.
+    """
+    del dblock
+    return SelectiveScanHIP.apply(x, dt, aneg, b_in, c_in, chunk, return_state)
 
 
 def selective_scan(x: torch.Tensor, dt: torch.Tensor, aneg: torch.Tensor,

@@ -1,0 +1,131 @@
+"""The C-ABI library on the CPU: it loads, exports every symbol the header
+declares, and rejects bad arguments with MHS_EINVAL and a message before any
+HIP call is made (no GPU needed; no kernel is launched here).
+"""
+from __future__ import annotations
+
+import ctypes
+import re
+from pathlib import Path
+
+import pytest
+import torch
+
+from mamba_metal_scan_amd import _native
+
+HEADER = Path(__file__).resolve().parents[1] / "include" / "mamba_hip_scan.h"
+MHS_OK, MHS_EINVAL = 0, 1
+
+# Fake device addresses: the calls below fail validation before any use. So
+# that a regression in validation can never turn them into kernel launches on
+# bogus pointers, the module runs only on hosts without a GPU.
+pytestmark = pytest.mark.skipif(torch.cuda.is_available(),
+                                reason="argument checks with fake device addresses: CPU hosts only")
+A16 = ctypes.c_void_p(0x7F0000001000)     # 16-byte (and 256-byte) aligned
+MIS = ctypes.c_void_p(0x7F0000001004)     # misaligned
+
+
+def _declared_symbols():
+    text = HEADER.read_text()
+    return sorted(set(re.findall(r"\b(mhs_\w+)\s*\(", text)))
+
+
+def _err(lib) -> str:
+    return lib.mhs_last_error().decode()
+
+
+def test_header_and_binding_agree():
+    assert _declared_symbols() == sorted(_native.EXPORTED_SYMBOLS)
+
+
+def test_library_exports_every_declared_symbol():
+    lib = _native.library()
+    for name in _declared_symbols():
+        assert hasattr(lib, name), name
+    assert lib.mhs_version() >> 16 == 0 and (lib.mhs_version() >> 8) & 0xFF >= 1
+
+
+def test_chunk_arithmetic():
+    lib = _native.library()
+    assert lib.mhs_num_chunks(512, 16) == 32
+    assert lib.mhs_num_chunks(512, 64) == 8
+    assert lib.mhs_num_chunks(100, 7) == 15
+    assert lib.mhs_num_chunks(1, 512) == 1
+    assert lib.mhs_num_chunks(0, 16) == 0
+    for n in (1, 5, 8, 16, 17, 32, 40, 64):
+        assert lib.mhs_preferred_chunk(n) == 16
+    assert lib.mhs_preferred_chunk(0) == 0
+    assert lib.mhs_preferred_chunk(65) == 0
+
+
+def test_workspace_size_formula():
+    """dB/dC block partials (48 blocks of 32 channels) + dAneg batch partials,
+    + fine checkpoints when the stride exceeds the 16-step window."""
+    lib = _native.library()
+    nblk, s, a = 48, 16 * 512 * 16, 16 * 1536 * 16
+    base = 2 * nblk * s * 4 + a * 4
+    assert lib.mhs_scan_bwd_workspace_bytes(16, 512, 1536, 16, 16) == base
+    assert lib.mhs_scan_bwd_workspace_bytes(16, 512, 1536, 16, 64) == base + 32 * a * 4
+    assert lib.mhs_scan_bwd_workspace_bytes(16, 512, 1536, 0, 16) == 0
+
+
+def test_set_variant_rejects_unknown_splits():
+    lib = _native.library()
+    with pytest.raises(_native.HipScanError, match="states per lane"):
+        _native.set_variant(3)
+    assert lib.mhs_set_variant(1) == MHS_EINVAL
+    assert lib.mhs_set_variant(0) == MHS_OK
+    # With two states per lane, d_state above 32 has no plan.
+    try:
+        _native.set_variant(2)
+        assert lib.mhs_preferred_chunk(40) == 0
+    finally:
+        _native.set_variant(0)
+    assert lib.mhs_preferred_chunk(40) == 16
+
+
+def _fwd(lib, ptrs, sizes):
+    return lib.mhs_scan_fwd_f32(*ptrs, *sizes, None)
+
+
+def test_forward_argument_errors():
+    lib = _native.library()
+    good = [A16] * 8
+    assert _fwd(lib, [None] + good[1:], (2, 8, 32, 16, 16)) == MHS_EINVAL
+    assert "null" in _err(lib)
+    assert _fwd(lib, [MIS] + good[1:], (2, 8, 32, 16, 16)) == MHS_EINVAL
+    assert "16-byte aligned" in _err(lib)
+    assert _fwd(lib, good, (2, 8, 32, 65, 16)) == MHS_EINVAL
+    assert "d_state" in _err(lib)
+    assert _fwd(lib, good, (0, 8, 32, 16, 16)) == MHS_EINVAL
+    assert "positive" in _err(lib)
+    assert _fwd(lib, good, (2, 8, 32, 16, 0)) == MHS_EINVAL
+    assert "chunk" in _err(lib)
+    assert _fwd(lib, good, (70000, 8, 32, 16, 16)) == MHS_EINVAL
+    assert "batch" in _err(lib)
+    assert _fwd(lib, good, (1, 8, 1 << 25, 16, 16)) == MHS_EINVAL
+    assert "too large" in _err(lib)
+
+
+def test_backward_argument_errors():
+    lib = _native.library()
+    sizes = (2, 8, 32, 16, 16)
+    ptrs = [A16] * 13
+    need = lib.mhs_scan_bwd_workspace_bytes(*sizes)
+    assert need > 0
+    rc = lib.mhs_scan_bwd_f32(*ptrs, A16, need - 4, *sizes, None)
+    assert rc == MHS_EINVAL and "workspace too small" in _err(lib)
+    rc = lib.mhs_scan_bwd_f32(*ptrs, MIS, need, *sizes, None)
+    assert rc == MHS_EINVAL and "256-byte" in _err(lib)
+    bad = list(ptrs)
+    bad[7] = None       # ckpt
+    rc = lib.mhs_scan_bwd_f32(*bad, A16, need, *sizes, None)
+    assert rc == MHS_EINVAL and "null" in _err(lib)
+
+
+def test_step_argument_errors():
+    lib = _native.library()
+    rc = lib.mhs_scan_step_f32(*([A16] * 6), None, 2, 32, 16, None)
+    assert rc == MHS_EINVAL and "null" in _err(lib)
+    rc = lib.mhs_scan_step_f32(*([A16] * 6), MIS, 2, 32, 16, None)
+    assert rc == MHS_EINVAL and "aligned" in _err(lib)

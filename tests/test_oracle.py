@@ -1,0 +1,228 @@
+"""Pins of the float64 oracle (oracle/scan_oracle.c) on the CPU.
+
+The reference holds no data files or golden vectors for the scan, so the
+oracle is pinned by what the mathematics fixes (mamba_metal/scan.py:13-41):
+
+* forward: an independent O(T^2) closed-form evaluation with no recurrence;
+  T = 1, Aneg = 0 (prefix sum), constant inputs (geometric series), x = 0;
+  linearity in x, causality, checkpoint = state at the chunk's last step,
+  decode steps chained = the scan;
+* backward: central finite differences of the oracle's own forward for every
+  input (and for the returned state, dh_last), a directional (JVP/VJP)
+  dot-product test, and the brute-force dC = sum_d dy * h;
+* each check rejects a planted mistake (a transposed operand, a dropped term,
+  a wrong sign), so a plausible slip in the oracle cannot pass it.
+"""
+from __future__ import annotations
+
+import numpy as np
+import pytest
+
+from oracle import oracle
+
+RNG_SEED = 20240
+
+
+def _inputs(bt, t_len, d, n, seed, style="ref"):
+    return [a.astype(np.float64) for a in oracle.make_inputs(bt, t_len, d, n, seed, style)]
+
+
+def _h_all(x, dt, aneg, b_in, c_in):
+    """Every state h[b,t,d,n] from the decode-step oracle chained over t."""
+    bt, t_len, d = x.shape
+    n = aneg.shape[1]
+    h = np.zeros((bt, d, n))
+    hs = []
+    for t in range(t_len):
+        h, _ = oracle.scan_step(h, x[:, t], dt[:, t], aneg, b_in[:, t], c_in[:, t])
+        hs.append(h)
+    return np.stack(hs, axis=1)
+
+
+# ------------------------------------------------------------------ forward
+
+@pytest.mark.parametrize("shape", [(2, 1, 3, 4), (1, 17, 5, 8), (2, 40, 7, 5), (1, 33, 4, 16)])
+def test_forward_matches_the_closed_form(shape):
+    arrs = _inputs(*shape, seed=RNG_SEED + shape[1])
+    y, _, h_last = oracle.scan_fwd(*arrs)
+    y_cf, h_cf = oracle.scan_fwd_closed_form(*arrs)
+    assert np.abs(y - y_cf).max() <= 1e-12 * max(1.0, np.abs(y_cf).max())
+    assert np.abs(h_last - h_cf).max() <= 1e-12 * max(1.0, np.abs(h_cf).max())
+
+
+def test_single_step_is_dt_x_times_c_dot_b():
+    x, dt, aneg, b_in, c_in = _inputs(3, 1, 6, 8, seed=1)
+    y, _, h = oracle.scan_fwd(x, dt, aneg, b_in, c_in)
+    expect = dt[:, 0] * x[:, 0] * (c_in[:, 0] * b_in[:, 0]).sum(-1)[:, None]
+    np.testing.assert_allclose(y[:, 0], expect, rtol=1e-13, atol=1e-15)
+    np.testing.assert_allclose(h, (dt * x)[:, 0, :, None] * b_in[:, 0, None, :], rtol=1e-13)
+
+
+def test_zero_decay_is_a_prefix_sum():
+    x, dt, aneg, b_in, c_in = _inputs(2, 25, 4, 6, seed=2)
+    aneg = np.zeros_like(aneg)
+    y, _, h_last = oracle.scan_fwd(x, dt, aneg, b_in, c_in)
+    h = np.cumsum((dt * x)[..., None] * b_in[:, :, None, :], axis=1)
+    np.testing.assert_allclose(y, (h * c_in[:, :, None, :]).sum(-1), rtol=1e-12, atol=1e-12)
+    np.testing.assert_allclose(h_last, h[:, -1], rtol=1e-12, atol=1e-12)
+
+
+def test_constant_inputs_give_a_geometric_series():
+    bt, t_len, d, n = 1, 30, 2, 3
+    x = np.full((bt, t_len, d), 0.7)
+    dt = np.full((bt, t_len, d), 0.05)
+    aneg = np.array([[1.0, 2.0, 3.0], [0.5, 4.0, 8.0]])
+    b_in = np.tile(np.array([0.3, -1.2, 2.0]), (bt, t_len, 1))
+    c_in = np.ones((bt, t_len, n))
+    _, _, h_last = oracle.scan_fwd(x, dt, aneg, b_in, c_in)
+    a = np.exp(-0.05 * aneg)                       # (d, n)
+    b = 0.05 * 0.7 * np.array([0.3, -1.2, 2.0])    # (n,)
+    expect = b * (1 - a ** t_len) / (1 - a)
+    np.testing.assert_allclose(h_last[0], expect, rtol=1e-12)
+
+
+def test_zero_input_gives_zero_output():
+    x, dt, aneg, b_in, c_in = _inputs(2, 19, 5, 4, seed=3)
+    y, _, h = oracle.scan_fwd(np.zeros_like(x), dt, aneg, b_in, c_in)
+    assert not y.any() and not h.any()
+
+
+def test_forward_is_linear_in_x():
+    x, dt, aneg, b_in, c_in = _inputs(2, 21, 5, 4, seed=4)
+    x2 = _inputs(2, 21, 5, 4, seed=5)[0]
+    y1 = oracle.scan_fwd(x, dt, aneg, b_in, c_in)[0]
+    y2 = oracle.scan_fwd(x2, dt, aneg, b_in, c_in)[0]
+    y12 = oracle.scan_fwd(2.5 * x - 0.5 * x2, dt, aneg, b_in, c_in)[0]
+    np.testing.assert_allclose(y12, 2.5 * y1 - 0.5 * y2, rtol=1e-11, atol=1e-12)
+
+
+def test_forward_is_causal():
+    arrs = _inputs(1, 30, 4, 4, seed=6)
+    y = oracle.scan_fwd(*arrs)[0]
+    pert = [a.copy() for a in arrs]
+    for i in (0, 1, 3, 4):
+        pert[i][:, 12:] += 1.0
+    y2 = oracle.scan_fwd(*pert)[0]
+    assert np.array_equal(y[:, :12], y2[:, :12])
+    assert not np.allclose(y[:, 12:], y2[:, 12:])
+
+
+@pytest.mark.parametrize("chunk", [1, 4, 7, 16, 30, 64])
+def test_checkpoints_are_the_state_at_each_chunk_end(chunk):
+    arrs = _inputs(2, 30, 3, 4, seed=7)
+    _, ckpt, h_last = oracle.scan_fwd(*arrs, chunk=chunk)
+    h = _h_all(*arrs)
+    ends = [min((c + 1) * chunk, 30) - 1 for c in range((30 + chunk - 1) // chunk)]
+    assert ckpt.shape == (2, len(ends), 3, 4)
+    np.testing.assert_allclose(ckpt, h[:, ends], rtol=1e-13, atol=1e-15)
+    np.testing.assert_allclose(h_last, h[:, -1], rtol=1e-13, atol=1e-15)
+
+
+def test_decode_steps_chain_to_the_scan():
+    arrs = _inputs(2, 23, 5, 8, seed=8)
+    y, _, _ = oracle.scan_fwd(*arrs)
+    h = _h_all(*arrs)
+    np.testing.assert_allclose(y, (h * arrs[4][:, :, None, :]).sum(-1), rtol=1e-12, atol=1e-14)
+
+
+def test_state_passing_continues_the_scan():
+    """Scanning [:t0], then stepping on from its h_last, equals the full scan."""
+    x, dt, aneg, b_in, c_in = _inputs(1, 26, 4, 4, seed=9)
+    y_full = oracle.scan_fwd(x, dt, aneg, b_in, c_in)[0]
+    _, _, h = oracle.scan_fwd(x[:, :11], dt[:, :11], aneg, b_in[:, :11], c_in[:, :11])
+    for t in range(11, 26):
+        h, yt = oracle.scan_step(h, x[:, t], dt[:, t], aneg, b_in[:, t], c_in[:, t])
+        np.testing.assert_allclose(yt, y_full[:, t], rtol=1e-12, atol=1e-14)
+
+
+# ----------------------------------------------------------------- backward
+
+def _loss(arrs, dy, dh=None):
+    y, _, h_last = oracle.scan_fwd(*arrs)
+    v = float((y * dy).sum())
+    if dh is not None:
+        v += float((h_last * dh).sum())
+    return v
+
+
+def _fd_check(grads, arrs, dy, dh=None, per_tensor=8, seed=0, eps=1e-6):
+    """max relative deviation of grads from central differences."""
+    rng = np.random.default_rng(seed)
+    worst = 0.0
+    for i, (g, a) in enumerate(zip(grads, arrs)):
+        flat = a.reshape(-1)
+        for j in rng.permutation(flat.size)[:per_tensor]:
+            p, m = [t.copy() for t in arrs], [t.copy() for t in arrs]
+            p[i].reshape(-1)[j] += eps
+            m[i].reshape(-1)[j] -= eps
+            fd = (_loss(p, dy, dh) - _loss(m, dy, dh)) / (2 * eps)
+            scale = max(np.abs(g).max(), 1e-12)
+            worst = max(worst, abs(g.reshape(-1)[j] - fd) / scale)
+    return worst
+
+
+@pytest.mark.parametrize("shape", [(1, 9, 3, 4), (2, 14, 2, 5)])
+def test_gradients_match_finite_differences(shape):
+    arrs = _inputs(*shape, seed=11)
+    dy = np.random.default_rng(12).standard_normal(arrs[0].shape)
+    grads = oracle.scan_bwd(*arrs, dy)
+    assert _fd_check(grads, arrs, dy) < 1e-7
+
+
+def test_state_gradient_matches_finite_differences():
+    arrs = _inputs(1, 12, 3, 4, seed=13)
+    rng = np.random.default_rng(14)
+    dy = rng.standard_normal(arrs[0].shape)
+    dh = rng.standard_normal((1, 3, 4))
+    grads = oracle.scan_bwd(*arrs, dy, dh_last=dh)
+    assert _fd_check(grads, arrs, dy, dh) < 1e-7
+
+
+def test_vjp_dot_product():
+    """<dy, J v> == <J^T dy, v> for a random direction v over all inputs."""
+    arrs = _inputs(2, 16, 3, 4, seed=15)
+    rng = np.random.default_rng(16)
+    dy = rng.standard_normal(arrs[0].shape)
+    v = [rng.standard_normal(a.shape) for a in arrs]
+    eps = 1e-6
+    yp = oracle.scan_fwd(*[a + eps * w for a, w in zip(arrs, v)])[0]
+    ym = oracle.scan_fwd(*[a - eps * w for a, w in zip(arrs, v)])[0]
+    jv = ((yp - ym) / (2 * eps) * dy).sum()
+    vjp = sum(float((g * w).sum()) for g, w in zip(oracle.scan_bwd(*arrs, dy), v))
+    assert abs(jv - vjp) <= 1e-7 * max(1.0, abs(vjp))
+
+
+def test_dc_is_dy_times_state_summed_over_channels():
+    arrs = _inputs(2, 13, 4, 3, seed=17)
+    dy = np.random.default_rng(18).standard_normal(arrs[0].shape)
+    dc = oracle.scan_bwd(*arrs, dy)[4]
+    h = _h_all(*arrs)
+    np.testing.assert_allclose(dc, np.einsum("btd,btdn->btn", dy, h), rtol=1e-12, atol=1e-14)
+
+
+# ------------------------------------------------------- planted mistakes
+
+def test_checks_reject_planted_mistakes():
+    """Each pin above fails for a plausible slip in the oracle."""
+    arrs = _inputs(1, 10, 3, 4, seed=19)
+    dy = np.random.default_rng(20).standard_normal(arrs[0].shape)
+    grads = list(oracle.scan_bwd(*arrs, dy))
+    # Transposed operands: B and C swapped in the forward.
+    x, dt, aneg, b_in, c_in = arrs
+    y_swapped = oracle.scan_fwd(x, dt, aneg, c_in, b_in)[0]
+    y_cf = oracle.scan_fwd_closed_form(*arrs)[0]
+    assert np.abs(y_swapped - y_cf).max() > 1e-3
+    # Wrong sign of the decay (exp(+dt*Aneg)).
+    assert np.abs(oracle.scan_fwd(x, dt, -aneg, b_in, c_in)[0] - y_cf).max() > 1e-3
+    # Gradient mistakes: dB and dC exchanged, dAneg sign flipped, ddt missing
+    # its x * sum(G*B) term (ddt - dx * x / dt).
+    bad_bc = grads[:3] + [grads[4], grads[3]]
+    assert _fd_check(bad_bc, arrs, dy) > 1e-2
+    bad_sign = grads[:2] + [-grads[2]] + grads[3:]
+    assert _fd_check(bad_sign, arrs, dy) > 1e-2
+    bad_ddt = [grads[0], grads[1] - grads[0] * x / dt] + grads[2:]
+    assert _fd_check(bad_ddt, arrs, dy) > 1e-2
+    # The dC pin rejects dC computed from the pre-update state.
+    h = _h_all(*arrs)
+    h_prev = np.concatenate([np.zeros_like(h[:, :1]), h[:, :-1]], axis=1)
+    assert np.abs(np.einsum("btd,btdn->btn", dy, h_prev) - grads[4]).max() > 1e-3
