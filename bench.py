@@ -36,6 +36,7 @@ sys.path.insert(0, str(ROOT))
 
 METRIC = ("fwd+bwd scan ms & % HBM roofline (16x512x1536x16 fp32); 80M train tok/s")
 HBM_PEAK_GBS = 8000.0
+COPY_BYTES = 50_331_648      # calibration copy for the --pmc traffic figures
 
 
 def scan_bytes(bt: int, t_len: int, d: int, n: int) -> dict:
@@ -109,6 +110,110 @@ def cpu_baseline_scan(bt, t_len, d, n) -> dict:
             "ms_per_step": el * 1e3, "cpu": cpu_model,
             "sample": f"selective_scan(impl='torch') fwd+bwd, full {bt}x{t_len}x{d}x{n} "
                       f"workload, 1 rep, torch CPU threads={threads}"}
+
+
+def run_launches(args) -> None:
+    """Profiling driver: the scan's forward and backward launches (no timing,
+    no CPU work) and a calibration copy of a known byte count, for
+    `rocprofv3 --kernel-trace --stats` and `rocprofv3 --pmc ...` passes."""
+    import torch
+    from mamba_metal_scan_amd import _native   # registers the mamba_hip ops
+    _native.library()
+    bt, t_len, d, n = args.batch, args.seqlen, args.d_inner, args.d_state
+    dev = torch.device("cuda", 0)
+    x, dt, aneg, b_in, c_in, dy = (t.to(dev) for t in make_inputs(bt, t_len, d, n))
+    for i in range(args.launches):
+        _, ckpt, _ = torch.ops.mamba_hip.scan_fwd(x, dt, aneg, b_in, c_in, args.chunk, True)
+        torch.ops.mamba_hip.scan_bwd(x, dt, aneg, b_in, c_in, dy, None, ckpt, args.chunk)
+    src = torch.empty(COPY_BYTES // 4, device=dev)
+    dst = torch.empty_like(src)
+    for _ in range(args.launches):
+        dst.copy_(src)
+    torch.cuda.synchronize()
+    print(f"launches done: {args.launches} x (scan_fwd, scan_bwd) at {bt}x{t_len}x{d}x{n} "
+          f"chunk {args.chunk}, {args.launches} x copy of {COPY_BYTES} B", flush=True)
+
+
+def _short_kernel(name: str) -> str:
+    for key, short in (("fwd_kernel", "fwd_kernel"), ("bwd_reduce", "bwd_reduce_kernel"),
+                       ("bwd_kernel", "bwd_kernel"), ("copyBuffer", "copy")):
+        if key in name:
+            return short
+    return name[:40]
+
+
+def pmc_summary(args) -> None:
+    """Per-launch HBM traffic from two rocprofv3 --pmc passes (FETCH_SIZE, then
+    WRITE_SIZE, KiB per dispatch) under args.pmc_summary, each scaled by what
+    the counter reads for the calibration copy of COPY_BYTES; writes the
+    traffic file bench.py reports from and prints a markdown table."""
+    import csv
+    import glob
+    vals: dict = {}
+    for f in glob.glob(os.path.join(args.pmc_summary, "**", "*counter_collection.csv"),
+                       recursive=True):
+        for r in csv.DictReader(open(f)):
+            k = (_short_kernel(r["Kernel_Name"]), r["Counter_Name"])
+            vals.setdefault(k, []).append(float(r["Counter_Value"]))
+    mean = {k: sum(v) / len(v) for k, v in vals.items()}
+    fetch_factor = COPY_BYTES / (mean[("copy", "FETCH_SIZE")] * 1024)
+    write_factor = COPY_BYTES / (mean[("copy", "WRITE_SIZE")] * 1024)
+    shape = (args.batch, args.seqlen, args.d_inner, args.d_state)
+    nbytes = scan_bytes(*shape)
+    rows = {}
+    for kern in ("fwd_kernel", "bwd_kernel", "bwd_reduce_kernel"):
+        rd = mean[(kern, "FETCH_SIZE")] * 1024 * fetch_factor
+        wr = mean[(kern, "WRITE_SIZE")] * 1024 * write_factor
+        rows[kern] = {"read_bytes": rd, "write_bytes": wr, "hbm_bytes": rd + wr}
+    bwd_total = rows["bwd_kernel"]["hbm_bytes"] + rows["bwd_reduce_kernel"]["hbm_bytes"]
+    tag = "x".join(map(str, shape))
+    out = {
+        "workload": f"selective_scan {tag} chunk {args.chunk}",
+        "hbm_bytes_per_launch": bwd_total,
+        "launch": "scan backward (bwd_kernel + bwd_reduce_kernel)",
+        "algorithmic_bytes": nbytes["bwd"],
+        "fwd_hbm_bytes_per_launch": rows["fwd_kernel"]["hbm_bytes"],
+        "fwd_algorithmic_bytes": nbytes["fwd"],
+        "kernels": rows,
+        "calibration": {"copy_bytes": COPY_BYTES, "fetch_factor": fetch_factor,
+                        "write_factor": write_factor},
+    }
+    path = ROOT / "profiles" / f"scan_bwd_{tag}_traffic.json"
+    path.write_text(json.dumps(out, indent=1) + "\n")
+    extra = " ".join(f"--{k.replace('_', '-')} {getattr(args, k)}"
+                     for k, dflt in (("batch", 16), ("seqlen", 512), ("d_inner", 1536),
+                                     ("d_state", 16), ("chunk", 16)) if getattr(args, k) != dflt)
+    lines = [f"# Scan kernels at {tag}, chunk {args.chunk} (fp32): kernel time and HBM traffic",
+             "", "All commands run from /tmp with `TMPDIR=/tmp`; OUT is the output folder.", ""]
+    stats = os.path.join(args.pmc_summary, "kt", "run_kernel_stats.csv")
+    if os.path.exists(stats):
+        lines += ["## Kernel trace", "",
+                  "    rocprofv3 --kernel-trace --stats -d OUT/kt -o run --output-format csv -- \\",
+                  f"        python3 bench.py --steps 20 --warmup 5 --no-cpu-baseline {extra}", "",
+                  "| kernel | calls | avg us | min us | max us |", "|---|---|---|---|---|"]
+        for r in csv.DictReader(open(stats)):
+            lines.append(f"| `{r['Name'][:60]}` | {r['Calls']} | {float(r['AverageNs']) / 1e3:.1f} "
+                         f"| {float(r['MinNs']) / 1e3:.1f} | {float(r['MaxNs']) / 1e3:.1f} |")
+        lines += ["", "The backward launch (the `scan_bwd` op) is `bwd_kernel` + "
+                  "`bwd_reduce_kernel`.", ""]
+    lines += ["## HBM traffic per launch", "",
+              f"    rocprofv3 --pmc FETCH_SIZE -d OUT/fetch -o run --output-format csv -- "
+              f"python3 bench.py --launches 5 {extra}",
+              f"    rocprofv3 --pmc WRITE_SIZE -d OUT/write -o run --output-format csv -- "
+              f"python3 bench.py --launches 5 {extra}",
+              f"    python3 bench.py --pmc-summary OUT {extra}", "",
+              f"Calibration: a {COPY_BYTES} B device copy reads FETCH_SIZE x{fetch_factor:.3f} and "
+              f"WRITE_SIZE x{write_factor:.3f} of its true bytes; the figures below are scaled by "
+              f"those factors (KiB counters x 1024 x factor).", "",
+              "| kernel | read MB | write MB | HBM MB | algorithmic MB |", "|---|---|---|---|---|"]
+    for kern, r in rows.items():
+        alg = {"fwd_kernel": nbytes["fwd"], "bwd_kernel": nbytes["bwd"]}.get(kern)
+        lines.append(f"| {kern} | {r['read_bytes'] / 1e6:.1f} | {r['write_bytes'] / 1e6:.1f} | "
+                     f"{r['hbm_bytes'] / 1e6:.1f} | {'' if alg is None else f'{alg / 1e6:.1f}'} |")
+    md = ROOT / "profiles" / f"scan_{tag}.md"
+    md.write_text("\n".join(lines) + "\n")
+    print("\n".join(lines))
+    print(f"\nwrote {path.relative_to(ROOT)} and {md.relative_to(ROOT)}")
 
 
 def bench_scan(args) -> dict:
@@ -200,7 +305,15 @@ def main() -> int:
     ap.add_argument("--d-state", dest="d_state", type=int, default=16)
     ap.add_argument("--chunk", type=int, default=16)
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--launches", type=int, default=0,
+                    help="profiling driver: only N scan_fwd/scan_bwd launches + N copies")
+    ap.add_argument("--pmc-summary", default=None, metavar="DIR",
+                    help="summarise rocprofv3 FETCH_SIZE / WRITE_SIZE passes under DIR")
     args = ap.parse_args()
+
+    if args.pmc_summary:
+        pmc_summary(args)
+        return 0
 
     if args.gpus != 1:
         print(f"bench.py measures one GPU: this build runs on a single MI355X and has no "
@@ -210,6 +323,9 @@ def main() -> int:
     if not torch.cuda.is_available():
         print("bench.py needs a ROCm GPU (torch.cuda.is_available() is False)", file=sys.stderr)
         return 1
+    if args.launches:
+        run_launches(args)
+        return 0
     out = bench_scan(args)
     print(json.dumps(out), flush=True)
     return 0
