@@ -16,9 +16,12 @@ Reported:
   cpu_baseline   selective_scan(impl="torch") fwd+bwd on the host CPU, same
                  inputs, all threads of the process's CPU share
 
-Other workloads (--workload): "train" (80M TinyMamba train step), "longt"
-(4 x 16384 x 2048 x 16 fwd+bwd, checkpoint-stride sweep), "infer" (prefill
-32 x 2048 x 4096 x 16 + recurrent decode steps).
+  train_80m      the 80M TinyMamba train step (fwd + bwd + AdamW) with the HIP
+                 scan at batch 16 x seq 512: tokens/s and peak HBM
+
+Other workloads (--workload): "longt" (4 x 16384 x 2048 x 16 fwd+bwd,
+checkpoint-stride sweep), "infer" (prefill 32 x 2048 x 4096 x 16 + 256
+recurrent decode steps).
 
 Only one GPU is used: --gpus N > 1 exits with a message.
 """
@@ -216,6 +219,115 @@ def pmc_summary(args) -> None:
     print(f"\nwrote {path.relative_to(ROOT)} and {md.relative_to(ROOT)}")
 
 
+def bench_train(steps: int = 10, warmup: int = 3) -> dict:
+    """The 80M TinyMamba train step (fwd + bwd + AdamW lr 3e-4) with the HIP
+    scan: vocab 32768, d_model 640, 12 layers, d_ff 2560 (d_inner 1432),
+    d_state 16, batch 16 x seq 512, random init, tokens uniform in [0, 32768)."""
+    import torch
+    from mamba_metal_scan_amd import MambaConfig, TinyMamba
+    torch.manual_seed(1337)
+    dev = torch.device("cuda", 0)
+    cfg = MambaConfig(vocab_size=32768, d_model=640, n_layers=12, d_ff=2560, max_seq_len=512,
+                      d_state=16, d_conv=4, scan_impl="hip")
+    model = TinyMamba(cfg).to(dev)
+    opt = torch.optim.AdamW(model.parameters(), lr=3e-4)
+    idx = torch.randint(0, 32768, (16, 513), generator=torch.Generator().manual_seed(1337)).to(dev)
+    x, y = idx[:, :-1], idx[:, 1:]
+
+    def step():
+        _, loss = model(x, y)
+        opt.zero_grad(set_to_none=True)
+        loss.backward()
+        opt.step()
+        return loss
+
+    for _ in range(warmup):
+        step()
+    torch.cuda.synchronize()
+    torch.cuda.reset_peak_memory_stats(dev)
+    t0 = time.perf_counter()
+    for _ in range(steps):
+        loss = step()
+    torch.cuda.synchronize()
+    el = time.perf_counter() - t0
+    out = {"tokens_per_s": 16 * 512 * steps / el, "ms_per_step": el * 1e3 / steps,
+           "steps": steps, "warmup": warmup, "loss": float(loss.item()),
+           "params": model.count_params(), "d_inner": model.d_inner,
+           "peak_hbm_GB": torch.cuda.max_memory_allocated(dev) / 1e9,
+           "config": "TinyMamba 80M (vocab 32768, d_model 640, 12 layers, d_state 16), "
+                     "batch 16 x seq 512, fp32, AdamW, scan_impl=hip"}
+    del model, opt
+    torch.cuda.empty_cache()
+    return out
+
+
+def bench_longt(args) -> dict:
+    """Long-sequence scan 4 x 16384 x 2048 x 16 fwd+bwd, checkpoint strides 16/32/64/128."""
+    import torch
+    from mamba_metal_scan_amd import _native
+    _native.library()
+    bt, t_len, d, n = 4, 16384, 2048, 16
+    dev = torch.device("cuda", 0)
+    x, dt, aneg, b_in, c_in, dy = (t.to(dev) for t in make_inputs(bt, t_len, d, n))
+    nbytes = scan_bytes(bt, t_len, d, n)
+    rows = []
+    for chunk in (16, 32, 64, 128):
+        fwd = lambda: torch.ops.mamba_hip.scan_fwd(x, dt, aneg, b_in, c_in, chunk, True)
+        _, ckpt, _ = fwd()
+        bwd = lambda: torch.ops.mamba_hip.scan_bwd(x, dt, aneg, b_in, c_in, dy, None, ckpt, chunk)
+        bwd()
+        f_ms, b_ms = time_events(fwd, 5), time_events(bwd, 5)
+        rows.append({"chunk": chunk, "fwd_ms": f_ms, "bwd_ms": b_ms, "fwd_bwd_ms": f_ms + b_ms,
+                     "fwd_bwd_GBs": nbytes["fwd_bwd"] / ((f_ms + b_ms) * 1e-3) / 1e9,
+                     "ckpt_bytes": ckpt.numel() * 4})
+        print(f"longt chunk {chunk}: fwd {f_ms:.3f} ms bwd {b_ms:.3f} ms", file=sys.stderr,
+              flush=True)
+    best = min(rows, key=lambda r: r["fwd_bwd_ms"])
+    return {"metric": "long-sequence scan fwd+bwd GB/s (4x16384x2048x16 fp32)",
+            "value": best["fwd_bwd_GBs"], "unit": "GB/s", "n_gpus": 1,
+            "ms_per_step": best["fwd_bwd_ms"], "higher_is_better": True, "dtype": "f32",
+            "data": "synthetic", "algorithmic_bytes": nbytes["fwd_bwd"],
+            "config": {"workload": "selective_scan fwd+bwd 4x16384x2048x16, stride sweep"},
+            "strides": rows}
+
+
+def bench_infer(args) -> dict:
+    """Prefill 32 x 2048 x 4096 x 16 (forward + final state), then 256 decode steps."""
+    import torch
+    from mamba_metal_scan_amd import _native, selective_state_step
+    _native.library()
+    bt, t_len, d, n = 32, 2048, 4096, 16
+    dev = torch.device("cuda", 0)
+    x, dt, aneg, b_in, c_in, _ = (t.to(dev) for t in make_inputs(bt, t_len, d, n))
+    prefill = lambda: torch.ops.mamba_hip.scan_fwd(x, dt, aneg, b_in, c_in, t_len, False)
+    prefill()
+    p_ms = time_events(prefill, 5)
+    p_bytes = 4 * (3 * bt * t_len * d + 2 * bt * t_len * n + d * n) + 4 * bt * d * n
+    _, _, h = prefill()
+    g = torch.Generator().manual_seed(7)
+    steps = 256
+    xs = torch.randn(steps, bt, d, generator=g).to(dev)
+    dts = torch.nn.functional.softplus(torch.randn(steps, bt, d, generator=g) - 4.0).to(dev)
+    bs = torch.randn(steps, bt, n, generator=g).to(dev)
+    cs = torch.randn(steps, bt, n, generator=g).to(dev)
+    selective_state_step(h, xs[0], dts[0], aneg, bs[0], cs[0])
+    torch.cuda.synchronize()
+    start, stop = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    start.record()
+    for i in range(steps):
+        selective_state_step(h, xs[i], dts[i], aneg, bs[i], cs[i])
+    stop.record()
+    torch.cuda.synchronize()
+    s_us = start.elapsed_time(stop) * 1e3 / steps
+    s_bytes = 4 * (2 * bt * d * n + 3 * bt * d + 2 * bt * n + d * n)
+    return {"metric": "prefill GB/s and decode us/step (32x2048x4096x16 fp32)",
+            "value": p_bytes / (p_ms * 1e-3) / 1e9, "unit": "GB/s", "n_gpus": 1,
+            "ms_per_step": p_ms, "higher_is_better": True, "dtype": "f32", "data": "synthetic",
+            "config": {"workload": "prefill 32x2048x4096x16 + 256 decode steps"},
+            "decode_us_per_step": s_us, "decode_GBs": s_bytes / (s_us * 1e-6) / 1e9,
+            "prefill_algorithmic_bytes": p_bytes, "decode_algorithmic_bytes": s_bytes}
+
+
 def bench_scan(args) -> dict:
     import torch
     from mamba_metal_scan_amd import _native, selective_scan_hip
@@ -287,6 +399,8 @@ def bench_scan(args) -> dict:
                          "algorithmic_bytes": nbytes["fwd_bwd"]},
         "library_version": hex(_native.library().mhs_version()),
     }
+    if not args.no_train:
+        out["train_80m"] = bench_train()
     if not args.no_cpu_baseline:
         out["cpu_baseline"] = cpu_baseline_scan(bt, t_len, d, n)
     return out
@@ -298,7 +412,8 @@ def main() -> int:
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=50)
     ap.add_argument("--warmup", type=int, default=10)
-    ap.add_argument("--workload", default="scan", choices=["scan"])
+    ap.add_argument("--workload", default="scan", choices=["scan", "longt", "infer"])
+    ap.add_argument("--no-train", action="store_true", help="skip the 80M train-step figure")
     ap.add_argument("--batch", type=int, default=16)
     ap.add_argument("--seqlen", type=int, default=512)
     ap.add_argument("--d-inner", dest="d_inner", type=int, default=1536)
@@ -326,7 +441,7 @@ def main() -> int:
     if args.launches:
         run_launches(args)
         return 0
-    out = bench_scan(args)
+    out = {"scan": bench_scan, "longt": bench_longt, "infer": bench_infer}[args.workload](args)
     print(json.dumps(out), flush=True)
     return 0
 
