@@ -17,14 +17,16 @@
 //     into VGPRs (da[16][NPL], hs[16][NPL]; nothing goes to global scratch):
 //     all dA and inputs b = B*dt*x first (independent), then the short chain
 //     h = dA*h + b. In the same straight-line code the waves also finish the
-//     previous (later-in-time) chunk (dx, ddt, dB/dC block sums), store the
-//     staged inputs of the next chunk into the other LDS buffer and issue the
-//     global loads of the chunk after that. All global accesses are
-//     bounds-checked buffer accesses whose resources end at the chunk's last
-//     step, so chunk and tensor edges need no branches.
+//     previous (later-in-time) chunk: dx, ddt from the per-wave sums and the
+//     x, dt tiles still in that chunk's LDS buffer, and the dB/dC block sums.
 //   reverse: walks the chunk backwards carrying G in VGPRs across chunk
 //     boundaries, with hm = dA * h_{t-1} from the recomputed chunk (no
-//     h_t - b_t cancellation).
+//     h_t - b_t cancellation). In the same code the waves store the staged
+//     inputs of the next chunk into the other LDS buffer (free once the
+//     previous chunk is finished) and issue the global loads of the chunk
+//     after that. All global accesses are bounds-checked buffer accesses
+//     whose resources end at the chunk's last step, so chunk and tensor edges
+//     need no branches.
 // Steps k >= len of a chunk (K < 16, or the tail of the sequence) see zero
 // inputs: dA = 1 and b = 0 there, so they are identity steps for h and G, add
 // zero to every accumulated gradient, and their outputs are not written.
@@ -36,13 +38,15 @@
 //             once, coalesced.
 //   dAneg:    accumulated per lane over the whole walk, written once per
 //             (b, d, n) to a workspace slot.
-//   dB / dC:  sums over the block's 32 channels. Each wave writes its
-//             per-lane G rows (weight dt*x) and h rows (weight dy) for two
-//             steps to LDS and reduces them: each lane does RR fused
-//             multiply-adds over a slice of channels (128-bit reads), then a
-//             DPP tree over the L lanes of the slice. The block sums are
-//             copied to a workspace slot; bwd_reduce_kernel adds the blocks in
-//             a fixed order, so the backward is bit-for-bit reproducible.
+//   dB / dC:  sums over the block's 32 channels, i.e. over the 32 lanes of a
+//             half-wave. Every two steps each lane forms its 4*NPL products
+//             G*(dt*x) and h*dy and the wave sums them over its half-waves
+//             with a register-only reduce-scatter (v_permlane16_swap, then
+//             DPP stages): no LDS round trip, and each lane ends with one
+//             total, which goes to the chunk's LDS tile of block sums. These
+//             are copied to a workspace slot; bwd_reduce_kernel adds the
+//             blocks in a fixed order, so the backward is bit-for-bit
+//             reproducible.
 #pragma once
 
 #include "mhs_common.hpp"
@@ -67,20 +71,15 @@ struct BwdArgs {
   int batch, T, D, N, K, nchunk;
 };
 
-constexpr int kRowStride = 68;   // reduction row pitch (64 lanes + 4: conflict-free reads)
-constexpr int kSB = 2;           // steps per reduction batch
-
 // One staging buffer (the kernel keeps two) and the single-buffered rest.
 __host__ __device__ constexpr int bwd_buf_floats(int G, int NPL) {
-  return 3 * kCH * kSteps               // dt, dy, dt*x (channel-major)
-         + 2 * kSteps * kCH             // dt*x, dy (step-major weights)
+  return 3 * kCH * kSteps               // dt, dy, x (channel-major)
          + 2 * kSteps * 2 * G * NPL;    // B, C tiles
 }
 __host__ __device__ constexpr int bwd_lds_floats(int G, int NPL) {
   return 2 * bwd_buf_floats(G, NPL)
          + G * 64 * kSteps                       // (s1, s2) per wave
-         + 2 * kSteps * 2 * G * NPL              // dB, dC block sums of a chunk
-         + G * (2 * NPL * kSB) * kRowStride;     // reduction rows
+         + 2 * kSteps * 2 * G * NPL;             // dB, dC block sums of a chunk
 }
 
 template <int NPL, int G, int MINW>
@@ -93,11 +92,8 @@ bwd_kernel(BwdArgs a) {
   constexpr int PERS = (kSteps * NP + NT - 1) / NT;
   constexpr int FT = (kSteps / 2 * kCH + NT - 1) / NT;      // dx/ddt tasks per thread
   constexpr int FK = kSteps * NP / NT;                      // dB (or dC) copies per thread
-  constexpr int RPS = 2 * NPL;          // reduction rows per time step
-  constexpr int RR = RPS * kSB;         // rows per reduction batch (= partials per lane)
-  constexpr int L = 64 / (RR * 2);      // lanes per half-row
+  constexpr int M = 4 * NPL;            // dB/dC products per lane per two steps
   static_assert(NPL == 2 || NPL == 4, "two or four states per lane");
-  static_assert(RR % 4 == 0 && 64 % (RR * 2) == 0 && L >= 1 && L <= 16, "bad reduction shape");
   static_assert(FK * NT == kSteps * NP, "dB/dC copy-out must tile the block");
 
   extern __shared__ float lds[];
@@ -119,10 +115,15 @@ bwd_kernel(BwdArgs a) {
 
   float* tS = lds + 2 * BUF;                          // [G][64][16]
   float* tDBC = tS + G * 64 * kSteps;                 // [2][16][NP]
-  float* tR = tDBC + 2 * kSteps * NP + wave * RR * kRowStride;
-  // Staging buffer j: dt, dy, dt*x (channel-major), dt*x, dy (step-major), B, C.
-  constexpr int oDY = kCH * kSteps, oDTX = 2 * kCH * kSteps, oWDTX = 3 * kCH * kSteps,
-                oWDY = 4 * kCH * kSteps, oB = 5 * kCH * kSteps, oC = oB + kSteps * NP;
+  // Staging buffer j: dt, dy, x (channel-major), B, C (per lane group).
+  constexpr int oDY = kCH * kSteps, oX = 2 * kCH * kSteps, oB = 3 * kCH * kSteps,
+                oC = oB + kSteps * NP;
+  // The reduce-scatter leaves lane `lane` with the total of product rs_index:
+  // products are numbered kind * 2NPL + slot * NPL + j (kind 0: dB, 1: dC;
+  // slot: step k + slot; j: state n0 + j of this half-wave's group).
+  const int rs = rs_index<M>(lane);
+  const int rs_kind = rs / (2 * NPL), rs_slot = (rs / NPL) & 1;
+  float* const dbc_out = tDBC + rs_kind * kSteps * NP + rs_slot * NP + n0 + (rs % NPL);
 
   const size_t slice = (size_t)D * N;
   const unsigned slice_bytes = 4u * (unsigned)slice;
@@ -171,17 +172,16 @@ bwd_kernel(BwdArgs a) {
     float* s0 = lds + j * BUF;
     ql.store_cm(s0, pd);
     ql.store_cm(s0 + oDY, py);
-    ql.store_cm_product(s0 + oDTX, pd, px);
-    ql.store_sm_product(s0 + oWDTX, pd, px);
-    ql.store_sm(s0 + oWDY, py);
+    ql.store_cm(s0 + oX, px);
     rl.store(s0 + oB, pb);
     rl.store(s0 + oC, pc);
   };
-  // dx, ddt and the dB, dC block sums of chunk ci, from tS and tDBC (which
-  // hold them until the next reverse phase). x and dt come from global memory
-  // (L2): the chunk's staging buffer is being refilled at the same time.
-  auto finalize = [&](int ci) {
-    const GBuf gx = chunk_buf(a.x, ci), gdt = chunk_buf(a.dt, ci);
+  // dx, ddt and the dB, dC block sums of chunk ci, staged in buffer j: from
+  // tS and tDBC (which hold them until the next reverse phase) and the
+  // chunk's x and dt tiles.
+  auto finalize = [&](int ci, int j) {
+    const float* sx = lds + j * BUF + oX;
+    const float* sdt = lds + j * BUF;
     const GBuf gdx = chunk_buf(a.dx, ci), gddt = chunk_buf(a.ddt, ci);
 #pragma unroll
     for (int f = 0; f < FT; ++f) {
@@ -191,7 +191,8 @@ bwd_kernel(BwdArgs a) {
       const int cc = task % kCH, k = 2 * (task / kCH);
       const unsigned o0 = (ok && d0 + cc < D) ? 4u * ((unsigned)k * (unsigned)D + cc) : kOOB;
       const unsigned o1 = o0 == kOOB ? kOOB : o0 + 4u * (unsigned)D;
-      const float x0 = gx.ld(o0), x1 = gx.ld(o1), t0v = gdt.ld(o0), t1v = gdt.ld(o1);
+      const float2 xv = lds2(sx + cm_elem(cc, k)), dtv = lds2(sdt + cm_elem(cc, k));
+      const float x0 = xv.x, x1 = xv.y, t0v = dtv.x, t1v = dtv.y;
       float s1a = 0.f, s1b = 0.f, s2a = 0.f, s2b = 0.f;
 #pragma unroll
       for (int w = 0; w < G; ++w) {
@@ -241,41 +242,42 @@ bwd_kernel(BwdArgs a) {
     float da[kSteps][NPL], hs[kSteps][NPL];
 #pragma unroll
     for (int m = 0; m < kQuads; ++m) {
-      float dts[4], dtxs[4], Bq[4][NPL];
+      float dts[4], xs[4], Bq[4][NPL];
       f4_to(dts, lds4(s0 + cm_quad(c, m)));
-      f4_to(dtxs, lds4(s0 + oDTX + cm_quad(c, m)));
+      f4_to(xs, lds4(s0 + oX + cm_quad(c, m)));
       load_quad_rows<NPL>(Bq, gB, m);
 #pragma unroll
-      for (int s = 0; s < 4; ++s)
+      for (int s = 0; s < 4; ++s) {
+        const float dtx = dts[s] * xs[s];
 #pragma unroll
         for (int j = 0; j < NPL; ++j) {
           da[4 * m + s][j] = exp2_hw(dts[s] * a2[j]);
-          hs[4 * m + s][j] = Bq[s][j] * dtxs[s];      // b_k, turned into h_k below
+          hs[4 * m + s][j] = Bq[s][j] * dtx;          // b_k, turned into h_k below
         }
-      if (m == 0) finalize(ci + 1);        // no-op stores past the sequence end
-      if (m == 1) store_sub((i + 1) & 1);  // chunk ci-1 (unused when ci == 0)
-      if (m == 2) load_sub(ci - 2);        // loads nothing when ci < 2
-      step_fence();
+      }
+      if (m == 0) finalize(ci + 1, (i + 1) & 1);   // no-op stores past the sequence end
     }
 #pragma unroll
     for (int k = 0; k < kSteps; ++k)
 #pragma unroll
       for (int j = 0; j < NPL; ++j)
         hs[k][j] = __builtin_fmaf(da[k][j], k == 0 ? hc[j] : hs[k - 1][j], hs[k][j]);
-    __syncthreads();   // finalize(ci+1) is done with tS / tDBC
+    __syncthreads();   // finalize(ci+1) is done with tS, tDBC and its buffer
 
     // ---- reverse phase
 #pragma unroll
     for (int m = kQuads - 1; m >= 0; --m) {
-      float dts[4], dys[4], Bq[4][NPL], Cq[4][NPL], s1q[4], s2q[4];
+      float dts[4], dys[4], xs[4], Bq[4][NPL], Cq[4][NPL], s1q[4], s2q[4];
       f4_to(dts, lds4(s0 + cm_quad(c, m)));
       f4_to(dys, lds4(s0 + oDY + cm_quad(c, m)));
+      f4_to(xs, lds4(s0 + oX + cm_quad(c, m)));
       load_quad_rows<NPL>(Bq, gB, m);
       load_quad_rows<NPL>(Cq, gC, m);
+      float pv[M];   // dB/dC products of the step pair (k, k+1), k even, numbered as for rs_index
 #pragma unroll
       for (int s = 3; s >= 0; --s) {
         const int k = 4 * m + s;
-        const int slot = k % kSB;
+        const int slot = k & 1;
         float s1 = 0.f, s2 = 0.f;
 #pragma unroll
         for (int j = 0; j < NPL; ++j) {
@@ -290,38 +292,13 @@ bwd_kernel(BwdArgs a) {
         }
         s1q[s] = s1;
         s2q[s] = s2;
+        const float w = dts[s] * xs[s];
 #pragma unroll
         for (int j = 0; j < NPL; ++j) {
-          tR[(slot * RPS + j) * kRowStride + lane] = g[j];
-          tR[(slot * RPS + NPL + j) * kRowStride + lane] = hs[k][j];
+          pv[slot * NPL + j] = g[j] * w;                  // dB: G * dt * x
+          pv[2 * NPL + slot * NPL + j] = hs[k][j] * dys[s];   // dC: h * dy
         }
-        if (slot == 0) {
-          // Rows of steps k, k+1 are in place (this wave's own LDS writes,
-          // executed in order). Lane slice: row r of half h2, RR channels.
-          const int hr = lane / L;
-          const int seg = lane % L;
-          const int r = hr >> 1;
-          const int h2 = hr & 1;
-          const int slot_r = r / RPS;
-          const int kind = (r % RPS) / NPL;
-          const int j = r % NPL;
-          const int kr = k + slot_r;
-          const float* rr = tR + r * kRowStride + h2 * kCH + seg * RR;
-          const float* ww = s0 + (kind ? oWDY : oWDTX) + kr * kCH + seg * RR;
-          float sum = 0.f;
-#pragma unroll
-          for (int e = 0; e < RR; e += 4) {
-            const float4 v = lds4(rr + e);
-            const float4 w = lds4(ww + e);
-            sum = __builtin_fmaf(v.x, w.x, sum);
-            sum = __builtin_fmaf(v.y, w.y, sum);
-            sum = __builtin_fmaf(v.z, w.z, sum);
-            sum = __builtin_fmaf(v.w, w.w, sum);
-          }
-          sum = group_sum<L>(sum);
-          // All L lanes of the slice hold the sum and store the same value.
-          tDBC[(kind * kSteps + kr) * NP + (wave * 2 + h2) * NPL + j] = sum;
-        }
+        if (slot == 0) *(dbc_out + k * NP) = half_wave_reduce_scatter<M>(pv, lane);
       }
       // Add the two half-waves: lanes 0-31 end with s1, lanes 32-63 with s2.
       float o[4];
@@ -332,14 +309,15 @@ bwd_kernel(BwdArgs a) {
         o[s] = __uint_as_float(sw[0]) + __uint_as_float(sw[1]);
       }
       sts4(tS + wave * 64 * kSteps + cm_quad(lane, m), make_float4(o[0], o[1], o[2], o[3]));
-      step_fence();
+      if (m == 2) store_sub((i + 1) & 1);  // chunk ci-1 (unused when ci == 0)
+      if (m == 1) load_sub(ci - 2);        // loads nothing when ci < 2
     }
 #pragma unroll
     for (int j = 0; j < NPL; ++j) hc[j] = ph[j];   // h at the start of chunk ci-1
     load_h0(ci - 2);
     __syncthreads();   // tS / tDBC complete; chunk ci-1 staged
   }
-  finalize(0);
+  finalize(0, (nch - 1) & 1);
 
   float out[NPL];
 #pragma unroll

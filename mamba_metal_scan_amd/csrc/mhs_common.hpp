@@ -48,6 +48,65 @@ __device__ __forceinline__ float group_sum(float v) {
   return v;
 }
 
+constexpr int kDppRor8 = 0x128;       // row_ror:8: lane i <-> i^8 inside each row of 16
+
+template <int CTRL>
+__device__ __forceinline__ float dpp_get(float v) {
+  return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), CTRL, 0xF, 0xF, true));
+}
+
+// One reduce-scatter stage over lane bit b: the values are paired (v[2i],
+// v[2i+1]); a lane whose bit b is 0 keeps the pair sum of v[2i] over itself
+// and its partner, a lane whose bit is 1 the sum of v[2i+1]. The partner
+// (DPP control CTRL) must differ from the lane in bit b and otherwise only in
+// bits not yet reduced.
+template <int CTRL, int M>
+__device__ __forceinline__ void rs_stage_dpp(const float (&v)[M], float (&o)[M / 2], bool bit) {
+#pragma unroll
+  for (int i = 0; i < M / 2; ++i) {
+    const float send = bit ? v[2 * i] : v[2 * i + 1];
+    const float keep = bit ? v[2 * i + 1] : v[2 * i];
+    o[i] = keep + dpp_get<CTRL>(send);
+  }
+}
+
+// Sums M values (M in {8, 16}) over the 32 lanes of each half-wave, as a
+// reduce-scatter: v_permlane16_swap across lane bit 4, then DPP row_ror:8
+// (bit 3), row_half_mirror (bit 2) and quad_perm xor 2 (bit 1), each halving
+// the values a lane holds, then plain DPP adds over the lane bits left. Lane l
+// returns the half-wave total of v[rs_index<M>(l)]. Summation order is fixed:
+// the result is bit-for-bit reproducible.
+template <int M>
+__device__ __forceinline__ float half_wave_reduce_scatter(const float (&v)[M], int lane) {
+  static_assert(M == 8 || M == 16, "8 or 16 values per lane");
+  float a[M / 2];
+#pragma unroll
+  for (int i = 0; i < M / 2; ++i) {
+    const auto sw = __builtin_amdgcn_permlane16_swap(__float_as_uint(v[2 * i]),
+                                                    __float_as_uint(v[2 * i + 1]), false, false);
+    a[i] = __uint_as_float(sw[0]) + __uint_as_float(sw[1]);
+  }
+  float b[M / 4];
+  rs_stage_dpp<kDppRor8>(a, b, (lane >> 3) & 1);
+  float c[M / 8];
+  rs_stage_dpp<kDppHalfMirror>(b, c, (lane >> 2) & 1);
+  float r;
+  if constexpr (M == 8) {
+    r = dpp_add<kDppXor2>(c[0]);
+  } else {
+    float d[1];
+    rs_stage_dpp<kDppXor2>(c, d, (lane >> 1) & 1);
+    r = d[0];
+  }
+  return dpp_add<kDppXor1>(r);
+}
+// Index of the value whose total half_wave_reduce_scatter<M> leaves in lane l.
+template <int M>
+__device__ __forceinline__ int rs_index(int lane) {
+  const int i = 4 * ((lane >> 2) & 1) + 2 * ((lane >> 3) & 1) + ((lane >> 4) & 1);
+  return M == 8 ? i : i + 8 * ((lane >> 1) & 1);
+}
+
 // Ordering point for LDS traffic that stays inside one wavefront: the wave's
 // LDS instructions execute in issue order, so only the compiler must be kept
 // from moving accesses across this point.
