@@ -192,7 +192,7 @@ def pmc_summary(args) -> None:
     if os.path.exists(stats):
         lines += ["## Kernel trace", "",
                   "    rocprofv3 --kernel-trace --stats -d OUT/kt -o run --output-format csv -- \\",
-                  f"        python3 bench.py --steps 20 --warmup 5 --no-cpu-baseline {extra}", "",
+                  f"        python3 bench.py --steps 20 --warmup 5 --no-cpu-baseline --no-train {extra}", "",
                   "| kernel | calls | avg us | min us | max us |", "|---|---|---|---|---|"]
         for r in csv.DictReader(open(stats)):
             lines.append(f"| `{r['Name'][:60]}` | {r['Calls']} | {float(r['AverageNs']) / 1e3:.1f} "

@@ -52,7 +52,8 @@ constexpr int kMaxG = 8;                   // waves per block
 struct Plan {
   int npl = 0;      // states per lane
   int G = 0;        // waves per block (d_state padded to 2*G*npl)
-  FwdFn fwd = nullptr;
+  FwdFn fwd = nullptr;      // checkpoint stride a multiple of 16 (or >= T)
+  FwdFn fwd_any = nullptr;  // any checkpoint stride
   int fwd_lds = 0;  // bytes
   BwdFn bwd = nullptr;
   int bwd_ki = 0;   // largest chunk the backward walks directly
@@ -66,7 +67,8 @@ struct Plan {
 template <int NPL, int G>
 void fill(Plan& p) {
   constexpr int MINW = NPL == 2 ? 3 : 2;
-  p.fwd = &mhs::fwd_kernel<NPL, G, MINW>;
+  p.fwd = &mhs::fwd_kernel<NPL, G, MINW, true>;
+  p.fwd_any = &mhs::fwd_kernel<NPL, G, MINW, false>;
   p.bwd = &mhs::bwd_kernel<NPL, G, MINW>;
   p.fwd_lds = mhs::fwd_lds_floats(G, NPL) * 4;
   p.bwd_lds = mhs::bwd_lds_floats(G, NPL) * 4;
@@ -169,10 +171,12 @@ WsLayout ws_layout(int64_t batch, int64_t T, int64_t D, int64_t N, int64_t chunk
 }
 
 int launch_fwd(const Plan& p, const mhs::FwdArgs& a, int batch, hipStream_t s) {
-  int rc = ensure_lds(reinterpret_cast<const void*>(p.fwd), p.fwd_lds);
+  const bool aligned = a.K % mhs::kSteps == 0 || a.K >= a.T;
+  const FwdFn fn = aligned ? p.fwd : p.fwd_any;
+  int rc = ensure_lds(reinterpret_cast<const void*>(fn), p.fwd_lds);
   if (rc) return rc;
   const dim3 grid((unsigned)((a.D + mhs::kCH - 1) / mhs::kCH), (unsigned)batch);
-  hipLaunchKernelGGL(p.fwd, grid, dim3(64 * p.G), p.fwd_lds, s, a);
+  hipLaunchKernelGGL(fn, grid, dim3(64 * p.G), p.fwd_lds, s, a);
   return check_launch("forward scan kernel");
 }
 

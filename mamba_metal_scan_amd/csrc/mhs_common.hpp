@@ -157,13 +157,15 @@ __device__ __forceinline__ void store_vec(float* p, const float (&v)[NPL]) {
 // operands live in channel-major tiles: row c holds the 16 steps of channel
 // c, so a lane reads 4 consecutive steps with one 128-bit LDS read (gfx950
 // moves ~2x the bytes per clock with ds_read_b128 than with b32/b64). The
-// quad index inside a row is rotated by c/4 ("quad swizzle") so that the 16
-// lanes of one 128-bit read phase hit 16 different 4-bank groups.
+// quad slot inside a row is m ^ c ^ (c >> 2) (mod 4): measured on gfx950,
+// this makes both the 128-bit reads (lane c reads row c) and the 128-bit
+// writes of such tiles free of bank conflicts, where a rotation by c/4 costs
+// 8 conflict cycles per 128-bit write.
 constexpr int kSteps = 16;   // steps per sub-chunk
 constexpr int kQuads = 4;    // quads per sub-chunk
 
 __device__ __forceinline__ int cm_quad(int row, int m) {
-  return row * kSteps + ((((m + (row >> 2)) & 3)) << 2);
+  return row * kSteps + (((m ^ row ^ (row >> 2)) & 3) << 2);
 }
 __device__ __forceinline__ int cm_elem(int row, int k) { return cm_quad(row, k >> 2) + (k & 3); }
 
@@ -179,10 +181,21 @@ __device__ __forceinline__ float2 lds2(const float* p) { return *reinterpret_cas
 // to kOOB, and the hot loops stay single basic blocks.
 constexpr unsigned kOOB = 0x80000000u;   // resources are < 2 GiB (checked on the host)
 
+// Base and size must be wave-uniform; they are moved to SGPRs explicitly
+// (readfirstlane), so that the compiler never has to wrap an access in a
+// loop over the distinct descriptors of the wave. __builtin_amdgcn_readfirstlane
+// moves 32 bits: the 64-bit base goes through it as two halves.
+__device__ __forceinline__ float* uniform_ptr(const float* p) {
+  const uint64_t v = reinterpret_cast<uintptr_t>(p);
+  const uint32_t lo = (uint32_t)__builtin_amdgcn_readfirstlane((int)(uint32_t)v);
+  const uint32_t hi = (uint32_t)__builtin_amdgcn_readfirstlane((int)(uint32_t)(v >> 32));
+  return reinterpret_cast<float*>(((uint64_t)hi << 32) | lo);
+}
 struct GBuf {
   __amdgpu_buffer_rsrc_t r;
   __device__ __forceinline__ GBuf(const float* base, unsigned bytes)
-      : r(__builtin_amdgcn_make_buffer_rsrc(const_cast<float*>(base), 0, (int)bytes, 0x00020000)) {}
+      : r(__builtin_amdgcn_make_buffer_rsrc(uniform_ptr(base), 0,
+                                            __builtin_amdgcn_readfirstlane((int)bytes), 0x00020000)) {}
   // The b32 builtins move raw 32-bit words (unsigned int): bit-cast, never convert.
   __device__ __forceinline__ float ld(unsigned byte_off) const {
     return __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(r, byte_off, 0, 0));

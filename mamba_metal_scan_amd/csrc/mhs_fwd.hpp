@@ -56,7 +56,9 @@ __host__ __device__ constexpr int fwd_lds_floats(int G, int NPL) {
   return 2 * fwd_buf_floats(G, NPL);
 }
 
-template <int NPL, int G, int MINW>
+// KALIGNED: the checkpoint stride K is a multiple of 16, so checkpoints fall
+// on sub-chunk ends (and the last one on the final state): no per-step tests.
+template <int NPL, int G, int MINW, bool KALIGNED>
 __global__ void __launch_bounds__(64 * G, MINW)
 fwd_kernel(FwdArgs a) {
   constexpr int NT = 64 * G;                    // threads
@@ -116,9 +118,25 @@ fwd_kernel(FwdArgs a) {
     rl.store(buf + 2 * kCH * kSteps + kSteps * NP, pc);
   };
   // y of sub-chunk i: task (step pair kp, channel cc) sums the partials of
-  // its two steps over the 2G lane groups in a fixed order.
-  auto finalize_y = [&](int i) {
+  // its two steps over the 2G lane groups in a fixed order. Split in two so
+  // that the LDS reads (y_read) and their use (y_write) sit in different
+  // scheduling regions.
+  float2 ypart[FT][2 * G];
+  auto y_read = [&](int i) {
     const float* yp = lds + (i & 1) * BUF + 2 * kCH * kSteps + 2 * kSteps * NP;
+#pragma unroll
+    for (int f = 0; f < FT; ++f) {
+      const int task0 = tid + f * NT;
+      const int task = task0 < kSteps / 2 * kCH ? task0 : 0;
+      const int cc = task % kCH, k = 2 * (task / kCH);
+#pragma unroll
+      for (int w = 0; w < G; ++w)
+#pragma unroll
+        for (int h2 = 0; h2 < 2; ++h2)
+          ypart[f][2 * w + h2] = lds2(yp + w * 64 * kSteps + cm_elem(h2 * kCH + cc, k));
+    }
+  };
+  auto y_write = [&](int i) {
     const GBuf yo = sub_buf(a.y != nullptr ? a.y : a.x, a.y != nullptr ? i : -1);
 #pragma unroll
     for (int f = 0; f < FT; ++f) {
@@ -126,15 +144,11 @@ fwd_kernel(FwdArgs a) {
       const bool ok = task0 < kSteps / 2 * kCH;
       const int task = ok ? task0 : 0;
       const int cc = task % kCH, k = 2 * (task / kCH);
-      float s0 = 0.f, s1 = 0.f;
+      float s0 = ypart[f][0].x, s1 = ypart[f][0].y;
 #pragma unroll
-      for (int w = 0; w < G; ++w) {
-#pragma unroll
-        for (int h2 = 0; h2 < 2; ++h2) {
-          const float2 v = lds2(yp + w * 64 * kSteps + cm_elem(h2 * kCH + cc, k));
-          s0 += v.x;
-          s1 += v.y;
-        }
+      for (int p = 1; p < 2 * G; ++p) {
+        s0 += ypart[f][p].x;
+        s1 += ypart[f][p].y;
       }
       const unsigned o = (ok && d0 + cc < D) ? 4u * ((unsigned)k * (unsigned)D + cc) : kOOB;
       yo.st(s0, o);
@@ -155,8 +169,10 @@ fwd_kernel(FwdArgs a) {
   const unsigned slice_bytes = 4u * (unsigned)ck_stride;
   const unsigned ck_lane = act ? 4u * ((unsigned)d * (unsigned)N + (unsigned)n0) : kOOB;
   const int nvalid = N - n0;
-  int next_ck = min(a.K, T);
-  int ck = 0;
+  constexpr int kDone = 0x7FFFFFFF;
+  int next_ck = a.ckpt != nullptr ? min(a.K, T) : kDone;   // step count after the next checkpoint
+  const float* ck_base = a.ckpt != nullptr ? a.ckpt + (size_t)b * a.nchunk * ck_stride : a.x;
+  const float* ck_ptr = ck_base;
   for (int i = 0; i < nsub; ++i) {
     const int t0 = i * kSteps;
     const float* buf = lds + (i & 1) * BUF;
@@ -166,15 +182,34 @@ fwd_kernel(FwdArgs a) {
     const float* gC = buf + 2 * kCH * kSteps + kSteps * NP + q * kSteps * NPL;
     float* myY = lds + (i & 1) * BUF + 2 * kCH * kSteps + 2 * kSteps * NP + wave * 64 * kSteps;
 
+    // A quad's LDS operands, read one quad ahead of their use.
+    float4 qdt, qbx, qB[NPL], qC[NPL];
+    auto read_quad = [&](int m) {
+      qdt = lds4(cDT + cm_quad(c, m));
+      qbx = lds4(cBX + cm_quad(c, m));
+#pragma unroll
+      for (int j = 0; j < NPL; ++j) {
+        qB[j] = lds4(gB + 4 * m * NPL + 4 * j);
+        qC[j] = lds4(gC + 4 * m * NPL + 4 * j);
+      }
+    };
+    read_quad(0);
+
     // Steps past T in the last sub-chunk see zero inputs: dA = 1 and u = 0
     // there, so h passes through unchanged and nothing is stored.
 #pragma unroll
     for (int m = 0; m < kQuads; ++m) {
       float dts[4], bxs[4], Bq[4][NPL], Cq[4][NPL];
-      f4_to(dts, lds4(cDT + cm_quad(c, m)));
-      f4_to(bxs, lds4(cBX + cm_quad(c, m)));
-      load_quad_rows<NPL>(Bq, gB, m);
-      load_quad_rows<NPL>(Cq, gC, m);
+      f4_to(dts, qdt);
+      f4_to(bxs, qbx);
+#pragma unroll
+      for (int e = 0; e < 4 * NPL; ++e) {
+        const float4 tb = qB[e / 4], tc = qC[e / 4];
+        const float vb[4] = {tb.x, tb.y, tb.z, tb.w}, vc[4] = {tc.x, tc.y, tc.z, tc.w};
+        Bq[e / NPL][e % NPL] = vb[e % 4];
+        Cq[e / NPL][e % NPL] = vc[e % 4];
+      }
+      if (m + 1 < kQuads) read_quad(m + 1);
       float da[4][NPL], u[4][NPL];
 #pragma unroll
       for (int s = 0; s < 4; ++s)
@@ -201,26 +236,41 @@ fwd_kernel(FwdArgs a) {
       // scheduling region. Unconditional: past either end of the sequence the
       // resources are empty (loads return 0, stores are dropped) and the LDS
       // buffer written is not read again.
-      if (m == 0) finalize_y(i - 1);
+      if (m == 0) y_read(i - 1);
+      if (m == 1) y_write(i - 1);
       if (m == 1) store_sub(i + 1);
       if (m == 2) load_sub(i + 2);
 
-      // Checkpoints inside this quad.
+      if constexpr (!KALIGNED) {
+        // Checkpoints inside this quad (any stride; uniform tests per step).
 #pragma unroll
-      for (int s = 0; s < 4; ++s) {
-        if (t0 + 4 * m + s + 1 == next_ck) {
-          if (a.ckpt != nullptr)
-            store_states<NPL>(GBuf(a.ckpt + ((size_t)b * a.nchunk + ck) * ck_stride, slice_bytes),
-                              ck_lane, nvalid, hq[s]);
-          ++ck;
-          next_ck = min(next_ck + a.K, T);
+        for (int s = 0; s < 4; ++s) {
+          if (t0 + 4 * m + s + 1 == next_ck) {
+            store_states<NPL>(GBuf(ck_ptr, slice_bytes), ck_lane, nvalid, hq[s]);
+            ck_ptr += ck_stride;
+            next_ck = next_ck == T ? kDone : min(next_ck + a.K, T);
+          }
         }
       }
       step_fence();
     }
+    if constexpr (KALIGNED) {
+      // A checkpoint at the end of this sub-chunk (uniform test).
+      if (next_ck == t0 + kSteps && next_ck < T) {
+        store_states<NPL>(GBuf(ck_ptr, slice_bytes), ck_lane, nvalid, h);
+        ck_ptr += ck_stride;
+        next_ck += a.K;
+      }
+    }
     __syncthreads();
   }
-  finalize_y(nsub - 1);
+  // KALIGNED: the last checkpoint (slot nchunk-1) is the state after step T-1,
+  // which is h now (steps past T are identity steps).
+  if (KALIGNED && a.ckpt != nullptr)
+    store_states<NPL>(GBuf(ck_base + (size_t)(a.nchunk - 1) * ck_stride, slice_bytes), ck_lane,
+                      nvalid, h);
+  y_read(nsub - 1);
+  y_write(nsub - 1);
 
   if (a.h_last != nullptr)
     store_states<NPL>(GBuf(a.h_last + (size_t)b * ck_stride, slice_bytes), ck_lane, nvalid, h);
