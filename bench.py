@@ -310,11 +310,9 @@ def bench_infer(args) -> dict:
     dts = torch.nn.functional.softplus(torch.randn(steps, bt, d, generator=g) - 4.0).to(dev)
     bs = torch.randn(steps, bt, n, generator=g).to(dev)
     cs = torch.randn(steps, bt, n, generator=g).to(dev)
-    ys = torch.empty(steps, bt, d, device=dev)
-
     def decode():
         for i in range(steps):
-            ys[i] = selective_state_step(h, xs[i], dts[i], aneg, bs[i], cs[i])
+            selective_state_step(h, xs[i], dts[i], aneg, bs[i], cs[i])
 
     decode()
     torch.cuda.synchronize()

@@ -2,46 +2,60 @@
 // mamba_metal/model.py:234-241):
 //   h[b,d,:] <- h[b,d,:] * exp(-dt[b,d] * Aneg[d,:]) + dt[b,d] * x[b,d] * B[b,:]
 //   y[b,d]    = sum_n C[b,n] * h[b,d,n]
-// Memory-bound (h is read and written once). Four lanes share a channel, each
-// holding a float4 of its state, so one wave touches 16 channels x 64 B = 1 KiB
-// of contiguous h per access; the y sum is a two-level DPP add inside the quad.
+// Memory-bound (h is read and written once): the lanes of a wave read and
+// write contiguous h, VPL float4s per lane.
 #pragma once
 
 #include "mhs_common.hpp"
 
 namespace mhs {
 
-// N % 4 == 0 and N <= 16: lane q of a quad owns n in [4q, 4q+4) of one channel
-// (lanes beyond N/4 in the quad idle). One thread per (b, d, quad-lane).
+// N == 4 * VPL * LPC: LPC lanes share a channel, lane q holding the VPL
+// float4s n in [4*VPL*q, 4*VPL*(q+1)). One thread per (b, d, q); y is summed
+// over the LPC lanes with DPP (fixed order). h is read and written once, with
+// non-temporal hints (it is not reused within the step).
+template <int VPL, int LPC>
 __global__ void __launch_bounds__(256)
 step_kernel_vec(float* __restrict__ h, const float* __restrict__ x,
                 const float* __restrict__ dt, const float* __restrict__ aneg,
                 const float* __restrict__ Bm, const float* __restrict__ Cm,
-                float* __restrict__ y, int batch, int D, int N) {
+                float* __restrict__ y, int batch, int D) {
+  constexpr int N = 4 * VPL * LPC;
   const long long gid = (long long)blockIdx.x * blockDim.x + threadIdx.x;
-  const long long ch = gid >> 2;           // (b, d)
-  const int q = (int)(gid & 3);
+  const long long ch = gid / LPC;          // (b, d)
+  const int q = (int)(gid % LPC);
   const bool valid = ch < (long long)batch * D;
-  const bool own = valid && 4 * q < N;
   float part = 0.f;
-  if (own) {
+  if (valid) {
     const int b = (int)(ch / D);
     const int d = (int)(ch % D);
     const float dtv = dt[ch];
     const float bx = dtv * x[ch];
-    const int n = 4 * q;
-    float4 hv = *reinterpret_cast<const float4*>(h + ch * N + n);
-    const float4 av = *reinterpret_cast<const float4*>(aneg + (size_t)d * N + n);
-    const float4 bv = *reinterpret_cast<const float4*>(Bm + (size_t)b * N + n);
-    const float4 cv = *reinterpret_cast<const float4*>(Cm + (size_t)b * N + n);
-    hv.x = __builtin_fmaf(exp2_hw(-dtv * av.x * kLog2e), hv.x, bv.x * bx);
-    hv.y = __builtin_fmaf(exp2_hw(-dtv * av.y * kLog2e), hv.y, bv.y * bx);
-    hv.z = __builtin_fmaf(exp2_hw(-dtv * av.z * kLog2e), hv.z, bv.z * bx);
-    hv.w = __builtin_fmaf(exp2_hw(-dtv * av.w * kLog2e), hv.w, bv.w * bx);
-    *reinterpret_cast<float4*>(h + ch * N + n) = hv;
-    part = cv.x * hv.x + cv.y * hv.y + cv.z * hv.z + cv.w * hv.w;
+    const float a2 = -dtv * kLog2e;
+    using v4f = float __attribute__((ext_vector_type(4)));
+    v4f* hp = reinterpret_cast<v4f*>(h + ch * N) + q * VPL;
+    const float4* ap = reinterpret_cast<const float4*>(aneg + (size_t)d * N) + q * VPL;
+    const float4* bp = reinterpret_cast<const float4*>(Bm + (size_t)b * N) + q * VPL;
+    const float4* cp = reinterpret_cast<const float4*>(Cm + (size_t)b * N) + q * VPL;
+    v4f hv[VPL];
+#pragma unroll
+    for (int v = 0; v < VPL; ++v) hv[v] = __builtin_nontemporal_load(hp + v);
+#pragma unroll
+    for (int v = 0; v < VPL; ++v) {
+      const float4 av = ap[v], bv = bp[v], cv = cp[v];
+      v4f o;
+      o.x = __builtin_fmaf(exp2_hw(a2 * av.x), hv[v].x, bv.x * bx);
+      o.y = __builtin_fmaf(exp2_hw(a2 * av.y), hv[v].y, bv.y * bx);
+      o.z = __builtin_fmaf(exp2_hw(a2 * av.z), hv[v].z, bv.z * bx);
+      o.w = __builtin_fmaf(exp2_hw(a2 * av.w), hv[v].w, bv.w * bx);
+      __builtin_nontemporal_store(o, hp + v);
+      part = __builtin_fmaf(cv.x, o.x, part);
+      part = __builtin_fmaf(cv.y, o.y, part);
+      part = __builtin_fmaf(cv.z, o.z, part);
+      part = __builtin_fmaf(cv.w, o.w, part);
+    }
   }
-  part = group_sum<4>(part);
+  part = group_sum<LPC>(part);
   if (valid && q == 0) y[ch] = part;
 }
 
