@@ -66,7 +66,6 @@ fwd_kernel(FwdArgs a) {
   constexpr int BUF = fwd_buf_floats(G, NPL);
   constexpr int PER = (kCH * kQuads + NT - 1) / NT;
   constexpr int PERS = (kSteps * NP + NT - 1) / NT;
-  constexpr int FT = (kSteps / 2 * kCH + NT - 1) / NT;   // y tasks per thread
   extern __shared__ float lds[];
   const int N = a.N;
   const int tid = threadIdx.x;
@@ -117,42 +116,51 @@ fwd_kernel(FwdArgs a) {
     rl.store(buf + 2 * kCH * kSteps, pb);
     rl.store(buf + 2 * kCH * kSteps + kSteps * NP, pc);
   };
-  // y of sub-chunk i: task (step pair kp, channel cc) sums the partials of
-  // its two steps over the 2G lane groups in a fixed order. Split in two so
-  // that the LDS reads (y_read) and their use (y_write) sit in different
-  // scheduling regions.
-  float2 ypart[FT][2 * G];
+  // y of sub-chunk i: task (channel cc, quad m) sums the partials of its four
+  // steps over the 2G lane groups in a fixed order (128-bit reads). Tasks go
+  // to the threads from NT/2 on, i.e. to the waves that hold no staging tasks
+  // (those are threads 0..127). Split in two so that the LDS reads (y_read)
+  // and their use (y_write) sit in different scheduling regions.
+  constexpr int YT = (kCH * kQuads + NT - 1) / NT;          // y tasks per thread
+  float4 ypart[YT][2 * G];
+  auto y_task = [&](int f) { return (tid + NT / 2) % NT + f * NT; };
   auto y_read = [&](int i) {
     const float* yp = lds + (i & 1) * BUF + 2 * kCH * kSteps + 2 * kSteps * NP;
 #pragma unroll
-    for (int f = 0; f < FT; ++f) {
-      const int task0 = tid + f * NT;
-      const int task = task0 < kSteps / 2 * kCH ? task0 : 0;
-      const int cc = task % kCH, k = 2 * (task / kCH);
+    for (int f = 0; f < YT; ++f) {
+      const int t0 = y_task(f);
+      const int t = t0 < kCH * kQuads ? t0 : 0;
+      const int cc = t % kCH, m = t / kCH;
 #pragma unroll
       for (int w = 0; w < G; ++w)
 #pragma unroll
         for (int h2 = 0; h2 < 2; ++h2)
-          ypart[f][2 * w + h2] = lds2(yp + w * 64 * kSteps + cm_elem(h2 * kCH + cc, k));
+          ypart[f][2 * w + h2] = lds4(yp + w * 64 * kSteps + cm_quad(h2 * kCH + cc, m));
     }
   };
   auto y_write = [&](int i) {
     const GBuf yo = sub_buf(a.y != nullptr ? a.y : a.x, a.y != nullptr ? i : -1);
 #pragma unroll
-    for (int f = 0; f < FT; ++f) {
-      const int task0 = tid + f * NT;
-      const bool ok = task0 < kSteps / 2 * kCH;
-      const int task = ok ? task0 : 0;
-      const int cc = task % kCH, k = 2 * (task / kCH);
-      float s0 = ypart[f][0].x, s1 = ypart[f][0].y;
+    for (int f = 0; f < YT; ++f) {
+      const int t0 = y_task(f);
+      const bool ok = t0 < kCH * kQuads;
+      const int t = ok ? t0 : 0;
+      const int cc = t % kCH, m = t / kCH;
+      float4 sum = ypart[f][0];
 #pragma unroll
       for (int p = 1; p < 2 * G; ++p) {
-        s0 += ypart[f][p].x;
-        s1 += ypart[f][p].y;
+        sum.x += ypart[f][p].x;
+        sum.y += ypart[f][p].y;
+        sum.z += ypart[f][p].z;
+        sum.w += ypart[f][p].w;
       }
-      const unsigned o = (ok && d0 + cc < D) ? 4u * ((unsigned)k * (unsigned)D + cc) : kOOB;
-      yo.st(s0, o);
-      yo.st(s1, o == kOOB ? kOOB : o + 4u * (unsigned)D);
+      const unsigned o = (ok && d0 + cc < D) ? 4u * ((unsigned)(4 * m) * (unsigned)D + cc) : kOOB;
+      const unsigned rs = 4u * (unsigned)D;
+      const bool okk = o != kOOB;
+      yo.st(sum.x, o);
+      yo.st(sum.y, okk ? o + rs : kOOB);
+      yo.st(sum.z, okk ? o + 2 * rs : kOOB);
+      yo.st(sum.w, okk ? o + 3 * rs : kOOB);
     }
   };
 
