@@ -19,7 +19,8 @@ Reported:
   train_80m      the 80M TinyMamba train step (fwd + bwd + AdamW) with the HIP
                  scan at batch 16 x seq 512: tokens/s and peak HBM
 
-Other workloads (--workload): "longt" (4 x 16384 x 2048 x 16 fwd+bwd,
+Other workloads (--workload): "train" (the 80M train step alone), "longt"
+(4 x 16384 x 2048 x 16 fwd+bwd,
 checkpoint-stride sweep), "infer" (prefill 32 x 2048 x 4096 x 16 + 256
 recurrent decode steps).
 
@@ -434,7 +435,7 @@ def main() -> int:
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=50)
     ap.add_argument("--warmup", type=int, default=10)
-    ap.add_argument("--workload", default="scan", choices=["scan", "longt", "infer"])
+    ap.add_argument("--workload", default="scan", choices=["scan", "train", "longt", "infer"])
     ap.add_argument("--no-train", action="store_true", help="skip the 80M train-step figure")
     ap.add_argument("--batch", type=int, default=16)
     ap.add_argument("--seqlen", type=int, default=512)
@@ -463,7 +464,16 @@ def main() -> int:
     if args.launches:
         run_launches(args)
         return 0
-    out = {"scan": bench_scan, "longt": bench_longt, "infer": bench_infer}[args.workload](args)
+    if args.workload == "train":
+        t = bench_train(steps=args.steps, warmup=args.warmup)
+        out = {"metric": "80M TinyMamba fp32 train step tok/s (batch 16 x seq 512)",
+               "value": t["tokens_per_s"], "unit": "tokens/s", "n_gpus": 1,
+               "steps": args.steps, "warmup": args.warmup, "ms_per_step": t["ms_per_step"],
+               "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "f32",
+               "data": "synthetic tokens U[0, 32768)", "config": {"workload": t["config"]},
+               "train_80m": t}
+    else:
+        out = {"scan": bench_scan, "longt": bench_longt, "infer": bench_infer}[args.workload](args)
     print(json.dumps(out), flush=True)
     return 0
 

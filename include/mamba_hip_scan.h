@@ -118,6 +118,40 @@ int mhs_scan_step_f32(float* h, const float* x, const float* dt, const float* an
                       const float* B, const float* C, float* y,
                       int64_t batch, int64_t d_inner, int64_t d_state, void* stream);
 
+/*
+ * Causal depthwise conv1d + SiLU, forward. Replaces the reference block's
+ * `F.silu(self.conv(xt)[:, :, :T])` with `self.conv = nn.Conv1d(d_inner,
+ * d_inner, kernel_size=K, padding=K-1, groups=d_inner, bias=True)`
+ * (mamba_metal/model.py:174-175, applied at :244):
+ *     pre[b,t,d] = bias[d] + sum_{k<K} w[d,k] * x[b, t-K+1+k, d]   (x = 0 for t < 0)
+ *     out[b,t,d] = pre * sigmoid(pre)
+ *   x   : (batch, seqlen, d_inner), rows `x_row_stride` floats apart
+ *         (>= d_inner; the block's x half of its in_proj output has 2*d_inner),
+ *         batch rows seqlen * x_row_stride apart
+ *   w   : (d_inner, K) (the Conv1d weight (d_inner, 1, K)), bias : (d_inner)
+ *   out : (batch, seqlen, d_inner) contiguous
+ * K in [1, 8]. Pointers need 4-byte alignment only.
+ */
+int mhs_conv1d_silu_fwd_f32(const float* x, int64_t x_row_stride, const float* w,
+                            const float* bias, float* out, int64_t batch, int64_t seqlen,
+                            int64_t d_inner, int64_t kernel_size, void* stream);
+
+/* Bytes of device workspace mhs_conv1d_silu_bwd_f32 needs for this shape. */
+size_t mhs_conv1d_silu_bwd_workspace_bytes(int64_t batch, int64_t seqlen, int64_t d_inner,
+                                           int64_t kernel_size);
+
+/*
+ * Backward of mhs_conv1d_silu_fwd_f32 (the autograd of the same reference
+ * Conv1d + SiLU): dx (batch, seqlen, d_inner) contiguous, dw (d_inner, K),
+ * dbias (d_inner), all fully written. dw and dbias are summed over (batch,
+ * time) through the workspace in a fixed order (bit-for-bit reproducible).
+ */
+int mhs_conv1d_silu_bwd_f32(const float* x, int64_t x_row_stride, const float* w,
+                            const float* bias, const float* dout, float* dx, float* dw,
+                            float* dbias, void* workspace, size_t workspace_bytes,
+                            int64_t batch, int64_t seqlen, int64_t d_inner, int64_t kernel_size,
+                            void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -24,7 +24,8 @@ LIB_PATH = Path(__file__).resolve().with_name("libmamba_hip_scan.so")
 EXPORTED_SYMBOLS = (
     "mhs_version", "mhs_last_error", "mhs_num_chunks", "mhs_preferred_chunk",
     "mhs_set_variant", "mhs_scan_fwd_f32", "mhs_scan_bwd_workspace_bytes",
-    "mhs_scan_bwd_f32", "mhs_scan_step_f32",
+    "mhs_scan_bwd_f32", "mhs_scan_step_f32", "mhs_conv1d_silu_fwd_f32",
+    "mhs_conv1d_silu_bwd_workspace_bytes", "mhs_conv1d_silu_bwd_f32",
 )
 
 _lib: Optional[ctypes.CDLL] = None
@@ -68,6 +69,13 @@ def library() -> ctypes.CDLL:
             lib.mhs_scan_bwd_f32.argtypes = [_P] * 14 + [ctypes.c_size_t] + [_I64] * 5 + [_P]
             lib.mhs_scan_step_f32.restype = ctypes.c_int
             lib.mhs_scan_step_f32.argtypes = [_P] * 7 + [_I64] * 3 + [_P]
+            lib.mhs_conv1d_silu_fwd_f32.restype = ctypes.c_int
+            lib.mhs_conv1d_silu_fwd_f32.argtypes = [_P, _I64, _P, _P, _P] + [_I64] * 4 + [_P]
+            lib.mhs_conv1d_silu_bwd_workspace_bytes.restype = ctypes.c_size_t
+            lib.mhs_conv1d_silu_bwd_workspace_bytes.argtypes = [_I64] * 4
+            lib.mhs_conv1d_silu_bwd_f32.restype = ctypes.c_int
+            lib.mhs_conv1d_silu_bwd_f32.argtypes = ([_P, _I64] + [_P] * 7 + [ctypes.c_size_t]
+                                                    + [_I64] * 4 + [_P])
             _lib = lib
     return _lib
 
@@ -181,3 +189,58 @@ def scan_step(h: torch.Tensor, x: torch.Tensor, dt: torch.Tensor, aneg: torch.Te
 @scan_step.register_fake
 def _scan_step_fake(h, x, dt, aneg, b_in, c_in):
     return x.new_empty((h.shape[0], h.shape[1]))
+
+
+def _conv_rows(x: torch.Tensor) -> int:
+    """Row stride (floats) of a (B,T,D) tensor whose rows are dense and whose
+    batch rows follow each other; raises for other layouts."""
+    bt, t_len, d = x.shape
+    if x.stride(2) != 1 or x.stride(1) < d or (bt > 1 and x.stride(0) != t_len * x.stride(1)):
+        raise HipScanError(f"conv1d_silu: unsupported x strides {x.stride()} for shape "
+                           f"{tuple(x.shape)}")
+    return x.stride(1)
+
+
+@torch.library.custom_op("mamba_hip::conv1d_silu_fwd", mutates_args=())
+def conv1d_silu_fwd(x: torch.Tensor, w: torch.Tensor, bias: torch.Tensor) -> torch.Tensor:
+    """silu(causal depthwise conv1d) of (B,T,D) x (rows may be strided), w (D,K): (B,T,D)."""
+    bt, t_len, d = x.shape
+    out = x.new_empty((bt, t_len, d))
+    with torch.cuda.device(x.device):
+        rc = library().mhs_conv1d_silu_fwd_f32(
+            _ptr(x), _conv_rows(x), _ptr(w), _ptr(bias), _ptr(out), bt, t_len, d, w.shape[1],
+            _stream(x.device))
+    _check(rc, "mhs_conv1d_silu_fwd_f32")
+    return out
+
+
+@conv1d_silu_fwd.register_fake
+def _conv1d_silu_fwd_fake(x, w, bias):
+    return x.new_empty(x.shape)
+
+
+@torch.library.custom_op("mamba_hip::conv1d_silu_bwd", mutates_args=())
+def conv1d_silu_bwd(x: torch.Tensor, w: torch.Tensor, bias: torch.Tensor, dout: torch.Tensor
+                    ) -> tuple[torch.Tensor, torch.Tensor, torch.Tensor]:
+    """(dx (B,T,D) contiguous, dw (D,K), dbias (D))."""
+    bt, t_len, d = x.shape
+    k = w.shape[1]
+    lib = library()
+    dx = x.new_empty((bt, t_len, d))
+    dw = torch.empty_like(w)
+    dbias = torch.empty_like(bias)
+    ws_bytes = int(lib.mhs_conv1d_silu_bwd_workspace_bytes(bt, t_len, d, k))
+    if ws_bytes == 0:
+        raise HipScanError(f"no conv workspace size for shape {(bt, t_len, d)} kernel {k}")
+    ws = torch.empty(ws_bytes, dtype=torch.uint8, device=x.device)
+    with torch.cuda.device(x.device):
+        rc = lib.mhs_conv1d_silu_bwd_f32(
+            _ptr(x), _conv_rows(x), _ptr(w), _ptr(bias), _ptr(dout), _ptr(dx), _ptr(dw),
+            _ptr(dbias), _ptr(ws), ws_bytes, bt, t_len, d, k, _stream(x.device))
+    _check(rc, "mhs_conv1d_silu_bwd_f32")
+    return dx, dw, dbias
+
+
+@conv1d_silu_bwd.register_fake
+def _conv1d_silu_bwd_fake(x, w, bias, dout):
+    return x.new_empty(x.shape), torch.empty_like(w), torch.empty_like(bias)

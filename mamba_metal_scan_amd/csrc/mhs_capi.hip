@@ -14,6 +14,7 @@
 
 #include "mamba_hip_scan.h"
 #include "mhs_bwd.hpp"
+#include "mhs_conv.hpp"
 #include "mhs_fwd.hpp"
 #include "mhs_step.hpp"
 
@@ -337,6 +338,119 @@ int mhs_scan_step_f32(float* h, const float* x, const float* dt, const float* an
                          h, x, dt, aneg, B, C, y, (int)batch, (int)d_inner, (int)d_state);
   }
   return check_launch("decode step kernel");
+}
+
+}  // extern "C"
+
+// ------------------------------------------------------------- conv1d + SiLU
+
+namespace {
+
+constexpr int kConvTPT = 16;   // steps per thread
+
+int check_conv(int64_t batch, int64_t seqlen, int64_t d_inner, int64_t k, int64_t x_rs) {
+  if (batch < 1 || seqlen < 1 || d_inner < 1)
+    return fail(MHS_EINVAL, "sizes must be positive: batch %lld seqlen %lld d_inner %lld",
+                (long long)batch, (long long)seqlen, (long long)d_inner);
+  if (k < 1 || k > mhs::kConvMaxK)
+    return fail(MHS_EINVAL, "kernel_size %lld unsupported (1..%d)", (long long)k, mhs::kConvMaxK);
+  if (x_rs < d_inner) return fail(MHS_EINVAL, "x_row_stride %lld < d_inner %lld", (long long)x_rs,
+                                  (long long)d_inner);
+  if (batch > 65535) return fail(MHS_EINVAL, "batch %lld exceeds 65535", (long long)batch);
+  if (seqlen > (1LL << 30) || d_inner > (1LL << 30)) return fail(MHS_EINVAL, "sizes too large");
+  return MHS_OK;
+}
+
+dim3 conv_grid(int64_t batch, int64_t seqlen, int64_t d_inner) {
+  return dim3((unsigned)((d_inner + mhs::kConvCh - 1) / mhs::kConvCh),
+              (unsigned)((seqlen + mhs::kConvTG * kConvTPT - 1) / (mhs::kConvTG * kConvTPT)),
+              (unsigned)batch);
+}
+
+template <int K>
+void conv_fwd_launch(const float* x, long long x_rs, const float* w, const float* bias, float* out,
+                     dim3 grid, int T, int D, hipStream_t s) {
+  hipLaunchKernelGGL((mhs::conv_silu_fwd_kernel<K, kConvTPT>), grid, dim3(mhs::kConvCh * mhs::kConvTG),
+                     0, s, x, x_rs, w, bias, out, T, D);
+}
+template <int K>
+void conv_bwd_launch(const float* x, long long x_rs, const float* w, const float* bias,
+                     const float* dout, float* dx, float* wsp, dim3 grid, int T, int D,
+                     hipStream_t s) {
+  hipLaunchKernelGGL((mhs::conv_silu_bwd_kernel<K, kConvTPT>), grid,
+                     dim3(mhs::kConvCh * mhs::kConvTG), 0, s, x, x_rs, w, bias, dout, dx, wsp, T, D);
+}
+
+}  // namespace
+
+extern "C" {
+
+int mhs_conv1d_silu_fwd_f32(const float* x, int64_t x_row_stride, const float* w,
+                            const float* bias, float* out, int64_t batch, int64_t seqlen,
+                            int64_t d_inner, int64_t kernel_size, void* stream) {
+  g_err[0] = '\0';
+  int rc = check_conv(batch, seqlen, d_inner, kernel_size, x_row_stride);
+  if (rc) return rc;
+  if (!x || !w || !bias || !out) return fail(MHS_EINVAL, "null pointer argument");
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  const dim3 grid = conv_grid(batch, seqlen, d_inner);
+  const int T = (int)seqlen, D = (int)d_inner;
+  switch (kernel_size) {
+    case 1: conv_fwd_launch<1>(x, x_row_stride, w, bias, out, grid, T, D, s); break;
+    case 2: conv_fwd_launch<2>(x, x_row_stride, w, bias, out, grid, T, D, s); break;
+    case 3: conv_fwd_launch<3>(x, x_row_stride, w, bias, out, grid, T, D, s); break;
+    case 4: conv_fwd_launch<4>(x, x_row_stride, w, bias, out, grid, T, D, s); break;
+    case 5: conv_fwd_launch<5>(x, x_row_stride, w, bias, out, grid, T, D, s); break;
+    case 6: conv_fwd_launch<6>(x, x_row_stride, w, bias, out, grid, T, D, s); break;
+    case 7: conv_fwd_launch<7>(x, x_row_stride, w, bias, out, grid, T, D, s); break;
+    default: conv_fwd_launch<8>(x, x_row_stride, w, bias, out, grid, T, D, s); break;
+  }
+  return check_launch("conv1d+silu forward kernel");
+}
+
+size_t mhs_conv1d_silu_bwd_workspace_bytes(int64_t batch, int64_t seqlen, int64_t d_inner,
+                                           int64_t kernel_size) {
+  if (check_conv(batch, seqlen, d_inner, kernel_size, d_inner)) return 0;
+  const dim3 grid = conv_grid(batch, seqlen, d_inner);
+  return (size_t)grid.y * grid.z * (size_t)(kernel_size + 1) * (size_t)d_inner * 4;
+}
+
+int mhs_conv1d_silu_bwd_f32(const float* x, int64_t x_row_stride, const float* w,
+                            const float* bias, const float* dout, float* dx, float* dw,
+                            float* dbias, void* workspace, size_t workspace_bytes,
+                            int64_t batch, int64_t seqlen, int64_t d_inner, int64_t kernel_size,
+                            void* stream) {
+  g_err[0] = '\0';
+  int rc = check_conv(batch, seqlen, d_inner, kernel_size, x_row_stride);
+  if (rc) return rc;
+  if (!x || !w || !bias || !dout || !dx || !dw || !dbias || !workspace)
+    return fail(MHS_EINVAL, "null pointer argument");
+  const size_t need = mhs_conv1d_silu_bwd_workspace_bytes(batch, seqlen, d_inner, kernel_size);
+  if (workspace_bytes < need)
+    return fail(MHS_EINVAL, "workspace too small: %zu < %zu bytes", workspace_bytes, need);
+  if (reinterpret_cast<uintptr_t>(workspace) & 15u)
+    return fail(MHS_EINVAL, "workspace must be 16-byte aligned");
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  const dim3 grid = conv_grid(batch, seqlen, d_inner);
+  const int T = (int)seqlen, D = (int)d_inner;
+  float* wsp = static_cast<float*>(workspace);
+  switch (kernel_size) {
+    case 1: conv_bwd_launch<1>(x, x_row_stride, w, bias, dout, dx, wsp, grid, T, D, s); break;
+    case 2: conv_bwd_launch<2>(x, x_row_stride, w, bias, dout, dx, wsp, grid, T, D, s); break;
+    case 3: conv_bwd_launch<3>(x, x_row_stride, w, bias, dout, dx, wsp, grid, T, D, s); break;
+    case 4: conv_bwd_launch<4>(x, x_row_stride, w, bias, dout, dx, wsp, grid, T, D, s); break;
+    case 5: conv_bwd_launch<5>(x, x_row_stride, w, bias, dout, dx, wsp, grid, T, D, s); break;
+    case 6: conv_bwd_launch<6>(x, x_row_stride, w, bias, dout, dx, wsp, grid, T, D, s); break;
+    case 7: conv_bwd_launch<7>(x, x_row_stride, w, bias, dout, dx, wsp, grid, T, D, s); break;
+    default: conv_bwd_launch<8>(x, x_row_stride, w, bias, dout, dx, wsp, grid, T, D, s); break;
+  }
+  rc = check_launch("conv1d+silu backward kernel");
+  if (rc) return rc;
+  const int K = (int)kernel_size;
+  const int n = (K + 1) * D;
+  hipLaunchKernelGGL(mhs::conv_reduce_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, s,
+                     wsp, dw, dbias, (int)(grid.y * grid.z), K, D);
+  return check_launch("conv1d+silu reduction kernel");
 }
 
 }  // extern "C"

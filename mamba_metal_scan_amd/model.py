@@ -8,7 +8,7 @@ plain torch; the selective scan is the only custom kernel:
   ("metal" = "hip"). "auto" uses the gfx950 scan for ROCm tensors and the
   associative ``parallel_scan`` on CPU.
 * ``MambaBlock`` (model.py:161-256): RMSNorm -> in_proj -> (x, z); causal
-  depthwise conv + SiLU; dt = dt_min + (dt_max-dt_min)*sigmoid(dt_proj(x));
+  depthwise conv + SiLU (on a ROCm device the fused ``conv1d_silu`` kernel); dt = dt_min + (dt_max-dt_min)*sigmoid(dt_proj(x));
   Aneg = softplus(A); the scan; + D_skip (a per-channel bias); * silu(z);
   out_proj; residual.
 * ``TinyMamba`` (model.py:259-302): embedding, blocks, final RMSNorm, head tied
@@ -30,6 +30,7 @@ import torch
 import torch.nn as nn
 import torch.nn.functional as F
 
+from .conv import conv1d_silu
 from .scan import SSM_CHUNK, _hip_device, selective_scan, selective_state_step
 
 
@@ -216,6 +217,17 @@ class MambaBlock(nn.Module):
         cache["h"] = h
         return (h * c_t[:, 0].unsqueeze(1)).sum(-1).unsqueeze(1)        # (B, 1, D)
 
+    def _conv_silu(self, x):
+        """silu(causal depthwise conv) of the (B, T, d_inner) x half of in_proj.
+
+        On a ROCm device (scan_impl other than 'torch') this is the fused HIP
+        kernel, reading x in place; elsewhere the framework's Conv1d on the
+        transposed view, as the reference does (model.py:244)."""
+        if self.scan_impl != "torch" and _hip_device(x) and x.dtype == torch.float32:
+            return conv1d_silu(x, self.conv.weight, self.conv.bias)
+        xt = x.transpose(1, 2)                                           # (B, d_inner, T)
+        return F.silu(self.conv(xt)[:, :, :xt.shape[2]]).transpose(1, 2)
+
     def forward(self, x, cache=None):
         residual = x
         x, z = self.in_proj(self.norm(x)).chunk(2, dim=-1)
@@ -224,7 +236,7 @@ class MambaBlock(nn.Module):
             y = self._step(x, cache)
         else:
             xt = x.transpose(1, 2)                                       # (B, d_inner, T)
-            x = F.silu(self.conv(xt)[:, :, :xt.shape[2]]).transpose(1, 2)
+            x = self._conv_silu(x)
             if cache is not None:
                 tail = xt[:, :, -(k - 1):]
                 if tail.shape[2] < k - 1:

@@ -8,6 +8,8 @@
  *   forward  -- the recurrence of scan.py:13-15 (and README.md:35-39), with
  *               checkpoints of h at the end of every chunk of K steps and at
  *               t = T-1 (scan.py:117-125);
+ *   conv     -- the block's causal depthwise conv1d + SiLU (model.py:174-175,
+ *               :244), forward and backward (oracle_conv_fwd / _bwd below);
  *   backward -- the adjoint recurrence of scan.py:22-34 (dx, ddt, dAneg, dB,
  *               dC), computed here from the fully stored h (no checkpoints),
  *               plus the gradient of the final state (dh_last), which the
@@ -118,4 +120,56 @@ void oracle_scan_step(double* h, const double* x, const double* dt, const double
       y[b * D + d] = yv;
     }
   }
+}
+
+/*
+ * Causal depthwise conv1d + SiLU, the reference block's
+ * F.silu(nn.Conv1d(D, D, K, padding=K-1, groups=D)(x^T)[:, :, :T])
+ * (mamba_metal/model.py:174-175, :244), on contiguous (B,T,D) x:
+ *   pre[b,t,d] = bias[d] + sum_k w[d,k] x[b, t-K+1+k, d]  (x = 0 before t = 0)
+ *   out = pre * sigmoid(pre)
+ */
+static double sig(double v) { return 1.0 / (1.0 + exp(-v)); }
+
+static double conv_pre(const double* x, const double* w, const double* bias, int64_t b,
+                       int64_t t, int64_t d, int64_t T, int64_t D, int64_t K) {
+  double p = bias[d];
+  for (int64_t k = 0; k < K; ++k) {
+    const int64_t s = t - K + 1 + k;
+    if (s >= 0) p += w[d * K + k] * x[(b * T + s) * D + d];
+  }
+  return p;
+}
+
+void oracle_conv_fwd(const double* x, const double* w, const double* bias, double* out,
+                     int64_t Bt, int64_t T, int64_t D, int64_t K) {
+  for (int64_t b = 0; b < Bt; ++b)
+    for (int64_t t = 0; t < T; ++t)
+      for (int64_t d = 0; d < D; ++d) {
+        const double p = conv_pre(x, w, bias, b, t, d, T, D, K);
+        out[(b * T + t) * D + d] = p * sig(p);
+      }
+}
+
+/* Gradients of sum(out * dout) with respect to x, w and bias. */
+void oracle_conv_bwd(const double* x, const double* w, const double* bias, const double* dout,
+                     double* dx, double* dw, double* dbias, int64_t Bt, int64_t T, int64_t D,
+                     int64_t K) {
+  memset(dx, 0, sizeof(double) * (size_t)(Bt * T * D));
+  memset(dw, 0, sizeof(double) * (size_t)(D * K));
+  memset(dbias, 0, sizeof(double) * (size_t)D);
+  for (int64_t b = 0; b < Bt; ++b)
+    for (int64_t t = 0; t < T; ++t)
+      for (int64_t d = 0; d < D; ++d) {
+        const double p = conv_pre(x, w, bias, b, t, d, T, D, K);
+        const double sg = sig(p);
+        const double s = dout[(b * T + t) * D + d] * (sg + p * sg * (1.0 - sg));
+        dbias[d] += s;
+        for (int64_t k = 0; k < K; ++k) {
+          const int64_t src = t - K + 1 + k;
+          if (src < 0) continue;
+          dw[d * K + k] += s * x[(b * T + src) * D + d];
+          dx[(b * T + src) * D + d] += s * w[d * K + k];
+        }
+      }
 }

@@ -11,7 +11,10 @@ oracle is pinned by what the mathematics fixes (mamba_metal/scan.py:13-41):
   input (and for the returned state, dh_last), a directional (JVP/VJP)
   dot-product test, and the brute-force dC = sum_d dy * h;
 * each check rejects a planted mistake (a transposed operand, a dropped term,
-  a wrong sign), so a plausible slip in the oracle cannot pass it.
+  a wrong sign), so a plausible slip in the oracle cannot pass it;
+* the block's causal depthwise conv1d + SiLU (model.py:174-175, :244):
+  numpy's full convolution with the reversed kernel, the pointwise K = 1
+  case, causality, finite differences and the VJP dot product.
 """
 from __future__ import annotations
 
@@ -226,3 +229,93 @@ def test_checks_reject_planted_mistakes():
     h = _h_all(*arrs)
     h_prev = np.concatenate([np.zeros_like(h[:, :1]), h[:, :-1]], axis=1)
     assert np.abs(np.einsum("btd,btdn->btn", dy, h_prev) - grads[4]).max() > 1e-3
+
+
+# ------------------------------------------------ conv1d + SiLU (oracle_conv_*)
+
+def _silu(v):
+    return v / (1.0 + np.exp(-v))
+
+
+def _conv_inputs(bt, t_len, d, k, seed):
+    rng = np.random.default_rng(seed)
+    return (rng.standard_normal((bt, t_len, d)), 0.5 * rng.standard_normal((d, k)),
+            0.1 * rng.standard_normal(d))
+
+
+@pytest.mark.parametrize("shape", [(2, 9, 3, 4), (1, 2, 5, 4), (1, 17, 2, 1), (2, 12, 3, 7)])
+def test_conv_matches_numpy_convolve(shape):
+    """pre[t] = bias + sum_k w[k] x[t-K+1+k] is numpy's full convolution with the
+    reversed kernel, cut to the first T outputs (the causal Conv1d)."""
+    x, w, bias = _conv_inputs(*shape, seed=31)
+    out = oracle.conv_fwd(x, w, bias)
+    bt, t_len, d, k = shape
+    ref = np.empty_like(out)
+    for b in range(bt):
+        for c in range(d):
+            ref[b, :, c] = _silu(np.convolve(x[b, :, c], w[c, ::-1])[:t_len] + bias[c])
+    np.testing.assert_allclose(out, ref, rtol=1e-13, atol=1e-15)
+    # A planted mistake: the kernel not reversed (an anti-causal filter) fails.
+    bad = _silu(np.convolve(x[0, :, 0], w[0])[:t_len] + bias[0])
+    if k > 1:
+        assert np.abs(bad - out[0, :, 0]).max() > 1e-3
+
+
+def test_conv_kernel_one_is_pointwise():
+    x, w, bias = _conv_inputs(2, 6, 4, 1, seed=32)
+    np.testing.assert_allclose(oracle.conv_fwd(x, w, bias), _silu(bias + w[:, 0] * x), rtol=1e-13)
+
+
+def test_conv_is_causal():
+    x, w, bias = _conv_inputs(1, 20, 3, 4, seed=33)
+    out = oracle.conv_fwd(x, w, bias)
+    x2 = x.copy()
+    x2[:, 9:] += 1.0
+    out2 = oracle.conv_fwd(x2, w, bias)
+    assert np.array_equal(out[:, :9], out2[:, :9]) and not np.allclose(out[:, 9:], out2[:, 9:])
+
+
+def _conv_fd(grads, arrs, dout, eps=1e-6, per=8, seed=0):
+    rng = np.random.default_rng(seed)
+    worst = 0.0
+    for i, (g, a) in enumerate(zip(grads, arrs)):
+        flat = a.reshape(-1)
+        for j in rng.permutation(flat.size)[:per]:
+            p, m = [t.copy() for t in arrs], [t.copy() for t in arrs]
+            p[i].reshape(-1)[j] += eps
+            m[i].reshape(-1)[j] -= eps
+            fd = ((oracle.conv_fwd(*p) - oracle.conv_fwd(*m)) * dout).sum() / (2 * eps)
+            worst = max(worst, abs(g.reshape(-1)[j] - fd) / max(np.abs(g).max(), 1e-12))
+    return worst
+
+
+@pytest.mark.parametrize("shape", [(2, 10, 3, 4), (1, 3, 2, 5)])
+def test_conv_gradients_match_finite_differences(shape):
+    arrs = list(_conv_inputs(*shape, seed=34))
+    dout = np.random.default_rng(35).standard_normal(arrs[0].shape)
+    grads = oracle.conv_bwd(*arrs, dout)
+    assert _conv_fd(grads, arrs, dout) < 1e-7
+    # Planted mistake: the SiLU derivative without its p * (1 - sig(p)) term.
+    x, w, bias = arrs
+    bt, t_len, d, k = shape
+    pre = np.empty_like(x)
+    for b in range(bt):
+        for c in range(d):
+            pre[b, :, c] = np.convolve(x[b, :, c], w[c, ::-1])[:t_len] + bias[c]
+    s_bad = dout / (1.0 + np.exp(-pre))
+    xp = np.concatenate([np.zeros((bt, k - 1, d)), x], axis=1)       # x[t - K + 1 + k]
+    dw_bad = np.stack([(s_bad * xp[:, j:j + t_len]).sum((0, 1)) for j in range(k)], axis=1)
+    bad = [grads[0], dw_bad, s_bad.sum((0, 1))]
+    assert _conv_fd(bad, arrs, dout) > 1e-2
+
+
+def test_conv_vjp_dot_product():
+    arrs = list(_conv_inputs(2, 11, 3, 4, seed=36))
+    rng = np.random.default_rng(37)
+    dout = rng.standard_normal(arrs[0].shape)
+    v = [rng.standard_normal(a.shape) for a in arrs]
+    eps = 1e-6
+    jv = ((oracle.conv_fwd(*[a + eps * u for a, u in zip(arrs, v)])
+           - oracle.conv_fwd(*[a - eps * u for a, u in zip(arrs, v)])) / (2 * eps) * dout).sum()
+    vjp = sum(float((g * u).sum()) for g, u in zip(oracle.conv_bwd(*arrs, dout), v))
+    assert abs(jv - vjp) <= 1e-7 * max(1.0, abs(vjp))
