@@ -448,7 +448,7 @@ int mhs_conv1d_silu_bwd_f32(const float* x, int64_t x_row_stride, const float* w
   if (rc) return rc;
   const int K = (int)kernel_size;
   const int n = (K + 1) * D;
-  hipLaunchKernelGGL(mhs::conv_reduce_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, s,
+  hipLaunchKernelGGL(mhs::conv_reduce_kernel, dim3((unsigned)((n + 3) / 4)), dim3(256), 0, s,
                      wsp, dw, dbias, (int)(grid.y * grid.z), K, D);
   return check_launch("conv1d+silu reduction kernel");
 }

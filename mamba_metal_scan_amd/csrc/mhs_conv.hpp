@@ -139,18 +139,30 @@ conv_silu_bwd_kernel(const float* __restrict__ x, long long x_rs, const float* _
   }
 }
 
-// dw[d,k], dbias[d]: sums of the nparts partials (fixed order).
+// dw[d,k], dbias[d]: sums of the nparts partials. One wave per output: lane
+// l adds partials l, l+64, ... in order, then a fixed DPP / permlane tree sums
+// the 64 lanes (a fixed summation order: bit-for-bit reproducible).
 __global__ void __launch_bounds__(256)
 conv_reduce_kernel(const float* __restrict__ wsp, float* __restrict__ dw, float* __restrict__ dbias,
                    int nparts, int K, int D) {
-  const int i = blockIdx.x * blockDim.x + threadIdx.x;   // (k, d), d fastest
-  if (i >= (K + 1) * D) return;
+  const int i = blockIdx.x * 4 + (threadIdx.x >> 6);   // (k, d), d fastest
+  const int lane = threadIdx.x & 63;
+  if (i >= (K + 1) * D) return;                        // uniform per wave
   const size_t stride = (size_t)(K + 1) * D;
   float s = 0.f;
-  for (int p = 0; p < nparts; ++p) s += wsp[(size_t)p * stride + i];
-  const int k = i / D, d = i % D;
-  if (k < K) dw[(size_t)d * K + k] = s;
-  else dbias[d] = s;
+  for (int p = lane; p < nparts; p += 64) s += wsp[(size_t)p * stride + i];
+  s = group_sum<16>(s);                                // row totals
+  const auto h32 = __builtin_amdgcn_permlane32_swap(__float_as_uint(s), __float_as_uint(s), false,
+                                                    false);
+  s = __uint_as_float(h32[0]) + __uint_as_float(h32[1]);
+  const auto h16 = __builtin_amdgcn_permlane16_swap(__float_as_uint(s), __float_as_uint(s), false,
+                                                    false);
+  s = __uint_as_float(h16[0]) + __uint_as_float(h16[1]);
+  if (lane == 0) {
+    const int k = i / D, d = i % D;
+    if (k < K) dw[(size_t)d * K + k] = s;
+    else dbias[d] = s;
+  }
 }
 
 }  // namespace mhs
