@@ -226,6 +226,8 @@ def bench_train(steps: int = 10, warmup: int = 3) -> dict:
     d_state 16, batch 16 x seq 512, random init, tokens uniform in [0, 32768)."""
     import torch
     from mamba_metal_scan_amd import MambaConfig, TinyMamba
+    from mamba_metal_scan_amd.gemm_tuning import TABLE, use_tuned_gemms
+    tuned = use_tuned_gemms()
     torch.manual_seed(1337)
     dev = torch.device("cuda", 0)
     cfg = MambaConfig(vocab_size=32768, d_model=640, n_layers=12, d_ff=2560, max_seq_len=512,
@@ -256,7 +258,8 @@ def bench_train(steps: int = 10, warmup: int = 3) -> dict:
            "params": model.count_params(), "d_inner": model.d_inner,
            "peak_hbm_GB": torch.cuda.max_memory_allocated(dev) / 1e9,
            "config": "TinyMamba 80M (vocab 32768, d_model 640, 12 layers, d_state 16), "
-                     "batch 16 x seq 512, fp32, AdamW, scan_impl=hip"}
+                     "batch 16 x seq 512, fp32, AdamW, scan_impl=hip",
+           "gemm_solutions": TABLE.name if tuned else "library default"}
     del model, opt
     torch.cuda.empty_cache()
     return out
