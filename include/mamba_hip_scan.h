@@ -109,6 +109,38 @@ int mhs_scan_bwd_f32(const float* x, const float* dt, const float* aneg,
                      int64_t chunk, void* stream);
 
 /*
+ * Forward scan with the block's dt gate and decay parametrisation fused in.
+ * Replaces the reference's `_proj` + `selective_scan` pair
+ * (mamba_metal/model.py:197 and :200 feeding scan.py:78-127): the kernels form
+ *     dt   = dt_min + (dt_max - dt_min) * sigmoid(dt_raw)    dt_raw : (batch, seqlen, d_inner)
+ *     Aneg = softplus(A)                                     A      : (d_inner, d_state)
+ * as they stage their inputs (dt is never written to memory), then run the
+ * recurrence of mhs_scan_fwd_f32 on (x, dt, Aneg, B, C). Needs finite
+ * dt_min < dt_max. Same outputs, layouts and checkpoints as mhs_scan_fwd_f32.
+ */
+int mhs_scan_gated_fwd_f32(const float* x, const float* dt_raw, const float* A,
+                           const float* B, const float* C, float dt_min, float dt_max,
+                           float* y, float* ckpt, float* h_last,
+                           int64_t batch, int64_t seqlen, int64_t d_inner, int64_t d_state,
+                           int64_t chunk, void* stream);
+
+/*
+ * Backward of mhs_scan_gated_fwd_f32 (the autograd of the same reference
+ * `_proj` + scan). Writes the gradients of the raw inputs:
+ *     ddt_raw = ddt * (dt_max - dt_min) * s * (1 - s),   s = sigmoid(dt_raw)
+ *     dA      = dAneg * sigmoid(A)
+ * and dx, dB, dC as mhs_scan_bwd_f32. Workspace: mhs_scan_bwd_workspace_bytes
+ * of the same shape. Bit-for-bit reproducible.
+ */
+int mhs_scan_gated_bwd_f32(const float* x, const float* dt_raw, const float* A,
+                           const float* B, const float* C, float dt_min, float dt_max,
+                           const float* dy, const float* dh_last, const float* ckpt,
+                           float* dx, float* ddt_raw, float* dA, float* dB, float* dC,
+                           void* workspace, size_t workspace_bytes,
+                           int64_t batch, int64_t seqlen, int64_t d_inner, int64_t d_state,
+                           int64_t chunk, void* stream);
+
+/*
  * One recurrent decode step, in place on h. Replaces the pure-torch step of
  * the reference's MambaBlock.forward (mamba_metal/model.py:234-241):
  *     h <- h * exp(-dt * Aneg) + dt * B * x ;  y = sum_n C * h
@@ -151,6 +183,38 @@ int mhs_conv1d_silu_bwd_f32(const float* x, int64_t x_row_stride, const float* w
                             float* dbias, void* workspace, size_t workspace_bytes,
                             int64_t batch, int64_t seqlen, int64_t d_inner, int64_t kernel_size,
                             void* stream);
+
+/*
+ * The block's output gate, forward. Replaces `y = y + self.D_skip` and the
+ * `y * F.silu(z)` feeding out_proj (mamba_metal/model.py:255-256):
+ *     out[b,t,d] = (y[b,t,d] + d_skip[d]) * silu(z[b,t,d])
+ *   y, out : (batch, seqlen, d_inner) contiguous
+ *   z      : (batch, seqlen, d_inner), rows `z_row_stride` floats apart (>= d_inner;
+ *            the z half of the block's in_proj output has 2*d_inner), batch rows
+ *            seqlen * z_row_stride apart
+ * Pointers need 4-byte alignment only.
+ */
+int mhs_out_gate_fwd_f32(const float* y, const float* d_skip, const float* z,
+                         int64_t z_row_stride, float* out,
+                         int64_t batch, int64_t seqlen, int64_t d_inner, void* stream);
+
+/* Bytes of device workspace mhs_out_gate_bwd_f32 needs for this shape. */
+size_t mhs_out_gate_bwd_workspace_bytes(int64_t batch, int64_t seqlen, int64_t d_inner);
+
+/*
+ * Backward of mhs_out_gate_fwd_f32 (the autograd of the same reference ops),
+ * with s = sigmoid(z):
+ *     dy = dout * z * s ;  dz = dout * (y + d_skip) * s * (1 + z * (1 - s)) ;
+ *     dd_skip[d] = sum_{b,t} dy[b,t,d]
+ * dy, dz : (batch, seqlen, d_inner) contiguous, dd_skip : (d_inner), all fully
+ * written; dd_skip is summed through the workspace (16-byte aligned) in a
+ * fixed order (bit-for-bit reproducible).
+ */
+int mhs_out_gate_bwd_f32(const float* y, const float* d_skip, const float* z,
+                         int64_t z_row_stride, const float* dout,
+                         float* dy, float* dz, float* dd_skip,
+                         void* workspace, size_t workspace_bytes,
+                         int64_t batch, int64_t seqlen, int64_t d_inner, void* stream);
 
 #ifdef __cplusplus
 }

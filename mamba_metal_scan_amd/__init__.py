@@ -4,10 +4,12 @@ Same public surface as the reference package ``mamba_metal``
 (mamba_metal/__init__.py:2-7), plus the HIP-specific names.
 """
 from .conv import ConvSiluHIP, conv1d_silu
+from .fused import OutGateHIP, SelectiveScanGatedHIP, out_gate, selective_scan_gated
 from .model import MambaConfig, TinyMamba
 from .scan import (SSM_CHUNK, SelectiveScanHIP, selective_scan, selective_scan_hip,
                    selective_scan_metal, selective_scan_ref, selective_state_step)
 
 __all__ = ["MambaConfig", "TinyMamba", "SSM_CHUNK", "SelectiveScanHIP", "selective_scan",
            "selective_scan_hip", "selective_scan_metal", "selective_scan_ref",
-           "selective_state_step", "conv1d_silu", "ConvSiluHIP"]
+           "selective_state_step", "conv1d_silu", "ConvSiluHIP", "selective_scan_gated",
+           "SelectiveScanGatedHIP", "out_gate", "OutGateHIP"]

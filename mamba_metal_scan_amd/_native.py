@@ -26,6 +26,8 @@ EXPORTED_SYMBOLS = (
     "mhs_set_variant", "mhs_scan_fwd_f32", "mhs_scan_bwd_workspace_bytes",
     "mhs_scan_bwd_f32", "mhs_scan_step_f32", "mhs_conv1d_silu_fwd_f32",
     "mhs_conv1d_silu_bwd_workspace_bytes", "mhs_conv1d_silu_bwd_f32",
+    "mhs_scan_gated_fwd_f32", "mhs_scan_gated_bwd_f32", "mhs_out_gate_fwd_f32",
+    "mhs_out_gate_bwd_workspace_bytes", "mhs_out_gate_bwd_f32",
 )
 
 _lib: Optional[ctypes.CDLL] = None
@@ -33,6 +35,7 @@ _lock = threading.Lock()
 
 _P = ctypes.c_void_p
 _I64 = ctypes.c_int64
+_F32 = ctypes.c_float
 
 
 class HipScanError(RuntimeError):
@@ -76,6 +79,18 @@ def library() -> ctypes.CDLL:
             lib.mhs_conv1d_silu_bwd_f32.restype = ctypes.c_int
             lib.mhs_conv1d_silu_bwd_f32.argtypes = ([_P, _I64] + [_P] * 7 + [ctypes.c_size_t]
                                                     + [_I64] * 4 + [_P])
+            lib.mhs_scan_gated_fwd_f32.restype = ctypes.c_int
+            lib.mhs_scan_gated_fwd_f32.argtypes = [_P] * 5 + [_F32] * 2 + [_P] * 3 + [_I64] * 5 + [_P]
+            lib.mhs_scan_gated_bwd_f32.restype = ctypes.c_int
+            lib.mhs_scan_gated_bwd_f32.argtypes = ([_P] * 5 + [_F32] * 2 + [_P] * 9
+                                                   + [ctypes.c_size_t] + [_I64] * 5 + [_P])
+            lib.mhs_out_gate_fwd_f32.restype = ctypes.c_int
+            lib.mhs_out_gate_fwd_f32.argtypes = [_P] * 3 + [_I64, _P] + [_I64] * 3 + [_P]
+            lib.mhs_out_gate_bwd_workspace_bytes.restype = ctypes.c_size_t
+            lib.mhs_out_gate_bwd_workspace_bytes.argtypes = [_I64] * 3
+            lib.mhs_out_gate_bwd_f32.restype = ctypes.c_int
+            lib.mhs_out_gate_bwd_f32.argtypes = ([_P] * 3 + [_I64] + [_P] * 5 + [ctypes.c_size_t]
+                                                 + [_I64] * 3 + [_P])
             _lib = lib
     return _lib
 
@@ -244,3 +259,108 @@ def conv1d_silu_bwd(x: torch.Tensor, w: torch.Tensor, bias: torch.Tensor, dout: 
 @conv1d_silu_bwd.register_fake
 def _conv1d_silu_bwd_fake(x, w, bias, dout):
     return x.new_empty(x.shape), torch.empty_like(w), torch.empty_like(bias)
+
+
+@torch.library.custom_op("mamba_hip::scan_gated_fwd", mutates_args=())
+def scan_gated_fwd(x: torch.Tensor, dt_raw: torch.Tensor, a_raw: torch.Tensor,
+                   b_in: torch.Tensor, c_in: torch.Tensor, dt_min: float, dt_max: float,
+                   chunk: int, with_ckpt: bool
+                   ) -> tuple[torch.Tensor, torch.Tensor, torch.Tensor]:
+    """scan_fwd with dt = dt_min + (dt_max - dt_min) * sigmoid(dt_raw) and
+    Aneg = softplus(a_raw) formed inside the kernels."""
+    bt, t_len, d = x.shape
+    n = a_raw.shape[1]
+    y = torch.empty_like(x)
+    ckpt = (x.new_empty((bt, num_chunks(t_len, chunk), d, n)) if with_ckpt
+            else x.new_empty((0,)))
+    h_last = x.new_empty((bt, d, n))
+    with torch.cuda.device(x.device):
+        rc = library().mhs_scan_gated_fwd_f32(
+            _ptr(x), _ptr(dt_raw), _ptr(a_raw), _ptr(b_in), _ptr(c_in), dt_min, dt_max, _ptr(y),
+            _ptr(ckpt) if with_ckpt else None, _ptr(h_last),
+            bt, t_len, d, n, chunk, _stream(x.device))
+    _check(rc, "mhs_scan_gated_fwd_f32")
+    return y, ckpt, h_last
+
+
+@scan_gated_fwd.register_fake
+def _scan_gated_fwd_fake(x, dt_raw, a_raw, b_in, c_in, dt_min, dt_max, chunk, with_ckpt):
+    return _scan_fwd_fake(x, dt_raw, a_raw, b_in, c_in, chunk, with_ckpt)
+
+
+@torch.library.custom_op("mamba_hip::scan_gated_bwd", mutates_args=())
+def scan_gated_bwd(x: torch.Tensor, dt_raw: torch.Tensor, a_raw: torch.Tensor,
+                   b_in: torch.Tensor, c_in: torch.Tensor, dt_min: float, dt_max: float,
+                   dy: torch.Tensor, dh_last: Optional[torch.Tensor], ckpt: torch.Tensor,
+                   chunk: int
+                   ) -> tuple[torch.Tensor, torch.Tensor, torch.Tensor, torch.Tensor, torch.Tensor]:
+    """(dx, d dt_raw, d a_raw, dB, dC) for the gated forward that produced `ckpt`."""
+    bt, t_len, d = x.shape
+    n = a_raw.shape[1]
+    lib = library()
+    dx = torch.empty_like(x)
+    ddt = torch.empty_like(dt_raw)
+    da = torch.empty_like(a_raw)
+    db = torch.empty_like(b_in)
+    dc = torch.empty_like(c_in)
+    ws_bytes = int(lib.mhs_scan_bwd_workspace_bytes(bt, t_len, d, n, chunk))
+    if ws_bytes == 0:
+        raise HipScanError(f"no backward workspace size for shape {(bt, t_len, d, n)} chunk {chunk}")
+    ws = torch.empty(ws_bytes, dtype=torch.uint8, device=x.device)
+    with torch.cuda.device(x.device):
+        rc = lib.mhs_scan_gated_bwd_f32(
+            _ptr(x), _ptr(dt_raw), _ptr(a_raw), _ptr(b_in), _ptr(c_in), dt_min, dt_max, _ptr(dy),
+            _ptr(dh_last), _ptr(ckpt), _ptr(dx), _ptr(ddt), _ptr(da), _ptr(db), _ptr(dc),
+            _ptr(ws), ws_bytes, bt, t_len, d, n, chunk, _stream(x.device))
+    _check(rc, "mhs_scan_gated_bwd_f32")
+    return dx, ddt, da, db, dc
+
+
+@scan_gated_bwd.register_fake
+def _scan_gated_bwd_fake(x, dt_raw, a_raw, b_in, c_in, dt_min, dt_max, dy, dh_last, ckpt, chunk):
+    return (torch.empty_like(x), torch.empty_like(dt_raw), torch.empty_like(a_raw),
+            torch.empty_like(b_in), torch.empty_like(c_in))
+
+
+@torch.library.custom_op("mamba_hip::out_gate_fwd", mutates_args=())
+def out_gate_fwd(y: torch.Tensor, d_skip: torch.Tensor, z: torch.Tensor) -> torch.Tensor:
+    """(y + d_skip) * silu(z) for (B,T,D) y and z (z rows may be strided)."""
+    bt, t_len, d = y.shape
+    out = y.new_empty((bt, t_len, d))
+    with torch.cuda.device(y.device):
+        rc = library().mhs_out_gate_fwd_f32(
+            _ptr(y), _ptr(d_skip), _ptr(z), _conv_rows(z), _ptr(out), bt, t_len, d,
+            _stream(y.device))
+    _check(rc, "mhs_out_gate_fwd_f32")
+    return out
+
+
+@out_gate_fwd.register_fake
+def _out_gate_fwd_fake(y, d_skip, z):
+    return y.new_empty(y.shape)
+
+
+@torch.library.custom_op("mamba_hip::out_gate_bwd", mutates_args=())
+def out_gate_bwd(y: torch.Tensor, d_skip: torch.Tensor, z: torch.Tensor, dout: torch.Tensor
+                 ) -> tuple[torch.Tensor, torch.Tensor, torch.Tensor]:
+    """(dy, dd_skip, dz), dy and dz (B,T,D) contiguous."""
+    bt, t_len, d = y.shape
+    lib = library()
+    dy = y.new_empty((bt, t_len, d))
+    dz = y.new_empty((bt, t_len, d))
+    dd = torch.empty_like(d_skip)
+    ws_bytes = int(lib.mhs_out_gate_bwd_workspace_bytes(bt, t_len, d))
+    if ws_bytes == 0:
+        raise HipScanError(f"no output-gate workspace size for shape {(bt, t_len, d)}")
+    ws = torch.empty(ws_bytes, dtype=torch.uint8, device=y.device)
+    with torch.cuda.device(y.device):
+        rc = lib.mhs_out_gate_bwd_f32(
+            _ptr(y), _ptr(d_skip), _ptr(z), _conv_rows(z), _ptr(dout), _ptr(dy), _ptr(dz),
+            _ptr(dd), _ptr(ws), ws_bytes, bt, t_len, d, _stream(y.device))
+    _check(rc, "mhs_out_gate_bwd_f32")
+    return dy, dd, dz
+
+
+@out_gate_bwd.register_fake
+def _out_gate_bwd_fake(y, d_skip, z, dout):
+    return y.new_empty(y.shape), torch.empty_like(d_skip), y.new_empty(y.shape)

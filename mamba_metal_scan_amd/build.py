@@ -20,7 +20,8 @@ LIB_PATH = PKG_DIR / LIB_NAME
 ARCH = "gfx950"
 
 SOURCES = ["mhs_capi.hip"]
-HEADERS = ["mhs_common.hpp", "mhs_fwd.hpp", "mhs_bwd.hpp", "mhs_step.hpp"]
+HEADERS = ["mhs_common.hpp", "mhs_fwd.hpp", "mhs_bwd.hpp", "mhs_step.hpp", "mhs_conv.hpp",
+           "mhs_gate.hpp"]
 
 
 def hipcc() -> str:

@@ -69,6 +69,10 @@ struct BwdArgs {
   float* wsC;            // (nblk, batch, T, N)
   float* wsA;            // (batch, D, N)
   int batch, T, D, N, K, nchunk;
+  // Gated kernels only (GATED): dt holds the raw gate input and aneg holds A
+  // (dt = dt_lo + dt_span * sigmoid(raw), Aneg = softplus(A); mamba_metal/
+  // model.py:197, :200), and ddt receives the gradient of the raw input.
+  float dt_lo, dt_span, dt_inv_span;
 };
 
 // One staging buffer (the kernel keeps two) and the single-buffered rest.
@@ -82,7 +86,10 @@ __host__ __device__ constexpr int bwd_lds_floats(int G, int NPL) {
          + 2 * kSteps * 2 * G * NPL;             // dB, dC block sums of a chunk
 }
 
-template <int NPL, int G, int MINW>
+// GATED: see BwdArgs. The staging threads gate each dt once per block as they
+// move it to LDS; finalize turns ddt into the raw input's gradient
+// ddt * span * s * (1 - s), s = sigmoid(raw) = (dt - lo) / span.
+template <int NPL, int G, int MINW, bool GATED>
 __global__ void __launch_bounds__(64 * G, MINW)
 bwd_kernel(BwdArgs a) {
   constexpr int NT = 64 * G;
@@ -132,6 +139,7 @@ bwd_kernel(BwdArgs a) {
 #pragma unroll
   for (int j = 0; j < NPL; ++j) {
     an[j] = (act && j < nvalid) ? a.aneg[(size_t)d * N + n0 + j] : 0.f;
+    if constexpr (GATED) an[j] = (act && j < nvalid) ? softplus_f(an[j]) : 0.f;
     a2[j] = -an[j] * kLog2e;
     acc[j] = 0.f;
     dan[j] = 1.f;
@@ -168,8 +176,9 @@ bwd_kernel(BwdArgs a) {
     load_states<NPL>(ph, GBuf(a.ckpt + ((size_t)b * nch + max(ci - 1, 0)) * slice,
                               ci > 0 ? slice_bytes : 0u), st_lane, nvalid);
   };
-  auto store_sub = [&](int j) {           // staging registers -> buffer j
+  auto store_sub = [&](int j, int ci) {   // staging registers (chunk ci) -> buffer j
     float* s0 = lds + j * BUF;
+    if constexpr (GATED) ql.gate(pd, chunk_len(ci), a.dt_lo, a.dt_span);
     ql.store_cm(s0, pd);
     ql.store_cm(s0 + oDY, py);
     ql.store_cm(s0 + oX, px);
@@ -203,8 +212,14 @@ bwd_kernel(BwdArgs a) {
       }
       gdx.st(t0v * s1a, o0);
       gdx.st(t1v * s1b, o1);
-      gddt.st(__builtin_fmaf(x0, s1a, -s2a), o0);
-      gddt.st(__builtin_fmaf(x1, s1b, -s2b), o1);
+      float g0 = __builtin_fmaf(x0, s1a, -s2a), g1 = __builtin_fmaf(x1, s1b, -s2b);
+      if constexpr (GATED) {
+        const float u0 = t0v - a.dt_lo, u1 = t1v - a.dt_lo;   // span * s
+        g0 *= u0 * (a.dt_span - u0) * a.dt_inv_span;
+        g1 *= u1 * (a.dt_span - u1) * a.dt_inv_span;
+      }
+      gddt.st(g0, o0);
+      gddt.st(g1, o1);
     }
     const int len = chunk_len(ci);
     const size_t wrow = ((size_t)blockIdx.x * a.batch + b) * T + chunk_t0(ci);
@@ -224,7 +239,7 @@ bwd_kernel(BwdArgs a) {
   // the staging registers.
   load_sub(nch - 1);
   load_h0(nch - 1);
-  store_sub(0);
+  store_sub(0, nch - 1);
   float hc[NPL];                          // h at the start of the current chunk
 #pragma unroll
   for (int j = 0; j < NPL; ++j) hc[j] = ph[j];
@@ -309,7 +324,7 @@ bwd_kernel(BwdArgs a) {
         o[s] = __uint_as_float(sw[0]) + __uint_as_float(sw[1]);
       }
       sts4(tS + wave * 64 * kSteps + cm_quad(lane, m), make_float4(o[0], o[1], o[2], o[3]));
-      if (m == 2) store_sub((i + 1) & 1);  // chunk ci-1 (unused when ci == 0)
+      if (m == 2) store_sub((i + 1) & 1, ci - 1);  // unused when ci == 0
       if (m == 1) load_sub(ci - 2);        // loads nothing when ci < 2
     }
 #pragma unroll
@@ -351,10 +366,12 @@ __device__ __forceinline__ void ordered_sum2(const float* __restrict__ p, const 
   }
 }
 
+// a_raw: null, or A for the gated backward: then daneg receives dAneg *
+// softplus'(A) = dAneg * sigmoid(A), the gradient of A.
 __global__ void __launch_bounds__(256)
 bwd_reduce_kernel(const float* __restrict__ wsB, const float* __restrict__ wsC,
-                  const float* __restrict__ wsA, float* __restrict__ dB,
-                  float* __restrict__ dC, float* __restrict__ daneg,
+                  const float* __restrict__ wsA, const float* __restrict__ a_raw,
+                  float* __restrict__ dB, float* __restrict__ dC, float* __restrict__ daneg,
                   int nblk, int batch, long long S, long long A) {
   const long long stride = (long long)gridDim.x * blockDim.x;
   for (long long i = (long long)blockIdx.x * blockDim.x + threadIdx.x; i < S + A; i += stride) {
@@ -367,7 +384,7 @@ bwd_reduce_kernel(const float* __restrict__ wsB, const float* __restrict__ wsC,
       const long long j = i - S;
       float s = 0.f;
       for (int bb = 0; bb < batch; ++bb) s += wsA[(size_t)bb * A + j];
-      daneg[j] = s;
+      daneg[j] = a_raw != nullptr ? s / (1.f + expf(-a_raw[j])) : s;
     }
   }
 }

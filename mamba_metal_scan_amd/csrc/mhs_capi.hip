@@ -7,6 +7,7 @@
 #include <hip/hip_runtime.h>
 
 #include <atomic>
+#include <cmath>
 #include <cstdarg>
 #include <cstdio>
 #include <cstring>
@@ -16,6 +17,7 @@
 #include "mhs_bwd.hpp"
 #include "mhs_conv.hpp"
 #include "mhs_fwd.hpp"
+#include "mhs_gate.hpp"
 #include "mhs_step.hpp"
 
 namespace {
@@ -55,8 +57,11 @@ struct Plan {
   int G = 0;        // waves per block (d_state padded to 2*G*npl)
   FwdFn fwd = nullptr;      // checkpoint stride a multiple of 16 (or >= T)
   FwdFn fwd_any = nullptr;  // any checkpoint stride
+  FwdFn fwd_g = nullptr;    // the same two with the dt gate and softplus(A) fused
+  FwdFn fwd_any_g = nullptr;
   int fwd_lds = 0;  // bytes
   BwdFn bwd = nullptr;
+  BwdFn bwd_g = nullptr;    // gated
   int bwd_ki = 0;   // largest chunk the backward walks directly
   int bwd_lds = 0;  // bytes
 };
@@ -68,9 +73,12 @@ struct Plan {
 template <int NPL, int G>
 void fill(Plan& p) {
   constexpr int MINW = NPL == 2 ? 3 : 2;
-  p.fwd = &mhs::fwd_kernel<NPL, G, MINW, true>;
-  p.fwd_any = &mhs::fwd_kernel<NPL, G, MINW, false>;
-  p.bwd = &mhs::bwd_kernel<NPL, G, MINW>;
+  p.fwd = &mhs::fwd_kernel<NPL, G, MINW, true, false>;
+  p.fwd_any = &mhs::fwd_kernel<NPL, G, MINW, false, false>;
+  p.fwd_g = &mhs::fwd_kernel<NPL, G, MINW, true, true>;
+  p.fwd_any_g = &mhs::fwd_kernel<NPL, G, MINW, false, true>;
+  p.bwd = &mhs::bwd_kernel<NPL, G, MINW, false>;
+  p.bwd_g = &mhs::bwd_kernel<NPL, G, MINW, true>;
   p.fwd_lds = mhs::fwd_lds_floats(G, NPL) * 4;
   p.bwd_lds = mhs::bwd_lds_floats(G, NPL) * 4;
 }
@@ -171,9 +179,29 @@ WsLayout ws_layout(int64_t batch, int64_t T, int64_t D, int64_t N, int64_t chunk
   return w;
 }
 
-int launch_fwd(const Plan& p, const mhs::FwdArgs& a, int batch, hipStream_t s) {
+// The block's dt gate (mamba_metal/model.py:197): dt = lo + span * sigmoid(raw).
+struct Gate {
+  bool on = false;
+  float lo = 0.f, span = 0.f;
+};
+
+int check_gate(float dt_min, float dt_max, Gate& g) {
+  if (!std::isfinite(dt_min) || !std::isfinite(dt_max) || !(dt_max > dt_min))
+    return fail(MHS_EINVAL, "need finite dt_min < dt_max, got %g, %g", (double)dt_min,
+                (double)dt_max);
+  g.on = true;
+  g.lo = dt_min;
+  g.span = dt_max - dt_min;
+  if (!(g.span > 0.f) || !std::isfinite(g.span))
+    return fail(MHS_EINVAL, "dt_max - dt_min must be a positive finite float");
+  return MHS_OK;
+}
+
+int launch_fwd(const Plan& p, mhs::FwdArgs a, int batch, hipStream_t s, const Gate& g) {
   const bool aligned = a.K % mhs::kSteps == 0 || a.K >= a.T;
-  const FwdFn fn = aligned ? p.fwd : p.fwd_any;
+  const FwdFn fn = aligned ? (g.on ? p.fwd_g : p.fwd) : (g.on ? p.fwd_any_g : p.fwd_any);
+  a.dt_lo = g.lo;
+  a.dt_span = g.span;
   int rc = ensure_lds(reinterpret_cast<const void*>(fn), p.fwd_lds);
   if (rc) return rc;
   const dim3 grid((unsigned)((a.D + mhs::kCH - 1) / mhs::kCH), (unsigned)batch);
@@ -181,37 +209,9 @@ int launch_fwd(const Plan& p, const mhs::FwdArgs& a, int batch, hipStream_t s) {
   return check_launch("forward scan kernel");
 }
 
-}  // namespace
-
-extern "C" {
-
-int mhs_version(void) { return kVersion; }
-
-const char* mhs_last_error(void) { return g_err; }
-
-int64_t mhs_num_chunks(int64_t seqlen, int64_t chunk) {
-  if (seqlen < 1 || chunk < 1) return 0;
-  return (seqlen + chunk - 1) / chunk;
-}
-
-int mhs_set_variant(int npl) {
-  if (npl != 0 && npl != 2 && npl != 4)
-    return fail(MHS_EINVAL, "states per lane must be 0 (auto), 2 or 4; got %d", npl);
-  g_npl_override.store(npl, std::memory_order_relaxed);
-  return MHS_OK;
-}
-
-int64_t mhs_preferred_chunk(int64_t d_state) {
-  Plan p;
-  if (!make_plan((int)d_state, p)) return 0;
-  return p.bwd_ki;
-}
-
-int mhs_scan_fwd_f32(const float* x, const float* dt, const float* aneg, const float* B,
-                     const float* C, float* y, float* ckpt, float* h_last, int64_t batch,
-                     int64_t seqlen, int64_t d_inner, int64_t d_state, int64_t chunk,
-                     void* stream) {
-  g_err[0] = '\0';
+int scan_fwd(const float* x, const float* dt, const float* aneg, const float* B, const float* C,
+             float* y, float* ckpt, float* h_last, int64_t batch, int64_t seqlen, int64_t d_inner,
+             int64_t d_state, int64_t chunk, void* stream, const Gate& g) {
   int rc = check_shape(batch, seqlen, d_inner, d_state, chunk);
   if (rc) return rc;
   if (!x || !dt || !aneg || !B || !C) return fail(MHS_EINVAL, "null input pointer");
@@ -226,23 +226,14 @@ int mhs_scan_fwd_f32(const float* x, const float* dt, const float* aneg, const f
   a.T = (int)seqlen; a.D = (int)d_inner; a.N = (int)d_state;
   a.K = (int)std::min<int64_t>(chunk, seqlen);
   a.nchunk = (int)mhs_num_chunks(seqlen, chunk);
-  return launch_fwd(p, a, (int)batch, static_cast<hipStream_t>(stream));
+  return launch_fwd(p, a, (int)batch, static_cast<hipStream_t>(stream), g);
 }
 
-size_t mhs_scan_bwd_workspace_bytes(int64_t batch, int64_t seqlen, int64_t d_inner,
-                                    int64_t d_state, int64_t chunk) {
-  if (check_shape(batch, seqlen, d_inner, d_state, chunk)) return 0;
-  Plan p;
-  if (!make_plan((int)d_state, p)) return 0;
-  return ws_layout(batch, seqlen, d_inner, d_state, chunk, p.bwd_ki).total;
-}
-
-int mhs_scan_bwd_f32(const float* x, const float* dt, const float* aneg, const float* B,
-                     const float* C, const float* dy, const float* dh_last, const float* ckpt,
-                     float* dx, float* ddt, float* daneg, float* dB, float* dC, void* workspace,
-                     size_t workspace_bytes, int64_t batch, int64_t seqlen, int64_t d_inner,
-                     int64_t d_state, int64_t chunk, void* stream) {
-  g_err[0] = '\0';
+int scan_bwd(const float* x, const float* dt, const float* aneg, const float* B, const float* C,
+             const float* dy, const float* dh_last, const float* ckpt, float* dx, float* ddt,
+             float* daneg, float* dB, float* dC, void* workspace, size_t workspace_bytes,
+             int64_t batch, int64_t seqlen, int64_t d_inner, int64_t d_state, int64_t chunk,
+             void* stream, const Gate& g) {
   int rc = check_shape(batch, seqlen, d_inner, d_state, chunk);
   if (rc) return rc;
   if (!x || !dt || !aneg || !B || !C || !dy || !ckpt || !dx || !ddt || !daneg || !dB || !dC ||
@@ -276,7 +267,7 @@ int mhs_scan_bwd_f32(const float* x, const float* dt, const float* aneg, const f
     f.h_last = nullptr;
     f.T = T; f.D = D; f.N = N; f.K = p.bwd_ki;
     f.nchunk = (int)mhs_num_chunks(T, p.bwd_ki);
-    rc = launch_fwd(p, f, (int)batch, s);
+    rc = launch_fwd(p, f, (int)batch, s, g);
     if (rc) return rc;
     ck = f.ckpt;
     Kb = p.bwd_ki;
@@ -291,10 +282,14 @@ int mhs_scan_bwd_f32(const float* x, const float* dt, const float* aneg, const f
   a.wsA = reinterpret_cast<float*>(ws + w.partA);
   a.batch = (int)batch; a.T = T; a.D = D; a.N = N; a.K = Kb;
   a.nchunk = (int)mhs_num_chunks(T, Kb);
-  rc = ensure_lds(reinterpret_cast<const void*>(p.bwd), p.bwd_lds);
+  a.dt_lo = g.lo;
+  a.dt_span = g.span;
+  a.dt_inv_span = g.on ? 1.f / g.span : 0.f;
+  const BwdFn fn = g.on ? p.bwd_g : p.bwd;
+  rc = ensure_lds(reinterpret_cast<const void*>(fn), p.bwd_lds);
   if (rc) return rc;
   const dim3 grid((unsigned)((D + ch - 1) / ch), (unsigned)batch);
-  hipLaunchKernelGGL(p.bwd, grid, dim3(64 * p.G), p.bwd_lds, s, a);
+  hipLaunchKernelGGL(fn, grid, dim3(64 * p.G), p.bwd_lds, s, a);
   rc = check_launch("backward scan kernel");
   if (rc) return rc;
 
@@ -303,8 +298,87 @@ int mhs_scan_bwd_f32(const float* x, const float* dt, const float* aneg, const f
   const long long total = S + A;
   const int blocks = (int)std::min<long long>((total + 255) / 256, 4096);
   hipLaunchKernelGGL(mhs::bwd_reduce_kernel, dim3(blocks), dim3(256), 0, s, a.wsB, a.wsC, a.wsA,
-                     dB, dC, daneg, (D + ch - 1) / ch, (int)batch, S, A);
+                     g.on ? aneg : nullptr, dB, dC, daneg, (D + ch - 1) / ch, (int)batch, S, A);
   return check_launch("backward reduction kernel");
+}
+
+}  // namespace
+
+extern "C" {
+
+int mhs_version(void) { return kVersion; }
+
+const char* mhs_last_error(void) { return g_err; }
+
+int64_t mhs_num_chunks(int64_t seqlen, int64_t chunk) {
+  if (seqlen < 1 || chunk < 1) return 0;
+  return (seqlen + chunk - 1) / chunk;
+}
+
+int mhs_set_variant(int npl) {
+  if (npl != 0 && npl != 2 && npl != 4)
+    return fail(MHS_EINVAL, "states per lane must be 0 (auto), 2 or 4; got %d", npl);
+  g_npl_override.store(npl, std::memory_order_relaxed);
+  return MHS_OK;
+}
+
+int64_t mhs_preferred_chunk(int64_t d_state) {
+  Plan p;
+  if (!make_plan((int)d_state, p)) return 0;
+  return p.bwd_ki;
+}
+
+size_t mhs_scan_bwd_workspace_bytes(int64_t batch, int64_t seqlen, int64_t d_inner,
+                                    int64_t d_state, int64_t chunk) {
+  if (check_shape(batch, seqlen, d_inner, d_state, chunk)) return 0;
+  Plan p;
+  if (!make_plan((int)d_state, p)) return 0;
+  return ws_layout(batch, seqlen, d_inner, d_state, chunk, p.bwd_ki).total;
+}
+
+int mhs_scan_fwd_f32(const float* x, const float* dt, const float* aneg, const float* B,
+                     const float* C, float* y, float* ckpt, float* h_last, int64_t batch,
+                     int64_t seqlen, int64_t d_inner, int64_t d_state, int64_t chunk,
+                     void* stream) {
+  g_err[0] = '\0';
+  return scan_fwd(x, dt, aneg, B, C, y, ckpt, h_last, batch, seqlen, d_inner, d_state, chunk,
+                  stream, Gate{});
+}
+
+int mhs_scan_bwd_f32(const float* x, const float* dt, const float* aneg, const float* B,
+                     const float* C, const float* dy, const float* dh_last, const float* ckpt,
+                     float* dx, float* ddt, float* daneg, float* dB, float* dC, void* workspace,
+                     size_t workspace_bytes, int64_t batch, int64_t seqlen, int64_t d_inner,
+                     int64_t d_state, int64_t chunk, void* stream) {
+  g_err[0] = '\0';
+  return scan_bwd(x, dt, aneg, B, C, dy, dh_last, ckpt, dx, ddt, daneg, dB, dC, workspace,
+                  workspace_bytes, batch, seqlen, d_inner, d_state, chunk, stream, Gate{});
+}
+
+int mhs_scan_gated_fwd_f32(const float* x, const float* dt_raw, const float* A, const float* B,
+                           const float* C, float dt_min, float dt_max, float* y, float* ckpt,
+                           float* h_last, int64_t batch, int64_t seqlen, int64_t d_inner,
+                           int64_t d_state, int64_t chunk, void* stream) {
+  g_err[0] = '\0';
+  Gate g;
+  const int rc = check_gate(dt_min, dt_max, g);
+  if (rc) return rc;
+  return scan_fwd(x, dt_raw, A, B, C, y, ckpt, h_last, batch, seqlen, d_inner, d_state, chunk,
+                  stream, g);
+}
+
+int mhs_scan_gated_bwd_f32(const float* x, const float* dt_raw, const float* A, const float* B,
+                           const float* C, float dt_min, float dt_max, const float* dy,
+                           const float* dh_last, const float* ckpt, float* dx, float* ddt_raw,
+                           float* dA, float* dB, float* dC, void* workspace,
+                           size_t workspace_bytes, int64_t batch, int64_t seqlen, int64_t d_inner,
+                           int64_t d_state, int64_t chunk, void* stream) {
+  g_err[0] = '\0';
+  Gate g;
+  const int rc = check_gate(dt_min, dt_max, g);
+  if (rc) return rc;
+  return scan_bwd(x, dt_raw, A, B, C, dy, dh_last, ckpt, dx, ddt_raw, dA, dB, dC, workspace,
+                  workspace_bytes, batch, seqlen, d_inner, d_state, chunk, stream, g);
 }
 
 int mhs_scan_step_f32(float* h, const float* x, const float* dt, const float* aneg, const float* B,
@@ -354,7 +428,7 @@ int check_conv(int64_t batch, int64_t seqlen, int64_t d_inner, int64_t k, int64_
                 (long long)batch, (long long)seqlen, (long long)d_inner);
   if (k < 1 || k > mhs::kConvMaxK)
     return fail(MHS_EINVAL, "kernel_size %lld unsupported (1..%d)", (long long)k, mhs::kConvMaxK);
-  if (x_rs < d_inner) return fail(MHS_EINVAL, "x_row_stride %lld < d_inner %lld", (long long)x_rs,
+  if (x_rs < d_inner) return fail(MHS_EINVAL, "row stride %lld < d_inner %lld", (long long)x_rs,
                                   (long long)d_inner);
   if (batch > 65535) return fail(MHS_EINVAL, "batch %lld exceeds 65535", (long long)batch);
   if (seqlen > (1LL << 30) || d_inner > (1LL << 30)) return fail(MHS_EINVAL, "sizes too large");
@@ -451,6 +525,60 @@ int mhs_conv1d_silu_bwd_f32(const float* x, int64_t x_row_stride, const float* w
   hipLaunchKernelGGL(mhs::conv_reduce_kernel, dim3((unsigned)((n + 3) / 4)), dim3(256), 0, s,
                      wsp, dw, dbias, (int)(grid.y * grid.z), K, D);
   return check_launch("conv1d+silu reduction kernel");
+}
+
+}  // extern "C"
+
+// ------------------------------------------------------------- output gate
+
+extern "C" {
+
+int mhs_out_gate_fwd_f32(const float* y, const float* d_skip, const float* z, int64_t z_row_stride,
+                         float* out, int64_t batch, int64_t seqlen, int64_t d_inner,
+                         void* stream) {
+  g_err[0] = '\0';
+  int rc = check_conv(batch, seqlen, d_inner, 1, z_row_stride);
+  if (rc) return rc;
+  if (!y || !d_skip || !z || !out) return fail(MHS_EINVAL, "null pointer argument");
+  const dim3 grid = conv_grid(batch, seqlen, d_inner);
+  hipLaunchKernelGGL(mhs::out_gate_fwd_kernel<kConvTPT>, grid, dim3(mhs::kConvCh * mhs::kConvTG),
+                     0, static_cast<hipStream_t>(stream), y, d_skip, z, (long long)z_row_stride,
+                     out, (int)seqlen, (int)d_inner);
+  return check_launch("output gate forward kernel");
+}
+
+size_t mhs_out_gate_bwd_workspace_bytes(int64_t batch, int64_t seqlen, int64_t d_inner) {
+  if (check_conv(batch, seqlen, d_inner, 1, d_inner)) return 0;
+  const dim3 grid = conv_grid(batch, seqlen, d_inner);
+  return (size_t)grid.y * grid.z * (size_t)d_inner * 4;
+}
+
+int mhs_out_gate_bwd_f32(const float* y, const float* d_skip, const float* z, int64_t z_row_stride,
+                         const float* dout, float* dy, float* dz, float* dd_skip, void* workspace,
+                         size_t workspace_bytes, int64_t batch, int64_t seqlen, int64_t d_inner,
+                         void* stream) {
+  g_err[0] = '\0';
+  int rc = check_conv(batch, seqlen, d_inner, 1, z_row_stride);
+  if (rc) return rc;
+  if (!y || !d_skip || !z || !dout || !dy || !dz || !dd_skip || !workspace)
+    return fail(MHS_EINVAL, "null pointer argument");
+  const size_t need = mhs_out_gate_bwd_workspace_bytes(batch, seqlen, d_inner);
+  if (workspace_bytes < need)
+    return fail(MHS_EINVAL, "workspace too small: %zu < %zu bytes", workspace_bytes, need);
+  if (reinterpret_cast<uintptr_t>(workspace) & 15u)
+    return fail(MHS_EINVAL, "workspace must be 16-byte aligned");
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  const dim3 grid = conv_grid(batch, seqlen, d_inner);
+  float* wsp = static_cast<float*>(workspace);
+  const int D = (int)d_inner;
+  hipLaunchKernelGGL(mhs::out_gate_bwd_kernel<kConvTPT>, grid, dim3(mhs::kConvCh * mhs::kConvTG),
+                     0, s, y, d_skip, z, (long long)z_row_stride, dout, dy, dz, wsp, (int)seqlen,
+                     D);
+  rc = check_launch("output gate backward kernel");
+  if (rc) return rc;
+  hipLaunchKernelGGL(mhs::conv_reduce_kernel, dim3((unsigned)((D + 3) / 4)), dim3(256), 0, s, wsp,
+                     nullptr, dd_skip, (int)(grid.y * grid.z), 0, D);
+  return check_launch("output gate reduction kernel");
 }
 
 }  // extern "C"

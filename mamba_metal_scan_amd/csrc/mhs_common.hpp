@@ -25,6 +25,24 @@ constexpr float kLog2e = 1.4426950408889634f;
 // such a decay factor erases the state exactly as an exact underflow would).
 __device__ __forceinline__ float exp2_hw(float v) { return __builtin_amdgcn_exp2f(v); }
 
+// sigmoid(v) = 1 / (1 + 2^(-v log2 e)) with the hardware exp2 and reciprocal
+// (about 2 ulp; v -> -inf gives 0, v -> +inf gives 1).
+__device__ __forceinline__ float sigmoid_f(float v) {
+  return __builtin_amdgcn_rcpf(1.f + exp2_hw(-v * kLog2e));
+}
+
+// The block's dt gate (mamba_metal/model.py:197): dt = lo + span * sigmoid(raw).
+__device__ __forceinline__ float gate_dt(float raw, float lo, float span) {
+  return __builtin_fmaf(span, sigmoid_f(raw), lo);
+}
+
+// softplus(a) = log(1 + e^a) (mamba_metal/model.py:200, Aneg = softplus(A)),
+// written as max(a, 0) + log1p(e^-|a|) so that it neither overflows for large
+// a nor loses the small values for very negative a.
+__device__ __forceinline__ float softplus_f(float a) {
+  return fmaxf(a, 0.f) + log1pf(expf(-fabsf(a)));
+}
+
 // v_add_f32 with a DPP source permutation: a cross-lane add in one VALU slot.
 template <int CTRL>
 __device__ __forceinline__ float dpp_add(float v) {
@@ -257,6 +275,20 @@ struct QuadLoader {
       v[i].y = g.ld(ok ? o + rs : kOOB);
       v[i].z = g.ld(ok ? o + 2 * rs : kOOB);
       v[i].w = g.ld(ok ? o + 3 * rs : kOOB);
+    }
+  }
+  // Gate staged dt values in place: dt = lo + span * sigmoid(raw) for the
+  // steps below len; steps at or past len (and channels past d_inner) get
+  // dt = 0, which makes them identity steps of the recurrence, as the zeros
+  // an ungated load returns there.
+  __device__ __forceinline__ void gate(float4 (&v)[PER], int len, float lo, float span) const {
+#pragma unroll
+    for (int i = 0; i < PER; ++i) {
+      const int s0 = toff[i] != kOOB ? 4 * quad(i) : kSteps;
+      v[i].x = s0 < len ? gate_dt(v[i].x, lo, span) : 0.f;
+      v[i].y = s0 + 1 < len ? gate_dt(v[i].y, lo, span) : 0.f;
+      v[i].z = s0 + 2 < len ? gate_dt(v[i].z, lo, span) : 0.f;
+      v[i].w = s0 + 3 < len ? gate_dt(v[i].w, lo, span) : 0.f;
     }
   }
   // Channel-major swizzled tile [CH][16].

@@ -21,10 +21,6 @@ constexpr int kConvMaxK = 8;
 constexpr int kConvCh = 64;    // channels per block
 constexpr int kConvTG = 4;     // step groups per block (block = 64 x 4 threads)
 
-__device__ __forceinline__ float sigmoid_f(float v) {
-  return __builtin_amdgcn_rcpf(1.f + exp2_hw(-v * kLog2e));
-}
-
 // Forward: thread (d, step group g) of block (db, tb, b) computes TPT
 // outputs t in [t0, t0 + TPT).
 template <int K, int TPT>

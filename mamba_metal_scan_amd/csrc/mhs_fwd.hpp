@@ -42,6 +42,10 @@ struct FwdArgs {
   float* ckpt;     // may be null
   float* h_last;   // may be null
   int T, D, N, K, nchunk;
+  // Gated kernels only (GATED): dt holds the raw gate input and aneg holds A;
+  // dt = dt_lo + dt_span * sigmoid(raw) and Aneg = softplus(A) are formed in
+  // the kernel (mamba_metal/model.py:197, :200).
+  float dt_lo, dt_span;
 };
 
 constexpr int kCH = 32;   // channels per block
@@ -58,7 +62,9 @@ __host__ __device__ constexpr int fwd_lds_floats(int G, int NPL) {
 
 // KALIGNED: the checkpoint stride K is a multiple of 16, so checkpoints fall
 // on sub-chunk ends (and the last one on the final state): no per-step tests.
-template <int NPL, int G, int MINW, bool KALIGNED>
+// GATED: dt and Aneg come from the block's raw projections (see FwdArgs); the
+// staging threads gate each dt once per block as they move it to LDS.
+template <int NPL, int G, int MINW, bool KALIGNED, bool GATED>
 __global__ void __launch_bounds__(64 * G, MINW)
 fwd_kernel(FwdArgs a) {
   constexpr int NT = 64 * G;                    // threads
@@ -85,7 +91,9 @@ fwd_kernel(FwdArgs a) {
   float a2[NPL], h[NPL];
 #pragma unroll
   for (int j = 0; j < NPL; ++j) {
-    a2[j] = (act && n0 + j < N) ? -a.aneg[(size_t)d * N + n0 + j] * kLog2e : 0.f;
+    float an = (act && n0 + j < N) ? a.aneg[(size_t)d * N + n0 + j] : 0.f;
+    if constexpr (GATED) an = (act && n0 + j < N) ? softplus_f(an) : 0.f;
+    a2[j] = -an * kLog2e;
     h[j] = 0.f;
   }
 
@@ -111,6 +119,7 @@ fwd_kernel(FwdArgs a) {
   };
   auto store_sub = [&](int i) {           // staging registers -> LDS buffer i&1
     float* buf = lds + (i & 1) * BUF;
+    if constexpr (GATED) ql.gate(pd, sub_len(i), a.dt_lo, a.dt_span);
     ql.store_cm(buf, pd);
     ql.store_cm_product(buf + kCH * kSteps, pd, px);
     rl.store(buf + 2 * kCH * kSteps, pb);

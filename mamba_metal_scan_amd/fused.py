@@ -1,0 +1,128 @@
+"""The MambaBlock's producer and consumer ops around the scan, fused on MI355X.
+
+The reference block computes, around its selective scan
+(mamba_metal/model.py:197-200 and :255-256):
+
+    dt   = dt_min + (dt_max - dt_min) * sigmoid(dt_proj(x))     # 3 elementwise ops
+    Aneg = softplus(A)
+    y    = selective_scan(x, dt, Aneg, B, C)
+    out  = out_proj((y + D_skip) * silu(z))                    # 3 elementwise ops
+
+Each elementwise op is a full pass over a (batch, T, d_inner) tensor in the
+forward and another one or two in the backward. Here:
+
+* ``selective_scan_gated`` takes the raw ``dt_proj`` output and ``A``: the
+  scan kernels gate dt and take softplus(A) while they stage their inputs,
+  and the backward kernels return the raw inputs' gradients. dt is never
+  materialised.
+* ``out_gate`` computes ``(y + D_skip) * silu(z)`` in one kernel per
+  direction, reading z in place from the in_proj output, with a deterministic
+  reduction for D_skip's gradient.
+"""
+from __future__ import annotations
+
+import torch
+
+from . import _native
+from .scan import SSM_CHUNK, _validate, _hip_device
+
+
+class SelectiveScanGatedHIP(torch.autograd.Function):
+    """selective_scan_gated(...) -> y (or (y, h_last)), forward and backward."""
+
+    @staticmethod
+    def forward(ctx, x, dt_raw, a_raw, b_in, c_in, dt_min, dt_max, chunk=SSM_CHUNK,
+                return_state=False):
+        _validate(x, dt_raw, a_raw, b_in, c_in, chunk)
+        x, dt_raw, a_raw, b_in, c_in = (t.contiguous() for t in (x, dt_raw, a_raw, b_in, c_in))
+        ctx.set_materialize_grads(False)
+        ctx.chunk = chunk
+        ctx.gate = (float(dt_min), float(dt_max))
+        ctx.return_state = return_state
+        ctx.empty = x.numel() == 0 or a_raw.numel() == 0
+        if ctx.empty:
+            bt, t_len, d = x.shape
+            y = x.new_zeros((bt, t_len, d))
+            h_last = x.new_zeros((bt, d, a_raw.shape[1]))
+            ctx.save_for_backward(x, dt_raw, a_raw, b_in, c_in)
+        else:
+            need_grad = any(ctx.needs_input_grad[:5])
+            y, ckpt, h_last = torch.ops.mamba_hip.scan_gated_fwd(
+                x, dt_raw, a_raw, b_in, c_in, ctx.gate[0], ctx.gate[1], chunk, need_grad)
+            ctx.save_for_backward(x, dt_raw, a_raw, b_in, c_in, ckpt)
+        if return_state:
+            return y, h_last
+        return y
+
+    @staticmethod
+    def backward(ctx, *grads):
+        dy = grads[0]
+        dh_last = grads[1] if ctx.return_state and len(grads) > 1 else None
+        if ctx.empty:
+            x, dt_raw, a_raw, b_in, c_in = ctx.saved_tensors
+            return (torch.zeros_like(x), torch.zeros_like(dt_raw), torch.zeros_like(a_raw),
+                    torch.zeros_like(b_in), torch.zeros_like(c_in), None, None, None, None)
+        x, dt_raw, a_raw, b_in, c_in, ckpt = ctx.saved_tensors
+        if dy is None:
+            dy = torch.zeros_like(x)
+        dy = dy.contiguous()
+        if dh_last is not None:
+            dh_last = dh_last.contiguous()
+        dx, ddt, da, db, dc = torch.ops.mamba_hip.scan_gated_bwd(
+            x, dt_raw, a_raw, b_in, c_in, ctx.gate[0], ctx.gate[1], dy, dh_last, ckpt, ctx.chunk)
+        return dx, ddt, da, db, dc, None, None, None, None
+
+
+def selective_scan_gated(x: torch.Tensor, dt_raw: torch.Tensor, a_raw: torch.Tensor,
+                         b_in: torch.Tensor, c_in: torch.Tensor, dt_min: float, dt_max: float,
+                         chunk: int = SSM_CHUNK, return_state: bool = False):
+    """``selective_scan(x, dt_min + (dt_max - dt_min) * sigmoid(dt_raw), softplus(a_raw),
+    B, C)`` in the fused gfx950 kernels (the reference's MambaBlock._proj +
+    _scan, mamba_metal/model.py:197-200, :213-215). Inputs on one ROCm device,
+    fp32; needs dt_min < dt_max."""
+    if not (float(dt_min) < float(dt_max)):
+        raise ValueError(f"need dt_min < dt_max; got {dt_min}, {dt_max}")
+    return SelectiveScanGatedHIP.apply(x, dt_raw, a_raw, b_in, c_in, dt_min, dt_max, chunk,
+                                       return_state)
+
+
+class OutGateHIP(torch.autograd.Function):
+    """out_gate(y, d_skip, z) forward and backward on the HIP kernels."""
+
+    @staticmethod
+    def forward(ctx, y, d_skip, z):
+        y = y.contiguous()
+        d_skip = d_skip.contiguous()
+        try:
+            _native._conv_rows(z)
+        except _native.HipScanError:
+            z = z.contiguous()
+        ctx.empty = y.numel() == 0
+        ctx.save_for_backward(y, d_skip, z)
+        if ctx.empty:
+            return y.new_zeros(y.shape)
+        return torch.ops.mamba_hip.out_gate_fwd(y, d_skip, z)
+
+    @staticmethod
+    def backward(ctx, dout):
+        y, d_skip, z = ctx.saved_tensors
+        if ctx.empty:
+            return torch.zeros_like(y), torch.zeros_like(d_skip), torch.zeros_like(z)
+        dy, dd, dz = torch.ops.mamba_hip.out_gate_bwd(y, d_skip, z, dout.contiguous())
+        return dy, dd, dz
+
+
+def out_gate(y: torch.Tensor, d_skip: torch.Tensor, z: torch.Tensor) -> torch.Tensor:
+    """``(y + d_skip) * silu(z)`` (mamba_metal/model.py:255-256) for y, z
+    (B, T, d_inner) and d_skip (d_inner), fp32 on one ROCm device; z's rows may
+    be strided (the z half of the in_proj output). Returns a contiguous tensor."""
+    tensors = (y, d_skip, z)
+    if not all(_hip_device(t) for t in tensors):
+        raise RuntimeError("out_gate needs every input on the ROCm device; saw devices "
+                           + ", ".join(str(t.device) for t in tensors))
+    if not all(t.dtype == torch.float32 for t in tensors):
+        raise RuntimeError("out_gate is fp32-only; got " + ", ".join(str(t.dtype) for t in tensors))
+    if y.dim() != 3 or z.shape != y.shape or d_skip.shape != (y.shape[2],):
+        raise ValueError(f"bad shapes: y {tuple(y.shape)}, d_skip {tuple(d_skip.shape)}, "
+                         f"z {tuple(z.shape)}")
+    return OutGateHIP.apply(y, d_skip, z)

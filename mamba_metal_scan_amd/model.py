@@ -31,6 +31,7 @@ import torch.nn as nn
 import torch.nn.functional as F
 
 from .conv import conv1d_silu
+from .fused import out_gate, selective_scan_gated
 from .scan import SSM_CHUNK, _hip_device, selective_scan, selective_state_step
 
 
@@ -182,8 +183,21 @@ class MambaBlock(nn.Module):
         dt = self.dt_min + (self.dt_max - self.dt_min) * gate
         return dt, self.B_proj(x), self.C_proj(x), F.softplus(self.A)
 
+    def _fused(self, t) -> bool:
+        """True where the block runs its fused HIP ops: fp32 ROCm tensors and a
+        scan_impl other than 'torch'."""
+        return self.scan_impl != "torch" and _hip_device(t) and t.dtype == torch.float32
+
     def _scan(self, x, return_state=False):
-        """y_t = sum_n C_tn h_tn over the selective recurrence (+ final state)."""
+        """y_t = sum_n C_tn h_tn over the selective recurrence (+ final state).
+
+        On a ROCm device the dt gate and softplus(A) of _proj run inside the
+        scan kernels (selective_scan_gated): the same function as _proj followed
+        by selective_scan (mamba_metal/model.py:197-200, :213-215)."""
+        if self._fused(x):
+            return selective_scan_gated(x, self.dt_proj(x), self.A, self.B_proj(x),
+                                        self.C_proj(x), self.dt_min, self.dt_max,
+                                        chunk=self.ckpt_chunk, return_state=return_state)
         dt, b_t, c_t, aneg = self._proj(x)
         r = selective_scan(x, dt, aneg, b_t, c_t, impl=self.scan_impl,
                            chunk=self.ckpt_chunk, return_state=return_state)
@@ -223,7 +237,7 @@ class MambaBlock(nn.Module):
         On a ROCm device (scan_impl other than 'torch') this is the fused HIP
         kernel, reading x in place; elsewhere the framework's Conv1d on the
         transposed view, as the reference does (model.py:244)."""
-        if self.scan_impl != "torch" and _hip_device(x) and x.dtype == torch.float32:
+        if self._fused(x):
             return conv1d_silu(x, self.conv.weight, self.conv.bias)
         xt = x.transpose(1, 2)                                           # (B, d_inner, T)
         return F.silu(self.conv(xt)[:, :, :xt.shape[2]]).transpose(1, 2)
@@ -245,6 +259,8 @@ class MambaBlock(nn.Module):
             y, h_last = self._scan(x, return_state=True)
             if cache is not None:
                 cache["h"] = h_last
+        if self._fused(y):
+            return residual + self.out_proj(out_gate(y, self.D_skip, z))
         y = y + self.D_skip
         return residual + self.out_proj(y * F.silu(z))
 

@@ -129,3 +129,33 @@ def test_step_argument_errors():
     assert rc == MHS_EINVAL and "null" in _err(lib)
     rc = lib.mhs_scan_step_f32(*([A16] * 6), MIS, 2, 32, 16, None)
     assert rc == MHS_EINVAL and "aligned" in _err(lib)
+
+
+def test_gated_scan_argument_errors():
+    lib = _native.library()
+    sizes = (2, 8, 32, 16, 16)
+    rc = lib.mhs_scan_gated_fwd_f32(*([A16] * 5), 0.1, 0.1, *([A16] * 3), *sizes, None)
+    assert rc == MHS_EINVAL and "dt_min < dt_max" in _err(lib)
+    rc = lib.mhs_scan_gated_fwd_f32(*([A16] * 5), 0.001, float("nan"), *([A16] * 3), *sizes, None)
+    assert rc == MHS_EINVAL and "dt_min < dt_max" in _err(lib)
+    rc = lib.mhs_scan_gated_fwd_f32(*([A16] * 5), 0.001, 0.1, *([A16] * 3), 2, 8, 32, 65, 16, None)
+    assert rc == MHS_EINVAL and "d_state" in _err(lib)
+    need = lib.mhs_scan_bwd_workspace_bytes(*sizes)
+    rc = lib.mhs_scan_gated_bwd_f32(*([A16] * 5), 0.001, 0.1, *([A16] * 8), A16, need - 4,
+                                    *sizes, None)
+    assert rc == MHS_EINVAL and "workspace too small" in _err(lib)
+    rc = lib.mhs_scan_gated_bwd_f32(*([A16] * 5), 1.0, 0.5, *([A16] * 8), A16, need, *sizes, None)
+    assert rc == MHS_EINVAL and "dt_min < dt_max" in _err(lib)
+
+
+def test_out_gate_argument_errors():
+    lib = _native.library()
+    assert lib.mhs_out_gate_bwd_workspace_bytes(16, 512, 1432) == 8 * 16 * 1432 * 4
+    rc = lib.mhs_out_gate_fwd_f32(A16, A16, A16, 31, A16, 2, 8, 32, None)
+    assert rc == MHS_EINVAL and "row stride" in _err(lib)
+    rc = lib.mhs_out_gate_fwd_f32(A16, None, A16, 64, A16, 2, 8, 32, None)
+    assert rc == MHS_EINVAL and "null" in _err(lib)
+    need = lib.mhs_out_gate_bwd_workspace_bytes(2, 8, 32)
+    rc = lib.mhs_out_gate_bwd_f32(A16, A16, A16, 64, A16, A16, A16, A16, A16, need - 4, 2, 8, 32,
+                                  None)
+    assert rc == MHS_EINVAL and "workspace too small" in _err(lib)

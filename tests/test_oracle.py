@@ -319,3 +319,115 @@ def test_conv_vjp_dot_product():
            - oracle.conv_fwd(*[a - eps * u for a, u in zip(arrs, v)])) / (2 * eps) * dout).sum()
     vjp = sum(float((g * u).sum()) for g, u in zip(oracle.conv_bwd(*arrs, dout), v))
     assert abs(jv - vjp) <= 1e-7 * max(1.0, abs(vjp))
+
+
+# ------------------------------- dt gate + softplus(A) (oracle.scan_gated_*)
+
+LO, HI = 0.001, 0.1   # the reference's MambaConfig dt_min, dt_max (model.py:53-54)
+
+
+def _gated_inputs(bt, t_len, d, n, seed):
+    rng = np.random.default_rng(seed)
+    return [rng.standard_normal((bt, t_len, d)), rng.standard_normal((bt, t_len, d)),
+            np.tile(np.arange(1.0, n + 1), (d, 1)) + 0.3 * rng.standard_normal((d, n)),
+            rng.standard_normal((bt, t_len, n)), rng.standard_normal((bt, t_len, n))]
+
+
+def _gated_fd(grads, arrs, dy, eps=1e-6, per=8, seed=0):
+    rng = np.random.default_rng(seed)
+    worst = 0.0
+    for i, (g, a) in enumerate(zip(grads, arrs)):
+        flat = a.reshape(-1)
+        for j in rng.permutation(flat.size)[:per]:
+            p, m = [t.copy() for t in arrs], [t.copy() for t in arrs]
+            p[i].reshape(-1)[j] += eps
+            m[i].reshape(-1)[j] -= eps
+            fd = ((oracle.scan_gated_fwd(*p, LO, HI)[0] - oracle.scan_gated_fwd(*m, LO, HI)[0])
+                  * dy).sum() / (2 * eps)
+            worst = max(worst, abs(g.reshape(-1)[j] - fd) / max(np.abs(g).max(), 1e-12))
+    return worst
+
+
+def test_gate_and_softplus_closed_forms():
+    np.testing.assert_allclose(oracle.gate_dt(np.array([0.0]), LO, HI), [(LO + HI) / 2], rtol=1e-15)
+    np.testing.assert_allclose(oracle.gate_dt(np.array([-800.0, 800.0]), LO, HI), [LO, HI],
+                               rtol=1e-15)
+    np.testing.assert_allclose(oracle.softplus(np.array([0.0])), [np.log(2.0)], rtol=1e-15)
+    # Large a: softplus(a) = a + log1p(e^-a); very negative a: e^a (no underflow to 0).
+    np.testing.assert_allclose(oracle.softplus(np.array([40.0, -40.0])),
+                               [40.0 + np.exp(-40.0), np.exp(-40.0)], rtol=1e-12)
+
+
+@pytest.mark.parametrize("shape", [(1, 9, 3, 4), (2, 14, 2, 5)])
+def test_gated_gradients_match_finite_differences(shape):
+    arrs = _gated_inputs(*shape, seed=41)
+    dy = np.random.default_rng(42).standard_normal(arrs[0].shape)
+    grads = list(oracle.scan_gated_bwd(*arrs, LO, HI, dy))
+    assert _gated_fd(grads, arrs, dy) < 1e-6
+    # Planted mistakes: the gate's span factor dropped; sigmoid'(raw) taken as
+    # sigmoid(raw); softplus' taken as 1 (dA = dAneg).
+    raw = arrs[1]
+    s = 1.0 / (1.0 + np.exp(-raw))
+    assert _gated_fd([grads[0], grads[1] / (HI - LO)] + grads[2:], arrs, dy) > 1e-2
+    assert _gated_fd([grads[0], grads[1] / (1.0 - s)] + grads[2:], arrs, dy) > 1e-2
+    daneg = oracle.scan_bwd(arrs[0], oracle.gate_dt(raw, LO, HI), oracle.softplus(arrs[2]),
+                            arrs[3], arrs[4], dy)[2]
+    assert _gated_fd(grads[:2] + [daneg] + grads[3:], arrs, dy) > 1e-2
+
+
+def test_gated_gradients_match_torch_autograd():
+    """The chain rule through the gate and softplus against torch's float64
+    autograd of the same expressions (dt and Aneg enter the scan as leaves)."""
+    import torch
+    arrs = _gated_inputs(2, 11, 3, 4, seed=43)
+    dy = np.random.default_rng(44).standard_normal(arrs[0].shape)
+    raw = torch.tensor(arrs[1], requires_grad=True)
+    a = torch.tensor(arrs[2], requires_grad=True)
+    dt = LO + (HI - LO) * torch.sigmoid(raw)
+    aneg = torch.nn.functional.softplus(a)
+    _, ddt, daneg, _, _ = oracle.scan_bwd(arrs[0], dt.detach().numpy(), aneg.detach().numpy(),
+                                          arrs[3], arrs[4], dy)
+    torch.autograd.backward([dt, aneg], [torch.tensor(ddt), torch.tensor(daneg)])
+    got = oracle.scan_gated_bwd(*arrs, LO, HI, dy)
+    np.testing.assert_allclose(got[1], raw.grad.numpy(), rtol=1e-12, atol=1e-300)
+    np.testing.assert_allclose(got[2], a.grad.numpy(), rtol=1e-12, atol=1e-300)
+
+
+# ---------------------------------- output gate (oracle.out_gate_*)
+
+def test_out_gate_closed_forms():
+    rng = np.random.default_rng(45)
+    y, d = rng.standard_normal((2, 5, 3)), rng.standard_normal(3)
+    assert np.all(oracle.out_gate_fwd(y, d, np.zeros_like(y)) == 0.0)
+    # silu(z) -> z for large z: out = (y + D) * z
+    z = np.full_like(y, 60.0)
+    np.testing.assert_allclose(oracle.out_gate_fwd(y, d, z), (y + d) * 60.0, rtol=1e-14)
+    # silu(1) = 1 / (1 + e^-1)
+    np.testing.assert_allclose(oracle.out_gate_fwd(np.ones((1, 1, 1)), np.zeros(1),
+                                                   np.ones((1, 1, 1))), [[[1 / (1 + np.exp(-1))]]])
+
+
+def test_out_gate_gradients_match_finite_differences():
+    rng = np.random.default_rng(46)
+    arrs = [rng.standard_normal((2, 7, 3)), rng.standard_normal(3), rng.standard_normal((2, 7, 3))]
+    dout = rng.standard_normal((2, 7, 3))
+    dy, dd, dz = oracle.out_gate_bwd(*arrs, dout)
+
+    def fd_check(grads):
+        worst, eps = 0.0, 1e-6
+        for i, g in enumerate(grads):
+            for j in range(arrs[i].size):
+                p, m = [t.copy() for t in arrs], [t.copy() for t in arrs]
+                p[i].reshape(-1)[j] += eps
+                m[i].reshape(-1)[j] -= eps
+                fd = ((oracle.out_gate_fwd(*p) - oracle.out_gate_fwd(*m)) * dout).sum() / (2 * eps)
+                worst = max(worst, abs(g.reshape(-1)[j] - fd) / max(np.abs(g).max(), 1e-12))
+        return worst
+
+    assert fd_check([dy, dd, dz]) < 1e-7
+    # Planted mistakes: silu' without its z * (1 - s) term; dD_skip not summed
+    # over time (last step only).
+    y, dsk, z = arrs
+    s = 1.0 / (1.0 + np.exp(-z))
+    assert fd_check([dy, dd, dout * (y + dsk) * s]) > 1e-2
+    assert fd_check([dy, dy[:, -1].sum(0), dz]) > 1e-2
