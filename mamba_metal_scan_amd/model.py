@@ -8,9 +8,12 @@ plain torch; the selective scan is the only custom kernel:
   ("metal" = "hip"). "auto" uses the gfx950 scan for ROCm tensors and the
   associative ``parallel_scan`` on CPU.
 * ``MambaBlock`` (model.py:161-256): RMSNorm -> in_proj -> (x, z); causal
-  depthwise conv + SiLU (on a ROCm device the fused ``conv1d_silu`` kernel); dt = dt_min + (dt_max-dt_min)*sigmoid(dt_proj(x));
+  depthwise conv + SiLU; dt = dt_min + (dt_max-dt_min)*sigmoid(dt_proj(x));
   Aneg = softplus(A); the scan; + D_skip (a per-channel bias); * silu(z);
-  out_proj; residual.
+  out_proj; residual. On a ROCm device the conv + SiLU is the fused
+  ``conv1d_silu`` kernel, the dt gate and softplus(A) run inside the scan
+  kernels (``selective_scan_gated``) and ``(y + D_skip) * silu(z)`` is the
+  fused ``out_gate`` kernel.
 * ``TinyMamba`` (model.py:259-302): embedding, blocks, final RMSNorm, head tied
   to the embedding, cross entropy.
 * Recurrent cache: a prefill stores each block's conv tail and final state;
@@ -85,6 +88,11 @@ def d_inner_for_budget(target: int, d_model: int, d_state: int, d_conv: int) -> 
 
 
 class RMSNorm(nn.Module):
+    """weight * x * rsqrt(mean(x^2) + eps) over the last dim, in fp32
+    (mamba_metal/model.py:85-95). Computed by the framework's fused rms_norm
+    (one kernel per direction on the device instead of five elementwise and
+    reduction passes); same parameter name and function as the reference's."""
+
     def __init__(self, d: int, eps: float = 1e-6):
         super().__init__()
         self.weight = nn.Parameter(torch.ones(d))
@@ -92,8 +100,7 @@ class RMSNorm(nn.Module):
 
     def forward(self, x):
         xf = x.float()
-        inv = torch.rsqrt(xf.pow(2).mean(dim=-1, keepdim=True) + self.eps)
-        return (self.weight * (xf * inv)).to(x.dtype)
+        return F.rms_norm(xf, (xf.shape[-1],), self.weight, self.eps).to(x.dtype)
 
 
 # ------------------------------------------------------------ CPU-side scans
