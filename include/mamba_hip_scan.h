@@ -66,6 +66,17 @@ int64_t mhs_preferred_chunk(int64_t d_state);
  * a channel in one thread, scan.py:67-69). */
 int mhs_set_variant(int states_per_lane);
 
+/* Tuning knob, process-wide: the number of time segments mhs_scan_bwd_f32
+ * (and the gated backward) split the sequence into (1..8; 0 restores the
+ * automatic choice: one segment while the grid has at least two blocks of 32
+ * channels per compute unit, otherwise enough segments of at least 128 steps
+ * for about three). Segments run in parallel after a short pass that carries
+ * the adjoint across segment boundaries; results equal the unsegmented
+ * backward up to rounding. mhs_scan_bwd_workspace_bytes depends on it. No
+ * counterpart in the reference (its backward walks each channel's whole
+ * sequence in one thread, scan.py:132-261). */
+int mhs_set_time_segments(int segments);
+
 /*
  * Forward scan. Replaces the reference's `lib.ssm_fwd(x, dt, Aneg, Bm, Cm, y,
  * ckpt, Bt, T, D, Kc)` launch (mamba_metal/scan.py:78-127, launched at :377-378).

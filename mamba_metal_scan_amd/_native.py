@@ -27,7 +27,7 @@ EXPORTED_SYMBOLS = (
     "mhs_scan_bwd_f32", "mhs_scan_step_f32", "mhs_conv1d_silu_fwd_f32",
     "mhs_conv1d_silu_bwd_workspace_bytes", "mhs_conv1d_silu_bwd_f32",
     "mhs_scan_gated_fwd_f32", "mhs_scan_gated_bwd_f32", "mhs_out_gate_fwd_f32",
-    "mhs_out_gate_bwd_workspace_bytes", "mhs_out_gate_bwd_f32",
+    "mhs_out_gate_bwd_workspace_bytes", "mhs_out_gate_bwd_f32", "mhs_set_time_segments",
 )
 
 _lib: Optional[ctypes.CDLL] = None
@@ -64,6 +64,8 @@ def library() -> ctypes.CDLL:
             lib.mhs_preferred_chunk.argtypes = [_I64]
             lib.mhs_set_variant.restype = ctypes.c_int
             lib.mhs_set_variant.argtypes = [ctypes.c_int]
+            lib.mhs_set_time_segments.restype = ctypes.c_int
+            lib.mhs_set_time_segments.argtypes = [ctypes.c_int]
             lib.mhs_scan_fwd_f32.restype = ctypes.c_int
             lib.mhs_scan_fwd_f32.argtypes = [_P] * 8 + [_I64] * 5 + [_P]
             lib.mhs_scan_bwd_workspace_bytes.restype = ctypes.c_size_t
@@ -121,6 +123,11 @@ def preferred_chunk(d_state: int) -> int:
 def set_variant(states_per_lane: int) -> None:
     """Force 2 or 4 states per lane (0 = automatic), process-wide."""
     _check(library().mhs_set_variant(int(states_per_lane)), "mhs_set_variant")
+
+
+def set_time_segments(segments: int) -> None:
+    """Force the backward's number of time segments (1..8; 0 = automatic), process-wide."""
+    _check(library().mhs_set_time_segments(int(segments)), "mhs_set_time_segments")
 
 
 # --------------------------------------------------------------- custom ops

@@ -73,6 +73,18 @@ struct BwdArgs {
   // (dt = dt_lo + dt_span * sigmoid(raw), Aneg = softplus(A); mamba_metal/
   // model.py:197, :200), and ddt receives the gradient of the raw input.
   float dt_lo, dt_span, dt_inv_span;
+  // Time segments (the chunk-parallel-over-time variant): the chunks split
+  // into nseg segments of cps chunks, one block per (channel block, batch
+  // row, segment), blockIdx.y = seg * batch + b. With nseg > 1:
+  //   carryL   (nseg, batch, D, N): slot s >= 1 holds L_s = dA_a * G_a of
+  //            segment s walked from a zero adjoint (a = its first step);
+  //   carrySdt (nseg, batch, D):    slot s >= 1 holds sum dt over segment s.
+  // The adjoint entering segment s from the later ones is then
+  //   K_{nseg-1} = dh_last (or 0),  K_{s-1} = L_s + exp(-Aneg * Sdt_s) * K_s,
+  // which each block of the gradient pass folds from the slots it needs.
+  int nseg, cps;
+  float* carryL;
+  float* carrySdt;
 };
 
 // One staging buffer (the kernel keeps two) and the single-buffered rest.
@@ -89,7 +101,11 @@ __host__ __device__ constexpr int bwd_lds_floats(int G, int NPL) {
 // GATED: see BwdArgs. The staging threads gate each dt once per block as they
 // move it to LDS; finalize turns ddt into the raw input's gradient
 // ddt * span * s * (1 - s), s = sigmoid(raw) = (dt - lo) / span.
-template <int NPL, int G, int MINW, bool GATED>
+// CARRY: the adjoint-carry pass of the time segments (see BwdArgs): blocks of
+// segments 1..nseg-1 walk their segment backwards carrying only the adjoint
+// (dA and G, no state, no gradients, no x or B traffic) and write L_s and
+// the segment's sum of dt.
+template <int NPL, int G, int MINW, bool GATED, bool CARRY>
 __global__ void __launch_bounds__(64 * G, MINW)
 bwd_kernel(BwdArgs a) {
   constexpr int NT = 64 * G;
@@ -112,13 +128,16 @@ bwd_kernel(BwdArgs a) {
   const int c = lane & 31;
   const int q = wave * 2 + hh;
   const int n0 = q * NPL;
-  const int b = blockIdx.y;
+  const int b = blockIdx.y % a.batch;
+  const int seg = blockIdx.y / a.batch + (CARRY ? 1 : 0);
   const int d0 = blockIdx.x * kCH;
   const int d = d0 + c;
   const bool act = d < a.D;
   const int T = a.T, D = a.D, K = a.K;
   const int nvalid = N - n0;
   const int nch = a.nchunk;
+  const int c_lo = seg * a.cps;                      // this block's chunks [c_lo, c_hi)
+  const int c_hi = min(c_lo + a.cps, nch);
 
   float* tS = lds + 2 * BUF;                          // [G][64][16]
   float* tDBC = tS + G * 64 * kSteps;                 // [2][16][NP]
@@ -143,9 +162,23 @@ bwd_kernel(BwdArgs a) {
     a2[j] = -an[j] * kLog2e;
     acc[j] = 0.f;
     dan[j] = 1.f;
+    g[j] = 0.f;
   }
-  const float* dhl = a.dh_last != nullptr ? a.dh_last + (size_t)b * slice : a.aneg;
-  load_states<NPL>(g, GBuf(dhl, a.dh_last != nullptr ? slice_bytes : 0u), st_lane, nvalid);
+  if constexpr (!CARRY) {
+    // The adjoint entering this segment: dh_last for the last one, folded
+    // with the carries of the later segments for the others.
+    const float* dhl = a.dh_last != nullptr ? a.dh_last + (size_t)b * slice : a.aneg;
+    load_states<NPL>(g, GBuf(dhl, a.dh_last != nullptr ? slice_bytes : 0u), st_lane, nvalid);
+    for (int s2 = a.nseg - 1; s2 > seg; --s2) {
+      float lv[NPL];
+      const size_t slot = (size_t)s2 * a.batch + b;
+      load_states<NPL>(lv, GBuf(a.carryL + slot * slice, slice_bytes), st_lane, nvalid);
+      const float sdt = act ? a.carrySdt[slot * D + d] : 0.f;
+#pragma unroll
+      for (int j = 0; j < NPL; ++j) g[j] = __builtin_fmaf(exp2_hw(sdt * a2[j]), g[j], lv[j]);
+    }
+  }
+  float sdt_acc = 0.f;   // CARRY: sum of dt over the segment
 
   const size_t row0 = (size_t)b * T;
   const QuadLoader<kCH, PER> ql(tid, NT, D, d0);
@@ -153,9 +186,12 @@ bwd_kernel(BwdArgs a) {
   float4 px[PER], pd[PER], py[PER];
   float pb[PERS], pc[PERS], ph[NPL];
 
-  // Chunk ci (any integer): first step and length (0 outside the sequence).
+  // Chunk ci (any integer): first step and length (0 outside this block's
+  // segment, so that every load and store of a chunk outside it is empty).
   auto chunk_t0 = [&](int ci) { return min(max(ci, 0) * K, T - 1); };
-  auto chunk_len = [&](int ci) { return ci < 0 ? 0 : max(0, min(K, T - ci * K)); };
+  auto chunk_len = [&](int ci) {
+    return (ci < c_lo || ci >= c_hi) ? 0 : max(0, min(K, T - ci * K));
+  };
   // Resource over one chunk of a (batch, T, D) tensor from channel d0 on.
   auto chunk_buf = [&](const float* base, int ci) {
     const int len = chunk_len(ci);
@@ -165,10 +201,10 @@ bwd_kernel(BwdArgs a) {
     const int len = chunk_len(ci);
     const GBuf gs_b(a.B + (row0 + chunk_t0(ci)) * N, 4u * (unsigned)(len * N));
     const GBuf gs_c(a.C + (row0 + chunk_t0(ci)) * N, 4u * (unsigned)(len * N));
-    ql.load(px, chunk_buf(a.x, ci), D);
+    if constexpr (!CARRY) ql.load(px, chunk_buf(a.x, ci), D);
     ql.load(pd, chunk_buf(a.dt, ci), D);
     ql.load(py, chunk_buf(a.dy, ci), D);
-    rl.load(pb, gs_b);
+    if constexpr (!CARRY) rl.load(pb, gs_b);
     rl.load(pc, gs_c);
   };
   // h at the start of chunk ci: checkpoint ci-1, or 0 for the first chunk.
@@ -181,8 +217,8 @@ bwd_kernel(BwdArgs a) {
     if constexpr (GATED) ql.gate(pd, chunk_len(ci), a.dt_lo, a.dt_span);
     ql.store_cm(s0, pd);
     ql.store_cm(s0 + oDY, py);
-    ql.store_cm(s0 + oX, px);
-    rl.store(s0 + oB, pb);
+    if constexpr (!CARRY) ql.store_cm(s0 + oX, px);
+    if constexpr (!CARRY) rl.store(s0 + oB, pb);
     rl.store(s0 + oC, pc);
   };
   // dx, ddt and the dB, dC block sums of chunk ci, staged in buffer j: from
@@ -235,23 +271,51 @@ bwd_kernel(BwdArgs a) {
     }
   };
 
-  // Prologue: the last chunk staged in LDS buffer 0, the one before it in
-  // the staging registers.
-  load_sub(nch - 1);
-  load_h0(nch - 1);
-  store_sub(0, nch - 1);
+  // Prologue: the segment's last chunk staged in LDS buffer 0, the one
+  // before it in the staging registers.
   float hc[NPL];                          // h at the start of the current chunk
+  load_sub(c_hi - 1);
+  if constexpr (!CARRY) load_h0(c_hi - 1);
+  store_sub(0, c_hi - 1);
+  if constexpr (!CARRY) {
 #pragma unroll
-  for (int j = 0; j < NPL; ++j) hc[j] = ph[j];
-  load_sub(nch - 2);
-  load_h0(nch - 2);
+    for (int j = 0; j < NPL; ++j) hc[j] = ph[j];
+  }
+  load_sub(c_hi - 2);
+  if constexpr (!CARRY) load_h0(c_hi - 2);
   __syncthreads();
 
-  for (int i = 0; i < nch; ++i) {
-    const int ci = nch - 1 - i;
+  const int nit = c_hi - c_lo;
+  for (int i = 0; i < nit; ++i) {
+    const int ci = c_hi - 1 - i;
     const float* s0 = lds + (i & 1) * BUF;
     const float* gB = s0 + oB + q * kSteps * NPL;
     const float* gC = s0 + oC + q * kSteps * NPL;
+
+    if constexpr (CARRY) {
+      // The adjoint alone: G_t = dy_t C_t + dA_{t+1} G_{t+1}, dA formed on
+      // the way (no state needed).
+#pragma unroll
+      for (int m = kQuads - 1; m >= 0; --m) {
+        float dts[4], dys[4], Cq[4][NPL];
+        f4_to(dts, lds4(s0 + cm_quad(c, m)));
+        f4_to(dys, lds4(s0 + oDY + cm_quad(c, m)));
+        load_quad_rows<NPL>(Cq, gC, m);
+#pragma unroll
+        for (int s = 3; s >= 0; --s) {
+          sdt_acc += dts[s];
+#pragma unroll
+          for (int j = 0; j < NPL; ++j) {
+            g[j] = __builtin_fmaf(dan[j], g[j], dys[s] * Cq[s][j]);
+            dan[j] = exp2_hw(dts[s] * a2[j]);
+          }
+        }
+        if (m == 2) store_sub((i + 1) & 1, ci - 1);
+        if (m == 1) load_sub(ci - 2);
+      }
+      __syncthreads();   // chunk ci-1 staged
+      continue;
+    }
 
     // ---- recompute phase, with the pipeline work of the neighbouring chunks
     float da[kSteps][NPL], hs[kSteps][NPL];
@@ -332,12 +396,22 @@ bwd_kernel(BwdArgs a) {
     load_h0(ci - 2);
     __syncthreads();   // tS / tDBC complete; chunk ci-1 staged
   }
-  finalize(0, (nch - 1) & 1);
+  const size_t slot = (size_t)seg * a.batch + b;
+  if constexpr (CARRY) {
+    // L_s = dA_a * G_a: dan holds dA of the segment's first step, g its adjoint.
+    float out[NPL];
+#pragma unroll
+    for (int j = 0; j < NPL; ++j) out[j] = dan[j] * g[j];
+    store_states<NPL>(GBuf(a.carryL + slot * slice, slice_bytes), st_lane, nvalid, out);
+    if (q == 0 && act) a.carrySdt[slot * D + d] = sdt_acc;
+    return;
+  }
+  finalize(c_lo, (nit - 1) & 1);
 
   float out[NPL];
 #pragma unroll
   for (int j = 0; j < NPL; ++j) out[j] = -acc[j];
-  store_states<NPL>(GBuf(a.wsA + (size_t)b * slice, slice_bytes), st_lane, nvalid, out);
+  store_states<NPL>(GBuf(a.wsA + slot * slice, slice_bytes), st_lane, nvalid, out);
 }
 
 // dB, dC: sum the per-block partials over the nblk channel blocks;

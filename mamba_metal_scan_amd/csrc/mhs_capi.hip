@@ -44,6 +44,31 @@ bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) ==
 
 // Forced states per lane (0 = automatic); see mhs_set_variant.
 std::atomic<int> g_npl_override{0};
+// Forced number of backward time segments (0 = automatic); see mhs_set_time_segments.
+std::atomic<int> g_seg_override{0};
+
+constexpr int kCUs = 256;        // MI355X compute units
+constexpr int kMaxSegments = 8;
+constexpr int kMinSegChunks = 8; // automatic split: at least 8 chunks per segment
+
+// Time segments of the backward for this shape (see BwdArgs in mhs_bwd.hpp).
+// Automatic: one segment while the grid has at least two blocks per CU;
+// below that, enough segments for about three blocks per CU, each at least
+// kMinSegChunks chunks long. Returns (segments, chunks per segment).
+void segments_for(int64_t batch, int64_t D, int nch, int& nseg, int& cps) {
+  const int64_t blocks = batch * ((D + mhs::kCH - 1) / mhs::kCH);
+  int want = g_seg_override.load(std::memory_order_relaxed);
+  if (want == 0) {
+    want = 1;
+    if (blocks < 2 * kCUs) {
+      want = (int)std::min<int64_t>(kMaxSegments, (3 * kCUs + blocks - 1) / blocks);
+      want = std::max(1, std::min(want, nch / kMinSegChunks));
+    }
+  }
+  want = std::max(1, std::min(want, nch));
+  cps = (nch + want - 1) / want;
+  nseg = (nch + cps - 1) / cps;    // no empty segment
+}
 
 using FwdFn = void (*)(mhs::FwdArgs);
 using BwdFn = void (*)(mhs::BwdArgs);
@@ -62,6 +87,8 @@ struct Plan {
   int fwd_lds = 0;  // bytes
   BwdFn bwd = nullptr;
   BwdFn bwd_g = nullptr;    // gated
+  BwdFn carry = nullptr;    // adjoint-carry pass of the time segments
+  BwdFn carry_g = nullptr;  // gated
   int bwd_ki = 0;   // largest chunk the backward walks directly
   int bwd_lds = 0;  // bytes
 };
@@ -77,8 +104,10 @@ void fill(Plan& p) {
   p.fwd_any = &mhs::fwd_kernel<NPL, G, MINW, false, false>;
   p.fwd_g = &mhs::fwd_kernel<NPL, G, MINW, true, true>;
   p.fwd_any_g = &mhs::fwd_kernel<NPL, G, MINW, false, true>;
-  p.bwd = &mhs::bwd_kernel<NPL, G, MINW, false>;
-  p.bwd_g = &mhs::bwd_kernel<NPL, G, MINW, true>;
+  p.bwd = &mhs::bwd_kernel<NPL, G, MINW, false, false>;
+  p.bwd_g = &mhs::bwd_kernel<NPL, G, MINW, true, false>;
+  p.carry = &mhs::bwd_kernel<NPL, G, MINW, false, true>;
+  p.carry_g = &mhs::bwd_kernel<NPL, G, MINW, true, true>;
   p.fwd_lds = mhs::fwd_lds_floats(G, NPL) * 4;
   p.bwd_lds = mhs::bwd_lds_floats(G, NPL) * 4;
 }
@@ -159,20 +188,29 @@ int check_shape(int64_t batch, int64_t seqlen, int64_t d_inner, int64_t d_state,
 size_t round_up(size_t n, size_t m) { return (n + m - 1) / m * m; }
 
 struct WsLayout {
-  size_t partB = 0, partC = 0, partA = 0, fine = 0, total = 0;  // offsets / bytes
+  size_t partB = 0, partC = 0, partA = 0, carryL = 0, carryS = 0, fine = 0, total = 0;
+  int nseg = 1, cps = 1;
 };
 
 WsLayout ws_layout(int64_t batch, int64_t T, int64_t D, int64_t N, int64_t chunk, int bwd_ki) {
   WsLayout w;
   const size_t nblk = (size_t)((D + mhs::kCH - 1) / mhs::kCH);
   const size_t S = (size_t)batch * T * N;
+  const int kb = (int)std::min<int64_t>(chunk, T) > bwd_ki ? bwd_ki : (int)std::min<int64_t>(chunk, T);
+  segments_for(batch, D, (int)((T + kb - 1) / kb), w.nseg, w.cps);
   size_t off = 0;
   w.partB = off;
   off += round_up(nblk * S * 4, 256);
   w.partC = off;
   off += round_up(nblk * S * 4, 256);
   w.partA = off;
-  off += round_up((size_t)batch * D * N * 4, 256);
+  off += round_up((size_t)w.nseg * batch * D * N * 4, 256);
+  if (w.nseg > 1) {
+    w.carryL = off;
+    off += round_up((size_t)w.nseg * batch * D * N * 4, 256);
+    w.carryS = off;
+    off += round_up((size_t)w.nseg * batch * D * 4, 256);
+  }
   w.fine = off;
   if (chunk > bwd_ki) off += round_up((size_t)batch * ((T + bwd_ki - 1) / bwd_ki) * D * N * 4, 256);
   w.total = off;
@@ -285,11 +323,25 @@ int scan_bwd(const float* x, const float* dt, const float* aneg, const float* B,
   a.dt_lo = g.lo;
   a.dt_span = g.span;
   a.dt_inv_span = g.on ? 1.f / g.span : 0.f;
+  a.nseg = w.nseg;
+  a.cps = w.cps;
+  a.carryL = w.nseg > 1 ? reinterpret_cast<float*>(ws + w.carryL) : nullptr;
+  a.carrySdt = w.nseg > 1 ? reinterpret_cast<float*>(ws + w.carryS) : nullptr;
+  const unsigned nblk = (unsigned)((D + ch - 1) / ch);
+  if (w.nseg > 1) {
+    // Adjoint carries of segments 1..nseg-1 (segment 0 passes nothing on).
+    const BwdFn cfn = g.on ? p.carry_g : p.carry;
+    rc = ensure_lds(reinterpret_cast<const void*>(cfn), p.bwd_lds);
+    if (rc) return rc;
+    hipLaunchKernelGGL(cfn, dim3(nblk, (unsigned)(batch * (w.nseg - 1))), dim3(64 * p.G),
+                       p.bwd_lds, s, a);
+    rc = check_launch("backward carry kernel");
+    if (rc) return rc;
+  }
   const BwdFn fn = g.on ? p.bwd_g : p.bwd;
   rc = ensure_lds(reinterpret_cast<const void*>(fn), p.bwd_lds);
   if (rc) return rc;
-  const dim3 grid((unsigned)((D + ch - 1) / ch), (unsigned)batch);
-  hipLaunchKernelGGL(fn, grid, dim3(64 * p.G), p.bwd_lds, s, a);
+  hipLaunchKernelGGL(fn, dim3(nblk, (unsigned)(batch * w.nseg)), dim3(64 * p.G), p.bwd_lds, s, a);
   rc = check_launch("backward scan kernel");
   if (rc) return rc;
 
@@ -298,7 +350,8 @@ int scan_bwd(const float* x, const float* dt, const float* aneg, const float* B,
   const long long total = S + A;
   const int blocks = (int)std::min<long long>((total + 255) / 256, 4096);
   hipLaunchKernelGGL(mhs::bwd_reduce_kernel, dim3(blocks), dim3(256), 0, s, a.wsB, a.wsC, a.wsA,
-                     g.on ? aneg : nullptr, dB, dC, daneg, (D + ch - 1) / ch, (int)batch, S, A);
+                     g.on ? aneg : nullptr, dB, dC, daneg, (D + ch - 1) / ch,
+                     (int)batch * w.nseg, S, A);
   return check_launch("backward reduction kernel");
 }
 
@@ -319,6 +372,14 @@ int mhs_set_variant(int npl) {
   if (npl != 0 && npl != 2 && npl != 4)
     return fail(MHS_EINVAL, "states per lane must be 0 (auto), 2 or 4; got %d", npl);
   g_npl_override.store(npl, std::memory_order_relaxed);
+  return MHS_OK;
+}
+
+int mhs_set_time_segments(int segments) {
+  if (segments < 0 || segments > kMaxSegments)
+    return fail(MHS_EINVAL, "time segments must be 0 (auto) .. %d; got %d", kMaxSegments,
+                segments);
+  g_seg_override.store(segments, std::memory_order_relaxed);
   return MHS_OK;
 }
 

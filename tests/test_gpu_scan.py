@@ -226,3 +226,58 @@ def test_empty_sequence():
     y, h = selective_scan_hip(x, x, aneg, b, b, return_state=True)
     assert y.shape == (2, 0, 8) and h.shape == (2, 8, 4)
     assert torch.count_nonzero(h) == 0
+
+
+# (B, T, D, N, chunk, segments): the chunk-parallel-over-time backward, forced
+# on small shapes (the automatic choice uses it only for grids under two
+# blocks per CU): segment counts above the chunk count, uneven last segments,
+# chunk strides off the 16-step window, the fine-checkpoint recompute path and
+# the state gradient entering the last segment.
+SEGMENT_CASES = [(2, 100, 64, 16, 16, 2), (1, 300, 96, 16, 16, 3), (2, 257, 40, 8, 7, 5),
+                 (1, 64, 64, 16, 16, 8), (3, 200, 130, 5, 64, 3), (1, 20, 32, 16, 16, 4),
+                 (2, 513, 64, 32, 16, 8)]
+
+
+@pytest.mark.parametrize("bt,t_len,d,n,chunk,segs", SEGMENT_CASES)
+def test_time_segments_match_the_oracle(bt, t_len, d, n, chunk, segs):
+    print(f"[case] time segments {segs}: {bt}x{t_len}x{d}x{n} chunk {chunk}", flush=True)
+    arrs = oracle.make_inputs(bt, t_len, d, n, seed=77 + d, style="bench")
+    rng = np.random.default_rng(78)
+    dy = rng.standard_normal((bt, t_len, d), dtype=np.float32)
+    dh = rng.standard_normal((bt, d, n), dtype=np.float32)
+    y_ref, _, h_ref = oracle.scan_fwd(*arrs)
+    g_ref = oracle.scan_bwd(*arrs, dy, dh_last=dh)
+    _native.set_time_segments(segs)
+    try:
+        y, h_last, grads = _run_hip(_to_dev(arrs), torch.from_numpy(dy).to(DEV), chunk=chunk,
+                                    dh_last=torch.from_numpy(dh).to(DEV))
+    finally:
+        _native.set_time_segments(0)
+    assert_close("y", y, y_ref)
+    assert_close("h_last", h_last, h_ref)
+    for name, g, r in zip(("dx", "ddt", "dAneg", "dB", "dC"), grads, g_ref):
+        assert_close(name, g, r)
+
+
+def test_time_segments_auto_split_at_the_long_sequence_shape():
+    """4 x 16384 x 2048 x 16 (256 blocks): the automatic split (3 segments)
+    against the single-segment backward on the same inputs."""
+    bt, t_len, d, n = 4, 16384, 2048, 16
+    print(f"[case] auto time segments {bt}x{t_len}x{d}x{n}", flush=True)
+    g = torch.Generator().manual_seed(5)
+    x = torch.randn(bt, t_len, d, generator=g).to(DEV)
+    dt = torch.nn.functional.softplus(torch.randn(bt, t_len, d, generator=g) - 4.0).to(DEV)
+    aneg = torch.arange(1, n + 1, dtype=torch.float32).repeat(d, 1).to(DEV)
+    b_in = torch.randn(bt, t_len, n, generator=g).to(DEV)
+    c_in = torch.randn(bt, t_len, n, generator=g).to(DEV)
+    dy = torch.randn(bt, t_len, d, generator=g).to(DEV)
+    _, ckpt, _ = torch.ops.mamba_hip.scan_fwd(x, dt, aneg, b_in, c_in, 16, True)
+    auto = torch.ops.mamba_hip.scan_bwd(x, dt, aneg, b_in, c_in, dy, None, ckpt, 16)
+    _native.set_time_segments(1)
+    try:
+        one = torch.ops.mamba_hip.scan_bwd(x, dt, aneg, b_in, c_in, dy, None, ckpt, 16)
+    finally:
+        _native.set_time_segments(0)
+    torch.cuda.synchronize()
+    for name, a_, b_ in zip(("dx", "ddt", "dAneg", "dB", "dC"), auto, one):
+        assert_close(name, a_, b_)

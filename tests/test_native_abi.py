@@ -159,3 +159,36 @@ def test_out_gate_argument_errors():
     rc = lib.mhs_out_gate_bwd_f32(A16, A16, A16, 64, A16, A16, A16, A16, A16, need - 4, 2, 8, 32,
                                   None)
     assert rc == MHS_EINVAL and "workspace too small" in _err(lib)
+
+
+def test_time_segments_knob_and_workspace():
+    """Automatic split: one segment at 16x512x1536x16 (768 blocks), three at
+    4x16384x2048x16 (256 blocks); forced splits add the per-segment dAneg
+    partials and the carries (L: segments x batch x D x N, sum dt: x batch x D)."""
+    lib = _native.library()
+    with pytest.raises(_native.HipScanError, match="time segments"):
+        _native.set_time_segments(9)
+    assert lib.mhs_set_time_segments(-1) == MHS_EINVAL
+
+    def ru(v):
+        return (v + 255) // 256 * 256
+
+    def expect(bt, t, d, n, segs):
+        nblk = (d + 31) // 32
+        s_ = bt * t * n
+        a = bt * d * n
+        base = 2 * ru(nblk * s_ * 4) + ru(segs * a * 4)
+        if segs > 1:
+            base += ru(segs * a * 4) + ru(segs * bt * d * 4)
+        return base
+
+    assert lib.mhs_scan_bwd_workspace_bytes(16, 512, 1536, 16, 16) == expect(16, 512, 1536, 16, 1)
+    assert lib.mhs_scan_bwd_workspace_bytes(4, 16384, 2048, 16, 16) == expect(4, 16384, 2048, 16, 3)
+    try:
+        _native.set_time_segments(3)
+        assert lib.mhs_scan_bwd_workspace_bytes(16, 512, 1536, 16, 16) == expect(16, 512, 1536, 16, 3)
+        # 5 chunks at most: 5 segments of one chunk
+        _native.set_time_segments(8)
+        assert lib.mhs_scan_bwd_workspace_bytes(1, 80, 64, 16, 16) == expect(1, 80, 64, 16, 5)
+    finally:
+        _native.set_time_segments(0)
