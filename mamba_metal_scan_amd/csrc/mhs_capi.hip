@@ -12,6 +12,7 @@
 #include <cstdio>
 #include <cstring>
 #include <mutex>
+#include <numeric>
 
 #include "mamba_hip_scan.h"
 #include "mhs_bwd.hpp"
@@ -235,14 +236,22 @@ int check_gate(float dt_min, float dt_max, Gate& g) {
   return MHS_OK;
 }
 
-int launch_fwd(const Plan& p, mhs::FwdArgs a, int batch, hipStream_t s, const Gate& g) {
+// One block per (channel block, batch row, time segment); a.seg_len and
+// a.h_init describe the segments (see FwdArgs), nseg = 1 for the whole sequence.
+int launch_fwd(const Plan& p, mhs::FwdArgs a, int batch, hipStream_t s, const Gate& g,
+               int nseg = 1) {
   const bool aligned = a.K % mhs::kSteps == 0 || a.K >= a.T;
   const FwdFn fn = aligned ? (g.on ? p.fwd_g : p.fwd) : (g.on ? p.fwd_any_g : p.fwd_any);
   a.dt_lo = g.lo;
   a.dt_span = g.span;
+  a.batch = batch;
+  if (nseg == 1) {
+    a.seg_len = a.T;
+    a.h_init = nullptr;
+  }
   int rc = ensure_lds(reinterpret_cast<const void*>(fn), p.fwd_lds);
   if (rc) return rc;
-  const dim3 grid((unsigned)((a.D + mhs::kCH - 1) / mhs::kCH), (unsigned)batch);
+  const dim3 grid((unsigned)((a.D + mhs::kCH - 1) / mhs::kCH), (unsigned)(batch * nseg));
   hipLaunchKernelGGL(fn, grid, dim3(64 * p.G), p.fwd_lds, s, a);
   return check_launch("forward scan kernel");
 }
@@ -305,7 +314,17 @@ int scan_bwd(const float* x, const float* dt, const float* aneg, const float* B,
     f.h_last = nullptr;
     f.T = T; f.D = D; f.N = N; f.K = p.bwd_ki;
     f.nchunk = (int)mhs_num_chunks(T, p.bwd_ki);
-    rc = launch_fwd(p, f, (int)batch, s, g);
+    // Time segments that start on the caller's checkpoints (stride K): each
+    // is a multiple of lcm(16, K) steps and starts from the exact state, so
+    // they run in parallel where the grid alone would leave CUs idle.
+    const int64_t unit = std::lcm<int64_t>(mhs::kSteps, K);
+    int nseg = 1, ups = 1;
+    segments_for(batch, D, (int)((T + unit - 1) / unit), nseg, ups);
+    f.seg_len = (int)std::min<int64_t>((int64_t)ups * unit, T);
+    f.h_init = ckpt;
+    f.init_K = K;
+    f.init_nchunk = (int)mhs_num_chunks(T, K);
+    rc = launch_fwd(p, f, (int)batch, s, g, nseg);
     if (rc) return rc;
     ck = f.ckpt;
     Kb = p.bwd_ki;

@@ -46,6 +46,15 @@ struct FwdArgs {
   // dt = dt_lo + dt_span * sigmoid(raw) and Aneg = softplus(A) are formed in
   // the kernel (mamba_metal/model.py:197, :200).
   float dt_lo, dt_span;
+  // Time segments: blockIdx.y = seg * batch + b; segment seg covers steps
+  // [seg * seg_len, min(T, (seg + 1) * seg_len)), seg_len a multiple of 16
+  // (nseg = 1, seg_len >= T: the whole sequence). A segment other than the
+  // first starts from h_init, a checkpoint buffer (batch, init_nchunk, D, N)
+  // of stride init_K that has a checkpoint at its first step (seg_len is a
+  // multiple of init_K): the segments are then independent and exact.
+  int batch, seg_len;
+  const float* h_init;
+  int init_K, init_nchunk;
 };
 
 constexpr int kCH = 32;   // channels per block
@@ -81,12 +90,15 @@ fwd_kernel(FwdArgs a) {
   const int c = lane & 31;
   const int q = wave * 2 + hh;
   const int n0 = q * NPL;
-  const int b = blockIdx.y;
+  const int b = blockIdx.y % a.batch;
+  const int seg = blockIdx.y / a.batch;
   const int d0 = blockIdx.x * kCH;
   const int d = d0 + c;
   const bool act = d < a.D;
   const int T = a.T, D = a.D;
-  const int nsub = (T + kSteps - 1) / kSteps;
+  const int t_beg = seg * a.seg_len;                      // this block's steps [t_beg, t_end)
+  const int t_end = min(T, t_beg + a.seg_len);
+  const int nsub = (t_end - t_beg + kSteps - 1) / kSteps;
 
   float a2[NPL], h[NPL];
 #pragma unroll
@@ -102,9 +114,12 @@ fwd_kernel(FwdArgs a) {
   const RowLoader<PERS, NPL> rl(tid, NT, N, NP);
   float4 px[PER], pd[PER];
   float pb[PERS], pc[PERS];
-  // Sub-chunk i (any i >= 0): first step and length (0 past the sequence).
-  auto sub_t0 = [&](int i) { return min(max(i, 0) * kSteps, T - 1); };
-  auto sub_len = [&](int i) { return i < 0 ? 0 : max(0, min(kSteps, T - i * kSteps)); };
+  // Sub-chunk i of the segment (any i >= 0): first step and length (0 past
+  // the segment).
+  auto sub_t0 = [&](int i) { return min(t_beg + max(i, 0) * kSteps, T - 1); };
+  auto sub_len = [&](int i) {
+    return i < 0 ? 0 : max(0, min(kSteps, t_end - t_beg - i * kSteps));
+  };
   // Resource over one sub-chunk of a (batch, T, D) tensor from channel d0 on.
   auto sub_buf = [&](const float* base, int i) {
     const int len = sub_len(i);
@@ -186,12 +201,17 @@ fwd_kernel(FwdArgs a) {
   const unsigned slice_bytes = 4u * (unsigned)ck_stride;
   const unsigned ck_lane = act ? 4u * ((unsigned)d * (unsigned)N + (unsigned)n0) : kOOB;
   const int nvalid = N - n0;
+  // A later segment starts from the checkpoint at its first step.
+  if (seg > 0 && a.h_init != nullptr)
+    load_states<NPL>(h, GBuf(a.h_init + ((size_t)b * a.init_nchunk + t_beg / a.init_K - 1) *
+                                            ck_stride, slice_bytes), ck_lane, nvalid);
   constexpr int kDone = 0x7FFFFFFF;
-  int next_ck = a.ckpt != nullptr ? min(a.K, T) : kDone;   // step count after the next checkpoint
+  // Step count after the next checkpoint, and its slot.
+  int next_ck = a.ckpt != nullptr ? min((t_beg / a.K + 1) * a.K, T) : kDone;
   const float* ck_base = a.ckpt != nullptr ? a.ckpt + (size_t)b * a.nchunk * ck_stride : a.x;
-  const float* ck_ptr = ck_base;
+  const float* ck_ptr = ck_base + (size_t)(t_beg / a.K) * ck_stride;
   for (int i = 0; i < nsub; ++i) {
-    const int t0 = i * kSteps;
+    const int t0 = t_beg + i * kSteps;
     const float* buf = lds + (i & 1) * BUF;
     const float* cDT = buf;
     const float* cBX = buf + kCH * kSteps;
@@ -282,14 +302,15 @@ fwd_kernel(FwdArgs a) {
     __syncthreads();
   }
   // KALIGNED: the last checkpoint (slot nchunk-1) is the state after step T-1,
-  // which is h now (steps past T are identity steps).
-  if (KALIGNED && a.ckpt != nullptr)
+  // which is h now in the last segment (steps past T are identity steps).
+  const bool last_seg = t_end == T;
+  if (KALIGNED && a.ckpt != nullptr && last_seg)
     store_states<NPL>(GBuf(ck_base + (size_t)(a.nchunk - 1) * ck_stride, slice_bytes), ck_lane,
                       nvalid, h);
   y_read(nsub - 1);
   y_write(nsub - 1);
 
-  if (a.h_last != nullptr)
+  if (a.h_last != nullptr && last_seg)
     store_states<NPL>(GBuf(a.h_last + (size_t)b * ck_stride, slice_bytes), ck_lane, nvalid, h);
 }
 

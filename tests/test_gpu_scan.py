@@ -233,9 +233,12 @@ def test_empty_sequence():
 # blocks per CU): segment counts above the chunk count, uneven last segments,
 # chunk strides off the 16-step window, the fine-checkpoint recompute path and
 # the state gradient entering the last segment.
+# With chunk > 16 the backward first recomputes stride-16 checkpoints, in
+# segments that start on the caller's checkpoints (lcm(16, chunk) steps).
 SEGMENT_CASES = [(2, 100, 64, 16, 16, 2), (1, 300, 96, 16, 16, 3), (2, 257, 40, 8, 7, 5),
                  (1, 64, 64, 16, 16, 8), (3, 200, 130, 5, 64, 3), (1, 20, 32, 16, 16, 4),
-                 (2, 513, 64, 32, 16, 8)]
+                 (2, 513, 64, 32, 16, 8), (1, 1000, 64, 16, 48, 4), (2, 777, 96, 16, 20, 6),
+                 (1, 2048, 64, 16, 64, 0)]
 
 
 @pytest.mark.parametrize("bt,t_len,d,n,chunk,segs", SEGMENT_CASES)
