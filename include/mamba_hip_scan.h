@@ -66,15 +66,15 @@ int64_t mhs_preferred_chunk(int64_t d_state);
  * a channel in one thread, scan.py:67-69). */
 int mhs_set_variant(int states_per_lane);
 
-/* Tuning knob, process-wide: the number of time segments mhs_scan_bwd_f32
- * (and the gated backward) split the sequence into (1..8; 0 restores the
+/* Tuning knob, process-wide: the number of time segments the forward (with
+ * a workspace) and the backward split the sequence into (1..8; 0 restores the
  * automatic choice: one segment while the grid has at least two blocks of 32
  * channels per compute unit, otherwise enough segments of at least 128 steps
  * for about three). Segments run in parallel after a short pass that carries
- * the adjoint across segment boundaries; results equal the unsegmented
- * backward up to rounding. mhs_scan_bwd_workspace_bytes depends on it. No
- * counterpart in the reference (its backward walks each channel's whole
- * sequence in one thread, scan.py:132-261). */
+ * the state (forward) or the adjoint (backward) across segment boundaries;
+ * results equal the unsegmented scan up to rounding. The workspace sizes
+ * depend on it. No counterpart in the reference (its kernels walk each
+ * channel's whole sequence in one thread, scan.py:78-127, :132-261). */
 int mhs_set_time_segments(int segments);
 
 /*
@@ -91,6 +91,29 @@ int mhs_scan_fwd_f32(const float* x, const float* dt, const float* aneg,
                      float* y, float* ckpt, float* h_last,
                      int64_t batch, int64_t seqlen, int64_t d_inner, int64_t d_state,
                      int64_t chunk, void* stream);
+
+/* Bytes of device workspace mhs_scan_fwd_ws_f32 (and the gated forward)
+ * can use for this shape: 0 when the forward runs as one time segment (grids
+ * of at least two blocks of 32 channels per compute unit), else the carried
+ * states of its time segments (see mhs_set_time_segments). */
+size_t mhs_scan_fwd_workspace_bytes(int64_t batch, int64_t seqlen, int64_t d_inner,
+                                    int64_t d_state);
+
+/*
+ * mhs_scan_fwd_f32 with a workspace (>= mhs_scan_fwd_workspace_bytes bytes,
+ * 256-byte aligned, contents irrelevant; NULL = none). With it, grids too small
+ * for the GPU run as time segments: a pass that scans segments 0..S-2 from a
+ * zero state and keeps their end states and dt sums, then all S segments at
+ * once, each from the state folded from the earlier ones. Same outputs up to
+ * rounding. No counterpart in the reference (its forward runs each channel's
+ * whole sequence in one thread, scan.py:78-127).
+ */
+int mhs_scan_fwd_ws_f32(const float* x, const float* dt, const float* aneg,
+                        const float* B, const float* C,
+                        float* y, float* ckpt, float* h_last,
+                        void* workspace, size_t workspace_bytes,
+                        int64_t batch, int64_t seqlen, int64_t d_inner, int64_t d_state,
+                        int64_t chunk, void* stream);
 
 /* Bytes of device workspace mhs_scan_bwd_f32 needs for this shape. */
 size_t mhs_scan_bwd_workspace_bytes(int64_t batch, int64_t seqlen, int64_t d_inner,
@@ -126,12 +149,14 @@ int mhs_scan_bwd_f32(const float* x, const float* dt, const float* aneg,
  *     dt   = dt_min + (dt_max - dt_min) * sigmoid(dt_raw)    dt_raw : (batch, seqlen, d_inner)
  *     Aneg = softplus(A)                                     A      : (d_inner, d_state)
  * as they stage their inputs (dt is never written to memory), then run the
- * recurrence of mhs_scan_fwd_f32 on (x, dt, Aneg, B, C). Needs finite
- * dt_min < dt_max. Same outputs, layouts and checkpoints as mhs_scan_fwd_f32.
+ * recurrence of mhs_scan_fwd_ws_f32 on (x, dt, Aneg, B, C). Needs finite
+ * dt_min < dt_max. Same outputs, layouts, checkpoints and workspace (may be
+ * NULL) as mhs_scan_fwd_ws_f32.
  */
 int mhs_scan_gated_fwd_f32(const float* x, const float* dt_raw, const float* A,
                            const float* B, const float* C, float dt_min, float dt_max,
                            float* y, float* ckpt, float* h_last,
+                           void* workspace, size_t workspace_bytes,
                            int64_t batch, int64_t seqlen, int64_t d_inner, int64_t d_state,
                            int64_t chunk, void* stream);
 

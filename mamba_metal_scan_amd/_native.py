@@ -28,6 +28,7 @@ EXPORTED_SYMBOLS = (
     "mhs_conv1d_silu_bwd_workspace_bytes", "mhs_conv1d_silu_bwd_f32",
     "mhs_scan_gated_fwd_f32", "mhs_scan_gated_bwd_f32", "mhs_out_gate_fwd_f32",
     "mhs_out_gate_bwd_workspace_bytes", "mhs_out_gate_bwd_f32", "mhs_set_time_segments",
+    "mhs_scan_fwd_workspace_bytes", "mhs_scan_fwd_ws_f32",
 )
 
 _lib: Optional[ctypes.CDLL] = None
@@ -68,6 +69,10 @@ def library() -> ctypes.CDLL:
             lib.mhs_set_time_segments.argtypes = [ctypes.c_int]
             lib.mhs_scan_fwd_f32.restype = ctypes.c_int
             lib.mhs_scan_fwd_f32.argtypes = [_P] * 8 + [_I64] * 5 + [_P]
+            lib.mhs_scan_fwd_workspace_bytes.restype = ctypes.c_size_t
+            lib.mhs_scan_fwd_workspace_bytes.argtypes = [_I64] * 4
+            lib.mhs_scan_fwd_ws_f32.restype = ctypes.c_int
+            lib.mhs_scan_fwd_ws_f32.argtypes = [_P] * 9 + [ctypes.c_size_t] + [_I64] * 5 + [_P]
             lib.mhs_scan_bwd_workspace_bytes.restype = ctypes.c_size_t
             lib.mhs_scan_bwd_workspace_bytes.argtypes = [_I64] * 5
             lib.mhs_scan_bwd_f32.restype = ctypes.c_int
@@ -82,7 +87,8 @@ def library() -> ctypes.CDLL:
             lib.mhs_conv1d_silu_bwd_f32.argtypes = ([_P, _I64] + [_P] * 7 + [ctypes.c_size_t]
                                                     + [_I64] * 4 + [_P])
             lib.mhs_scan_gated_fwd_f32.restype = ctypes.c_int
-            lib.mhs_scan_gated_fwd_f32.argtypes = [_P] * 5 + [_F32] * 2 + [_P] * 3 + [_I64] * 5 + [_P]
+            lib.mhs_scan_gated_fwd_f32.argtypes = ([_P] * 5 + [_F32] * 2 + [_P] * 4
+                                                   + [ctypes.c_size_t] + [_I64] * 5 + [_P])
             lib.mhs_scan_gated_bwd_f32.restype = ctypes.c_int
             lib.mhs_scan_gated_bwd_f32.argtypes = ([_P] * 5 + [_F32] * 2 + [_P] * 9
                                                    + [ctypes.c_size_t] + [_I64] * 5 + [_P])
@@ -132,6 +138,15 @@ def set_time_segments(segments: int) -> None:
 
 # --------------------------------------------------------------- custom ops
 
+def _fwd_workspace(x: torch.Tensor, n: int):
+    """(workspace tensor or None, bytes) for a forward on (B,T,D) x with d_state n."""
+    bt, t_len, d = x.shape
+    nbytes = int(library().mhs_scan_fwd_workspace_bytes(bt, t_len, d, n))
+    if nbytes == 0:
+        return None, 0
+    return torch.empty(nbytes, dtype=torch.uint8, device=x.device), nbytes
+
+
 @torch.library.custom_op("mamba_hip::scan_fwd", mutates_args=())
 def scan_fwd(x: torch.Tensor, dt: torch.Tensor, aneg: torch.Tensor, b_in: torch.Tensor,
              c_in: torch.Tensor, chunk: int, with_ckpt: bool
@@ -143,12 +158,13 @@ def scan_fwd(x: torch.Tensor, dt: torch.Tensor, aneg: torch.Tensor, b_in: torch.
     ckpt = (x.new_empty((bt, num_chunks(t_len, chunk), d, n)) if with_ckpt
             else x.new_empty((0,)))
     h_last = x.new_empty((bt, d, n))
+    ws, ws_bytes = _fwd_workspace(x, n)
     with torch.cuda.device(x.device):
-        rc = library().mhs_scan_fwd_f32(
+        rc = library().mhs_scan_fwd_ws_f32(
             _ptr(x), _ptr(dt), _ptr(aneg), _ptr(b_in), _ptr(c_in), _ptr(y),
-            _ptr(ckpt) if with_ckpt else None, _ptr(h_last),
+            _ptr(ckpt) if with_ckpt else None, _ptr(h_last), _ptr(ws), ws_bytes,
             bt, t_len, d, n, chunk, _stream(x.device))
-    _check(rc, "mhs_scan_fwd_f32")
+    _check(rc, "mhs_scan_fwd_ws_f32")
     return y, ckpt, h_last
 
 
@@ -281,10 +297,11 @@ def scan_gated_fwd(x: torch.Tensor, dt_raw: torch.Tensor, a_raw: torch.Tensor,
     ckpt = (x.new_empty((bt, num_chunks(t_len, chunk), d, n)) if with_ckpt
             else x.new_empty((0,)))
     h_last = x.new_empty((bt, d, n))
+    ws, ws_bytes = _fwd_workspace(x, n)
     with torch.cuda.device(x.device):
         rc = library().mhs_scan_gated_fwd_f32(
             _ptr(x), _ptr(dt_raw), _ptr(a_raw), _ptr(b_in), _ptr(c_in), dt_min, dt_max, _ptr(y),
-            _ptr(ckpt) if with_ckpt else None, _ptr(h_last),
+            _ptr(ckpt) if with_ckpt else None, _ptr(h_last), _ptr(ws), ws_bytes,
             bt, t_len, d, n, chunk, _stream(x.device))
     _check(rc, "mhs_scan_gated_fwd_f32")
     return y, ckpt, h_last

@@ -85,6 +85,8 @@ struct Plan {
   FwdFn fwd_any = nullptr;  // any checkpoint stride
   FwdFn fwd_g = nullptr;    // the same two with the dt gate and softplus(A) fused
   FwdFn fwd_any_g = nullptr;
+  FwdFn fcarry = nullptr;   // carry pass of the forward's time segments
+  FwdFn fcarry_g = nullptr; // gated
   int fwd_lds = 0;  // bytes
   BwdFn bwd = nullptr;
   BwdFn bwd_g = nullptr;    // gated
@@ -105,6 +107,8 @@ void fill(Plan& p) {
   p.fwd_any = &mhs::fwd_kernel<NPL, G, MINW, false, false>;
   p.fwd_g = &mhs::fwd_kernel<NPL, G, MINW, true, true>;
   p.fwd_any_g = &mhs::fwd_kernel<NPL, G, MINW, false, true>;
+  p.fcarry = &mhs::fwd_kernel<NPL, G, MINW, true, false, true>;
+  p.fcarry_g = &mhs::fwd_kernel<NPL, G, MINW, true, true, true>;
   p.bwd = &mhs::bwd_kernel<NPL, G, MINW, false, false>;
   p.bwd_g = &mhs::bwd_kernel<NPL, G, MINW, true, false>;
   p.carry = &mhs::bwd_kernel<NPL, G, MINW, false, true>;
@@ -256,9 +260,28 @@ int launch_fwd(const Plan& p, mhs::FwdArgs a, int batch, hipStream_t s, const Ga
   return check_launch("forward scan kernel");
 }
 
+// Workspace of the forward's time segments: carried end states and dt sums
+// (see FwdArgs in mhs_fwd.hpp); total 0 when the shape runs unsegmented.
+struct FwdWs {
+  size_t carryH = 0, carryS = 0, total = 0;
+  int nseg = 1, cps = 1;   // segments, sub-chunks of 16 steps per segment
+};
+
+FwdWs fwd_ws_layout(int64_t batch, int64_t T, int64_t D, int64_t N) {
+  FwdWs w;
+  segments_for(batch, D, (int)((T + mhs::kSteps - 1) / mhs::kSteps), w.nseg, w.cps);
+  if (w.nseg > 1) {
+    w.carryH = 0;
+    w.carryS = round_up((size_t)w.nseg * batch * D * N * 4, 256);
+    w.total = w.carryS + round_up((size_t)w.nseg * batch * D * 4, 256);
+  }
+  return w;
+}
+
 int scan_fwd(const float* x, const float* dt, const float* aneg, const float* B, const float* C,
-             float* y, float* ckpt, float* h_last, int64_t batch, int64_t seqlen, int64_t d_inner,
-             int64_t d_state, int64_t chunk, void* stream, const Gate& g) {
+             float* y, float* ckpt, float* h_last, void* workspace, size_t workspace_bytes,
+             int64_t batch, int64_t seqlen, int64_t d_inner, int64_t d_state, int64_t chunk,
+             void* stream, const Gate& g) {
   int rc = check_shape(batch, seqlen, d_inner, d_state, chunk);
   if (rc) return rc;
   if (!x || !dt || !aneg || !B || !C) return fail(MHS_EINVAL, "null input pointer");
@@ -273,7 +296,41 @@ int scan_fwd(const float* x, const float* dt, const float* aneg, const float* B,
   a.T = (int)seqlen; a.D = (int)d_inner; a.N = (int)d_state;
   a.K = (int)std::min<int64_t>(chunk, seqlen);
   a.nchunk = (int)mhs_num_chunks(seqlen, chunk);
-  return launch_fwd(p, a, (int)batch, static_cast<hipStream_t>(stream), g);
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  const FwdWs w = fwd_ws_layout(batch, seqlen, d_inner, d_state);
+  if (workspace == nullptr || w.nseg == 1) return launch_fwd(p, a, (int)batch, s, g);
+  if (workspace_bytes < w.total)
+    return fail(MHS_EINVAL, "workspace too small: %zu < %zu bytes", workspace_bytes, w.total);
+  if (reinterpret_cast<uintptr_t>(workspace) & 255u)
+    return fail(MHS_EINVAL, "workspace must be 256-byte aligned");
+  // Time segments: the carry pass over segments 0..nseg-2, then every
+  // segment from its folded start state.
+  char* ws = static_cast<char*>(workspace);
+  a.batch = (int)batch;
+  a.seg_len = w.cps * mhs::kSteps;
+  a.h_init = nullptr;
+  a.carryH = reinterpret_cast<float*>(ws + w.carryH);
+  a.carrySdt = reinterpret_cast<float*>(ws + w.carryS);
+  a.dt_lo = g.lo;
+  a.dt_span = g.span;
+  const unsigned nblk = (unsigned)((d_inner + mhs::kCH - 1) / mhs::kCH);
+  mhs::FwdArgs c = a;
+  c.y = nullptr;
+  c.ckpt = nullptr;
+  c.h_last = nullptr;
+  const FwdFn cfn = g.on ? p.fcarry_g : p.fcarry;
+  rc = ensure_lds(reinterpret_cast<const void*>(cfn), p.fwd_lds);
+  if (rc) return rc;
+  hipLaunchKernelGGL(cfn, dim3(nblk, (unsigned)(batch * (w.nseg - 1))), dim3(64 * p.G), p.fwd_lds,
+                     s, c);
+  rc = check_launch("forward carry kernel");
+  if (rc) return rc;
+  const bool aligned = a.K % mhs::kSteps == 0 || a.K >= a.T;
+  const FwdFn fn = aligned ? (g.on ? p.fwd_g : p.fwd) : (g.on ? p.fwd_any_g : p.fwd_any);
+  rc = ensure_lds(reinterpret_cast<const void*>(fn), p.fwd_lds);
+  if (rc) return rc;
+  hipLaunchKernelGGL(fn, dim3(nblk, (unsigned)(batch * w.nseg)), dim3(64 * p.G), p.fwd_lds, s, a);
+  return check_launch("forward scan kernel");
 }
 
 int scan_bwd(const float* x, const float* dt, const float* aneg, const float* B, const float* C,
@@ -421,8 +478,23 @@ int mhs_scan_fwd_f32(const float* x, const float* dt, const float* aneg, const f
                      int64_t seqlen, int64_t d_inner, int64_t d_state, int64_t chunk,
                      void* stream) {
   g_err[0] = '\0';
-  return scan_fwd(x, dt, aneg, B, C, y, ckpt, h_last, batch, seqlen, d_inner, d_state, chunk,
-                  stream, Gate{});
+  return scan_fwd(x, dt, aneg, B, C, y, ckpt, h_last, nullptr, 0, batch, seqlen, d_inner, d_state,
+                  chunk, stream, Gate{});
+}
+
+size_t mhs_scan_fwd_workspace_bytes(int64_t batch, int64_t seqlen, int64_t d_inner,
+                                    int64_t d_state) {
+  if (check_shape(batch, seqlen, d_inner, d_state, 1)) return 0;
+  return fwd_ws_layout(batch, seqlen, d_inner, d_state).total;
+}
+
+int mhs_scan_fwd_ws_f32(const float* x, const float* dt, const float* aneg, const float* B,
+                        const float* C, float* y, float* ckpt, float* h_last, void* workspace,
+                        size_t workspace_bytes, int64_t batch, int64_t seqlen, int64_t d_inner,
+                        int64_t d_state, int64_t chunk, void* stream) {
+  g_err[0] = '\0';
+  return scan_fwd(x, dt, aneg, B, C, y, ckpt, h_last, workspace, workspace_bytes, batch, seqlen,
+                  d_inner, d_state, chunk, stream, Gate{});
 }
 
 int mhs_scan_bwd_f32(const float* x, const float* dt, const float* aneg, const float* B,
@@ -437,14 +509,15 @@ int mhs_scan_bwd_f32(const float* x, const float* dt, const float* aneg, const f
 
 int mhs_scan_gated_fwd_f32(const float* x, const float* dt_raw, const float* A, const float* B,
                            const float* C, float dt_min, float dt_max, float* y, float* ckpt,
-                           float* h_last, int64_t batch, int64_t seqlen, int64_t d_inner,
-                           int64_t d_state, int64_t chunk, void* stream) {
+                           float* h_last, void* workspace, size_t workspace_bytes, int64_t batch,
+                           int64_t seqlen, int64_t d_inner, int64_t d_state, int64_t chunk,
+                           void* stream) {
   g_err[0] = '\0';
   Gate g;
   const int rc = check_gate(dt_min, dt_max, g);
   if (rc) return rc;
-  return scan_fwd(x, dt_raw, A, B, C, y, ckpt, h_last, batch, seqlen, d_inner, d_state, chunk,
-                  stream, g);
+  return scan_fwd(x, dt_raw, A, B, C, y, ckpt, h_last, workspace, workspace_bytes, batch, seqlen,
+                  d_inner, d_state, chunk, stream, g);
 }
 
 int mhs_scan_gated_bwd_f32(const float* x, const float* dt_raw, const float* A, const float* B,

@@ -52,9 +52,17 @@ struct FwdArgs {
   // first starts from h_init, a checkpoint buffer (batch, init_nchunk, D, N)
   // of stride init_K that has a checkpoint at its first step (seg_len is a
   // multiple of init_K): the segments are then independent and exact.
-  int batch, seg_len;
-  const float* h_init;
-  int init_K, init_nchunk;
+  int batch = 1, seg_len = 0;
+  const float* h_init = nullptr;
+  int init_K = 1, init_nchunk = 1;
+  // Carried segments (no h_init): segment s >= 1 starts from the state folded
+  // from the earlier segments' carries, H_0 = 0 and
+  //   H_{s+1} = exp(-Aneg * Sdt_s) * H_s + hend_s,
+  // where the carry pass (FCARRY) wrote hend_s, the state after segment s
+  // scanned from zero, to carryH (nseg, batch, D, N) and Sdt_s, its sum of
+  // dt, to carrySdt (nseg, batch, D).
+  float* carryH = nullptr;
+  float* carrySdt = nullptr;
 };
 
 constexpr int kCH = 32;   // channels per block
@@ -73,7 +81,10 @@ __host__ __device__ constexpr int fwd_lds_floats(int G, int NPL) {
 // on sub-chunk ends (and the last one on the final state): no per-step tests.
 // GATED: dt and Aneg come from the block's raw projections (see FwdArgs); the
 // staging threads gate each dt once per block as they move it to LDS.
-template <int NPL, int G, int MINW, bool KALIGNED, bool GATED>
+// FCARRY: the carry pass of the time segments (see FwdArgs): blocks of
+// segments 0..nseg-2 scan their segment from zero and write only its end
+// state and sum of dt (no C, no y, no checkpoints).
+template <int NPL, int G, int MINW, bool KALIGNED, bool GATED, bool FCARRY = false>
 __global__ void __launch_bounds__(64 * G, MINW)
 fwd_kernel(FwdArgs a) {
   constexpr int NT = 64 * G;                    // threads
@@ -130,7 +141,7 @@ fwd_kernel(FwdArgs a) {
     ql.load(px, sub_buf(a.x, i), D);
     ql.load(pd, sub_buf(a.dt, i), D);
     rl.load(pb, GBuf(a.B + (row0 + sub_t0(i)) * N, sbytes));
-    rl.load(pc, GBuf(a.C + (row0 + sub_t0(i)) * N, sbytes));
+    if constexpr (!FCARRY) rl.load(pc, GBuf(a.C + (row0 + sub_t0(i)) * N, sbytes));
   };
   auto store_sub = [&](int i) {           // staging registers -> LDS buffer i&1
     float* buf = lds + (i & 1) * BUF;
@@ -138,7 +149,7 @@ fwd_kernel(FwdArgs a) {
     ql.store_cm(buf, pd);
     ql.store_cm_product(buf + kCH * kSteps, pd, px);
     rl.store(buf + 2 * kCH * kSteps, pb);
-    rl.store(buf + 2 * kCH * kSteps + kSteps * NP, pc);
+    if constexpr (!FCARRY) rl.store(buf + 2 * kCH * kSteps + kSteps * NP, pc);
   };
   // y of sub-chunk i: task (channel cc, quad m) sums the partials of its four
   // steps over the 2G lane groups in a fixed order (128-bit reads). Tasks go
@@ -201,10 +212,22 @@ fwd_kernel(FwdArgs a) {
   const unsigned slice_bytes = 4u * (unsigned)ck_stride;
   const unsigned ck_lane = act ? 4u * ((unsigned)d * (unsigned)N + (unsigned)n0) : kOOB;
   const int nvalid = N - n0;
-  // A later segment starts from the checkpoint at its first step.
-  if (seg > 0 && a.h_init != nullptr)
+  // A later segment starts from the checkpoint at its first step, or from
+  // the state folded from the earlier segments' carries.
+  if (seg > 0 && a.h_init != nullptr) {
     load_states<NPL>(h, GBuf(a.h_init + ((size_t)b * a.init_nchunk + t_beg / a.init_K - 1) *
                                             ck_stride, slice_bytes), ck_lane, nvalid);
+  } else if (!FCARRY && seg > 0 && a.carryH != nullptr) {
+    for (int s2 = 0; s2 < seg; ++s2) {
+      const size_t slot = (size_t)s2 * a.batch + b;
+      float hv[NPL];
+      load_states<NPL>(hv, GBuf(a.carryH + slot * ck_stride, slice_bytes), ck_lane, nvalid);
+      const float sdt = act ? a.carrySdt[slot * D + d] : 0.f;
+#pragma unroll
+      for (int j = 0; j < NPL; ++j) h[j] = __builtin_fmaf(exp2_hw(sdt * a2[j]), h[j], hv[j]);
+    }
+  }
+  float sdt_acc = 0.f;   // FCARRY: sum of dt over the segment
   constexpr int kDone = 0x7FFFFFFF;
   // Step count after the next checkpoint, and its slot.
   int next_ck = a.ckpt != nullptr ? min((t_beg / a.K + 1) * a.K, T) : kDone;
@@ -227,7 +250,7 @@ fwd_kernel(FwdArgs a) {
 #pragma unroll
       for (int j = 0; j < NPL; ++j) {
         qB[j] = lds4(gB + 4 * m * NPL + 4 * j);
-        qC[j] = lds4(gC + 4 * m * NPL + 4 * j);
+        if constexpr (!FCARRY) qC[j] = lds4(gC + 4 * m * NPL + 4 * j);
       }
     };
     read_quad(0);
@@ -241,7 +264,7 @@ fwd_kernel(FwdArgs a) {
       f4_to(bxs, qbx);
 #pragma unroll
       for (int e = 0; e < 4 * NPL; ++e) {
-        const float4 tb = qB[e / 4], tc = qC[e / 4];
+        const float4 tb = qB[e / 4], tc = FCARRY ? tb : qC[e / 4];
         const float vb[4] = {tb.x, tb.y, tb.z, tb.w}, vc[4] = {tc.x, tc.y, tc.z, tc.w};
         Bq[e / NPL][e % NPL] = vb[e % 4];
         Cq[e / NPL][e % NPL] = vc[e % 4];
@@ -249,12 +272,14 @@ fwd_kernel(FwdArgs a) {
       if (m + 1 < kQuads) read_quad(m + 1);
       float da[4][NPL], u[4][NPL];
 #pragma unroll
-      for (int s = 0; s < 4; ++s)
+      for (int s = 0; s < 4; ++s) {
+        if constexpr (FCARRY) sdt_acc += dts[s];
 #pragma unroll
         for (int j = 0; j < NPL; ++j) {
           da[s][j] = exp2_hw(dts[s] * a2[j]);
           u[s][j] = Bq[s][j] * bxs[s];
         }
+      }
       float yq[4], hq[4][NPL];
 #pragma unroll
       for (int s = 0; s < 4; ++s) {
@@ -262,19 +287,19 @@ fwd_kernel(FwdArgs a) {
 #pragma unroll
         for (int j = 0; j < NPL; ++j) {
           h[j] = __builtin_fmaf(da[s][j], h[j], u[s][j]);
-          acc = __builtin_fmaf(Cq[s][j], h[j], acc);
+          if constexpr (!FCARRY) acc = __builtin_fmaf(Cq[s][j], h[j], acc);
           hq[s][j] = h[j];
         }
         yq[s] = acc;
       }
-      sts4(myY + cm_quad(lane, m), make_float4(yq[0], yq[1], yq[2], yq[3]));
+      if constexpr (!FCARRY) sts4(myY + cm_quad(lane, m), make_float4(yq[0], yq[1], yq[2], yq[3]));
 
       // Pipeline work for the neighbouring sub-chunks, in this quad's
       // scheduling region. Unconditional: past either end of the sequence the
       // resources are empty (loads return 0, stores are dropped) and the LDS
       // buffer written is not read again.
-      if (m == 0) y_read(i - 1);
-      if (m == 1) y_write(i - 1);
+      if (!FCARRY && m == 0) y_read(i - 1);
+      if (!FCARRY && m == 1) y_write(i - 1);
       if (m == 1) store_sub(i + 1);
       if (m == 2) load_sub(i + 2);
 
@@ -300,6 +325,12 @@ fwd_kernel(FwdArgs a) {
       }
     }
     __syncthreads();
+  }
+  if constexpr (FCARRY) {
+    const size_t slot = (size_t)seg * a.batch + b;
+    store_states<NPL>(GBuf(a.carryH + slot * ck_stride, slice_bytes), ck_lane, nvalid, h);
+    if (q == 0 && act) a.carrySdt[slot * D + d] = sdt_acc;
+    return;
   }
   // KALIGNED: the last checkpoint (slot nchunk-1) is the state after step T-1,
   // which is h now in the last segment (steps past T are identity steps).

@@ -254,10 +254,13 @@ def test_time_segments_match_the_oracle(bt, t_len, d, n, chunk, segs):
     try:
         y, h_last, grads = _run_hip(_to_dev(arrs), torch.from_numpy(dy).to(DEV), chunk=chunk,
                                     dh_last=torch.from_numpy(dh).to(DEV))
+        _, ckpt, _ = torch.ops.mamba_hip.scan_fwd(*_to_dev(arrs), chunk, True)
+        torch.cuda.synchronize()
     finally:
         _native.set_time_segments(0)
     assert_close("y", y, y_ref)
     assert_close("h_last", h_last, h_ref)
+    assert_close("ckpt", ckpt, oracle.scan_fwd(*arrs, chunk=chunk)[1])
     for name, g, r in zip(("dx", "ddt", "dAneg", "dB", "dC"), grads, g_ref):
         assert_close(name, g, r)
 
@@ -274,13 +277,16 @@ def test_time_segments_auto_split_at_the_long_sequence_shape():
     b_in = torch.randn(bt, t_len, n, generator=g).to(DEV)
     c_in = torch.randn(bt, t_len, n, generator=g).to(DEV)
     dy = torch.randn(bt, t_len, d, generator=g).to(DEV)
-    _, ckpt, _ = torch.ops.mamba_hip.scan_fwd(x, dt, aneg, b_in, c_in, 16, True)
-    auto = torch.ops.mamba_hip.scan_bwd(x, dt, aneg, b_in, c_in, dy, None, ckpt, 16)
+    fwd_auto = torch.ops.mamba_hip.scan_fwd(x, dt, aneg, b_in, c_in, 16, True)
+    auto = torch.ops.mamba_hip.scan_bwd(x, dt, aneg, b_in, c_in, dy, None, fwd_auto[1], 16)
     _native.set_time_segments(1)
     try:
-        one = torch.ops.mamba_hip.scan_bwd(x, dt, aneg, b_in, c_in, dy, None, ckpt, 16)
+        fwd_one = torch.ops.mamba_hip.scan_fwd(x, dt, aneg, b_in, c_in, 16, True)
+        one = torch.ops.mamba_hip.scan_bwd(x, dt, aneg, b_in, c_in, dy, None, fwd_one[1], 16)
     finally:
         _native.set_time_segments(0)
     torch.cuda.synchronize()
+    for name, a_, b_ in zip(("y", "ckpt", "h_last"), fwd_auto, fwd_one):
+        assert_close(name, a_, b_)
     for name, a_, b_ in zip(("dx", "ddt", "dAneg", "dB", "dC"), auto, one):
         assert_close(name, a_, b_)

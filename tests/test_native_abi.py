@@ -134,11 +134,12 @@ def test_step_argument_errors():
 def test_gated_scan_argument_errors():
     lib = _native.library()
     sizes = (2, 8, 32, 16, 16)
-    rc = lib.mhs_scan_gated_fwd_f32(*([A16] * 5), 0.1, 0.1, *([A16] * 3), *sizes, None)
+    outs = [A16] * 3 + [None, 0]          # y, ckpt, h_last; no workspace
+    rc = lib.mhs_scan_gated_fwd_f32(*([A16] * 5), 0.1, 0.1, *outs, *sizes, None)
     assert rc == MHS_EINVAL and "dt_min < dt_max" in _err(lib)
-    rc = lib.mhs_scan_gated_fwd_f32(*([A16] * 5), 0.001, float("nan"), *([A16] * 3), *sizes, None)
+    rc = lib.mhs_scan_gated_fwd_f32(*([A16] * 5), 0.001, float("nan"), *outs, *sizes, None)
     assert rc == MHS_EINVAL and "dt_min < dt_max" in _err(lib)
-    rc = lib.mhs_scan_gated_fwd_f32(*([A16] * 5), 0.001, 0.1, *([A16] * 3), 2, 8, 32, 65, 16, None)
+    rc = lib.mhs_scan_gated_fwd_f32(*([A16] * 5), 0.001, 0.1, *outs, 2, 8, 32, 65, 16, None)
     assert rc == MHS_EINVAL and "d_state" in _err(lib)
     need = lib.mhs_scan_bwd_workspace_bytes(*sizes)
     rc = lib.mhs_scan_gated_bwd_f32(*([A16] * 5), 0.001, 0.1, *([A16] * 8), A16, need - 4,
@@ -192,3 +193,20 @@ def test_time_segments_knob_and_workspace():
         assert lib.mhs_scan_bwd_workspace_bytes(1, 80, 64, 16, 16) == expect(1, 80, 64, 16, 5)
     finally:
         _native.set_time_segments(0)
+
+
+def test_forward_workspace():
+    """The forward needs no workspace where the grid fills the GPU; below two
+    blocks per CU it holds the segments' carried states and dt sums."""
+    lib = _native.library()
+    assert lib.mhs_scan_fwd_workspace_bytes(16, 512, 1536, 16) == 0
+    # 4 x 16384 x 2048 x 16: 256 blocks -> 3 segments
+    ru = lambda v: (v + 255) // 256 * 256
+    assert lib.mhs_scan_fwd_workspace_bytes(4, 16384, 2048, 16) == \
+        ru(3 * 4 * 2048 * 16 * 4) + ru(3 * 4 * 2048 * 4)
+    sizes = (4, 16384, 2048, 16, 16)
+    need = lib.mhs_scan_fwd_workspace_bytes(*sizes[:4])
+    rc = lib.mhs_scan_fwd_ws_f32(*([A16] * 8), A16, need - 4, *sizes, None)
+    assert rc == MHS_EINVAL and "workspace too small" in _err(lib)
+    rc = lib.mhs_scan_fwd_ws_f32(*([A16] * 8), MIS, need, *sizes, None)
+    assert rc == MHS_EINVAL and "256-byte" in _err(lib)
