@@ -199,7 +199,10 @@ def pmc_summary(args) -> None:
             lines.append(f"| `{r['Name'][:60]}` | {r['Calls']} | {float(r['AverageNs']) / 1e3:.1f} "
                          f"| {float(r['MinNs']) / 1e3:.1f} | {float(r['MaxNs']) / 1e3:.1f} |")
         lines += ["", "The backward launch (the `scan_bwd` op) is `bwd_kernel` + "
-                  "`bwd_reduce_kernel`.", ""]
+                  "`bwd_reduce_kernel`. Under kernel tracing each dispatch's duration reads "
+                  "about 7 us longer than the HIP-event average of the same launches run "
+                  "back to back without the profiler (bench.py's `avg_ms`): compare the "
+                  "`scan_fwd` and `roofline` figures of a plain `python bench.py` run.", ""]
     lines += ["## HBM traffic per launch", "",
               f"    rocprofv3 --pmc FETCH_SIZE -d OUT/fetch -o run --output-format csv -- "
               f"python3 bench.py --launches 5 {extra}",
