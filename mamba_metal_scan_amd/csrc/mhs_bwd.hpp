@@ -89,7 +89,7 @@ struct BwdArgs {
 
 // One staging buffer (the kernel keeps two) and the single-buffered rest.
 __host__ __device__ constexpr int bwd_buf_floats(int G, int NPL) {
-  return 3 * kCH * kSteps               // dt, dy, x (channel-major)
+  return 4 * kCH * kSteps               // dt, dy, x, dt*x (channel-major)
          + 2 * kSteps * 2 * G * NPL;    // B, C tiles
 }
 __host__ __device__ constexpr int bwd_lds_floats(int G, int NPL) {
@@ -142,8 +142,8 @@ bwd_kernel(BwdArgs a) {
   float* tS = lds + 2 * BUF;                          // [G][64][16]
   float* tDBC = tS + G * 64 * kSteps;                 // [2][16][NP]
   // Staging buffer j: dt, dy, x (channel-major), B, C (per lane group).
-  constexpr int oDY = kCH * kSteps, oX = 2 * kCH * kSteps, oB = 3 * kCH * kSteps,
-                oC = oB + kSteps * NP;
+  constexpr int oDY = kCH * kSteps, oX = 2 * kCH * kSteps, oDTX = 3 * kCH * kSteps,
+                oB = 4 * kCH * kSteps, oC = oB + kSteps * NP;
   // The reduce-scatter leaves lane `lane` with the total of product rs_index:
   // products are numbered kind * 2NPL + slot * NPL + j (kind 0: dB, 1: dC;
   // slot: step k + slot; j: state n0 + j of this half-wave's group).
@@ -154,28 +154,30 @@ bwd_kernel(BwdArgs a) {
   const size_t slice = (size_t)D * N;
   const unsigned slice_bytes = 4u * (unsigned)slice;
   const unsigned st_lane = act ? 4u * ((unsigned)d * (unsigned)N + (unsigned)n0) : kOOB;
-  float an[NPL], a2[NPL], g[NPL], acc[NPL], dan[NPL];
+  // u = dA_{t+1} * G_{t+1}, the adjoint already decayed into step t: the walk
+  // carries u, so that G_t = dy_t C_t + u and dA_t h_{t-1} G_t = u_t h_{t-1}
+  // each take one operation.
+  float an[NPL], a2[NPL], u[NPL], acc[NPL];
 #pragma unroll
   for (int j = 0; j < NPL; ++j) {
     an[j] = (act && j < nvalid) ? a.aneg[(size_t)d * N + n0 + j] : 0.f;
     if constexpr (GATED) an[j] = (act && j < nvalid) ? softplus_f(an[j]) : 0.f;
     a2[j] = -an[j] * kLog2e;
     acc[j] = 0.f;
-    dan[j] = 1.f;
-    g[j] = 0.f;
+    u[j] = 0.f;
   }
   if constexpr (!CARRY) {
     // The adjoint entering this segment: dh_last for the last one, folded
     // with the carries of the later segments for the others.
     const float* dhl = a.dh_last != nullptr ? a.dh_last + (size_t)b * slice : a.aneg;
-    load_states<NPL>(g, GBuf(dhl, a.dh_last != nullptr ? slice_bytes : 0u), st_lane, nvalid);
+    load_states<NPL>(u, GBuf(dhl, a.dh_last != nullptr ? slice_bytes : 0u), st_lane, nvalid);
     for (int s2 = a.nseg - 1; s2 > seg; --s2) {
       float lv[NPL];
       const size_t slot = (size_t)s2 * a.batch + b;
       load_states<NPL>(lv, GBuf(a.carryL + slot * slice, slice_bytes), st_lane, nvalid);
       const float sdt = act ? a.carrySdt[slot * D + d] : 0.f;
 #pragma unroll
-      for (int j = 0; j < NPL; ++j) g[j] = __builtin_fmaf(exp2_hw(sdt * a2[j]), g[j], lv[j]);
+      for (int j = 0; j < NPL; ++j) u[j] = __builtin_fmaf(exp2_hw(sdt * a2[j]), u[j], lv[j]);
     }
   }
   float sdt_acc = 0.f;   // CARRY: sum of dt over the segment
@@ -218,6 +220,7 @@ bwd_kernel(BwdArgs a) {
     ql.store_cm(s0, pd);
     ql.store_cm(s0 + oDY, py);
     if constexpr (!CARRY) ql.store_cm(s0 + oX, px);
+    if constexpr (!CARRY) ql.store_cm_product(s0 + oDTX, pd, px);   // dt * x, once per block
     if constexpr (!CARRY) rl.store(s0 + oB, pb);
     rl.store(s0 + oC, pc);
   };
@@ -305,10 +308,8 @@ bwd_kernel(BwdArgs a) {
         for (int s = 3; s >= 0; --s) {
           sdt_acc += dts[s];
 #pragma unroll
-          for (int j = 0; j < NPL; ++j) {
-            g[j] = __builtin_fmaf(dan[j], g[j], dys[s] * Cq[s][j]);
-            dan[j] = exp2_hw(dts[s] * a2[j]);
-          }
+          for (int j = 0; j < NPL; ++j)
+            u[j] = exp2_hw(dts[s] * a2[j]) * __builtin_fmaf(dys[s], Cq[s][j], u[j]);
         }
         if (m == 2) store_sub((i + 1) & 1, ci - 1);
         if (m == 1) load_sub(ci - 2);
@@ -321,17 +322,16 @@ bwd_kernel(BwdArgs a) {
     float da[kSteps][NPL], hs[kSteps][NPL];
 #pragma unroll
     for (int m = 0; m < kQuads; ++m) {
-      float dts[4], xs[4], Bq[4][NPL];
+      float dts[4], dtxs[4], Bq[4][NPL];
       f4_to(dts, lds4(s0 + cm_quad(c, m)));
-      f4_to(xs, lds4(s0 + oX + cm_quad(c, m)));
+      f4_to(dtxs, lds4(s0 + oDTX + cm_quad(c, m)));
       load_quad_rows<NPL>(Bq, gB, m);
 #pragma unroll
       for (int s = 0; s < 4; ++s) {
-        const float dtx = dts[s] * xs[s];
 #pragma unroll
         for (int j = 0; j < NPL; ++j) {
           da[4 * m + s][j] = exp2_hw(dts[s] * a2[j]);
-          hs[4 * m + s][j] = Bq[s][j] * dtx;          // b_k, turned into h_k below
+          hs[4 * m + s][j] = Bq[s][j] * dtxs[s];       // b_k, turned into h_k below
         }
       }
       if (m == 0) finalize(ci + 1, (i + 1) & 1);   // no-op stores past the sequence end
@@ -346,10 +346,10 @@ bwd_kernel(BwdArgs a) {
     // ---- reverse phase
 #pragma unroll
     for (int m = kQuads - 1; m >= 0; --m) {
-      float dts[4], dys[4], xs[4], Bq[4][NPL], Cq[4][NPL], s1q[4], s2q[4];
+      float dts[4], dys[4], dtxs[4], Bq[4][NPL], Cq[4][NPL], s1q[4], s2q[4];
       f4_to(dts, lds4(s0 + cm_quad(c, m)));
       f4_to(dys, lds4(s0 + oDY + cm_quad(c, m)));
-      f4_to(xs, lds4(s0 + oX + cm_quad(c, m)));
+      f4_to(dtxs, lds4(s0 + oDTX + cm_quad(c, m)));
       load_quad_rows<NPL>(Bq, gB, m);
       load_quad_rows<NPL>(Cq, gC, m);
       float pv[M];   // dB/dC products of the step pair (k, k+1), k even, numbered as for rs_index
@@ -357,24 +357,21 @@ bwd_kernel(BwdArgs a) {
       for (int s = 3; s >= 0; --s) {
         const int k = 4 * m + s;
         const int slot = k & 1;
-        float s1 = 0.f, s2 = 0.f;
+        float s1 = 0.f, s2 = 0.f, gk[NPL];
 #pragma unroll
         for (int j = 0; j < NPL; ++j) {
-          const float gj = __builtin_fmaf(dan[j], g[j], dys[s] * Cq[s][j]);
-          const float hm = da[k][j] * (k == 0 ? hc[j] : hs[k - 1][j]);
-          s1 = __builtin_fmaf(gj, Bq[s][j], s1);
-          const float qv = gj * hm;
+          gk[j] = __builtin_fmaf(dys[s], Cq[s][j], u[j]);            // G_k
+          u[j] = da[k][j] * gk[j];                                   // dA_k G_k
+          const float qv = u[j] * (k == 0 ? hc[j] : hs[k - 1][j]);   // G_k * hm_k
+          s1 = __builtin_fmaf(gk[j], Bq[s][j], s1);
           s2 = __builtin_fmaf(an[j], qv, s2);
           acc[j] = __builtin_fmaf(dts[s], qv, acc[j]);
-          g[j] = gj;
-          dan[j] = da[k][j];
         }
         s1q[s] = s1;
         s2q[s] = s2;
-        const float w = dts[s] * xs[s];
 #pragma unroll
         for (int j = 0; j < NPL; ++j) {
-          pv[slot * NPL + j] = g[j] * w;                  // dB: G * dt * x
+          pv[slot * NPL + j] = gk[j] * dtxs[s];             // dB: G * dt * x
           pv[2 * NPL + slot * NPL + j] = hs[k][j] * dys[s];   // dC: h * dy
         }
         if (slot == 0) *(dbc_out + k * NP) = half_wave_reduce_scatter<M>(pv, lane);
@@ -398,11 +395,8 @@ bwd_kernel(BwdArgs a) {
   }
   const size_t slot = (size_t)seg * a.batch + b;
   if constexpr (CARRY) {
-    // L_s = dA_a * G_a: dan holds dA of the segment's first step, g its adjoint.
-    float out[NPL];
-#pragma unroll
-    for (int j = 0; j < NPL; ++j) out[j] = dan[j] * g[j];
-    store_states<NPL>(GBuf(a.carryL + slot * slice, slice_bytes), st_lane, nvalid, out);
+    // L_s = dA_a * G_a, a the segment's first step: u after the walk.
+    store_states<NPL>(GBuf(a.carryL + slot * slice, slice_bytes), st_lane, nvalid, u);
     if (q == 0 && act) a.carrySdt[slot * D + d] = sdt_acc;
     return;
   }
