@@ -249,16 +249,17 @@ bwd_kernel(BwdArgs a) {
         s1a += v1.x; s1b += v1.y;
         s2a += v2.x; s2b += v2.y;
       }
-      gdx.st(t0v * s1a, o0);
-      gdx.st(t1v * s1b, o1);
+      // dx, ddt, dB/dC partials: written once, not read again here (NT).
+      gdx.st<kStream>(t0v * s1a, o0);
+      gdx.st<kStream>(t1v * s1b, o1);
       float g0 = __builtin_fmaf(x0, s1a, -s2a), g1 = __builtin_fmaf(x1, s1b, -s2b);
       if constexpr (GATED) {
         const float u0 = t0v - a.dt_lo, u1 = t1v - a.dt_lo;   // span * s
         g0 *= u0 * (a.dt_span - u0) * a.dt_inv_span;
         g1 *= u1 * (a.dt_span - u1) * a.dt_inv_span;
       }
-      gddt.st(g0, o0);
-      gddt.st(g1, o1);
+      gddt.st<kStream>(g0, o0);
+      gddt.st<kStream>(g1, o1);
     }
     const int len = chunk_len(ci);
     const size_t wrow = ((size_t)blockIdx.x * a.batch + b) * T + chunk_t0(ci);
@@ -269,8 +270,8 @@ bwd_kernel(BwdArgs a) {
       const int r = tid + f * NT;                 // (k, n) of the tile, n fastest
       const int k = r / NP, n = r % NP;
       const unsigned o = n < N ? 4u * (unsigned)(k * N + n) : kOOB;
-      gwb.st(tDBC[r], o);
-      gwc.st(tDBC[kSteps * NP + r], o);
+      gwb.st<kStream>(tDBC[r], o);
+      gwc.st<kStream>(tDBC[kSteps * NP + r], o);
     }
   };
 
@@ -388,8 +389,13 @@ bwd_kernel(BwdArgs a) {
       if (m == 2) store_sub((i + 1) & 1, ci - 1);  // unused when ci == 0
       if (m == 1) load_sub(ci - 2);        // loads nothing when ci < 2
     }
+    // h at the start of chunk ci-1, copied here and now (an opaque copy the
+    // compiler cannot sink): ph's registers are then free for the next
+    // checkpoint load. A copy left at the loop back-edge would move that load's
+    // result, i.e. wait for it, and vmcnt being in order, for every load and
+    // store still in flight: a full memory drain per chunk.
 #pragma unroll
-    for (int j = 0; j < NPL; ++j) hc[j] = ph[j];   // h at the start of chunk ci-1
+    for (int j = 0; j < NPL; ++j) asm volatile("v_mov_b32 %0, %1" : "=v"(hc[j]) : "v"(ph[j]));
     load_h0(ci - 2);
     __syncthreads();   // tS / tDBC complete; chunk ci-1 staged
   }

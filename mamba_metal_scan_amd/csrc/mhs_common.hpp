@@ -199,6 +199,11 @@ __device__ __forceinline__ float2 lds2(const float* p) { return *reinterpret_cas
 // to kOOB, and the hot loops stay single basic blocks.
 constexpr unsigned kOOB = 0x80000000u;   // resources are < 2 GiB (checked on the host)
 
+// Cache policy of a buffer access (the instruction's aux bits): kStream marks
+// it non-temporal (NT), so that data used once streams through the caches
+// without evicting the tiles that other blocks or later steps reuse.
+constexpr int kStream = 2;
+
 // Base and size must be wave-uniform; they are moved to SGPRs explicitly
 // (readfirstlane), so that the compiler never has to wrap an access in a
 // loop over the distinct descriptors of the wave. __builtin_amdgcn_readfirstlane
@@ -215,27 +220,33 @@ struct GBuf {
       : r(__builtin_amdgcn_make_buffer_rsrc(uniform_ptr(base), 0,
                                             __builtin_amdgcn_readfirstlane((int)bytes), 0x00020000)) {}
   // The b32 builtins move raw 32-bit words (unsigned int): bit-cast, never convert.
+  // POL is the cache policy (kStream: non-temporal, for data that is touched
+  // once and must not evict what is reused).
+  template <int POL = 0>
   __device__ __forceinline__ float ld(unsigned byte_off) const {
-    return __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(r, byte_off, 0, 0));
+    return __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(r, byte_off, 0, POL));
   }
+  template <int POL = 0>
   __device__ __forceinline__ void st(float v, unsigned byte_off) const {
-    __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(v), r, byte_off, 0, 0);
+    __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(v), r, byte_off, 0, POL);
   }
 };
 
 // NPL consecutive states of one lane at byte offset `off` (kOOB: none);
 // states at or beyond `nvalid` are padding and are not stored.
-template <int NPL>
+template <int NPL, int POL = 0>
 __device__ __forceinline__ void store_states(const GBuf& g, unsigned off, int nvalid,
                                              const float (&v)[NPL]) {
 #pragma unroll
-  for (int j = 0; j < NPL; ++j) g.st(v[j], (off != kOOB && j < nvalid) ? off + 4u * j : kOOB);
+  for (int j = 0; j < NPL; ++j)
+    g.st<POL>(v[j], (off != kOOB && j < nvalid) ? off + 4u * j : kOOB);
 }
-template <int NPL>
+template <int NPL, int POL = 0>
 __device__ __forceinline__ void load_states(float (&v)[NPL], const GBuf& g, unsigned off,
                                             int nvalid) {
 #pragma unroll
-  for (int j = 0; j < NPL; ++j) v[j] = g.ld((off != kOOB && j < nvalid) ? off + 4u * j : kOOB);
+  for (int j = 0; j < NPL; ++j)
+    v[j] = g.ld<POL>((off != kOOB && j < nvalid) ? off + 4u * j : kOOB);
 }
 
 __device__ __forceinline__ void sts4(float* p, float4 v) { *reinterpret_cast<float4*>(p) = v; }
@@ -265,16 +276,17 @@ struct QuadLoader {
   __device__ __forceinline__ int quad(int i) const { return (tid + i * nthreads) / CH; }
   // g covers (b, t0.., d0..) up to the end of the batch row (steps past T
   // are out of range).
+  template <int POL = 0>
   __device__ __forceinline__ void load(float4 (&v)[PER], const GBuf& g, int D) const {
     const unsigned rs = 4u * (unsigned)D;
 #pragma unroll
     for (int i = 0; i < PER; ++i) {
       const unsigned o = toff[i];
       const bool ok = o != kOOB;
-      v[i].x = g.ld(o);
-      v[i].y = g.ld(ok ? o + rs : kOOB);
-      v[i].z = g.ld(ok ? o + 2 * rs : kOOB);
-      v[i].w = g.ld(ok ? o + 3 * rs : kOOB);
+      v[i].x = g.ld<POL>(o);
+      v[i].y = g.ld<POL>(ok ? o + rs : kOOB);
+      v[i].z = g.ld<POL>(ok ? o + 2 * rs : kOOB);
+      v[i].w = g.ld<POL>(ok ? o + 3 * rs : kOOB);
     }
   }
   // Gate staged dt values in place: dt = lo + span * sigmoid(raw) for the

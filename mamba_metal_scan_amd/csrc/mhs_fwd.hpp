@@ -151,51 +151,45 @@ fwd_kernel(FwdArgs a) {
     rl.store(buf + 2 * kCH * kSteps, pb);
     if constexpr (!FCARRY) rl.store(buf + 2 * kCH * kSteps + kSteps * NP, pc);
   };
-  // y of sub-chunk i: task (channel cc, quad m) sums the partials of its four
-  // steps over the 2G lane groups in a fixed order (128-bit reads). Tasks go
-  // to the threads from NT/2 on, i.e. to the waves that hold no staging tasks
-  // (those are threads 0..127). Split in two so that the LDS reads (y_read)
-  // and their use (y_write) sit in different scheduling regions.
-  constexpr int YT = (kCH * kQuads + NT - 1) / NT;          // y tasks per thread
-  float4 ypart[YT][2 * G];
-  auto y_task = [&](int f) { return (tid + NT / 2) % NT + f * NT; };
+  // y of sub-chunk i: task (channel cc, step pair p) sums the partials of
+  // its two steps over the 2G lane groups in a fixed order (64-bit reads).
+  // There are 32 x 8 = 256 tasks: one per thread at G = 4. Split in two so
+  // that the LDS reads (y_read) and their use (y_write) sit in different
+  // scheduling regions.
+  constexpr int YTASKS = kCH * kSteps / 2;
+  constexpr int YT = (YTASKS + NT - 1) / NT;             // y tasks per thread
+  float2 ypart[YT][2 * G];
   auto y_read = [&](int i) {
     const float* yp = lds + (i & 1) * BUF + 2 * kCH * kSteps + 2 * kSteps * NP;
 #pragma unroll
     for (int f = 0; f < YT; ++f) {
-      const int t0 = y_task(f);
-      const int t = t0 < kCH * kQuads ? t0 : 0;
-      const int cc = t % kCH, m = t / kCH;
+      const int t0 = tid + f * NT;
+      const int t = t0 < YTASKS ? t0 : 0;
+      const int cc = t % kCH, p = t / kCH;
 #pragma unroll
       for (int w = 0; w < G; ++w)
 #pragma unroll
         for (int h2 = 0; h2 < 2; ++h2)
-          ypart[f][2 * w + h2] = lds4(yp + w * 64 * kSteps + cm_quad(h2 * kCH + cc, m));
+          ypart[f][2 * w + h2] = lds2(yp + w * 64 * kSteps + cm_elem(h2 * kCH + cc, 2 * p));
     }
   };
   auto y_write = [&](int i) {
     const GBuf yo = sub_buf(a.y != nullptr ? a.y : a.x, a.y != nullptr ? i : -1);
 #pragma unroll
     for (int f = 0; f < YT; ++f) {
-      const int t0 = y_task(f);
-      const bool ok = t0 < kCH * kQuads;
+      const int t0 = tid + f * NT;
+      const bool ok = t0 < YTASKS;
       const int t = ok ? t0 : 0;
-      const int cc = t % kCH, m = t / kCH;
-      float4 sum = ypart[f][0];
+      const int cc = t % kCH, p = t / kCH;
+      float2 sum = ypart[f][0];
 #pragma unroll
-      for (int p = 1; p < 2 * G; ++p) {
-        sum.x += ypart[f][p].x;
-        sum.y += ypart[f][p].y;
-        sum.z += ypart[f][p].z;
-        sum.w += ypart[f][p].w;
+      for (int q2 = 1; q2 < 2 * G; ++q2) {
+        sum.x += ypart[f][q2].x;
+        sum.y += ypart[f][q2].y;
       }
-      const unsigned o = (ok && d0 + cc < D) ? 4u * ((unsigned)(4 * m) * (unsigned)D + cc) : kOOB;
-      const unsigned rs = 4u * (unsigned)D;
-      const bool okk = o != kOOB;
-      yo.st(sum.x, o);
-      yo.st(sum.y, okk ? o + rs : kOOB);
-      yo.st(sum.z, okk ? o + 2 * rs : kOOB);
-      yo.st(sum.w, okk ? o + 3 * rs : kOOB);
+      const unsigned o = (ok && d0 + cc < D) ? 4u * ((unsigned)(2 * p) * (unsigned)D + cc) : kOOB;
+      yo.st<kStream>(sum.x, o);                          // y: written once (NT)
+      yo.st<kStream>(sum.y, o != kOOB ? o + 4u * (unsigned)D : kOOB);
     }
   };
 
