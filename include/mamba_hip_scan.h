@@ -177,6 +177,44 @@ int mhs_scan_gated_bwd_f32(const float* x, const float* dt_raw, const float* A,
                            int64_t chunk, void* stream);
 
 /*
+ * bf16 activations with fp32 state. The same four scan entry points with x,
+ * dt (or dt_raw), B, C, y, dy, dx, ddt (or ddt_raw), dB and dC as bf16
+ * (uint16_t bit patterns, the upper half of an fp32); aneg / A, daneg / dA,
+ * dh_last, ckpt and h_last stay fp32. Loads widen exactly; all arithmetic,
+ * the recurrent state and the reductions are fp32; each bf16 output is its
+ * fp32 value rounded to nearest even. Same layouts, workspaces and
+ * determinism as the fp32 entry points. No counterpart in the reference
+ * (its kernels are fp32-only, README.md:80).
+ */
+int mhs_scan_fwd_bf16(const uint16_t* x, const uint16_t* dt, const float* aneg,
+                      const uint16_t* B, const uint16_t* C,
+                      uint16_t* y, float* ckpt, float* h_last,
+                      void* workspace, size_t workspace_bytes,
+                      int64_t batch, int64_t seqlen, int64_t d_inner, int64_t d_state,
+                      int64_t chunk, void* stream);
+int mhs_scan_bwd_bf16(const uint16_t* x, const uint16_t* dt, const float* aneg,
+                      const uint16_t* B, const uint16_t* C, const uint16_t* dy,
+                      const float* dh_last, const float* ckpt,
+                      uint16_t* dx, uint16_t* ddt, float* daneg, uint16_t* dB, uint16_t* dC,
+                      void* workspace, size_t workspace_bytes,
+                      int64_t batch, int64_t seqlen, int64_t d_inner, int64_t d_state,
+                      int64_t chunk, void* stream);
+int mhs_scan_gated_fwd_bf16(const uint16_t* x, const uint16_t* dt_raw, const float* A,
+                            const uint16_t* B, const uint16_t* C, float dt_min, float dt_max,
+                            uint16_t* y, float* ckpt, float* h_last,
+                            void* workspace, size_t workspace_bytes,
+                            int64_t batch, int64_t seqlen, int64_t d_inner, int64_t d_state,
+                            int64_t chunk, void* stream);
+int mhs_scan_gated_bwd_bf16(const uint16_t* x, const uint16_t* dt_raw, const float* A,
+                            const uint16_t* B, const uint16_t* C, float dt_min, float dt_max,
+                            const uint16_t* dy, const float* dh_last, const float* ckpt,
+                            uint16_t* dx, uint16_t* ddt_raw, float* dA, uint16_t* dB,
+                            uint16_t* dC, void* workspace, size_t workspace_bytes,
+                            int64_t batch, int64_t seqlen, int64_t d_inner, int64_t d_state,
+                            int64_t chunk, void* stream);
+
+/*
+ * One recurrent decode step, in place on h./*
  * One recurrent decode step, in place on h. Replaces the pure-torch step of
  * the reference's MambaBlock.forward (mamba_metal/model.py:234-241):
  *     h <- h * exp(-dt * Aneg) + dt * B * x ;  y = sum_n C * h

@@ -28,7 +28,8 @@ EXPORTED_SYMBOLS = (
     "mhs_conv1d_silu_bwd_workspace_bytes", "mhs_conv1d_silu_bwd_f32",
     "mhs_scan_gated_fwd_f32", "mhs_scan_gated_bwd_f32", "mhs_out_gate_fwd_f32",
     "mhs_out_gate_bwd_workspace_bytes", "mhs_out_gate_bwd_f32", "mhs_set_time_segments",
-    "mhs_scan_fwd_workspace_bytes", "mhs_scan_fwd_ws_f32",
+    "mhs_scan_fwd_workspace_bytes", "mhs_scan_fwd_ws_f32", "mhs_scan_fwd_bf16",
+    "mhs_scan_bwd_bf16", "mhs_scan_gated_fwd_bf16", "mhs_scan_gated_bwd_bf16",
 )
 
 _lib: Optional[ctypes.CDLL] = None
@@ -99,6 +100,14 @@ def library() -> ctypes.CDLL:
             lib.mhs_out_gate_bwd_f32.restype = ctypes.c_int
             lib.mhs_out_gate_bwd_f32.argtypes = ([_P] * 3 + [_I64] + [_P] * 5 + [ctypes.c_size_t]
                                                  + [_I64] * 3 + [_P])
+            for name in ("mhs_scan_fwd_bf16", "mhs_scan_bwd_bf16"):
+                getattr(lib, name).restype = ctypes.c_int
+            lib.mhs_scan_fwd_bf16.argtypes = lib.mhs_scan_fwd_ws_f32.argtypes
+            lib.mhs_scan_bwd_bf16.argtypes = lib.mhs_scan_bwd_f32.argtypes
+            lib.mhs_scan_gated_fwd_bf16.restype = ctypes.c_int
+            lib.mhs_scan_gated_fwd_bf16.argtypes = lib.mhs_scan_gated_fwd_f32.argtypes
+            lib.mhs_scan_gated_bwd_bf16.restype = ctypes.c_int
+            lib.mhs_scan_gated_bwd_bf16.argtypes = lib.mhs_scan_gated_bwd_f32.argtypes
             _lib = lib
     return _lib
 
@@ -138,6 +147,15 @@ def set_time_segments(segments: int) -> None:
 
 # --------------------------------------------------------------- custom ops
 
+def _fwd_outputs(x: torch.Tensor, n: int, chunk: int, with_ckpt: bool):
+    """y (x's dtype), checkpoints and final state (fp32, the state's type)."""
+    bt, t_len, d = x.shape
+    f32 = dict(dtype=torch.float32, device=x.device)
+    ckpt = (torch.empty((bt, num_chunks(t_len, chunk), d, n), **f32) if with_ckpt
+            else torch.empty((0,), **f32))
+    return torch.empty_like(x), ckpt, torch.empty((bt, d, n), **f32)
+
+
 def _fwd_workspace(x: torch.Tensor, n: int):
     """(workspace tensor or None, bytes) for a forward on (B,T,D) x with d_state n."""
     bt, t_len, d = x.shape
@@ -154,27 +172,21 @@ def scan_fwd(x: torch.Tensor, dt: torch.Tensor, aneg: torch.Tensor, b_in: torch.
     """y (B,T,D), ckpt (B,ceil(T/chunk),D,N) or an empty tensor, h_last (B,D,N)."""
     bt, t_len, d = x.shape
     n = aneg.shape[1]
-    y = torch.empty_like(x)
-    ckpt = (x.new_empty((bt, num_chunks(t_len, chunk), d, n)) if with_ckpt
-            else x.new_empty((0,)))
-    h_last = x.new_empty((bt, d, n))
+    y, ckpt, h_last = _fwd_outputs(x, n, chunk, with_ckpt)
     ws, ws_bytes = _fwd_workspace(x, n)
+    lib = library()
+    fn = lib.mhs_scan_fwd_bf16 if x.dtype == torch.bfloat16 else lib.mhs_scan_fwd_ws_f32
     with torch.cuda.device(x.device):
-        rc = library().mhs_scan_fwd_ws_f32(
-            _ptr(x), _ptr(dt), _ptr(aneg), _ptr(b_in), _ptr(c_in), _ptr(y),
-            _ptr(ckpt) if with_ckpt else None, _ptr(h_last), _ptr(ws), ws_bytes,
-            bt, t_len, d, n, chunk, _stream(x.device))
-    _check(rc, "mhs_scan_fwd_ws_f32")
+        rc = fn(_ptr(x), _ptr(dt), _ptr(aneg), _ptr(b_in), _ptr(c_in), _ptr(y),
+                _ptr(ckpt) if with_ckpt else None, _ptr(h_last), _ptr(ws), ws_bytes,
+                bt, t_len, d, n, chunk, _stream(x.device))
+    _check(rc, "scan forward")
     return y, ckpt, h_last
 
 
 @scan_fwd.register_fake
 def _scan_fwd_fake(x, dt, aneg, b_in, c_in, chunk, with_ckpt):
-    bt, t_len, d = x.shape
-    n = aneg.shape[1]
-    ckpt = (x.new_empty((bt, num_chunks(t_len, chunk), d, n)) if with_ckpt
-            else x.new_empty((0,)))
-    return torch.empty_like(x), ckpt, x.new_empty((bt, d, n))
+    return _fwd_outputs(x, aneg.shape[1], chunk, with_ckpt)
 
 
 @torch.library.custom_op("mamba_hip::scan_bwd", mutates_args=())
@@ -195,12 +207,12 @@ def scan_bwd(x: torch.Tensor, dt: torch.Tensor, aneg: torch.Tensor, b_in: torch.
     if ws_bytes == 0:
         raise HipScanError(f"no backward workspace size for shape {(bt, t_len, d, n)} chunk {chunk}")
     ws = torch.empty(ws_bytes, dtype=torch.uint8, device=x.device)
+    fn = lib.mhs_scan_bwd_bf16 if x.dtype == torch.bfloat16 else lib.mhs_scan_bwd_f32
     with torch.cuda.device(x.device):
-        rc = lib.mhs_scan_bwd_f32(
-            _ptr(x), _ptr(dt), _ptr(aneg), _ptr(b_in), _ptr(c_in), _ptr(dy),
-            _ptr(dh_last), _ptr(ckpt), _ptr(dx), _ptr(ddt), _ptr(daneg), _ptr(db), _ptr(dc),
-            _ptr(ws), ws_bytes, bt, t_len, d, n, chunk, _stream(x.device))
-    _check(rc, "mhs_scan_bwd_f32")
+        rc = fn(_ptr(x), _ptr(dt), _ptr(aneg), _ptr(b_in), _ptr(c_in), _ptr(dy),
+                _ptr(dh_last), _ptr(ckpt), _ptr(dx), _ptr(ddt), _ptr(daneg), _ptr(db), _ptr(dc),
+                _ptr(ws), ws_bytes, bt, t_len, d, n, chunk, _stream(x.device))
+    _check(rc, "scan backward")
     return dx, ddt, daneg, db, dc
 
 
@@ -293,17 +305,15 @@ def scan_gated_fwd(x: torch.Tensor, dt_raw: torch.Tensor, a_raw: torch.Tensor,
     Aneg = softplus(a_raw) formed inside the kernels."""
     bt, t_len, d = x.shape
     n = a_raw.shape[1]
-    y = torch.empty_like(x)
-    ckpt = (x.new_empty((bt, num_chunks(t_len, chunk), d, n)) if with_ckpt
-            else x.new_empty((0,)))
-    h_last = x.new_empty((bt, d, n))
+    y, ckpt, h_last = _fwd_outputs(x, n, chunk, with_ckpt)
     ws, ws_bytes = _fwd_workspace(x, n)
+    lib = library()
+    fn = lib.mhs_scan_gated_fwd_bf16 if x.dtype == torch.bfloat16 else lib.mhs_scan_gated_fwd_f32
     with torch.cuda.device(x.device):
-        rc = library().mhs_scan_gated_fwd_f32(
-            _ptr(x), _ptr(dt_raw), _ptr(a_raw), _ptr(b_in), _ptr(c_in), dt_min, dt_max, _ptr(y),
-            _ptr(ckpt) if with_ckpt else None, _ptr(h_last), _ptr(ws), ws_bytes,
-            bt, t_len, d, n, chunk, _stream(x.device))
-    _check(rc, "mhs_scan_gated_fwd_f32")
+        rc = fn(_ptr(x), _ptr(dt_raw), _ptr(a_raw), _ptr(b_in), _ptr(c_in), dt_min, dt_max,
+                _ptr(y), _ptr(ckpt) if with_ckpt else None, _ptr(h_last), _ptr(ws), ws_bytes,
+                bt, t_len, d, n, chunk, _stream(x.device))
+    _check(rc, "gated scan forward")
     return y, ckpt, h_last
 
 
@@ -331,12 +341,12 @@ def scan_gated_bwd(x: torch.Tensor, dt_raw: torch.Tensor, a_raw: torch.Tensor,
     if ws_bytes == 0:
         raise HipScanError(f"no backward workspace size for shape {(bt, t_len, d, n)} chunk {chunk}")
     ws = torch.empty(ws_bytes, dtype=torch.uint8, device=x.device)
+    fn = lib.mhs_scan_gated_bwd_bf16 if x.dtype == torch.bfloat16 else lib.mhs_scan_gated_bwd_f32
     with torch.cuda.device(x.device):
-        rc = lib.mhs_scan_gated_bwd_f32(
-            _ptr(x), _ptr(dt_raw), _ptr(a_raw), _ptr(b_in), _ptr(c_in), dt_min, dt_max, _ptr(dy),
-            _ptr(dh_last), _ptr(ckpt), _ptr(dx), _ptr(ddt), _ptr(da), _ptr(db), _ptr(dc),
-            _ptr(ws), ws_bytes, bt, t_len, d, n, chunk, _stream(x.device))
-    _check(rc, "mhs_scan_gated_bwd_f32")
+        rc = fn(_ptr(x), _ptr(dt_raw), _ptr(a_raw), _ptr(b_in), _ptr(c_in), dt_min, dt_max,
+                _ptr(dy), _ptr(dh_last), _ptr(ckpt), _ptr(dx), _ptr(ddt), _ptr(da), _ptr(db),
+                _ptr(dc), _ptr(ws), ws_bytes, bt, t_len, d, n, chunk, _stream(x.device))
+    _check(rc, "gated scan backward")
     return dx, ddt, da, db, dc
 
 

@@ -55,16 +55,18 @@
 namespace mhs {
 
 struct BwdArgs {
-  const float* x;
-  const float* dt;
+  // x, dt, B, C, dy, dx, ddt: ES-byte elements (fp32 or bf16, see the
+  // kernel's ES); everything else fp32.
+  const void* x;
+  const void* dt;
   const float* aneg;
-  const float* B;
-  const float* C;
-  const float* dy;
+  const void* B;
+  const void* C;
+  const void* dy;
   const float* dh_last;  // may be null
   const float* ckpt;     // (batch, nchunk, D, N), stride K
-  float* dx;
-  float* ddt;
+  void* dx;
+  void* ddt;
   float* wsB;            // (nblk, batch, T, N)
   float* wsC;            // (nblk, batch, T, N)
   float* wsA;            // (batch, D, N)
@@ -105,7 +107,8 @@ __host__ __device__ constexpr int bwd_lds_floats(int G, int NPL) {
 // segments 1..nseg-1 walk their segment backwards carrying only the adjoint
 // (dA and G, no state, no gradients, no x or B traffic) and write L_s and
 // the segment's sum of dt.
-template <int NPL, int G, int MINW, bool GATED, bool CARRY>
+// ES: bytes per element of x, dt, B, C, dy, dx, ddt (4: fp32, 2: bf16).
+template <int NPL, int G, int MINW, bool GATED, bool CARRY, int ES = 4>
 __global__ void __launch_bounds__(64 * G, MINW)
 bwd_kernel(BwdArgs a) {
   constexpr int NT = 64 * G;
@@ -183,8 +186,8 @@ bwd_kernel(BwdArgs a) {
   float sdt_acc = 0.f;   // CARRY: sum of dt over the segment
 
   const size_t row0 = (size_t)b * T;
-  const QuadLoader<kCH, PER> ql(tid, NT, D, d0);
-  const RowLoader<PERS, NPL> rl(tid, NT, N, NP);
+  const QuadLoader<kCH, PER, ES> ql(tid, NT, D, d0);
+  const RowLoader<PERS, NPL, ES> rl(tid, NT, N, NP);
   float4 px[PER], pd[PER], py[PER];
   float pb[PERS], pc[PERS], ph[NPL];
 
@@ -195,14 +198,15 @@ bwd_kernel(BwdArgs a) {
     return (ci < c_lo || ci >= c_hi) ? 0 : max(0, min(K, T - ci * K));
   };
   // Resource over one chunk of a (batch, T, D) tensor from channel d0 on.
-  auto chunk_buf = [&](const float* base, int ci) {
+  auto chunk_buf = [&](const void* base, int ci) {
     const int len = chunk_len(ci);
-    return GBuf(base + (row0 + chunk_t0(ci)) * D + d0, len > 0 ? 4u * (unsigned)(len * D - d0) : 0u);
+    return GBuf(elem_at<ES>(base, (row0 + chunk_t0(ci)) * D + d0),
+                len > 0 ? (unsigned)ES * (unsigned)(len * D - d0) : 0u);
   };
   auto load_sub = [&](int ci) {           // global -> staging registers
     const int len = chunk_len(ci);
-    const GBuf gs_b(a.B + (row0 + chunk_t0(ci)) * N, 4u * (unsigned)(len * N));
-    const GBuf gs_c(a.C + (row0 + chunk_t0(ci)) * N, 4u * (unsigned)(len * N));
+    const GBuf gs_b(elem_at<ES>(a.B, (row0 + chunk_t0(ci)) * N), (unsigned)ES * (unsigned)(len * N));
+    const GBuf gs_c(elem_at<ES>(a.C, (row0 + chunk_t0(ci)) * N), (unsigned)ES * (unsigned)(len * N));
     if constexpr (!CARRY) ql.load(px, chunk_buf(a.x, ci), D);
     ql.load(pd, chunk_buf(a.dt, ci), D);
     ql.load(py, chunk_buf(a.dy, ci), D);
@@ -237,8 +241,8 @@ bwd_kernel(BwdArgs a) {
       const bool ok = task0 < kSteps / 2 * kCH;
       const int task = ok ? task0 : 0;
       const int cc = task % kCH, k = 2 * (task / kCH);
-      const unsigned o0 = (ok && d0 + cc < D) ? 4u * ((unsigned)k * (unsigned)D + cc) : kOOB;
-      const unsigned o1 = o0 == kOOB ? kOOB : o0 + 4u * (unsigned)D;
+      const unsigned o0 = (ok && d0 + cc < D) ? (unsigned)ES * ((unsigned)k * (unsigned)D + cc) : kOOB;
+      const unsigned o1 = o0 == kOOB ? kOOB : o0 + (unsigned)ES * (unsigned)D;
       const float2 xv = lds2(sx + cm_elem(cc, k)), dtv = lds2(sdt + cm_elem(cc, k));
       const float x0 = xv.x, x1 = xv.y, t0v = dtv.x, t1v = dtv.y;
       float s1a = 0.f, s1b = 0.f, s2a = 0.f, s2b = 0.f;
@@ -250,16 +254,16 @@ bwd_kernel(BwdArgs a) {
         s2a += v2.x; s2b += v2.y;
       }
       // dx, ddt, dB/dC partials: written once, not read again here (NT).
-      gdx.st<kStream>(t0v * s1a, o0);
-      gdx.st<kStream>(t1v * s1b, o1);
+      st_elem<ES, kStream>(gdx, t0v * s1a, o0);
+      st_elem<ES, kStream>(gdx, t1v * s1b, o1);
       float g0 = __builtin_fmaf(x0, s1a, -s2a), g1 = __builtin_fmaf(x1, s1b, -s2b);
       if constexpr (GATED) {
         const float u0 = t0v - a.dt_lo, u1 = t1v - a.dt_lo;   // span * s
         g0 *= u0 * (a.dt_span - u0) * a.dt_inv_span;
         g1 *= u1 * (a.dt_span - u1) * a.dt_inv_span;
       }
-      gddt.st<kStream>(g0, o0);
-      gddt.st<kStream>(g1, o1);
+      st_elem<ES, kStream>(gddt, g0, o0);
+      st_elem<ES, kStream>(gddt, g1, o1);
     }
     const int len = chunk_len(ci);
     const size_t wrow = ((size_t)blockIdx.x * a.batch + b) * T + chunk_t0(ci);
@@ -441,19 +445,26 @@ __device__ __forceinline__ void ordered_sum2(const float* __restrict__ p, const 
 }
 
 // a_raw: null, or A for the gated backward: then daneg receives dAneg *
-// softplus'(A) = dAneg * sigmoid(A), the gradient of A.
+// softplus'(A) = dAneg * sigmoid(A), the gradient of A. dB, dC: ES-byte
+// elements (fp32 or bf16).
+template <int ES = 4>
 __global__ void __launch_bounds__(256)
 bwd_reduce_kernel(const float* __restrict__ wsB, const float* __restrict__ wsC,
                   const float* __restrict__ wsA, const float* __restrict__ a_raw,
-                  float* __restrict__ dB, float* __restrict__ dC, float* __restrict__ daneg,
+                  void* __restrict__ dB, void* __restrict__ dC, float* __restrict__ daneg,
                   int nblk, int batch, long long S, long long A) {
   const long long stride = (long long)gridDim.x * blockDim.x;
   for (long long i = (long long)blockIdx.x * blockDim.x + threadIdx.x; i < S + A; i += stride) {
     if (i < S) {
       float sb = 0.f, sc = 0.f;
       ordered_sum2(wsB + i, wsC + i, (size_t)S, nblk, sb, sc);
-      dB[i] = sb;
-      dC[i] = sc;
+      if constexpr (ES == 4) {
+        static_cast<float*>(dB)[i] = sb;
+        static_cast<float*>(dC)[i] = sc;
+      } else {
+        static_cast<unsigned short*>(dB)[i] = f32_to_bf16(sb);
+        static_cast<unsigned short*>(dC)[i] = f32_to_bf16(sc);
+      }
     } else {
       const long long j = i - S;
       float s = 0.f;

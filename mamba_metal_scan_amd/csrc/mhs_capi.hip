@@ -78,20 +78,31 @@ constexpr int kKI = mhs::kSteps;           // backward register window (steps)
 constexpr int kMaxLdsBytes = 160 * 1024;   // gfx950 LDS per workgroup
 constexpr int kMaxG = 8;                   // waves per block
 
-struct Plan {
-  int npl = 0;      // states per lane
-  int G = 0;        // waves per block (d_state padded to 2*G*npl)
+// The kernels of one plan for one activation element type.
+struct Kernels {
   FwdFn fwd = nullptr;      // checkpoint stride a multiple of 16 (or >= T)
   FwdFn fwd_any = nullptr;  // any checkpoint stride
   FwdFn fwd_g = nullptr;    // the same two with the dt gate and softplus(A) fused
   FwdFn fwd_any_g = nullptr;
   FwdFn fcarry = nullptr;   // carry pass of the forward's time segments
   FwdFn fcarry_g = nullptr; // gated
-  int fwd_lds = 0;  // bytes
   BwdFn bwd = nullptr;
   BwdFn bwd_g = nullptr;    // gated
   BwdFn carry = nullptr;    // adjoint-carry pass of the time segments
   BwdFn carry_g = nullptr;  // gated
+  void (*reduce)(const float*, const float*, const float*, const float*, void*, void*, float*,
+                 int, int, long long, long long) = nullptr;
+};
+
+// Activation element types: x, dt, B, C, y, dy, dx, ddt, dB, dC in fp32 or
+// bf16 (states, checkpoints, Aneg and all arithmetic stay fp32).
+enum Elem { kF32 = 0, kBF16 = 1 };
+
+struct Plan {
+  int npl = 0;      // states per lane
+  int G = 0;        // waves per block (d_state padded to 2*G*npl)
+  Kernels k[2];     // by Elem
+  int fwd_lds = 0;  // bytes
   int bwd_ki = 0;   // largest chunk the backward walks directly
   int bwd_lds = 0;  // bytes
 };
@@ -100,19 +111,26 @@ struct Plan {
 // MINW is the waves-per-SIMD target the register budget is sized for: 3 for
 // two states per lane (<= 168 VGPRs: at batch 16 x d_inner 1536 x d_state 16
 // the grid is exactly 3 waves per SIMD), 2 for four (<= 256 VGPRs).
+template <int NPL, int G, int MINW, int ES>
+void fill_elem(Kernels& k) {
+  k.fwd = &mhs::fwd_kernel<NPL, G, MINW, true, false, false, ES>;
+  k.fwd_any = &mhs::fwd_kernel<NPL, G, MINW, false, false, false, ES>;
+  k.fwd_g = &mhs::fwd_kernel<NPL, G, MINW, true, true, false, ES>;
+  k.fwd_any_g = &mhs::fwd_kernel<NPL, G, MINW, false, true, false, ES>;
+  k.fcarry = &mhs::fwd_kernel<NPL, G, MINW, true, false, true, ES>;
+  k.fcarry_g = &mhs::fwd_kernel<NPL, G, MINW, true, true, true, ES>;
+  k.bwd = &mhs::bwd_kernel<NPL, G, MINW, false, false, ES>;
+  k.bwd_g = &mhs::bwd_kernel<NPL, G, MINW, true, false, ES>;
+  k.carry = &mhs::bwd_kernel<NPL, G, MINW, false, true, ES>;
+  k.carry_g = &mhs::bwd_kernel<NPL, G, MINW, true, true, ES>;
+  k.reduce = &mhs::bwd_reduce_kernel<ES>;
+}
+
 template <int NPL, int G>
 void fill(Plan& p) {
   constexpr int MINW = NPL == 2 ? 3 : 2;
-  p.fwd = &mhs::fwd_kernel<NPL, G, MINW, true, false>;
-  p.fwd_any = &mhs::fwd_kernel<NPL, G, MINW, false, false>;
-  p.fwd_g = &mhs::fwd_kernel<NPL, G, MINW, true, true>;
-  p.fwd_any_g = &mhs::fwd_kernel<NPL, G, MINW, false, true>;
-  p.fcarry = &mhs::fwd_kernel<NPL, G, MINW, true, false, true>;
-  p.fcarry_g = &mhs::fwd_kernel<NPL, G, MINW, true, true, true>;
-  p.bwd = &mhs::bwd_kernel<NPL, G, MINW, false, false>;
-  p.bwd_g = &mhs::bwd_kernel<NPL, G, MINW, true, false>;
-  p.carry = &mhs::bwd_kernel<NPL, G, MINW, false, true>;
-  p.carry_g = &mhs::bwd_kernel<NPL, G, MINW, true, true>;
+  fill_elem<NPL, G, MINW, 4>(p.k[kF32]);
+  fill_elem<NPL, G, MINW, 2>(p.k[kBF16]);
   p.fwd_lds = mhs::fwd_lds_floats(G, NPL) * 4;
   p.bwd_lds = mhs::bwd_lds_floats(G, NPL) * 4;
 }
@@ -242,10 +260,11 @@ int check_gate(float dt_min, float dt_max, Gate& g) {
 
 // One block per (channel block, batch row, time segment); a.seg_len and
 // a.h_init describe the segments (see FwdArgs), nseg = 1 for the whole sequence.
-int launch_fwd(const Plan& p, mhs::FwdArgs a, int batch, hipStream_t s, const Gate& g,
+int launch_fwd(const Plan& p, mhs::FwdArgs a, int batch, hipStream_t s, const Gate& g, Elem e,
                int nseg = 1) {
+  const Kernels& kk = p.k[e];
   const bool aligned = a.K % mhs::kSteps == 0 || a.K >= a.T;
-  const FwdFn fn = aligned ? (g.on ? p.fwd_g : p.fwd) : (g.on ? p.fwd_any_g : p.fwd_any);
+  const FwdFn fn = aligned ? (g.on ? kk.fwd_g : kk.fwd) : (g.on ? kk.fwd_any_g : kk.fwd_any);
   a.dt_lo = g.lo;
   a.dt_span = g.span;
   a.batch = batch;
@@ -278,10 +297,10 @@ FwdWs fwd_ws_layout(int64_t batch, int64_t T, int64_t D, int64_t N) {
   return w;
 }
 
-int scan_fwd(const float* x, const float* dt, const float* aneg, const float* B, const float* C,
-             float* y, float* ckpt, float* h_last, void* workspace, size_t workspace_bytes,
+int scan_fwd(const void* x, const void* dt, const float* aneg, const void* B, const void* C,
+             void* y, float* ckpt, float* h_last, void* workspace, size_t workspace_bytes,
              int64_t batch, int64_t seqlen, int64_t d_inner, int64_t d_state, int64_t chunk,
-             void* stream, const Gate& g) {
+             void* stream, const Gate& g, Elem e) {
   int rc = check_shape(batch, seqlen, d_inner, d_state, chunk);
   if (rc) return rc;
   if (!x || !dt || !aneg || !B || !C) return fail(MHS_EINVAL, "null input pointer");
@@ -298,7 +317,7 @@ int scan_fwd(const float* x, const float* dt, const float* aneg, const float* B,
   a.nchunk = (int)mhs_num_chunks(seqlen, chunk);
   hipStream_t s = static_cast<hipStream_t>(stream);
   const FwdWs w = fwd_ws_layout(batch, seqlen, d_inner, d_state);
-  if (workspace == nullptr || w.nseg == 1) return launch_fwd(p, a, (int)batch, s, g);
+  if (workspace == nullptr || w.nseg == 1) return launch_fwd(p, a, (int)batch, s, g, e);
   if (workspace_bytes < w.total)
     return fail(MHS_EINVAL, "workspace too small: %zu < %zu bytes", workspace_bytes, w.total);
   if (reinterpret_cast<uintptr_t>(workspace) & 255u)
@@ -318,7 +337,8 @@ int scan_fwd(const float* x, const float* dt, const float* aneg, const float* B,
   c.y = nullptr;
   c.ckpt = nullptr;
   c.h_last = nullptr;
-  const FwdFn cfn = g.on ? p.fcarry_g : p.fcarry;
+  const Kernels& kk = p.k[e];
+  const FwdFn cfn = g.on ? kk.fcarry_g : kk.fcarry;
   rc = ensure_lds(reinterpret_cast<const void*>(cfn), p.fwd_lds);
   if (rc) return rc;
   hipLaunchKernelGGL(cfn, dim3(nblk, (unsigned)(batch * (w.nseg - 1))), dim3(64 * p.G), p.fwd_lds,
@@ -326,18 +346,18 @@ int scan_fwd(const float* x, const float* dt, const float* aneg, const float* B,
   rc = check_launch("forward carry kernel");
   if (rc) return rc;
   const bool aligned = a.K % mhs::kSteps == 0 || a.K >= a.T;
-  const FwdFn fn = aligned ? (g.on ? p.fwd_g : p.fwd) : (g.on ? p.fwd_any_g : p.fwd_any);
+  const FwdFn fn = aligned ? (g.on ? kk.fwd_g : kk.fwd) : (g.on ? kk.fwd_any_g : kk.fwd_any);
   rc = ensure_lds(reinterpret_cast<const void*>(fn), p.fwd_lds);
   if (rc) return rc;
   hipLaunchKernelGGL(fn, dim3(nblk, (unsigned)(batch * w.nseg)), dim3(64 * p.G), p.fwd_lds, s, a);
   return check_launch("forward scan kernel");
 }
 
-int scan_bwd(const float* x, const float* dt, const float* aneg, const float* B, const float* C,
-             const float* dy, const float* dh_last, const float* ckpt, float* dx, float* ddt,
-             float* daneg, float* dB, float* dC, void* workspace, size_t workspace_bytes,
+int scan_bwd(const void* x, const void* dt, const float* aneg, const void* B, const void* C,
+             const void* dy, const float* dh_last, const float* ckpt, void* dx, void* ddt,
+             float* daneg, void* dB, void* dC, void* workspace, size_t workspace_bytes,
              int64_t batch, int64_t seqlen, int64_t d_inner, int64_t d_state, int64_t chunk,
-             void* stream, const Gate& g) {
+             void* stream, const Gate& g, Elem e) {
   int rc = check_shape(batch, seqlen, d_inner, d_state, chunk);
   if (rc) return rc;
   if (!x || !dt || !aneg || !B || !C || !dy || !ckpt || !dx || !ddt || !daneg || !dB || !dC ||
@@ -381,7 +401,7 @@ int scan_bwd(const float* x, const float* dt, const float* aneg, const float* B,
     f.h_init = ckpt;
     f.init_K = K;
     f.init_nchunk = (int)mhs_num_chunks(T, K);
-    rc = launch_fwd(p, f, (int)batch, s, g, nseg);
+    rc = launch_fwd(p, f, (int)batch, s, g, e, nseg);
     if (rc) return rc;
     ck = f.ckpt;
     Kb = p.bwd_ki;
@@ -406,7 +426,7 @@ int scan_bwd(const float* x, const float* dt, const float* aneg, const float* B,
   const unsigned nblk = (unsigned)((D + ch - 1) / ch);
   if (w.nseg > 1) {
     // Adjoint carries of segments 1..nseg-1 (segment 0 passes nothing on).
-    const BwdFn cfn = g.on ? p.carry_g : p.carry;
+    const BwdFn cfn = g.on ? p.k[e].carry_g : p.k[e].carry;
     rc = ensure_lds(reinterpret_cast<const void*>(cfn), p.bwd_lds);
     if (rc) return rc;
     hipLaunchKernelGGL(cfn, dim3(nblk, (unsigned)(batch * (w.nseg - 1))), dim3(64 * p.G),
@@ -414,7 +434,7 @@ int scan_bwd(const float* x, const float* dt, const float* aneg, const float* B,
     rc = check_launch("backward carry kernel");
     if (rc) return rc;
   }
-  const BwdFn fn = g.on ? p.bwd_g : p.bwd;
+  const BwdFn fn = g.on ? p.k[e].bwd_g : p.k[e].bwd;
   rc = ensure_lds(reinterpret_cast<const void*>(fn), p.bwd_lds);
   if (rc) return rc;
   hipLaunchKernelGGL(fn, dim3(nblk, (unsigned)(batch * w.nseg)), dim3(64 * p.G), p.bwd_lds, s, a);
@@ -425,7 +445,7 @@ int scan_bwd(const float* x, const float* dt, const float* aneg, const float* B,
   const long long A = (long long)D * N;
   const long long total = S + A;
   const int blocks = (int)std::min<long long>((total + 255) / 256, 4096);
-  hipLaunchKernelGGL(mhs::bwd_reduce_kernel, dim3(blocks), dim3(256), 0, s, a.wsB, a.wsC, a.wsA,
+  hipLaunchKernelGGL(p.k[e].reduce, dim3(blocks), dim3(256), 0, s, a.wsB, a.wsC, a.wsA,
                      g.on ? aneg : nullptr, dB, dC, daneg, (D + ch - 1) / ch,
                      (int)batch * w.nseg, S, A);
   return check_launch("backward reduction kernel");
@@ -479,7 +499,7 @@ int mhs_scan_fwd_f32(const float* x, const float* dt, const float* aneg, const f
                      void* stream) {
   g_err[0] = '\0';
   return scan_fwd(x, dt, aneg, B, C, y, ckpt, h_last, nullptr, 0, batch, seqlen, d_inner, d_state,
-                  chunk, stream, Gate{});
+                  chunk, stream, Gate{}, kF32);
 }
 
 size_t mhs_scan_fwd_workspace_bytes(int64_t batch, int64_t seqlen, int64_t d_inner,
@@ -494,7 +514,7 @@ int mhs_scan_fwd_ws_f32(const float* x, const float* dt, const float* aneg, cons
                         int64_t d_state, int64_t chunk, void* stream) {
   g_err[0] = '\0';
   return scan_fwd(x, dt, aneg, B, C, y, ckpt, h_last, workspace, workspace_bytes, batch, seqlen,
-                  d_inner, d_state, chunk, stream, Gate{});
+                  d_inner, d_state, chunk, stream, Gate{}, kF32);
 }
 
 int mhs_scan_bwd_f32(const float* x, const float* dt, const float* aneg, const float* B,
@@ -504,7 +524,7 @@ int mhs_scan_bwd_f32(const float* x, const float* dt, const float* aneg, const f
                      int64_t d_state, int64_t chunk, void* stream) {
   g_err[0] = '\0';
   return scan_bwd(x, dt, aneg, B, C, dy, dh_last, ckpt, dx, ddt, daneg, dB, dC, workspace,
-                  workspace_bytes, batch, seqlen, d_inner, d_state, chunk, stream, Gate{});
+                  workspace_bytes, batch, seqlen, d_inner, d_state, chunk, stream, Gate{}, kF32);
 }
 
 int mhs_scan_gated_fwd_f32(const float* x, const float* dt_raw, const float* A, const float* B,
@@ -517,7 +537,7 @@ int mhs_scan_gated_fwd_f32(const float* x, const float* dt_raw, const float* A, 
   const int rc = check_gate(dt_min, dt_max, g);
   if (rc) return rc;
   return scan_fwd(x, dt_raw, A, B, C, y, ckpt, h_last, workspace, workspace_bytes, batch, seqlen,
-                  d_inner, d_state, chunk, stream, g);
+                  d_inner, d_state, chunk, stream, g, kF32);
 }
 
 int mhs_scan_gated_bwd_f32(const float* x, const float* dt_raw, const float* A, const float* B,
@@ -531,7 +551,55 @@ int mhs_scan_gated_bwd_f32(const float* x, const float* dt_raw, const float* A, 
   const int rc = check_gate(dt_min, dt_max, g);
   if (rc) return rc;
   return scan_bwd(x, dt_raw, A, B, C, dy, dh_last, ckpt, dx, ddt_raw, dA, dB, dC, workspace,
-                  workspace_bytes, batch, seqlen, d_inner, d_state, chunk, stream, g);
+                  workspace_bytes, batch, seqlen, d_inner, d_state, chunk, stream, g, kF32);
+}
+
+int mhs_scan_fwd_bf16(const uint16_t* x, const uint16_t* dt, const float* aneg, const uint16_t* B,
+                      const uint16_t* C, uint16_t* y, float* ckpt, float* h_last, void* workspace,
+                      size_t workspace_bytes, int64_t batch, int64_t seqlen, int64_t d_inner,
+                      int64_t d_state, int64_t chunk, void* stream) {
+  g_err[0] = '\0';
+  return scan_fwd(x, dt, aneg, B, C, y, ckpt, h_last, workspace, workspace_bytes, batch, seqlen,
+                  d_inner, d_state, chunk, stream, Gate{}, kBF16);
+}
+
+int mhs_scan_bwd_bf16(const uint16_t* x, const uint16_t* dt, const float* aneg, const uint16_t* B,
+                      const uint16_t* C, const uint16_t* dy, const float* dh_last,
+                      const float* ckpt, uint16_t* dx, uint16_t* ddt, float* daneg, uint16_t* dB,
+                      uint16_t* dC, void* workspace, size_t workspace_bytes, int64_t batch,
+                      int64_t seqlen, int64_t d_inner, int64_t d_state, int64_t chunk,
+                      void* stream) {
+  g_err[0] = '\0';
+  return scan_bwd(x, dt, aneg, B, C, dy, dh_last, ckpt, dx, ddt, daneg, dB, dC, workspace,
+                  workspace_bytes, batch, seqlen, d_inner, d_state, chunk, stream, Gate{}, kBF16);
+}
+
+int mhs_scan_gated_fwd_bf16(const uint16_t* x, const uint16_t* dt_raw, const float* A,
+                            const uint16_t* B, const uint16_t* C, float dt_min, float dt_max,
+                            uint16_t* y, float* ckpt, float* h_last, void* workspace,
+                            size_t workspace_bytes, int64_t batch, int64_t seqlen,
+                            int64_t d_inner, int64_t d_state, int64_t chunk, void* stream) {
+  g_err[0] = '\0';
+  Gate g;
+  const int rc = check_gate(dt_min, dt_max, g);
+  if (rc) return rc;
+  return scan_fwd(x, dt_raw, A, B, C, y, ckpt, h_last, workspace, workspace_bytes, batch, seqlen,
+                  d_inner, d_state, chunk, stream, g, kBF16);
+}
+
+int mhs_scan_gated_bwd_bf16(const uint16_t* x, const uint16_t* dt_raw, const float* A,
+                            const uint16_t* B, const uint16_t* C, float dt_min, float dt_max,
+                            const uint16_t* dy, const float* dh_last, const float* ckpt,
+                            uint16_t* dx, uint16_t* ddt_raw, float* dA, uint16_t* dB,
+                            uint16_t* dC, void* workspace, size_t workspace_bytes, int64_t batch,
+                            int64_t seqlen, int64_t d_inner, int64_t d_state, int64_t chunk,
+                            void* stream) {
+  g_err[0] = '\0';
+  Gate g;
+  const int rc = check_gate(dt_min, dt_max, g);
+  if (rc) return rc;
+  return scan_bwd(x, dt_raw, A, B, C, dy, dh_last, ckpt, dx, ddt_raw, dA, dB, dC, workspace,
+                  workspace_bytes, batch, seqlen, d_inner, d_state, chunk, stream, g, kBF16);
 }
 
 int mhs_scan_step_f32(float* h, const float* x, const float* dt, const float* aneg, const float* B,

@@ -232,6 +232,40 @@ struct GBuf {
   }
 };
 
+// Element storage of the (batch, T, D) and (batch, T, N) activations: fp32
+// (ES = 4) or bf16 (ES = 2, the upper half of an fp32: loads widen exactly,
+// stores round to nearest even). Arithmetic is fp32 either way; states,
+// checkpoints and Aneg are always fp32.
+__device__ __forceinline__ unsigned short f32_to_bf16(float v) {
+  const unsigned u = __float_as_uint(v);
+  if ((u & 0x7fffffffu) > 0x7f800000u) return (unsigned short)((u >> 16) | 0x40u);   // quiet NaN
+  return (unsigned short)((u + 0x7fffu + ((u >> 16) & 1u)) >> 16);
+}
+template <int ES, int POL = 0>
+__device__ __forceinline__ float ld_elem(const GBuf& g, unsigned byte_off) {
+  static_assert(ES == 4 || ES == 2, "fp32 or bf16 elements");
+  if constexpr (ES == 4) {
+    return g.ld<POL>(byte_off);
+  } else {
+    return __uint_as_float((unsigned)__builtin_amdgcn_raw_buffer_load_b16(g.r, byte_off, 0, POL)
+                           << 16);
+  }
+}
+template <int ES, int POL = 0>
+__device__ __forceinline__ void st_elem(const GBuf& g, float v, unsigned byte_off) {
+  if constexpr (ES == 4) {
+    g.st<POL>(v, byte_off);
+  } else {
+    __builtin_amdgcn_raw_buffer_store_b16(f32_to_bf16(v), g.r, byte_off, 0, POL);
+  }
+}
+// Element idx of an activation tensor of ES-byte elements, as the float
+// pointer GBuf takes (a byte address; only GBuf dereferences it).
+template <int ES>
+__device__ __forceinline__ const float* elem_at(const void* base, size_t idx) {
+  return reinterpret_cast<const float*>(static_cast<const char*>(base) + idx * ES);
+}
+
 // NPL consecutive states of one lane at byte offset `off` (kOOB: none);
 // states at or beyond `nvalid` are padding and are not stored.
 template <int NPL, int POL = 0>
@@ -256,7 +290,7 @@ __device__ __forceinline__ void sts4(float* p, float4 v) { *reinterpret_cast<flo
 // numbered c-fastest so that each load instruction reads consecutive
 // channels. Thread tid owns tasks tid, tid+nthreads, ... (PER of them; tasks
 // beyond TASKS and channels beyond d_inner load zeros).
-template <int CH, int PER>
+template <int CH, int PER, int ES = 4>
 struct QuadLoader {
   static constexpr int TASKS = CH * kQuads;
   int tid, nthreads;
@@ -267,8 +301,9 @@ struct QuadLoader {
     for (int i = 0; i < PER; ++i) {
       const int e = tid + i * nthreads;
       const int c = e % CH, m = e / CH;
-      toff[i] = (e < TASKS && d0 + c < D) ? 4u * ((unsigned)(4 * m) * (unsigned)D + (unsigned)c)
-                                          : kOOB;
+      toff[i] = (e < TASKS && d0 + c < D)
+                    ? (unsigned)ES * ((unsigned)(4 * m) * (unsigned)D + (unsigned)c)
+                    : kOOB;
     }
   }
   __device__ __forceinline__ bool valid(int i) const { return tid + i * nthreads < TASKS; }
@@ -278,15 +313,15 @@ struct QuadLoader {
   // are out of range).
   template <int POL = 0>
   __device__ __forceinline__ void load(float4 (&v)[PER], const GBuf& g, int D) const {
-    const unsigned rs = 4u * (unsigned)D;
+    const unsigned rs = (unsigned)ES * (unsigned)D;
 #pragma unroll
     for (int i = 0; i < PER; ++i) {
       const unsigned o = toff[i];
       const bool ok = o != kOOB;
-      v[i].x = g.ld<POL>(o);
-      v[i].y = g.ld<POL>(ok ? o + rs : kOOB);
-      v[i].z = g.ld<POL>(ok ? o + 2 * rs : kOOB);
-      v[i].w = g.ld<POL>(ok ? o + 3 * rs : kOOB);
+      v[i].x = ld_elem<ES, POL>(g, o);
+      v[i].y = ld_elem<ES, POL>(g, ok ? o + rs : kOOB);
+      v[i].z = ld_elem<ES, POL>(g, ok ? o + 2 * rs : kOOB);
+      v[i].w = ld_elem<ES, POL>(g, ok ? o + 3 * rs : kOOB);
     }
   }
   // Gate staged dt values in place: dt = lo + span * sigmoid(raw) for the
@@ -348,7 +383,7 @@ struct QuadLoader {
 // q reads NPL states of 4 steps as NPL float4s at q*16*NPL + 4*m*NPL.
 // Thread tid moves tile elements tid, tid+nthreads, ... (PERS of them);
 // padded states and steps past T are zero.
-template <int PERS, int NPL>
+template <int PERS, int NPL, int ES = 4>
 struct RowLoader {
   unsigned src[PERS];  // byte offset in the sub-chunk's global [16][N] block, or kOOB
   int dst[PERS];       // slot in the tile, or -1
@@ -358,13 +393,13 @@ struct RowLoader {
       const int e = tid + i * nthreads;       // tile element (k, n), n fastest
       const int k = e / NP, n = e % NP;
       const bool in_tile = e < kSteps * NP;
-      src[i] = (in_tile && n < N) ? 4u * (unsigned)(k * N + n) : kOOB;
+      src[i] = (in_tile && n < N) ? (unsigned)ES * (unsigned)(k * N + n) : kOOB;
       dst[i] = in_tile ? (n / NPL) * (kSteps * NPL) + k * NPL + (n % NPL) : -1;
     }
   }
   __device__ __forceinline__ void load(float (&v)[PERS], const GBuf& g) const {
 #pragma unroll
-    for (int i = 0; i < PERS; ++i) v[i] = g.ld(src[i]);
+    for (int i = 0; i < PERS; ++i) v[i] = ld_elem<ES>(g, src[i]);
   }
   __device__ __forceinline__ void store(float* tile, const float (&v)[PERS]) const {
 #pragma unroll

@@ -33,12 +33,13 @@
 namespace mhs {
 
 struct FwdArgs {
-  const float* x;
-  const float* dt;
+  // x, dt, B, C, y: ES-byte elements (fp32 or bf16, see the kernel's ES).
+  const void* x;
+  const void* dt;
   const float* aneg;
-  const float* B;
-  const float* C;
-  float* y;        // may be null: then no y traffic at all
+  const void* B;
+  const void* C;
+  void* y;         // may be null: then no y traffic at all
   float* ckpt;     // may be null
   float* h_last;   // may be null
   int T, D, N, K, nchunk;
@@ -84,7 +85,8 @@ __host__ __device__ constexpr int fwd_lds_floats(int G, int NPL) {
 // FCARRY: the carry pass of the time segments (see FwdArgs): blocks of
 // segments 0..nseg-2 scan their segment from zero and write only its end
 // state and sum of dt (no C, no y, no checkpoints).
-template <int NPL, int G, int MINW, bool KALIGNED, bool GATED, bool FCARRY = false>
+// ES: bytes per element of x, dt, B, C and y (4: fp32, 2: bf16).
+template <int NPL, int G, int MINW, bool KALIGNED, bool GATED, bool FCARRY = false, int ES = 4>
 __global__ void __launch_bounds__(64 * G, MINW)
 fwd_kernel(FwdArgs a) {
   constexpr int NT = 64 * G;                    // threads
@@ -121,8 +123,8 @@ fwd_kernel(FwdArgs a) {
   }
 
   const size_t row0 = (size_t)b * T;
-  const QuadLoader<kCH, PER> ql(tid, NT, D, d0);
-  const RowLoader<PERS, NPL> rl(tid, NT, N, NP);
+  const QuadLoader<kCH, PER, ES> ql(tid, NT, D, d0);
+  const RowLoader<PERS, NPL, ES> rl(tid, NT, N, NP);
   float4 px[PER], pd[PER];
   float pb[PERS], pc[PERS];
   // Sub-chunk i of the segment (any i >= 0): first step and length (0 past
@@ -132,16 +134,17 @@ fwd_kernel(FwdArgs a) {
     return i < 0 ? 0 : max(0, min(kSteps, t_end - t_beg - i * kSteps));
   };
   // Resource over one sub-chunk of a (batch, T, D) tensor from channel d0 on.
-  auto sub_buf = [&](const float* base, int i) {
+  auto sub_buf = [&](const void* base, int i) {
     const int len = sub_len(i);
-    return GBuf(base + (row0 + sub_t0(i)) * D + d0, len > 0 ? 4u * (unsigned)(len * D - d0) : 0u);
+    return GBuf(elem_at<ES>(base, (row0 + sub_t0(i)) * D + d0),
+                len > 0 ? (unsigned)ES * (unsigned)(len * D - d0) : 0u);
   };
   auto load_sub = [&](int i) {            // global -> staging registers
-    const unsigned sbytes = 4u * (unsigned)(sub_len(i) * N);
+    const unsigned sbytes = (unsigned)ES * (unsigned)(sub_len(i) * N);
     ql.load(px, sub_buf(a.x, i), D);
     ql.load(pd, sub_buf(a.dt, i), D);
-    rl.load(pb, GBuf(a.B + (row0 + sub_t0(i)) * N, sbytes));
-    if constexpr (!FCARRY) rl.load(pc, GBuf(a.C + (row0 + sub_t0(i)) * N, sbytes));
+    rl.load(pb, GBuf(elem_at<ES>(a.B, (row0 + sub_t0(i)) * N), sbytes));
+    if constexpr (!FCARRY) rl.load(pc, GBuf(elem_at<ES>(a.C, (row0 + sub_t0(i)) * N), sbytes));
   };
   auto store_sub = [&](int i) {           // staging registers -> LDS buffer i&1
     float* buf = lds + (i & 1) * BUF;
@@ -187,9 +190,10 @@ fwd_kernel(FwdArgs a) {
         sum.x += ypart[f][q2].x;
         sum.y += ypart[f][q2].y;
       }
-      const unsigned o = (ok && d0 + cc < D) ? 4u * ((unsigned)(2 * p) * (unsigned)D + cc) : kOOB;
-      yo.st<kStream>(sum.x, o);                          // y: written once (NT)
-      yo.st<kStream>(sum.y, o != kOOB ? o + 4u * (unsigned)D : kOOB);
+      const unsigned o =
+          (ok && d0 + cc < D) ? (unsigned)ES * ((unsigned)(2 * p) * (unsigned)D + cc) : kOOB;
+      st_elem<ES, kStream>(yo, sum.x, o);                // y: written once (NT)
+      st_elem<ES, kStream>(yo, sum.y, o != kOOB ? o + (unsigned)ES * (unsigned)D : kOOB);
     }
   };
 
@@ -225,7 +229,7 @@ fwd_kernel(FwdArgs a) {
   constexpr int kDone = 0x7FFFFFFF;
   // Step count after the next checkpoint, and its slot.
   int next_ck = a.ckpt != nullptr ? min((t_beg / a.K + 1) * a.K, T) : kDone;
-  const float* ck_base = a.ckpt != nullptr ? a.ckpt + (size_t)b * a.nchunk * ck_stride : a.x;
+  const float* ck_base = a.ckpt != nullptr ? a.ckpt + (size_t)b * a.nchunk * ck_stride : a.aneg;
   const float* ck_ptr = ck_base + (size_t)(t_beg / a.K) * ck_stride;
   for (int i = 0; i < nsub; ++i) {
     const int t0 = t_beg + i * kSteps;

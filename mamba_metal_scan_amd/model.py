@@ -195,13 +195,19 @@ class MambaBlock(nn.Module):
         scan_impl other than 'torch'."""
         return self.scan_impl != "torch" and _hip_device(t) and t.dtype == torch.float32
 
+    def _fused_scan(self, t) -> bool:
+        """The gated HIP scan also takes bf16 activations (fp32 state), e.g.
+        under autocast."""
+        return (self.scan_impl != "torch" and _hip_device(t)
+                and t.dtype in (torch.float32, torch.bfloat16))
+
     def _scan(self, x, return_state=False):
         """y_t = sum_n C_tn h_tn over the selective recurrence (+ final state).
 
         On a ROCm device the dt gate and softplus(A) of _proj run inside the
         scan kernels (selective_scan_gated): the same function as _proj followed
         by selective_scan (mamba_metal/model.py:197-200, :213-215)."""
-        if self._fused(x):
+        if self._fused_scan(x):
             return selective_scan_gated(x, self.dt_proj(x), self.A, self.B_proj(x),
                                         self.C_proj(x), self.dt_min, self.dt_max,
                                         chunk=self.ckpt_chunk, return_state=return_state)

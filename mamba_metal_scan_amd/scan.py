@@ -90,8 +90,11 @@ def _validate(x, dt, aneg, b_in, c_in, chunk) -> None:
     if len({t.device for t in tensors}) != 1:
         raise RuntimeError("scan_impl='hip' needs every input on the same device; saw "
                            + ", ".join(str(t.device) for t in tensors))
-    if not all(t.dtype == torch.float32 for t in tensors):
-        raise RuntimeError("scan_impl='hip' is fp32-only (the kernels are float32); got "
+    acts = (x, dt, b_in, c_in)
+    if aneg.dtype != torch.float32 or not (all(t.dtype == torch.float32 for t in acts)
+                                           or all(t.dtype == torch.bfloat16 for t in acts)):
+        raise RuntimeError("scan_impl='hip' takes fp32 tensors, or bf16 x, dt, B, C with an "
+                           "fp32 Aneg (fp32 state and arithmetic either way); got "
                            + ", ".join(str(t.dtype) for t in tensors))
     if x.dim() != 3 or dt.shape != x.shape or aneg.dim() != 2:
         raise ValueError(f"bad shapes: x {tuple(x.shape)}, dt {tuple(dt.shape)}, "
