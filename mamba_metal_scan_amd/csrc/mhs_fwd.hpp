@@ -72,7 +72,7 @@ constexpr int kCH = 32;   // channels per block
 __host__ __device__ constexpr int fwd_buf_floats(int G, int NPL) {
   return 2 * kCH * kSteps               // dt, dt*x tiles (channel-major)
          + 2 * kSteps * 2 * G * NPL     // B, C tiles
-         + G * 64 * kSteps;             // per-lane y partials
+         + G * kCH * kSteps;            // per-wave y partials (both half-waves added)
 }
 __host__ __device__ constexpr int fwd_lds_floats(int G, int NPL) {
   return 2 * fwd_buf_floats(G, NPL);
@@ -154,14 +154,15 @@ fwd_kernel(FwdArgs a) {
     rl.store(buf + 2 * kCH * kSteps, pb);
     if constexpr (!FCARRY) rl.store(buf + 2 * kCH * kSteps + kSteps * NP, pc);
   };
-  // y of sub-chunk i: task (channel cc, step pair p) sums the partials of
-  // its two steps over the 2G lane groups in a fixed order (64-bit reads).
-  // There are 32 x 8 = 256 tasks: one per thread at G = 4. Split in two so
-  // that the LDS reads (y_read) and their use (y_write) sit in different
-  // scheduling regions.
+  // y of sub-chunk i: every wave leaves, per channel and step, the sum over
+  // its two half-waves (added in registers); task (channel cc, step pair p)
+  // sums those over the G waves in a fixed order (64-bit reads). There are
+  // 32 x 8 = 256 tasks: one per thread at G = 4. Split in two so that the LDS
+  // reads (y_read) and their use (y_write) sit in different scheduling
+  // regions.
   constexpr int YTASKS = kCH * kSteps / 2;
   constexpr int YT = (YTASKS + NT - 1) / NT;             // y tasks per thread
-  float2 ypart[YT][2 * G];
+  float2 ypart[YT][G];
   auto y_read = [&](int i) {
     const float* yp = lds + (i & 1) * BUF + 2 * kCH * kSteps + 2 * kSteps * NP;
 #pragma unroll
@@ -170,10 +171,7 @@ fwd_kernel(FwdArgs a) {
       const int t = t0 < YTASKS ? t0 : 0;
       const int cc = t % kCH, p = t / kCH;
 #pragma unroll
-      for (int w = 0; w < G; ++w)
-#pragma unroll
-        for (int h2 = 0; h2 < 2; ++h2)
-          ypart[f][2 * w + h2] = lds2(yp + w * 64 * kSteps + cm_elem(h2 * kCH + cc, 2 * p));
+      for (int w = 0; w < G; ++w) ypart[f][w] = lds2(yp + w * kCH * kSteps + cm_elem(cc, 2 * p));
     }
   };
   auto y_write = [&](int i) {
@@ -186,7 +184,7 @@ fwd_kernel(FwdArgs a) {
       const int cc = t % kCH, p = t / kCH;
       float2 sum = ypart[f][0];
 #pragma unroll
-      for (int q2 = 1; q2 < 2 * G; ++q2) {
+      for (int q2 = 1; q2 < G; ++q2) {
         sum.x += ypart[f][q2].x;
         sum.y += ypart[f][q2].y;
       }
@@ -238,7 +236,7 @@ fwd_kernel(FwdArgs a) {
     const float* cBX = buf + kCH * kSteps;
     const float* gB = buf + 2 * kCH * kSteps + q * kSteps * NPL;
     const float* gC = buf + 2 * kCH * kSteps + kSteps * NP + q * kSteps * NPL;
-    float* myY = lds + (i & 1) * BUF + 2 * kCH * kSteps + 2 * kSteps * NP + wave * 64 * kSteps;
+    float* myY = lds + (i & 1) * BUF + 2 * kCH * kSteps + 2 * kSteps * NP + wave * kCH * kSteps;
 
     // A quad's LDS operands, read one quad ahead of their use.
     float4 qdt, qbx, qB[NPL], qC[NPL];
@@ -290,7 +288,17 @@ fwd_kernel(FwdArgs a) {
         }
         yq[s] = acc;
       }
-      if constexpr (!FCARRY) sts4(myY + cm_quad(lane, m), make_float4(yq[0], yq[1], yq[2], yq[3]));
+      if constexpr (!FCARRY) {
+        // Add the two half-waves (same channels, different states): lanes
+        // 0-31 end with steps 0, 1 of the quad, lanes 32-63 with steps 2, 3.
+        const auto s02 = __builtin_amdgcn_permlane32_swap(__float_as_uint(yq[0]),
+                                                          __float_as_uint(yq[2]), false, false);
+        const auto s13 = __builtin_amdgcn_permlane32_swap(__float_as_uint(yq[1]),
+                                                          __float_as_uint(yq[3]), false, false);
+        *reinterpret_cast<float2*>(myY + cm_quad(c, m) + 2 * hh) =
+            make_float2(__uint_as_float(s02[0]) + __uint_as_float(s02[1]),
+                        __uint_as_float(s13[0]) + __uint_as_float(s13[1]));
+      }
 
       // Pipeline work for the neighbouring sub-chunks, in this quad's
       // scheduling region. Unconditional: past either end of the sequence the
