@@ -10,6 +10,8 @@ import os
 import shutil
 import subprocess
 import sys
+import tempfile
+from concurrent.futures import ThreadPoolExecutor
 from pathlib import Path
 
 PKG_DIR = Path(__file__).resolve().parent
@@ -19,9 +21,12 @@ LIB_NAME = "libmamba_hip_scan.so"
 LIB_PATH = PKG_DIR / LIB_NAME
 ARCH = "gfx950"
 
-SOURCES = ["mhs_capi.hip"]
+# The host code and small kernels, and the scan kernels' instantiations in
+# four units (forward / backward x fp32 / bf16) compiled in parallel.
+SOURCES = ["mhs_capi.hip", "mhs_kern_fwd_f32.hip", "mhs_kern_fwd_bf16.hip",
+           "mhs_kern_bwd_f32.hip", "mhs_kern_bwd_bf16.hip"]
 HEADERS = ["mhs_common.hpp", "mhs_fwd.hpp", "mhs_bwd.hpp", "mhs_step.hpp", "mhs_conv.hpp",
-           "mhs_gate.hpp"]
+           "mhs_gate.hpp", "mhs_instances.hpp"]
 
 
 def hipcc() -> str:
@@ -41,12 +46,7 @@ def compile_flags() -> list[str]:
     ]
 
 
-def build_library(verbose: bool = False, out: Path | None = None) -> Path:
-    """Compile csrc/*.hip into the in-tree shared library; returns its path."""
-    out = Path(out) if out is not None else LIB_PATH
-    tmp = out.with_suffix(".so.tmp")
-    cmd = [hipcc(), *compile_flags(), "-shared", "-o", str(tmp),
-           *[str(CSRC / s) for s in SOURCES]]
+def _run(cmd: list[str], verbose: bool) -> None:
     if verbose:
         print(" ".join(cmd), flush=True)
     res = subprocess.run(cmd, capture_output=True, text=True)
@@ -56,6 +56,23 @@ def build_library(verbose: bool = False, out: Path | None = None) -> Path:
     msgs = [ln for ln in (res.stdout + res.stderr).splitlines() if noise not in ln and ln.strip()]
     if verbose and msgs:
         print("\n".join(msgs), file=sys.stderr)
+
+
+def build_library(verbose: bool = False, out: Path | None = None) -> Path:
+    """Compile csrc/*.hip into the in-tree shared library; returns its path.
+
+    Each source compiles to an object in a temporary folder, in parallel;
+    hipcc then links them into the library."""
+    out = Path(out) if out is not None else LIB_PATH
+    tmp = out.with_suffix(".so.tmp")
+    with tempfile.TemporaryDirectory(prefix="mhs_build_") as objdir:
+        objs = [str(Path(objdir) / (Path(src).stem + ".o")) for src in SOURCES]
+        cmds = [[hipcc(), *compile_flags(), "-c", "-o", obj, str(CSRC / src)]
+                for src, obj in zip(SOURCES, objs)]
+        with ThreadPoolExecutor(max_workers=min(len(cmds), os.cpu_count() or 1)) as pool:
+            for f in [pool.submit(_run, c, verbose) for c in cmds]:
+                f.result()
+        _run([hipcc(), *compile_flags(), "-shared", "-o", str(tmp), *objs], verbose)
     os.replace(tmp, out)
     return out
 

@@ -19,7 +19,16 @@
 #include "mhs_conv.hpp"
 #include "mhs_fwd.hpp"
 #include "mhs_gate.hpp"
+#include "mhs_instances.hpp"
 #include "mhs_step.hpp"
+
+// The scan kernels are instantiated in the mhs_kern_*.hip units.
+namespace mhs {
+MHS_FOR_PLANS(MHS_FWD_INST, extern, 4)
+MHS_FOR_PLANS(MHS_FWD_INST, extern, 2)
+MHS_FOR_PLANS(MHS_BWD_INST, extern, 4)
+MHS_FOR_PLANS(MHS_BWD_INST, extern, 2)
+}  // namespace mhs
 
 namespace {
 

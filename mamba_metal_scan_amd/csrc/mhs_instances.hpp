@@ -1,0 +1,36 @@
+// The scan kernels' instantiations, listed once. mhs_capi.hip declares them
+// `extern template` and takes their addresses; the mhs_kern_*.hip units define
+// them, so that the four groups compile in parallel.
+//
+// Plans: NPL states per lane in {2, 4}, G waves in 1..8, MINW the
+// waves-per-SIMD target (3 for NPL 2, 2 for NPL 4). ES: element bytes of the
+// activations (4: fp32, 2: bf16).
+#pragma once
+
+#include "mhs_bwd.hpp"
+#include "mhs_fwd.hpp"
+
+#define MHS_FOR_PLANS(X, PREFIX, ES)                                                   \
+  X(PREFIX, 2, 1, 3, ES) X(PREFIX, 2, 2, 3, ES) X(PREFIX, 2, 3, 3, ES)                 \
+  X(PREFIX, 2, 4, 3, ES) X(PREFIX, 2, 5, 3, ES) X(PREFIX, 2, 6, 3, ES)                 \
+  X(PREFIX, 2, 7, 3, ES) X(PREFIX, 2, 8, 3, ES)                                        \
+  X(PREFIX, 4, 1, 2, ES) X(PREFIX, 4, 2, 2, ES) X(PREFIX, 4, 3, 2, ES)                 \
+  X(PREFIX, 4, 4, 2, ES) X(PREFIX, 4, 5, 2, ES) X(PREFIX, 4, 6, 2, ES)                 \
+  X(PREFIX, 4, 7, 2, ES) X(PREFIX, 4, 8, 2, ES)
+
+// Forward: checkpoint stride aligned / any, ungated / gated, and the carry
+// pass of the time segments (ungated / gated).
+#define MHS_FWD_INST(PREFIX, NPL, G, MINW, ES)                                                 \
+  PREFIX template __global__ void fwd_kernel<NPL, G, MINW, true, false, false, ES>(FwdArgs);   \
+  PREFIX template __global__ void fwd_kernel<NPL, G, MINW, false, false, false, ES>(FwdArgs);  \
+  PREFIX template __global__ void fwd_kernel<NPL, G, MINW, true, true, false, ES>(FwdArgs);    \
+  PREFIX template __global__ void fwd_kernel<NPL, G, MINW, false, true, false, ES>(FwdArgs);   \
+  PREFIX template __global__ void fwd_kernel<NPL, G, MINW, true, false, true, ES>(FwdArgs);    \
+  PREFIX template __global__ void fwd_kernel<NPL, G, MINW, true, true, true, ES>(FwdArgs);
+
+// Backward: ungated / gated, gradient pass / adjoint-carry pass.
+#define MHS_BWD_INST(PREFIX, NPL, G, MINW, ES)                                    \
+  PREFIX template __global__ void bwd_kernel<NPL, G, MINW, false, false, ES>(BwdArgs); \
+  PREFIX template __global__ void bwd_kernel<NPL, G, MINW, true, false, ES>(BwdArgs);  \
+  PREFIX template __global__ void bwd_kernel<NPL, G, MINW, false, true, ES>(BwdArgs);  \
+  PREFIX template __global__ void bwd_kernel<NPL, G, MINW, true, true, ES>(BwdArgs);

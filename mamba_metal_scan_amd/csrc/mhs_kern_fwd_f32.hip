@@ -1,0 +1,6 @@
+// Instantiations of the fwd scan kernels for f32 activations (see mhs_instances.hpp).
+#include "mhs_instances.hpp"
+
+namespace mhs {
+MHS_FOR_PLANS(MHS_FWD_INST, , 4)
+}  // namespace mhs
