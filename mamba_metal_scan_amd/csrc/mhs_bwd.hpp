@@ -183,6 +183,12 @@ bwd_kernel(BwdArgs a) {
       for (int j = 0; j < NPL; ++j) u[j] = __builtin_fmaf(exp2_hw(sdt * a2[j]), u[j], lv[j]);
     }
   }
+  // u (dh_last) and Aneg come from loads before the walk.
+#pragma unroll
+  for (int j = 0; j < NPL; ++j) {
+    u[j] = opaque_copy(u[j]);
+    an[j] = opaque_copy(an[j]);
+  }
   float sdt_acc = 0.f;   // CARRY: sum of dt over the segment
 
   const size_t row0 = (size_t)b * T;
@@ -287,7 +293,7 @@ bwd_kernel(BwdArgs a) {
   store_sub(0, c_hi - 1);
   if constexpr (!CARRY) {
 #pragma unroll
-    for (int j = 0; j < NPL; ++j) hc[j] = ph[j];
+    for (int j = 0; j < NPL; ++j) hc[j] = opaque_copy(ph[j]);
   }
   load_sub(c_hi - 2);
   if constexpr (!CARRY) load_h0(c_hi - 2);
@@ -295,6 +301,7 @@ bwd_kernel(BwdArgs a) {
 
   const int nit = c_hi - c_lo;
   for (int i = 0; i < nit; ++i) {
+    progress_priority(i, nit);
     const int ci = c_hi - 1 - i;
     const float* s0 = lds + (i & 1) * BUF;
     const float* gB = s0 + oB + q * kSteps * NPL;
@@ -399,7 +406,7 @@ bwd_kernel(BwdArgs a) {
     // result, i.e. wait for it, and vmcnt being in order, for every load and
     // store still in flight: a full memory drain per chunk.
 #pragma unroll
-    for (int j = 0; j < NPL; ++j) asm volatile("v_mov_b32 %0, %1" : "=v"(hc[j]) : "v"(ph[j]));
+    for (int j = 0; j < NPL; ++j) hc[j] = opaque_copy(ph[j]);
     load_h0(ci - 2);
     __syncthreads();   // tS / tDBC complete; chunk ci-1 staged
   }

@@ -88,6 +88,52 @@ __device__ __forceinline__ void rs_stage_dpp(const float (&v)[M], float (&o)[M /
   }
 }
 
+// The reduce-scatter stages over lane bits 3 and 2 as bank-masked DPP adds
+// (a bank is 4 lanes of a 16-lane row; bit 3 splits banks {0,1} from {2,3},
+// bit 2 banks {0,2} from {1,3}): the pair (x, y) becomes x + x' in the banks
+// whose bit is 0 and y + y' in the others (x' the partner's x: row_ror:8 is
+// lane i <-> i^8, row_half_mirror lane i <-> 7-i), two instructions per
+// pair. Same sums, in the same order, as rs_stage_dpp (a + b == b + a).
+// The s_nop's give the 2 wait states a DPP read of a VGPR needs after a VALU
+// write of it (the compiler does not look inside the asm): before the first
+// reads of inputs written by compiled code, between the two stages, and
+// after the block for compiled DPP reads of its outputs.
+__device__ __forceinline__ float rs_bits32_8(const float (&a)[4]) {
+  float b0, b1, c;
+  asm("s_nop 1\n\t"
+      "v_add_f32_dpp %1, %3, %3 row_ror:8 row_mask:0xf bank_mask:0x3\n\t"
+      "v_add_f32_dpp %1, %4, %4 row_ror:8 row_mask:0xf bank_mask:0xc\n\t"
+      "v_add_f32_dpp %2, %5, %5 row_ror:8 row_mask:0xf bank_mask:0x3\n\t"
+      "v_add_f32_dpp %2, %6, %6 row_ror:8 row_mask:0xf bank_mask:0xc\n\t"
+      "s_nop 0\n\t"
+      "v_add_f32_dpp %0, %1, %1 row_half_mirror row_mask:0xf bank_mask:0x5\n\t"
+      "v_add_f32_dpp %0, %2, %2 row_half_mirror row_mask:0xf bank_mask:0xa\n\t"
+      "s_nop 1"
+      : "=&v"(c), "=&v"(b0), "=&v"(b1)
+      : "v"(a[0]), "v"(a[1]), "v"(a[2]), "v"(a[3]));
+  return c;
+}
+__device__ __forceinline__ void rs_bits32_16(const float (&a)[8], float (&c)[2]) {
+  float b0, b1, b2, b3;
+  asm("s_nop 1\n\t"
+      "v_add_f32_dpp %2, %6, %6 row_ror:8 row_mask:0xf bank_mask:0x3\n\t"
+      "v_add_f32_dpp %2, %7, %7 row_ror:8 row_mask:0xf bank_mask:0xc\n\t"
+      "v_add_f32_dpp %3, %8, %8 row_ror:8 row_mask:0xf bank_mask:0x3\n\t"
+      "v_add_f32_dpp %3, %9, %9 row_ror:8 row_mask:0xf bank_mask:0xc\n\t"
+      "v_add_f32_dpp %4, %10, %10 row_ror:8 row_mask:0xf bank_mask:0x3\n\t"
+      "v_add_f32_dpp %4, %11, %11 row_ror:8 row_mask:0xf bank_mask:0xc\n\t"
+      "v_add_f32_dpp %5, %12, %12 row_ror:8 row_mask:0xf bank_mask:0x3\n\t"
+      "v_add_f32_dpp %5, %13, %13 row_ror:8 row_mask:0xf bank_mask:0xc\n\t"
+      "v_add_f32_dpp %0, %2, %2 row_half_mirror row_mask:0xf bank_mask:0x5\n\t"
+      "v_add_f32_dpp %0, %3, %3 row_half_mirror row_mask:0xf bank_mask:0xa\n\t"
+      "v_add_f32_dpp %1, %4, %4 row_half_mirror row_mask:0xf bank_mask:0x5\n\t"
+      "v_add_f32_dpp %1, %5, %5 row_half_mirror row_mask:0xf bank_mask:0xa\n\t"
+      "s_nop 1"
+      : "=&v"(c[0]), "=&v"(c[1]), "=&v"(b0), "=&v"(b1), "=&v"(b2), "=&v"(b3)
+      : "v"(a[0]), "v"(a[1]), "v"(a[2]), "v"(a[3]), "v"(a[4]), "v"(a[5]), "v"(a[6]),
+        "v"(a[7]));
+}
+
 // Sums M values (M in {8, 16}) over the 32 lanes of each half-wave, as a
 // reduce-scatter: v_permlane16_swap across lane bit 4, then DPP row_ror:8
 // (bit 3), row_half_mirror (bit 2) and quad_perm xor 2 (bit 1), each halving
@@ -104,10 +150,12 @@ __device__ __forceinline__ float half_wave_reduce_scatter(const float (&v)[M], i
                                                     __float_as_uint(v[2 * i + 1]), false, false);
     a[i] = __uint_as_float(sw[0]) + __uint_as_float(sw[1]);
   }
-  float b[M / 4];
-  rs_stage_dpp<kDppRor8>(a, b, (lane >> 3) & 1);
   float c[M / 8];
-  rs_stage_dpp<kDppHalfMirror>(b, c, (lane >> 2) & 1);
+  if constexpr (M == 8) {
+    c[0] = rs_bits32_8(a);
+  } else {
+    rs_bits32_16(a, c);
+  }
   float r;
   if constexpr (M == 8) {
     r = dpp_add<kDppXor2>(c[0]);
@@ -132,6 +180,33 @@ __device__ __forceinline__ void wave_lds_sync() {
   __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
   __builtin_amdgcn_wave_barrier();
   __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+}
+
+// Wave issue priority from progress: 3 in the first quarter of a block's
+// iterations, then 2, 1, 0. A CU holds several blocks that all run the whole
+// sequence; the issue arbiter favours the oldest waves at equal priority, so
+// without this the blocks of a CU finish one after the other and the last
+// one runs its final stretch alone, its latencies no longer hidden by other
+// waves. A block ahead of the others drops below them and yields its issue
+// slots until they catch up. (The wave's own arbitration priority only.)
+__device__ __forceinline__ void progress_priority(int i, int n) {
+  const int q = (10 * i) / max(n, 1);
+  if (q < 4) __builtin_amdgcn_s_setprio(3);
+  else if (q < 7) __builtin_amdgcn_s_setprio(2);
+  else if (q < 9) __builtin_amdgcn_s_setprio(1);
+  else __builtin_amdgcn_s_setprio(0);
+}
+
+// An opaque register copy. A loop-carried value that comes from a global
+// load on some path into the loop (a state or parameter read before it) is
+// copied once before the loop: the wait for the load is then placed at the
+// copy, once, instead of at the value's first use inside the loop, where it
+// would be repeated every iteration and, the counter being in order, would
+// also wait for every later load or store still in flight.
+__device__ __forceinline__ float opaque_copy(float v) {
+  float r;
+  asm volatile("v_mov_b32 %0, %1" : "=v"(r) : "v"(v));
+  return r;
 }
 
 // Compiler-only memory clobber: values read from LDS before this point are
@@ -285,6 +360,15 @@ __device__ __forceinline__ void load_states(float (&v)[NPL], const GBuf& g, unsi
 
 __device__ __forceinline__ void sts4(float* p, float4 v) { *reinterpret_cast<float4*>(p) = v; }
 
+// Marks loaded registers as used here, without an instruction: the wait for
+// their loads is placed at this point on every path, also on the paths where
+// a branch skipped their real use (threads without a staging task), rather
+// than at a later reuse of the registers, where the in-order counter would
+// make it wait for every later load or store in flight as well.
+__device__ __forceinline__ void consume(const float4& v) {
+  asm volatile("" ::"v"(v.x), "v"(v.y), "v"(v.z), "v"(v.w));
+}
+
 // Staging of one sub-chunk of a (batch, T, D) tensor for the block's CH
 // channels: task (c, quad m) holds steps 4m..4m+3 of channel d0+c. Tasks are
 // numbered c-fastest so that each load instruction reads consecutive
@@ -341,16 +425,21 @@ struct QuadLoader {
   // Channel-major swizzled tile [CH][16].
   __device__ __forceinline__ void store_cm(float* tile, const float4 (&v)[PER]) const {
 #pragma unroll
-    for (int i = 0; i < PER; ++i)
+    for (int i = 0; i < PER; ++i) {
       if (valid(i)) sts4(tile + cm_quad(chan(i), quad(i)), v[i]);
+      consume(v[i]);
+    }
   }
   __device__ __forceinline__ void store_cm_product(float* tile, const float4 (&a)[PER],
                                                    const float4 (&b)[PER]) const {
 #pragma unroll
-    for (int i = 0; i < PER; ++i)
+    for (int i = 0; i < PER; ++i) {
       if (valid(i))
         sts4(tile + cm_quad(chan(i), quad(i)),
              make_float4(a[i].x * b[i].x, a[i].y * b[i].y, a[i].z * b[i].z, a[i].w * b[i].w));
+      consume(a[i]);
+      consume(b[i]);
+    }
   }
   // Step-major tile [16][CH] (consecutive channels contiguous).
   __device__ __forceinline__ void store_sm(float* tile, const float4 (&v)[PER]) const {
@@ -403,8 +492,10 @@ struct RowLoader {
   }
   __device__ __forceinline__ void store(float* tile, const float (&v)[PERS]) const {
 #pragma unroll
-    for (int i = 0; i < PERS; ++i)
+    for (int i = 0; i < PERS; ++i) {
       if (dst[i] >= 0) tile[dst[i]] = v[i];
+      asm volatile("" ::"v"(v[i]));   // as consume(): the wait happens here on every path
+    }
   }
 };
 

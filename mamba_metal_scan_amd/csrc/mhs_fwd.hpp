@@ -223,6 +223,8 @@ fwd_kernel(FwdArgs a) {
       for (int j = 0; j < NPL; ++j) h[j] = __builtin_fmaf(exp2_hw(sdt * a2[j]), h[j], hv[j]);
     }
   }
+#pragma unroll
+  for (int j = 0; j < NPL; ++j) h[j] = opaque_copy(h[j]);   // h may come from a load
   float sdt_acc = 0.f;   // FCARRY: sum of dt over the segment
   constexpr int kDone = 0x7FFFFFFF;
   // Step count after the next checkpoint, and its slot.
@@ -230,6 +232,7 @@ fwd_kernel(FwdArgs a) {
   const float* ck_base = a.ckpt != nullptr ? a.ckpt + (size_t)b * a.nchunk * ck_stride : a.aneg;
   const float* ck_ptr = ck_base + (size_t)(t_beg / a.K) * ck_stride;
   for (int i = 0; i < nsub; ++i) {
+    progress_priority(i, nsub);
     const int t0 = t_beg + i * kSteps;
     const float* buf = lds + (i & 1) * BUF;
     const float* cDT = buf;
