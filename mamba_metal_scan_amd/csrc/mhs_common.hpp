@@ -182,13 +182,15 @@ __device__ __forceinline__ void wave_lds_sync() {
   __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
 }
 
-// Wave issue priority from progress: 3 in the first quarter of a block's
-// iterations, then 2, 1, 0. A CU holds several blocks that all run the whole
-// sequence; the issue arbiter favours the oldest waves at equal priority, so
-// without this the blocks of a CU finish one after the other and the last
-// one runs its final stretch alone, its latencies no longer hidden by other
-// waves. A block ahead of the others drops below them and yields its issue
-// slots until they catch up. (The wave's own arbitration priority only.)
+// Wave issue priority from progress: 3 for the first 40% of a block's
+// iterations, 2 to 70%, 1 to 90% and 0 for the rest (shorter levels towards
+// the end, where the order of finishing is set). A CU holds several blocks
+// that all run the whole sequence; the issue arbiter favours the oldest waves
+// at equal priority, so without this the blocks of a CU finish one after the
+// other and the last one runs its final stretch alone, its latencies no
+// longer hidden by other waves. A block ahead of the others drops below them
+// and yields its issue slots until they catch up. (The wave's own
+// arbitration priority only.)
 __device__ __forceinline__ void progress_priority(int i, int n) {
   const int q = (10 * i) / max(n, 1);
   if (q < 4) __builtin_amdgcn_s_setprio(3);

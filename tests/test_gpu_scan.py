@@ -29,6 +29,10 @@ EDGE_SHAPES = [(2, 128, 64, 16), (2, 1000, 64, 16), (2, 96, 1000, 16), (1, 1, 15
                (1, 512, 1536, 16), (4, 512, 256, 8), (2, 33, 70, 4), (2, 40, 64, 12),
                (1, 20, 64, 5), (2, 48, 96, 32), (1, 24, 128, 64), (2, 37, 96, 40),
                (1, 50, 33, 1)]
+# Grids of two to three blocks per CU (of 256 CUs), as at the training shape:
+# d_inner 1500 and 3000 end in a partial channel block, T 50 in a partial
+# sub-chunk.
+GROUPED_SHAPES = [(16, 96, 1500, 16), (12, 64, 2048, 16), (6, 50, 3000, 16)]
 
 
 def _to_dev(arrs):
@@ -49,7 +53,7 @@ def _run_hip(inp, dy, chunk=None, dh_last=None):
     return y.detach(), h_last.detach(), grads
 
 
-@pytest.mark.parametrize("shape", REF_SHAPES + EDGE_SHAPES)
+@pytest.mark.parametrize("shape", REF_SHAPES + EDGE_SHAPES + GROUPED_SHAPES)
 def test_forward_and_gradients_match_the_oracle(shape):
     bt, t_len, d, n = shape
     print(f"[case] oracle parity {shape}", flush=True)
