@@ -254,8 +254,8 @@ bwd_kernel(BwdArgs a) {
       float s1a = 0.f, s1b = 0.f, s2a = 0.f, s2b = 0.f;
 #pragma unroll
       for (int w = 0; w < G; ++w) {
-        const float2 v1 = lds2(tS + w * 64 * kSteps + cm_elem(cc, k));
-        const float2 v2 = lds2(tS + w * 64 * kSteps + cm_elem(kCH + cc, k));
+        const float2 v1 = lds2(tS + w * 64 * kSteps + ((k / 2) * 64 + cc) * 2);
+        const float2 v2 = lds2(tS + w * 64 * kSteps + ((k / 2) * 64 + kCH + cc) * 2);
         s1a += v1.x; s1b += v1.y;
         s2a += v2.x; s2b += v2.y;
       }
@@ -396,7 +396,12 @@ bwd_kernel(BwdArgs a) {
                                                         __float_as_uint(s2q[s]), false, false);
         o[s] = __uint_as_float(sw[0]) + __uint_as_float(sw[1]);
       }
-      sts4(tS + wave * 64 * kSteps + cm_quad(lane, m), make_float4(o[0], o[1], o[2], o[3]));
+      // tS: per wave a step-pair-major tile [8 pairs][64 rows][2] (rows 0-31:
+      // s1 of the channels, 32-63: s2), so that finalize's 64-bit reads of
+      // one pair over 32 rows are contiguous (no bank conflicts).
+      float* const ts = tS + wave * 64 * kSteps;
+      *reinterpret_cast<float2*>(ts + (2 * m * 64 + lane) * 2) = make_float2(o[0], o[1]);
+      *reinterpret_cast<float2*>(ts + ((2 * m + 1) * 64 + lane) * 2) = make_float2(o[2], o[3]);
       if (m == 2) store_sub((i + 1) & 1, ci - 1);  // unused when ci == 0
       if (m == 1) load_sub(ci - 2);        // loads nothing when ci < 2
     }

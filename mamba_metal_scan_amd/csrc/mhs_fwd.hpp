@@ -155,8 +155,10 @@ fwd_kernel(FwdArgs a) {
     if constexpr (!FCARRY) rl.store(buf + 2 * kCH * kSteps + kSteps * NP, pc);
   };
   // y of sub-chunk i: every wave leaves, per channel and step, the sum over
-  // its two half-waves (added in registers); task (channel cc, step pair p)
-  // sums those over the G waves in a fixed order (64-bit reads). There are
+  // its two half-waves (added in registers), in a step-pair-major tile
+  // [8 pairs][32 channels][2] (each 64-bit write or read of a pair by 32
+  // lanes is one contiguous, bank-conflict-free run); task (channel cc,
+  // step pair p) sums those over the G waves in a fixed order. There are
   // 32 x 8 = 256 tasks: one per thread at G = 4. Split in two so that the LDS
   // reads (y_read) and their use (y_write) sit in different scheduling
   // regions.
@@ -171,7 +173,7 @@ fwd_kernel(FwdArgs a) {
       const int t = t0 < YTASKS ? t0 : 0;
       const int cc = t % kCH, p = t / kCH;
 #pragma unroll
-      for (int w = 0; w < G; ++w) ypart[f][w] = lds2(yp + w * kCH * kSteps + cm_elem(cc, 2 * p));
+      for (int w = 0; w < G; ++w) ypart[f][w] = lds2(yp + w * kCH * kSteps + (p * kCH + cc) * 2);
     }
   };
   auto y_write = [&](int i) {
@@ -298,7 +300,7 @@ fwd_kernel(FwdArgs a) {
                                                           __float_as_uint(yq[2]), false, false);
         const auto s13 = __builtin_amdgcn_permlane32_swap(__float_as_uint(yq[1]),
                                                           __float_as_uint(yq[3]), false, false);
-        *reinterpret_cast<float2*>(myY + cm_quad(c, m) + 2 * hh) =
+        *reinterpret_cast<float2*>(myY + ((2 * m + hh) * kCH + c) * 2) =
             make_float2(__uint_as_float(s02[0]) + __uint_as_float(s02[1]),
                         __uint_as_float(s13[0]) + __uint_as_float(s13[1]));
       }
