@@ -146,6 +146,39 @@ def _short_kernel(name: str) -> str:
     return name[:40]
 
 
+ISSUE_COUNTERS = ("GRBM_GUI_ACTIVE SQ_WAVES SQ_ACTIVE_INST_VALU SQ_ACTIVE_INST_VALU2 SQ_INSTS_VALU "
+                  "SQ_INSTS_VALU_TRANS_F32 SQ_WAVE_CYCLES SQ_LDS_BANK_CONFLICT")
+N_XCD, N_CU = 8, 256   # MI355X: GRBM_GUI_ACTIVE is summed over its 8 XCDs
+
+
+def issue_counter_lines(mean: dict, extra: str) -> list:
+    """Markdown for the third pmc pass: per scan kernel, its GPU-clock cycles
+    and the shares of them the CUs spent issuing VALU instructions, with two
+    VALU instructions issued together (a transcendental beside another), with
+    resident waves, and stalled on LDS bank conflicts. SQ_* cycle counters
+    are in quad-cycles summed over the SIMDs of each CU."""
+    out = ["", "## Issue counters", "",
+           f"    rocprofv3 --pmc {ISSUE_COUNTERS} -d OUT/valu -o run --output-format csv -- "
+           f"python3 bench.py --launches 5 {extra}", "",
+           f"Kernel cycles = GRBM_GUI_ACTIVE / {N_XCD} (the counter is summed over the XCDs). "
+           f"VALU busy = SQ_ACTIVE_INST_VALU / ({N_CU} CUs x cycles); dual issue = "
+           "SQ_ACTIVE_INST_VALU2 / SQ_ACTIVE_INST_VALU; resident waves per CU = "
+           "4 x SQ_WAVE_CYCLES / (CUs x cycles); LDS conflict = SQ_LDS_BANK_CONFLICT / "
+           "(CUs x cycles); VALU instructions and v_exp_f32 per wave.", "",
+           "| kernel | cycles | VALU busy | dual issue | waves / CU | LDS conflict "
+           "| VALU / wave | exp / wave |", "|---|---|---|---|---|---|---|---|"]
+    for kern in ("fwd_kernel", "bwd_kernel"):
+        g = lambda c: mean.get((kern, c), 0.0)
+        cyc = g("GRBM_GUI_ACTIVE") / N_XCD
+        waves = max(g("SQ_WAVES"), 1.0)
+        out.append(f"| {kern} | {cyc:.0f} | {g('SQ_ACTIVE_INST_VALU') / (N_CU * cyc):.2f} | "
+                   f"{g('SQ_ACTIVE_INST_VALU2') / max(g('SQ_ACTIVE_INST_VALU'), 1):.2f} | "
+                   f"{4 * g('SQ_WAVE_CYCLES') / (N_CU * cyc):.1f} | "
+                   f"{g('SQ_LDS_BANK_CONFLICT') / (N_CU * cyc):.3f} | "
+                   f"{g('SQ_INSTS_VALU') / waves:.0f} | {g('SQ_INSTS_VALU_TRANS_F32') / waves:.0f} |")
+    return out
+
+
 def pmc_summary(args) -> None:
     """Per-launch HBM traffic from two rocprofv3 --pmc passes (FETCH_SIZE, then
     WRITE_SIZE, KiB per dispatch) under args.pmc_summary, each scaled by what
@@ -217,6 +250,8 @@ def pmc_summary(args) -> None:
         alg = {"fwd_kernel": nbytes["fwd"], "bwd_kernel": nbytes["bwd"]}.get(kern)
         lines.append(f"| {kern} | {r['read_bytes'] / 1e6:.1f} | {r['write_bytes'] / 1e6:.1f} | "
                      f"{r['hbm_bytes'] / 1e6:.1f} | {'' if alg is None else f'{alg / 1e6:.1f}'} |")
+    if ("bwd_kernel", "SQ_ACTIVE_INST_VALU") in mean:
+        lines += issue_counter_lines(mean, extra)
     md = ROOT / "profiles" / f"scan_{tag}.md"
     md.write_text("\n".join(lines) + "\n")
     print("\n".join(lines))
