@@ -147,3 +147,25 @@ def test_out_gate_backward_is_bitwise_deterministic():
         runs.append([t.grad for t in leaves])
     for a, b in zip(*runs):
         assert torch.equal(a, b)
+
+
+def test_out_gate_rejects_bad_dtypes_and_shapes():
+    y = torch.zeros(2, 8, 16, device=DEV)
+    d_skip = torch.zeros(16, device=DEV)
+    with pytest.raises(RuntimeError, match="fp32-only"):
+        out_gate(y.to(torch.bfloat16), d_skip, y)
+    with pytest.raises(ValueError, match="bad shapes"):
+        out_gate(y, torch.zeros(15, device=DEV), y)
+    with pytest.raises(ValueError, match="bad shapes"):
+        out_gate(y, d_skip, y[:, :7])
+
+
+def test_gated_scan_rejects_mismatched_shapes():
+    """The gated entry validates like selective_scan (ValueError on shapes)."""
+    x = torch.zeros(1, 8, 16, device=DEV)
+    a = torch.zeros(16, 4, device=DEV)
+    bc = torch.zeros(1, 8, 4, device=DEV)
+    with pytest.raises(ValueError):
+        selective_scan_gated(x, x, a[:15], bc, bc, LO, HI)
+    with pytest.raises(ValueError):
+        selective_scan_gated(x, x, a, bc[:, :7], bc, LO, HI)

@@ -92,3 +92,27 @@ def test_direct_entry_checks_device_before_dtype_and_shape():
         selective_scan_hip(x, dt, aneg[:, :3], b_in, c_in)
     with pytest.raises(RuntimeError, match="ROCm device"):
         selective_scan_metal(x, dt, aneg, b_in, c_in, 16, 64)
+
+
+def test_gated_scan_checks_the_gate_then_the_device():
+    """selective_scan_gated: dt_min < dt_max is checked first (ValueError),
+    then the inputs' device, with selective_scan's RuntimeError."""
+    from mamba_metal_scan_amd import selective_scan_gated
+    x, dt, aneg, b_in, c_in = _inputs(1, 8, 16, 4, dtype=torch.float32)
+    for lo, hi in ((0.1, 0.1), (0.2, 0.1)):
+        with pytest.raises(ValueError, match="dt_min < dt_max"):
+            selective_scan_gated(x, dt, aneg, b_in, c_in, lo, hi)
+    with pytest.raises(RuntimeError, match="ROCm device"):
+        selective_scan_gated(x, dt, aneg, b_in, c_in, 0.001, 0.1)
+    # wrong dtype and shape as well: still the device error first
+    with pytest.raises(RuntimeError, match="ROCm device"):
+        selective_scan_gated(x.double(), dt, aneg[:, :3], b_in, c_in, 0.001, 0.1)
+
+
+def test_out_gate_checks_device_before_dtype_and_shape():
+    from mamba_metal_scan_amd import out_gate
+    y = torch.zeros(1, 8, 16)
+    with pytest.raises(RuntimeError, match="ROCm device"):
+        out_gate(y, torch.zeros(16), y)
+    with pytest.raises(RuntimeError, match="ROCm device"):
+        out_gate(y.double(), torch.zeros(5), y[:, :3])
