@@ -11,6 +11,7 @@ fallback behind them: if the library is absent they raise.
 """
 from __future__ import annotations
 
+import contextlib
 import ctypes
 import threading
 from pathlib import Path
@@ -119,11 +120,25 @@ def _check(rc: int, what: str) -> None:
 
 
 def _ptr(t: Optional[torch.Tensor]):
-    return None if t is None else ctypes.c_void_p(t.data_ptr())
+    # plain ints: the c_void_p argtypes convert them (None is NULL)
+    return None if t is None else t.data_ptr()
 
 
-def _stream(dev: torch.device) -> ctypes.c_void_p:
-    return ctypes.c_void_p(torch.cuda.current_stream(dev).cuda_stream)
+_raw_stream = getattr(torch._C, "_cuda_getCurrentRawStream", None)
+
+
+def _stream(dev: torch.device) -> int:
+    """The device's current stream (hipStream_t as an int)."""
+    if _raw_stream is not None:
+        return _raw_stream(dev.index if dev.index is not None else torch.cuda.current_device())
+    return torch.cuda.current_stream(dev).cuda_stream
+
+
+def _on(dev: torch.device):
+    """torch.cuda.device(dev), or no context switch when dev is already current."""
+    if dev.index is None or dev.index == torch.cuda.current_device():
+        return contextlib.nullcontext()
+    return torch.cuda.device(dev)
 
 
 def num_chunks(seqlen: int, chunk: int) -> int:
@@ -165,8 +180,27 @@ def _fwd_workspace(x: torch.Tensor, n: int):
     return torch.empty(nbytes, dtype=torch.uint8, device=x.device), nbytes
 
 
-@torch.library.custom_op("mamba_hip::scan_fwd", mutates_args=())
-def scan_fwd(x: torch.Tensor, dt: torch.Tensor, aneg: torch.Tensor, b_in: torch.Tensor,
+_IMPLS: dict = {}
+
+
+def _register(name: str, impl, mutates_args):
+    """Register impl as the custom op mamba_hip::<name> (for torch.compile and
+    torch.ops callers) and keep the plain function for dispatch()."""
+    _IMPLS[name] = impl
+    return torch.library.custom_op(f"mamba_hip::{name}", impl, mutates_args=mutates_args)
+
+
+def dispatch(name: str):
+    """The op the autograd Functions call: the registered torch.ops.mamba_hip
+    op while torch.compile traces, else its plain implementation (the same
+    code without the dispatcher's per-call overhead, about as long as the
+    C-ABI call itself at the training shape)."""
+    if torch.compiler.is_compiling():
+        return getattr(torch.ops.mamba_hip, name)
+    return _IMPLS[name]
+
+
+def _scan_fwd_impl(x: torch.Tensor, dt: torch.Tensor, aneg: torch.Tensor, b_in: torch.Tensor,
              c_in: torch.Tensor, chunk: int, with_ckpt: bool
              ) -> tuple[torch.Tensor, torch.Tensor, torch.Tensor]:
     """y (B,T,D), ckpt (B,ceil(T/chunk),D,N) or an empty tensor, h_last (B,D,N)."""
@@ -176,7 +210,7 @@ def scan_fwd(x: torch.Tensor, dt: torch.Tensor, aneg: torch.Tensor, b_in: torch.
     ws, ws_bytes = _fwd_workspace(x, n)
     lib = library()
     fn = lib.mhs_scan_fwd_bf16 if x.dtype == torch.bfloat16 else lib.mhs_scan_fwd_ws_f32
-    with torch.cuda.device(x.device):
+    with _on(x.device):
         rc = fn(_ptr(x), _ptr(dt), _ptr(aneg), _ptr(b_in), _ptr(c_in), _ptr(y),
                 _ptr(ckpt) if with_ckpt else None, _ptr(h_last), _ptr(ws), ws_bytes,
                 bt, t_len, d, n, chunk, _stream(x.device))
@@ -184,13 +218,15 @@ def scan_fwd(x: torch.Tensor, dt: torch.Tensor, aneg: torch.Tensor, b_in: torch.
     return y, ckpt, h_last
 
 
+scan_fwd = _register("scan_fwd", _scan_fwd_impl, ())
+
+
 @scan_fwd.register_fake
 def _scan_fwd_fake(x, dt, aneg, b_in, c_in, chunk, with_ckpt):
     return _fwd_outputs(x, aneg.shape[1], chunk, with_ckpt)
 
 
-@torch.library.custom_op("mamba_hip::scan_bwd", mutates_args=())
-def scan_bwd(x: torch.Tensor, dt: torch.Tensor, aneg: torch.Tensor, b_in: torch.Tensor,
+def _scan_bwd_impl(x: torch.Tensor, dt: torch.Tensor, aneg: torch.Tensor, b_in: torch.Tensor,
              c_in: torch.Tensor, dy: torch.Tensor, dh_last: Optional[torch.Tensor],
              ckpt: torch.Tensor, chunk: int
              ) -> tuple[torch.Tensor, torch.Tensor, torch.Tensor, torch.Tensor, torch.Tensor]:
@@ -208,12 +244,15 @@ def scan_bwd(x: torch.Tensor, dt: torch.Tensor, aneg: torch.Tensor, b_in: torch.
         raise HipScanError(f"no backward workspace size for shape {(bt, t_len, d, n)} chunk {chunk}")
     ws = torch.empty(ws_bytes, dtype=torch.uint8, device=x.device)
     fn = lib.mhs_scan_bwd_bf16 if x.dtype == torch.bfloat16 else lib.mhs_scan_bwd_f32
-    with torch.cuda.device(x.device):
+    with _on(x.device):
         rc = fn(_ptr(x), _ptr(dt), _ptr(aneg), _ptr(b_in), _ptr(c_in), _ptr(dy),
                 _ptr(dh_last), _ptr(ckpt), _ptr(dx), _ptr(ddt), _ptr(daneg), _ptr(db), _ptr(dc),
                 _ptr(ws), ws_bytes, bt, t_len, d, n, chunk, _stream(x.device))
     _check(rc, "scan backward")
     return dx, ddt, daneg, db, dc
+
+
+scan_bwd = _register("scan_bwd", _scan_bwd_impl, ())
 
 
 @scan_bwd.register_fake
@@ -222,18 +261,20 @@ def _scan_bwd_fake(x, dt, aneg, b_in, c_in, dy, dh_last, ckpt, chunk):
             torch.empty_like(b_in), torch.empty_like(c_in))
 
 
-@torch.library.custom_op("mamba_hip::scan_step", mutates_args=("h",))
-def scan_step(h: torch.Tensor, x: torch.Tensor, dt: torch.Tensor, aneg: torch.Tensor,
+def _scan_step_impl(h: torch.Tensor, x: torch.Tensor, dt: torch.Tensor, aneg: torch.Tensor,
               b_in: torch.Tensor, c_in: torch.Tensor) -> torch.Tensor:
     """One decode step in place on h (B,D,N); returns y (B,D)."""
     bt, d, n = h.shape
     y = x.new_empty((bt, d))
-    with torch.cuda.device(h.device):
+    with _on(h.device):
         rc = library().mhs_scan_step_f32(
             _ptr(h), _ptr(x), _ptr(dt), _ptr(aneg), _ptr(b_in), _ptr(c_in), _ptr(y),
             bt, d, n, _stream(h.device))
     _check(rc, "mhs_scan_step_f32")
     return y
+
+
+scan_step = _register("scan_step", _scan_step_impl, ("h",))
 
 
 @scan_step.register_fake
@@ -251,12 +292,11 @@ def _conv_rows(x: torch.Tensor) -> int:
     return x.stride(1)
 
 
-@torch.library.custom_op("mamba_hip::conv1d_silu_fwd", mutates_args=())
-def conv1d_silu_fwd(x: torch.Tensor, w: torch.Tensor, bias: torch.Tensor) -> torch.Tensor:
+def _conv1d_silu_fwd_impl(x: torch.Tensor, w: torch.Tensor, bias: torch.Tensor) -> torch.Tensor:
     """silu(causal depthwise conv1d) of (B,T,D) x (rows may be strided), w (D,K): (B,T,D)."""
     bt, t_len, d = x.shape
     out = x.new_empty((bt, t_len, d))
-    with torch.cuda.device(x.device):
+    with _on(x.device):
         rc = library().mhs_conv1d_silu_fwd_f32(
             _ptr(x), _conv_rows(x), _ptr(w), _ptr(bias), _ptr(out), bt, t_len, d, w.shape[1],
             _stream(x.device))
@@ -264,13 +304,15 @@ def conv1d_silu_fwd(x: torch.Tensor, w: torch.Tensor, bias: torch.Tensor) -> tor
     return out
 
 
+conv1d_silu_fwd = _register("conv1d_silu_fwd", _conv1d_silu_fwd_impl, ())
+
+
 @conv1d_silu_fwd.register_fake
 def _conv1d_silu_fwd_fake(x, w, bias):
     return x.new_empty(x.shape)
 
 
-@torch.library.custom_op("mamba_hip::conv1d_silu_bwd", mutates_args=())
-def conv1d_silu_bwd(x: torch.Tensor, w: torch.Tensor, bias: torch.Tensor, dout: torch.Tensor
+def _conv1d_silu_bwd_impl(x: torch.Tensor, w: torch.Tensor, bias: torch.Tensor, dout: torch.Tensor
                     ) -> tuple[torch.Tensor, torch.Tensor, torch.Tensor]:
     """(dx (B,T,D) contiguous, dw (D,K), dbias (D))."""
     bt, t_len, d = x.shape
@@ -283,7 +325,7 @@ def conv1d_silu_bwd(x: torch.Tensor, w: torch.Tensor, bias: torch.Tensor, dout: 
     if ws_bytes == 0:
         raise HipScanError(f"no conv workspace size for shape {(bt, t_len, d)} kernel {k}")
     ws = torch.empty(ws_bytes, dtype=torch.uint8, device=x.device)
-    with torch.cuda.device(x.device):
+    with _on(x.device):
         rc = lib.mhs_conv1d_silu_bwd_f32(
             _ptr(x), _conv_rows(x), _ptr(w), _ptr(bias), _ptr(dout), _ptr(dx), _ptr(dw),
             _ptr(dbias), _ptr(ws), ws_bytes, bt, t_len, d, k, _stream(x.device))
@@ -291,13 +333,15 @@ def conv1d_silu_bwd(x: torch.Tensor, w: torch.Tensor, bias: torch.Tensor, dout: 
     return dx, dw, dbias
 
 
+conv1d_silu_bwd = _register("conv1d_silu_bwd", _conv1d_silu_bwd_impl, ())
+
+
 @conv1d_silu_bwd.register_fake
 def _conv1d_silu_bwd_fake(x, w, bias, dout):
     return x.new_empty(x.shape), torch.empty_like(w), torch.empty_like(bias)
 
 
-@torch.library.custom_op("mamba_hip::scan_gated_fwd", mutates_args=())
-def scan_gated_fwd(x: torch.Tensor, dt_raw: torch.Tensor, a_raw: torch.Tensor,
+def _scan_gated_fwd_impl(x: torch.Tensor, dt_raw: torch.Tensor, a_raw: torch.Tensor,
                    b_in: torch.Tensor, c_in: torch.Tensor, dt_min: float, dt_max: float,
                    chunk: int, with_ckpt: bool
                    ) -> tuple[torch.Tensor, torch.Tensor, torch.Tensor]:
@@ -309,7 +353,7 @@ def scan_gated_fwd(x: torch.Tensor, dt_raw: torch.Tensor, a_raw: torch.Tensor,
     ws, ws_bytes = _fwd_workspace(x, n)
     lib = library()
     fn = lib.mhs_scan_gated_fwd_bf16 if x.dtype == torch.bfloat16 else lib.mhs_scan_gated_fwd_f32
-    with torch.cuda.device(x.device):
+    with _on(x.device):
         rc = fn(_ptr(x), _ptr(dt_raw), _ptr(a_raw), _ptr(b_in), _ptr(c_in), dt_min, dt_max,
                 _ptr(y), _ptr(ckpt) if with_ckpt else None, _ptr(h_last), _ptr(ws), ws_bytes,
                 bt, t_len, d, n, chunk, _stream(x.device))
@@ -317,13 +361,15 @@ def scan_gated_fwd(x: torch.Tensor, dt_raw: torch.Tensor, a_raw: torch.Tensor,
     return y, ckpt, h_last
 
 
+scan_gated_fwd = _register("scan_gated_fwd", _scan_gated_fwd_impl, ())
+
+
 @scan_gated_fwd.register_fake
 def _scan_gated_fwd_fake(x, dt_raw, a_raw, b_in, c_in, dt_min, dt_max, chunk, with_ckpt):
     return _scan_fwd_fake(x, dt_raw, a_raw, b_in, c_in, chunk, with_ckpt)
 
 
-@torch.library.custom_op("mamba_hip::scan_gated_bwd", mutates_args=())
-def scan_gated_bwd(x: torch.Tensor, dt_raw: torch.Tensor, a_raw: torch.Tensor,
+def _scan_gated_bwd_impl(x: torch.Tensor, dt_raw: torch.Tensor, a_raw: torch.Tensor,
                    b_in: torch.Tensor, c_in: torch.Tensor, dt_min: float, dt_max: float,
                    dy: torch.Tensor, dh_last: Optional[torch.Tensor], ckpt: torch.Tensor,
                    chunk: int
@@ -342,12 +388,15 @@ def scan_gated_bwd(x: torch.Tensor, dt_raw: torch.Tensor, a_raw: torch.Tensor,
         raise HipScanError(f"no backward workspace size for shape {(bt, t_len, d, n)} chunk {chunk}")
     ws = torch.empty(ws_bytes, dtype=torch.uint8, device=x.device)
     fn = lib.mhs_scan_gated_bwd_bf16 if x.dtype == torch.bfloat16 else lib.mhs_scan_gated_bwd_f32
-    with torch.cuda.device(x.device):
+    with _on(x.device):
         rc = fn(_ptr(x), _ptr(dt_raw), _ptr(a_raw), _ptr(b_in), _ptr(c_in), dt_min, dt_max,
                 _ptr(dy), _ptr(dh_last), _ptr(ckpt), _ptr(dx), _ptr(ddt), _ptr(da), _ptr(db),
                 _ptr(dc), _ptr(ws), ws_bytes, bt, t_len, d, n, chunk, _stream(x.device))
     _check(rc, "gated scan backward")
     return dx, ddt, da, db, dc
+
+
+scan_gated_bwd = _register("scan_gated_bwd", _scan_gated_bwd_impl, ())
 
 
 @scan_gated_bwd.register_fake
@@ -356,12 +405,11 @@ def _scan_gated_bwd_fake(x, dt_raw, a_raw, b_in, c_in, dt_min, dt_max, dy, dh_la
             torch.empty_like(b_in), torch.empty_like(c_in))
 
 
-@torch.library.custom_op("mamba_hip::out_gate_fwd", mutates_args=())
-def out_gate_fwd(y: torch.Tensor, d_skip: torch.Tensor, z: torch.Tensor) -> torch.Tensor:
+def _out_gate_fwd_impl(y: torch.Tensor, d_skip: torch.Tensor, z: torch.Tensor) -> torch.Tensor:
     """(y + d_skip) * silu(z) for (B,T,D) y and z (z rows may be strided)."""
     bt, t_len, d = y.shape
     out = y.new_empty((bt, t_len, d))
-    with torch.cuda.device(y.device):
+    with _on(y.device):
         rc = library().mhs_out_gate_fwd_f32(
             _ptr(y), _ptr(d_skip), _ptr(z), _conv_rows(z), _ptr(out), bt, t_len, d,
             _stream(y.device))
@@ -369,13 +417,15 @@ def out_gate_fwd(y: torch.Tensor, d_skip: torch.Tensor, z: torch.Tensor) -> torc
     return out
 
 
+out_gate_fwd = _register("out_gate_fwd", _out_gate_fwd_impl, ())
+
+
 @out_gate_fwd.register_fake
 def _out_gate_fwd_fake(y, d_skip, z):
     return y.new_empty(y.shape)
 
 
-@torch.library.custom_op("mamba_hip::out_gate_bwd", mutates_args=())
-def out_gate_bwd(y: torch.Tensor, d_skip: torch.Tensor, z: torch.Tensor, dout: torch.Tensor
+def _out_gate_bwd_impl(y: torch.Tensor, d_skip: torch.Tensor, z: torch.Tensor, dout: torch.Tensor
                  ) -> tuple[torch.Tensor, torch.Tensor, torch.Tensor]:
     """(dy, dd_skip, dz), dy and dz (B,T,D) contiguous."""
     bt, t_len, d = y.shape
@@ -387,12 +437,15 @@ def out_gate_bwd(y: torch.Tensor, d_skip: torch.Tensor, z: torch.Tensor, dout: t
     if ws_bytes == 0:
         raise HipScanError(f"no output-gate workspace size for shape {(bt, t_len, d)}")
     ws = torch.empty(ws_bytes, dtype=torch.uint8, device=y.device)
-    with torch.cuda.device(y.device):
+    with _on(y.device):
         rc = lib.mhs_out_gate_bwd_f32(
             _ptr(y), _ptr(d_skip), _ptr(z), _conv_rows(z), _ptr(dout), _ptr(dy), _ptr(dz),
             _ptr(dd), _ptr(ws), ws_bytes, bt, t_len, d, _stream(y.device))
     _check(rc, "mhs_out_gate_bwd_f32")
     return dy, dd, dz
+
+
+out_gate_bwd = _register("out_gate_bwd", _out_gate_bwd_impl, ())
 
 
 @out_gate_bwd.register_fake

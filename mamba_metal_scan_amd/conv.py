@@ -35,7 +35,7 @@ class ConvSiluHIP(torch.autograd.Function):
             _native._conv_rows(x)
         except _native.HipScanError:
             x = x.contiguous()
-        out = torch.ops.mamba_hip.conv1d_silu_fwd(x, w, b)
+        out = _native.dispatch("conv1d_silu_fwd")(x, w, b)
         ctx.save_for_backward(x, w, b)
         return out
 
@@ -44,7 +44,7 @@ class ConvSiluHIP(torch.autograd.Function):
         x, w, b = ctx.saved_tensors
         if ctx.empty:
             return x.new_zeros(x.shape), w.new_zeros(ctx.wshape), torch.zeros_like(b)
-        dx, dw, db = torch.ops.mamba_hip.conv1d_silu_bwd(x, w, b, dout.contiguous())
+        dx, dw, db = _native.dispatch("conv1d_silu_bwd")(x, w, b, dout.contiguous())
         return dx, dw.reshape(ctx.wshape), db
 
 

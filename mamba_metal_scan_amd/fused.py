@@ -47,7 +47,7 @@ class SelectiveScanGatedHIP(torch.autograd.Function):
             ctx.save_for_backward(x, dt_raw, a_raw, b_in, c_in)
         else:
             need_grad = any(ctx.needs_input_grad[:5])
-            y, ckpt, h_last = torch.ops.mamba_hip.scan_gated_fwd(
+            y, ckpt, h_last = _native.dispatch("scan_gated_fwd")(
                 x, dt_raw, a_raw, b_in, c_in, ctx.gate[0], ctx.gate[1], chunk, need_grad)
             ctx.save_for_backward(x, dt_raw, a_raw, b_in, c_in, ckpt)
         if return_state:
@@ -68,7 +68,7 @@ class SelectiveScanGatedHIP(torch.autograd.Function):
         dy = dy.contiguous()
         if dh_last is not None:
             dh_last = dh_last.contiguous()
-        dx, ddt, da, db, dc = torch.ops.mamba_hip.scan_gated_bwd(
+        dx, ddt, da, db, dc = _native.dispatch("scan_gated_bwd")(
             x, dt_raw, a_raw, b_in, c_in, ctx.gate[0], ctx.gate[1], dy, dh_last, ckpt, ctx.chunk)
         return dx, ddt, da, db, dc, None, None, None, None
 
@@ -101,14 +101,14 @@ class OutGateHIP(torch.autograd.Function):
         ctx.save_for_backward(y, d_skip, z)
         if ctx.empty:
             return y.new_zeros(y.shape)
-        return torch.ops.mamba_hip.out_gate_fwd(y, d_skip, z)
+        return _native.dispatch("out_gate_fwd")(y, d_skip, z)
 
     @staticmethod
     def backward(ctx, dout):
         y, d_skip, z = ctx.saved_tensors
         if ctx.empty:
             return torch.zeros_like(y), torch.zeros_like(d_skip), torch.zeros_like(z)
-        dy, dd, dz = torch.ops.mamba_hip.out_gate_bwd(y, d_skip, z, dout.contiguous())
+        dy, dd, dz = _native.dispatch("out_gate_bwd")(y, d_skip, z, dout.contiguous())
         return dy, dd, dz
 
 

@@ -131,7 +131,7 @@ class SelectiveScanHIP(torch.autograd.Function):
             ctx.save_for_backward(x, dt, aneg, b_in, c_in)
         else:
             need_grad = any(ctx.needs_input_grad[:5])
-            y, ckpt, h_last = torch.ops.mamba_hip.scan_fwd(x, dt, aneg, b_in, c_in, chunk,
+            y, ckpt, h_last = _native.dispatch("scan_fwd")(x, dt, aneg, b_in, c_in, chunk,
                                                            need_grad)
             ctx.save_for_backward(x, dt, aneg, b_in, c_in, ckpt)
         if return_state:
@@ -152,7 +152,7 @@ class SelectiveScanHIP(torch.autograd.Function):
         dy = dy.contiguous()
         if dh_last is not None:
             dh_last = dh_last.contiguous()
-        dx, ddt, daneg, db, dc = torch.ops.mamba_hip.scan_bwd(
+        dx, ddt, daneg, db, dc = _native.dispatch("scan_bwd")(
             x, dt, aneg, b_in, c_in, dy, dh_last, ckpt, ctx.chunk)
         return dx, ddt, daneg, db, dc, None, None
 
@@ -227,6 +227,6 @@ def selective_state_step(h: torch.Tensor, x: torch.Tensor, dt: torch.Tensor,
                          f"C {tuple(c_in.shape)}")
     if not h.is_contiguous():
         raise ValueError("selective_state_step updates h in place; h must be contiguous")
-    return torch.ops.mamba_hip.scan_step(h, x.contiguous(), dt.contiguous(),
+    return _native.dispatch("scan_step")(h, x.contiguous(), dt.contiguous(),
                                          aneg.contiguous(), b_in.contiguous(),
                                          c_in.contiguous())
