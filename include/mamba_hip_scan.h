@@ -214,7 +214,6 @@ int mhs_scan_gated_bwd_bf16(const uint16_t* x, const uint16_t* dt_raw, const flo
                             int64_t chunk, void* stream);
 
 /*
- * One recurrent decode step, in place on h./*
  * One recurrent decode step, in place on h. Replaces the pure-torch step of
  * the reference's MambaBlock.forward (mamba_metal/model.py:234-241):
  *     h <- h * exp(-dt * Aneg) + dt * B * x ;  y = sum_n C * h
