@@ -152,13 +152,18 @@ int mhs_scan_bwd_f32(const float* x, const float* dt, const float* aneg,
  * recurrence of mhs_scan_fwd_ws_f32 on (x, dt, Aneg, B, C). Needs finite
  * dt_min < dt_max. Same outputs, layouts, checkpoints and workspace (may be
  * NULL) as mhs_scan_fwd_ws_f32.
+ * ld_dt, ld_bc: elements between consecutive time steps of dt_raw and of B,
+ * C (0: contiguous, i.e. d_inner and d_state). Larger strides read column
+ * slices of one wider tensor, e.g. a single projection whose rows hold
+ * [dt_raw | B | C] (ld_dt = ld_bc = d_inner + 2 d_state; the 16-byte
+ * alignment applies to the slices' first elements). x is contiguous.
  */
 int mhs_scan_gated_fwd_f32(const float* x, const float* dt_raw, const float* A,
                            const float* B, const float* C, float dt_min, float dt_max,
                            float* y, float* ckpt, float* h_last,
                            void* workspace, size_t workspace_bytes,
                            int64_t batch, int64_t seqlen, int64_t d_inner, int64_t d_state,
-                           int64_t chunk, void* stream);
+                           int64_t chunk, int64_t ld_dt, int64_t ld_bc, void* stream);
 
 /*
  * Backward of mhs_scan_gated_fwd_f32 (the autograd of the same reference
@@ -167,6 +172,10 @@ int mhs_scan_gated_fwd_f32(const float* x, const float* dt_raw, const float* A,
  *     dA      = dAneg * sigmoid(A)
  * and dx, dB, dC as mhs_scan_bwd_f32. Workspace: mhs_scan_bwd_workspace_bytes
  * of the same shape. Bit-for-bit reproducible.
+ * ld_dt, ld_bc: input row strides as in mhs_scan_gated_fwd_f32; ld_ddt,
+ * ld_dbc: row strides of the outputs ddt_raw and dB, dC (0: contiguous), so
+ * that they can be written into the column slices of one gradient tensor of
+ * the projection. dx is contiguous.
  */
 int mhs_scan_gated_bwd_f32(const float* x, const float* dt_raw, const float* A,
                            const float* B, const float* C, float dt_min, float dt_max,
@@ -174,7 +183,8 @@ int mhs_scan_gated_bwd_f32(const float* x, const float* dt_raw, const float* A,
                            float* dx, float* ddt_raw, float* dA, float* dB, float* dC,
                            void* workspace, size_t workspace_bytes,
                            int64_t batch, int64_t seqlen, int64_t d_inner, int64_t d_state,
-                           int64_t chunk, void* stream);
+                           int64_t chunk, int64_t ld_dt, int64_t ld_bc, int64_t ld_ddt,
+                           int64_t ld_dbc, void* stream);
 
 /*
  * bf16 activations with fp32 state. The same four scan entry points with x,
@@ -204,14 +214,15 @@ int mhs_scan_gated_fwd_bf16(const uint16_t* x, const uint16_t* dt_raw, const flo
                             uint16_t* y, float* ckpt, float* h_last,
                             void* workspace, size_t workspace_bytes,
                             int64_t batch, int64_t seqlen, int64_t d_inner, int64_t d_state,
-                            int64_t chunk, void* stream);
+                            int64_t chunk, int64_t ld_dt, int64_t ld_bc, void* stream);
 int mhs_scan_gated_bwd_bf16(const uint16_t* x, const uint16_t* dt_raw, const float* A,
                             const uint16_t* B, const uint16_t* C, float dt_min, float dt_max,
                             const uint16_t* dy, const float* dh_last, const float* ckpt,
                             uint16_t* dx, uint16_t* ddt_raw, float* dA, uint16_t* dB,
                             uint16_t* dC, void* workspace, size_t workspace_bytes,
                             int64_t batch, int64_t seqlen, int64_t d_inner, int64_t d_state,
-                            int64_t chunk, void* stream);
+                            int64_t chunk, int64_t ld_dt, int64_t ld_bc, int64_t ld_ddt,
+                            int64_t ld_dbc, void* stream);
 
 /*
  * One recurrent decode step, in place on h. Replaces the pure-torch step of
@@ -247,15 +258,17 @@ size_t mhs_conv1d_silu_bwd_workspace_bytes(int64_t batch, int64_t seqlen, int64_
 
 /*
  * Backward of mhs_conv1d_silu_fwd_f32 (the autograd of the same reference
- * Conv1d + SiLU): dx (batch, seqlen, d_inner) contiguous, dw (d_inner, K),
- * dbias (d_inner), all fully written. dw and dbias are summed over (batch,
- * time) through the workspace in a fixed order (bit-for-bit reproducible).
+ * Conv1d + SiLU): dx (batch, seqlen, d_inner) with rows dx_row_stride apart
+ * (0: contiguous; larger writes the x half of the in_proj output's
+ * gradient in place), dw (d_inner, K), dbias (d_inner), all fully written.
+ * dw and dbias are summed over (batch, time) through the workspace in a
+ * fixed order (bit-for-bit reproducible).
  */
 int mhs_conv1d_silu_bwd_f32(const float* x, int64_t x_row_stride, const float* w,
-                            const float* bias, const float* dout, float* dx, float* dw,
-                            float* dbias, void* workspace, size_t workspace_bytes,
-                            int64_t batch, int64_t seqlen, int64_t d_inner, int64_t kernel_size,
-                            void* stream);
+                            const float* bias, const float* dout, float* dx,
+                            int64_t dx_row_stride, float* dw, float* dbias, void* workspace,
+                            size_t workspace_bytes, int64_t batch, int64_t seqlen,
+                            int64_t d_inner, int64_t kernel_size, void* stream);
 
 /*
  * The block's output gate, forward. Replaces `y = y + self.D_skip` and the
@@ -279,13 +292,15 @@ size_t mhs_out_gate_bwd_workspace_bytes(int64_t batch, int64_t seqlen, int64_t d
  * with s = sigmoid(z):
  *     dy = dout * z * s ;  dz = dout * (y + d_skip) * s * (1 + z * (1 - s)) ;
  *     dd_skip[d] = sum_{b,t} dy[b,t,d]
- * dy, dz : (batch, seqlen, d_inner) contiguous, dd_skip : (d_inner), all fully
- * written; dd_skip is summed through the workspace (16-byte aligned) in a
- * fixed order (bit-for-bit reproducible).
+ * dy : (batch, seqlen, d_inner) contiguous; dz : the same, rows dz_row_stride
+ * apart (0: contiguous; larger writes the z half of the in_proj output's
+ * gradient in place); dd_skip : (d_inner); all fully written. dd_skip is
+ * summed through the workspace (16-byte aligned) in a fixed order (bit-for-bit
+ * reproducible).
  */
 int mhs_out_gate_bwd_f32(const float* y, const float* d_skip, const float* z,
                          int64_t z_row_stride, const float* dout,
-                         float* dy, float* dz, float* dd_skip,
+                         float* dy, float* dz, int64_t dz_row_stride, float* dd_skip,
                          void* workspace, size_t workspace_bytes,
                          int64_t batch, int64_t seqlen, int64_t d_inner, void* stream);
 

@@ -4,7 +4,8 @@ Same public surface as the reference package ``mamba_metal``
 (mamba_metal/__init__.py:2-7), plus the HIP-specific names.
 """
 from .conv import ConvSiluHIP, conv1d_silu
-from .fused import OutGateHIP, SelectiveScanGatedHIP, out_gate, selective_scan_gated
+from .fused import (MambaInnerHIP, OutGateHIP, SelectiveScanGatedHIP, mamba_inner, out_gate,
+                    selective_scan_gated)
 from .model import MambaConfig, TinyMamba
 from .scan import (SSM_CHUNK, SelectiveScanHIP, selective_scan, selective_scan_hip,
                    selective_scan_metal, selective_scan_ref, selective_state_step)
@@ -12,4 +13,4 @@ from .scan import (SSM_CHUNK, SelectiveScanHIP, selective_scan, selective_scan_h
 __all__ = ["MambaConfig", "TinyMamba", "SSM_CHUNK", "SelectiveScanHIP", "selective_scan",
            "selective_scan_hip", "selective_scan_metal", "selective_scan_ref",
            "selective_state_step", "conv1d_silu", "ConvSiluHIP", "selective_scan_gated",
-           "SelectiveScanGatedHIP", "out_gate", "OutGateHIP"]
+           "SelectiveScanGatedHIP", "out_gate", "OutGateHIP", "mamba_inner", "MambaInnerHIP"]

@@ -86,21 +86,21 @@ def library() -> ctypes.CDLL:
             lib.mhs_conv1d_silu_bwd_workspace_bytes.restype = ctypes.c_size_t
             lib.mhs_conv1d_silu_bwd_workspace_bytes.argtypes = [_I64] * 4
             lib.mhs_conv1d_silu_bwd_f32.restype = ctypes.c_int
-            lib.mhs_conv1d_silu_bwd_f32.argtypes = ([_P, _I64] + [_P] * 7 + [ctypes.c_size_t]
-                                                    + [_I64] * 4 + [_P])
+            lib.mhs_conv1d_silu_bwd_f32.argtypes = ([_P, _I64] + [_P] * 4 + [_I64] + [_P] * 3
+                                                    + [ctypes.c_size_t] + [_I64] * 4 + [_P])
             lib.mhs_scan_gated_fwd_f32.restype = ctypes.c_int
             lib.mhs_scan_gated_fwd_f32.argtypes = ([_P] * 5 + [_F32] * 2 + [_P] * 4
-                                                   + [ctypes.c_size_t] + [_I64] * 5 + [_P])
+                                                   + [ctypes.c_size_t] + [_I64] * 7 + [_P])
             lib.mhs_scan_gated_bwd_f32.restype = ctypes.c_int
             lib.mhs_scan_gated_bwd_f32.argtypes = ([_P] * 5 + [_F32] * 2 + [_P] * 9
-                                                   + [ctypes.c_size_t] + [_I64] * 5 + [_P])
+                                                   + [ctypes.c_size_t] + [_I64] * 9 + [_P])
             lib.mhs_out_gate_fwd_f32.restype = ctypes.c_int
             lib.mhs_out_gate_fwd_f32.argtypes = [_P] * 3 + [_I64, _P] + [_I64] * 3 + [_P]
             lib.mhs_out_gate_bwd_workspace_bytes.restype = ctypes.c_size_t
             lib.mhs_out_gate_bwd_workspace_bytes.argtypes = [_I64] * 3
             lib.mhs_out_gate_bwd_f32.restype = ctypes.c_int
-            lib.mhs_out_gate_bwd_f32.argtypes = ([_P] * 3 + [_I64] + [_P] * 5 + [ctypes.c_size_t]
-                                                 + [_I64] * 3 + [_P])
+            lib.mhs_out_gate_bwd_f32.argtypes = ([_P] * 3 + [_I64] + [_P] * 3 + [_I64] + [_P] * 2
+                                                 + [ctypes.c_size_t] + [_I64] * 3 + [_P])
             for name in ("mhs_scan_fwd_bf16", "mhs_scan_bwd_bf16"):
                 getattr(lib, name).restype = ctypes.c_int
             lib.mhs_scan_fwd_bf16.argtypes = lib.mhs_scan_fwd_ws_f32.argtypes
@@ -282,14 +282,27 @@ def _scan_step_fake(h, x, dt, aneg, b_in, c_in):
     return x.new_empty((h.shape[0], h.shape[1]))
 
 
-def _conv_rows(x: torch.Tensor) -> int:
-    """Row stride (floats) of a (B,T,D) tensor whose rows are dense and whose
-    batch rows follow each other; raises for other layouts."""
+def _rows(x: torch.Tensor) -> int:
+    """Row stride (elements) of a (B,T,D) tensor whose rows are dense and whose
+    batch rows follow each other (a contiguous tensor, or a column slice of a
+    wider one); raises for other layouts."""
     bt, t_len, d = x.shape
     if x.stride(2) != 1 or x.stride(1) < d or (bt > 1 and x.stride(0) != t_len * x.stride(1)):
-        raise HipScanError(f"conv1d_silu: unsupported x strides {x.stride()} for shape "
-                           f"{tuple(x.shape)}")
+        raise HipScanError(f"unsupported strides {x.stride()} for shape {tuple(x.shape)}: "
+                           "need dense rows, batch rows back to back")
     return x.stride(1)
+
+
+_conv_rows = _rows
+
+
+def _bc_rows(b_in: torch.Tensor, c_in: torch.Tensor) -> int:
+    """The common row stride of B and C (both contiguous, or both column
+    slices of one wider tensor)."""
+    ld = _rows(b_in)
+    if _rows(c_in) != ld:
+        raise HipScanError(f"B and C need one row stride; got {b_in.stride()} and {c_in.stride()}")
+    return ld
 
 
 def _conv1d_silu_fwd_impl(x: torch.Tensor, w: torch.Tensor, bias: torch.Tensor) -> torch.Tensor:
@@ -327,7 +340,7 @@ def _conv1d_silu_bwd_impl(x: torch.Tensor, w: torch.Tensor, bias: torch.Tensor, 
     ws = torch.empty(ws_bytes, dtype=torch.uint8, device=x.device)
     with _on(x.device):
         rc = lib.mhs_conv1d_silu_bwd_f32(
-            _ptr(x), _conv_rows(x), _ptr(w), _ptr(bias), _ptr(dout), _ptr(dx), _ptr(dw),
+            _ptr(x), _rows(x), _ptr(w), _ptr(bias), _ptr(dout), _ptr(dx), 0, _ptr(dw),
             _ptr(dbias), _ptr(ws), ws_bytes, bt, t_len, d, k, _stream(x.device))
     _check(rc, "mhs_conv1d_silu_bwd_f32")
     return dx, dw, dbias
@@ -341,14 +354,47 @@ def _conv1d_silu_bwd_fake(x, w, bias, dout):
     return x.new_empty(x.shape), torch.empty_like(w), torch.empty_like(bias)
 
 
+def _conv1d_silu_bwd_into_impl(x: torch.Tensor, w: torch.Tensor, bias: torch.Tensor,
+                               dout: torch.Tensor, dx: torch.Tensor
+                               ) -> tuple[torch.Tensor, torch.Tensor]:
+    """conv1d_silu_bwd writing dx into the given (B,T,D) tensor, which may be
+    a column slice of a wider one (the x half of the in_proj output's
+    gradient); returns (dw, dbias)."""
+    bt, t_len, d = x.shape
+    k = w.shape[1]
+    lib = library()
+    dw = torch.empty_like(w)
+    dbias = torch.empty_like(bias)
+    ws_bytes = int(lib.mhs_conv1d_silu_bwd_workspace_bytes(bt, t_len, d, k))
+    if ws_bytes == 0:
+        raise HipScanError(f"no conv workspace size for shape {(bt, t_len, d)} kernel {k}")
+    ws = torch.empty(ws_bytes, dtype=torch.uint8, device=x.device)
+    with _on(x.device):
+        rc = lib.mhs_conv1d_silu_bwd_f32(
+            _ptr(x), _rows(x), _ptr(w), _ptr(bias), _ptr(dout), _ptr(dx), _rows(dx), _ptr(dw),
+            _ptr(dbias), _ptr(ws), ws_bytes, bt, t_len, d, k, _stream(x.device))
+    _check(rc, "mhs_conv1d_silu_bwd_f32")
+    return dw, dbias
+
+
+conv1d_silu_bwd_into = _register("conv1d_silu_bwd_into", _conv1d_silu_bwd_into_impl, ("dx",))
+
+
+@conv1d_silu_bwd_into.register_fake
+def _conv1d_silu_bwd_into_fake(x, w, bias, dout, dx):
+    return torch.empty_like(w), torch.empty_like(bias)
+
+
 def _scan_gated_fwd_impl(x: torch.Tensor, dt_raw: torch.Tensor, a_raw: torch.Tensor,
                    b_in: torch.Tensor, c_in: torch.Tensor, dt_min: float, dt_max: float,
                    chunk: int, with_ckpt: bool
                    ) -> tuple[torch.Tensor, torch.Tensor, torch.Tensor]:
     """scan_fwd with dt = dt_min + (dt_max - dt_min) * sigmoid(dt_raw) and
-    Aneg = softplus(a_raw) formed inside the kernels."""
+    Aneg = softplus(a_raw) formed inside the kernels. dt_raw, B and C may be
+    column slices of a wider tensor (dense rows; B and C with one row stride)."""
     bt, t_len, d = x.shape
     n = a_raw.shape[1]
+    ld_dt, ld_bc = _rows(dt_raw), _bc_rows(b_in, c_in)
     y, ckpt, h_last = _fwd_outputs(x, n, chunk, with_ckpt)
     ws, ws_bytes = _fwd_workspace(x, n)
     lib = library()
@@ -356,7 +402,7 @@ def _scan_gated_fwd_impl(x: torch.Tensor, dt_raw: torch.Tensor, a_raw: torch.Ten
     with _on(x.device):
         rc = fn(_ptr(x), _ptr(dt_raw), _ptr(a_raw), _ptr(b_in), _ptr(c_in), dt_min, dt_max,
                 _ptr(y), _ptr(ckpt) if with_ckpt else None, _ptr(h_last), _ptr(ws), ws_bytes,
-                bt, t_len, d, n, chunk, _stream(x.device))
+                bt, t_len, d, n, chunk, ld_dt, ld_bc, _stream(x.device))
     _check(rc, "gated scan forward")
     return y, ckpt, h_last
 
@@ -374,15 +420,17 @@ def _scan_gated_bwd_impl(x: torch.Tensor, dt_raw: torch.Tensor, a_raw: torch.Ten
                    dy: torch.Tensor, dh_last: Optional[torch.Tensor], ckpt: torch.Tensor,
                    chunk: int
                    ) -> tuple[torch.Tensor, torch.Tensor, torch.Tensor, torch.Tensor, torch.Tensor]:
-    """(dx, d dt_raw, d a_raw, dB, dC) for the gated forward that produced `ckpt`."""
+    """(dx, d dt_raw, d a_raw, dB, dC) for the gated forward that produced
+    `ckpt`; the gradients are contiguous (inputs as scan_gated_fwd)."""
     bt, t_len, d = x.shape
     n = a_raw.shape[1]
+    ld_dt, ld_bc = _rows(dt_raw), _bc_rows(b_in, c_in)
     lib = library()
     dx = torch.empty_like(x)
-    ddt = torch.empty_like(dt_raw)
+    ddt = x.new_empty((bt, t_len, d))
     da = torch.empty_like(a_raw)
-    db = torch.empty_like(b_in)
-    dc = torch.empty_like(c_in)
+    db = x.new_empty((bt, t_len, n))
+    dc = x.new_empty((bt, t_len, n))
     ws_bytes = int(lib.mhs_scan_bwd_workspace_bytes(bt, t_len, d, n, chunk))
     if ws_bytes == 0:
         raise HipScanError(f"no backward workspace size for shape {(bt, t_len, d, n)} chunk {chunk}")
@@ -391,12 +439,57 @@ def _scan_gated_bwd_impl(x: torch.Tensor, dt_raw: torch.Tensor, a_raw: torch.Ten
     with _on(x.device):
         rc = fn(_ptr(x), _ptr(dt_raw), _ptr(a_raw), _ptr(b_in), _ptr(c_in), dt_min, dt_max,
                 _ptr(dy), _ptr(dh_last), _ptr(ckpt), _ptr(dx), _ptr(ddt), _ptr(da), _ptr(db),
-                _ptr(dc), _ptr(ws), ws_bytes, bt, t_len, d, n, chunk, _stream(x.device))
+                _ptr(dc), _ptr(ws), ws_bytes, bt, t_len, d, n, chunk, ld_dt, ld_bc, 0, 0,
+                _stream(x.device))
     _check(rc, "gated scan backward")
     return dx, ddt, da, db, dc
 
 
 scan_gated_bwd = _register("scan_gated_bwd", _scan_gated_bwd_impl, ())
+
+
+def _scan_gated_bwd_into_impl(x: torch.Tensor, dt_raw: torch.Tensor, a_raw: torch.Tensor,
+                              b_in: torch.Tensor, c_in: torch.Tensor, dt_min: float,
+                              dt_max: float, dy: torch.Tensor, dh_last: Optional[torch.Tensor],
+                              ckpt: torch.Tensor, chunk: int, dproj: torch.Tensor
+                              ) -> tuple[torch.Tensor, torch.Tensor]:
+    """scan_gated_bwd writing d dt_raw, dB and dC into the column slices
+    [0, D), [D, D+N), [D+N, D+2N) of dproj (B, T, D+2N, contiguous): the
+    gradient of one projection whose output rows are [dt_raw | B | C].
+    Returns (dx, d a_raw)."""
+    bt, t_len, d = x.shape
+    n = a_raw.shape[1]
+    if dproj.shape != (bt, t_len, d + 2 * n) or not dproj.is_contiguous():
+        raise HipScanError(f"dproj must be a contiguous {(bt, t_len, d + 2 * n)} tensor; got "
+                           f"{tuple(dproj.shape)} strides {dproj.stride()}")
+    ld_dt, ld_bc = _rows(dt_raw), _bc_rows(b_in, c_in)
+    lib = library()
+    dx = torch.empty_like(x)
+    da = torch.empty_like(a_raw)
+    ws_bytes = int(lib.mhs_scan_bwd_workspace_bytes(bt, t_len, d, n, chunk))
+    if ws_bytes == 0:
+        raise HipScanError(f"no backward workspace size for shape {(bt, t_len, d, n)} chunk {chunk}")
+    ws = torch.empty(ws_bytes, dtype=torch.uint8, device=x.device)
+    fn = lib.mhs_scan_gated_bwd_bf16 if x.dtype == torch.bfloat16 else lib.mhs_scan_gated_bwd_f32
+    es = dproj.element_size()
+    base = dproj.data_ptr()
+    w = d + 2 * n
+    with _on(x.device):
+        rc = fn(_ptr(x), _ptr(dt_raw), _ptr(a_raw), _ptr(b_in), _ptr(c_in), dt_min, dt_max,
+                _ptr(dy), _ptr(dh_last), _ptr(ckpt), _ptr(dx), base, _ptr(da), base + d * es,
+                base + (d + n) * es, _ptr(ws), ws_bytes, bt, t_len, d, n, chunk, ld_dt, ld_bc, w,
+                w, _stream(x.device))
+    _check(rc, "gated scan backward")
+    return dx, da
+
+
+scan_gated_bwd_into = _register("scan_gated_bwd_into", _scan_gated_bwd_into_impl, ("dproj",))
+
+
+@scan_gated_bwd_into.register_fake
+def _scan_gated_bwd_into_fake(x, dt_raw, a_raw, b_in, c_in, dt_min, dt_max, dy, dh_last, ckpt,
+                              chunk, dproj):
+    return torch.empty_like(x), torch.empty_like(a_raw)
 
 
 @scan_gated_bwd.register_fake
@@ -439,7 +532,7 @@ def _out_gate_bwd_impl(y: torch.Tensor, d_skip: torch.Tensor, z: torch.Tensor, d
     ws = torch.empty(ws_bytes, dtype=torch.uint8, device=y.device)
     with _on(y.device):
         rc = lib.mhs_out_gate_bwd_f32(
-            _ptr(y), _ptr(d_skip), _ptr(z), _conv_rows(z), _ptr(dout), _ptr(dy), _ptr(dz),
+            _ptr(y), _ptr(d_skip), _ptr(z), _rows(z), _ptr(dout), _ptr(dy), _ptr(dz), 0,
             _ptr(dd), _ptr(ws), ws_bytes, bt, t_len, d, _stream(y.device))
     _check(rc, "mhs_out_gate_bwd_f32")
     return dy, dd, dz
@@ -451,3 +544,33 @@ out_gate_bwd = _register("out_gate_bwd", _out_gate_bwd_impl, ())
 @out_gate_bwd.register_fake
 def _out_gate_bwd_fake(y, d_skip, z, dout):
     return y.new_empty(y.shape), torch.empty_like(d_skip), y.new_empty(y.shape)
+
+
+def _out_gate_bwd_into_impl(y: torch.Tensor, d_skip: torch.Tensor, z: torch.Tensor,
+                            dout: torch.Tensor, dz: torch.Tensor
+                            ) -> tuple[torch.Tensor, torch.Tensor]:
+    """out_gate_bwd writing dz into the given (B,T,D) tensor, which may be a
+    column slice of a wider one (the z half of the in_proj output's
+    gradient); returns (dy, dd_skip)."""
+    bt, t_len, d = y.shape
+    lib = library()
+    dy = y.new_empty((bt, t_len, d))
+    dd = torch.empty_like(d_skip)
+    ws_bytes = int(lib.mhs_out_gate_bwd_workspace_bytes(bt, t_len, d))
+    if ws_bytes == 0:
+        raise HipScanError(f"no output-gate workspace size for shape {(bt, t_len, d)}")
+    ws = torch.empty(ws_bytes, dtype=torch.uint8, device=y.device)
+    with _on(y.device):
+        rc = lib.mhs_out_gate_bwd_f32(
+            _ptr(y), _ptr(d_skip), _ptr(z), _rows(z), _ptr(dout), _ptr(dy), _ptr(dz), _rows(dz),
+            _ptr(dd), _ptr(ws), ws_bytes, bt, t_len, d, _stream(y.device))
+    _check(rc, "mhs_out_gate_bwd_f32")
+    return dy, dd
+
+
+out_gate_bwd_into = _register("out_gate_bwd_into", _out_gate_bwd_into_impl, ("dz",))
+
+
+@out_gate_bwd_into.register_fake
+def _out_gate_bwd_into_fake(y, d_skip, z, dout, dz):
+    return y.new_empty(y.shape), torch.empty_like(d_skip)

@@ -87,6 +87,10 @@ struct BwdArgs {
   int nseg, cps;
   float* carryL;
   float* carrySdt;
+  // Row strides (elements between consecutive time steps) of dt, of B and C,
+  // and of ddt: D, N and D for contiguous tensors, more for column slices of
+  // a wider projection output (and its gradient). x, dy, dx are contiguous.
+  int ld_dt, ld_bc, ld_ddt;
 };
 
 // One staging buffer (the kernel keeps two) and the single-buffered rest.
@@ -192,8 +196,9 @@ bwd_kernel(BwdArgs a) {
   float sdt_acc = 0.f;   // CARRY: sum of dt over the segment
 
   const size_t row0 = (size_t)b * T;
-  const QuadLoader<kCH, PER, ES> ql(tid, NT, D, d0);
-  const RowLoader<PERS, NPL, ES> rl(tid, NT, N, NP);
+  const QuadLoader<kCH, PER, ES> ql(tid, NT, D, d0, D);
+  const QuadLoader<kCH, PER, ES> qdt(tid, NT, D, d0, a.ld_dt);
+  const RowLoader<PERS, NPL, ES> rl(tid, NT, N, NP, a.ld_bc);
   float4 px[PER], pd[PER], py[PER];
   float pb[PERS], pc[PERS], ph[NPL];
 
@@ -203,19 +208,21 @@ bwd_kernel(BwdArgs a) {
   auto chunk_len = [&](int ci) {
     return (ci < c_lo || ci >= c_hi) ? 0 : max(0, min(K, T - ci * K));
   };
-  // Resource over one chunk of a (batch, T, D) tensor from channel d0 on.
-  auto chunk_buf = [&](const void* base, int ci) {
+  // Resource over one chunk of a (batch, T, D) tensor of row stride ld
+  // (channels d0 .. D-1 of its rows).
+  auto chunk_buf = [&](const void* base, int ci, int ld) {
     const int len = chunk_len(ci);
-    return GBuf(elem_at<ES>(base, (row0 + chunk_t0(ci)) * D + d0),
-                len > 0 ? (unsigned)ES * (unsigned)(len * D - d0) : 0u);
+    return GBuf(elem_at<ES>(base, (row0 + chunk_t0(ci)) * ld + d0),
+                len > 0 ? (unsigned)ES * (unsigned)((len - 1) * ld + D - d0) : 0u);
   };
   auto load_sub = [&](int ci) {           // global -> staging registers
     const int len = chunk_len(ci);
-    const GBuf gs_b(elem_at<ES>(a.B, (row0 + chunk_t0(ci)) * N), (unsigned)ES * (unsigned)(len * N));
-    const GBuf gs_c(elem_at<ES>(a.C, (row0 + chunk_t0(ci)) * N), (unsigned)ES * (unsigned)(len * N));
-    if constexpr (!CARRY) ql.load(px, chunk_buf(a.x, ci), D);
-    ql.load(pd, chunk_buf(a.dt, ci), D);
-    ql.load(py, chunk_buf(a.dy, ci), D);
+    const unsigned sbytes = len > 0 ? (unsigned)ES * (unsigned)((len - 1) * a.ld_bc + N) : 0u;
+    const GBuf gs_b(elem_at<ES>(a.B, (row0 + chunk_t0(ci)) * a.ld_bc), sbytes);
+    const GBuf gs_c(elem_at<ES>(a.C, (row0 + chunk_t0(ci)) * a.ld_bc), sbytes);
+    if constexpr (!CARRY) ql.load(px, chunk_buf(a.x, ci, D));
+    qdt.load(pd, chunk_buf(a.dt, ci, a.ld_dt));
+    ql.load(py, chunk_buf(a.dy, ci, D));
     if constexpr (!CARRY) rl.load(pb, gs_b);
     rl.load(pc, gs_c);
   };
@@ -240,15 +247,18 @@ bwd_kernel(BwdArgs a) {
   auto finalize = [&](int ci, int j) {
     const float* sx = lds + j * BUF + oX;
     const float* sdt = lds + j * BUF;
-    const GBuf gdx = chunk_buf(a.dx, ci), gddt = chunk_buf(a.ddt, ci);
+    const GBuf gdx = chunk_buf(a.dx, ci, D), gddt = chunk_buf(a.ddt, ci, a.ld_ddt);
 #pragma unroll
     for (int f = 0; f < FT; ++f) {
       const int task0 = tid + f * NT;
       const bool ok = task0 < kSteps / 2 * kCH;
       const int task = ok ? task0 : 0;
       const int cc = task % kCH, k = 2 * (task / kCH);
-      const unsigned o0 = (ok && d0 + cc < D) ? (unsigned)ES * ((unsigned)k * (unsigned)D + cc) : kOOB;
-      const unsigned o1 = o0 == kOOB ? kOOB : o0 + (unsigned)ES * (unsigned)D;
+      const bool okc = ok && d0 + cc < D;
+      const unsigned o0 = okc ? (unsigned)ES * ((unsigned)k * (unsigned)D + cc) : kOOB;
+      const unsigned o1 = okc ? o0 + (unsigned)ES * (unsigned)D : kOOB;
+      const unsigned od0 = okc ? (unsigned)ES * ((unsigned)k * (unsigned)a.ld_ddt + cc) : kOOB;
+      const unsigned od1 = okc ? od0 + (unsigned)ES * (unsigned)a.ld_ddt : kOOB;
       const float2 xv = lds2(sx + cm_elem(cc, k)), dtv = lds2(sdt + cm_elem(cc, k));
       const float x0 = xv.x, x1 = xv.y, t0v = dtv.x, t1v = dtv.y;
       float s1a = 0.f, s1b = 0.f, s2a = 0.f, s2b = 0.f;
@@ -268,8 +278,8 @@ bwd_kernel(BwdArgs a) {
         g0 *= u0 * (a.dt_span - u0) * a.dt_inv_span;
         g1 *= u1 * (a.dt_span - u1) * a.dt_inv_span;
       }
-      st_elem<ES, kStream>(gddt, g0, o0);
-      st_elem<ES, kStream>(gddt, g1, o1);
+      st_elem<ES, kStream>(gddt, g0, od0);
+      st_elem<ES, kStream>(gddt, g1, od1);
     }
     const int len = chunk_len(ci);
     const size_t wrow = ((size_t)blockIdx.x * a.batch + b) * T + chunk_t0(ci);
@@ -458,24 +468,25 @@ __device__ __forceinline__ void ordered_sum2(const float* __restrict__ p, const 
 
 // a_raw: null, or A for the gated backward: then daneg receives dAneg *
 // softplus'(A) = dAneg * sigmoid(A), the gradient of A. dB, dC: ES-byte
-// elements (fp32 or bf16).
+// elements (fp32 or bf16), rows of N elements ld_dbc apart.
 template <int ES = 4>
 __global__ void __launch_bounds__(256)
 bwd_reduce_kernel(const float* __restrict__ wsB, const float* __restrict__ wsC,
                   const float* __restrict__ wsA, const float* __restrict__ a_raw,
                   void* __restrict__ dB, void* __restrict__ dC, float* __restrict__ daneg,
-                  int nblk, int batch, long long S, long long A) {
+                  int nblk, int batch, long long S, long long A, int N, long long ld_dbc) {
   const long long stride = (long long)gridDim.x * blockDim.x;
   for (long long i = (long long)blockIdx.x * blockDim.x + threadIdx.x; i < S + A; i += stride) {
     if (i < S) {
       float sb = 0.f, sc = 0.f;
       ordered_sum2(wsB + i, wsC + i, (size_t)S, nblk, sb, sc);
+      const long long o = ld_dbc == N ? i : (i / N) * ld_dbc + i % N;   // row stride ld_dbc
       if constexpr (ES == 4) {
-        static_cast<float*>(dB)[i] = sb;
-        static_cast<float*>(dC)[i] = sc;
+        static_cast<float*>(dB)[o] = sb;
+        static_cast<float*>(dC)[o] = sc;
       } else {
-        static_cast<unsigned short*>(dB)[i] = f32_to_bf16(sb);
-        static_cast<unsigned short*>(dC)[i] = f32_to_bf16(sc);
+        static_cast<unsigned short*>(dB)[o] = f32_to_bf16(sb);
+        static_cast<unsigned short*>(dC)[o] = f32_to_bf16(sc);
       }
     } else {
       const long long j = i - S;

@@ -100,7 +100,7 @@ struct Kernels {
   BwdFn carry = nullptr;    // adjoint-carry pass of the time segments
   BwdFn carry_g = nullptr;  // gated
   void (*reduce)(const float*, const float*, const float*, const float*, void*, void*, float*,
-                 int, int, long long, long long) = nullptr;
+                 int, int, long long, long long, int, long long) = nullptr;
 };
 
 // Activation element types: x, dt, B, C, y, dy, dx, ddt, dB, dC in fp32 or
@@ -306,13 +306,37 @@ FwdWs fwd_ws_layout(int64_t batch, int64_t T, int64_t D, int64_t N) {
   return w;
 }
 
+// Row strides (elements between consecutive time steps) of dt, B/C, ddt and
+// dB/dC; 0 means contiguous (D, N, D, N).
+struct Strides {
+  int64_t dt = 0, bc = 0, ddt = 0, dbc = 0;
+};
+
+int resolve_strides(const Strides& in, int64_t D, int64_t N, Strides& out) {
+  out.dt = in.dt ? in.dt : D;
+  out.bc = in.bc ? in.bc : N;
+  out.ddt = in.ddt ? in.ddt : D;
+  out.dbc = in.dbc ? in.dbc : N;
+  if (out.dt < D || out.ddt < D || out.bc < N || out.dbc < N)
+    return fail(MHS_EINVAL, "row strides must be at least d_inner (dt, ddt) and d_state (B, C, "
+                "dB, dC); got %lld %lld %lld %lld", (long long)out.dt, (long long)out.bc,
+                (long long)out.ddt, (long long)out.dbc);
+  if (out.dt >= (1LL << 24) || out.ddt >= (1LL << 24) || out.bc >= (1LL << 24) ||
+      out.dbc >= (1LL << 24))
+    return fail(MHS_EINVAL, "row stride too large");
+  return MHS_OK;
+}
+
 int scan_fwd(const void* x, const void* dt, const float* aneg, const void* B, const void* C,
              void* y, float* ckpt, float* h_last, void* workspace, size_t workspace_bytes,
              int64_t batch, int64_t seqlen, int64_t d_inner, int64_t d_state, int64_t chunk,
-             void* stream, const Gate& g, Elem e) {
+             void* stream, const Gate& g, Elem e, const Strides& st_in = Strides{}) {
   int rc = check_shape(batch, seqlen, d_inner, d_state, chunk);
   if (rc) return rc;
   if (!x || !dt || !aneg || !B || !C) return fail(MHS_EINVAL, "null input pointer");
+  Strides st;
+  rc = resolve_strides(st_in, d_inner, d_state, st);
+  if (rc) return rc;
   const void* ptrs[] = {x, dt, aneg, B, C, y, ckpt, h_last};
   for (const void* q : ptrs)
     if (q && !aligned16(q)) return fail(MHS_EINVAL, "device pointers must be 16-byte aligned");
@@ -324,6 +348,8 @@ int scan_fwd(const void* x, const void* dt, const float* aneg, const void* B, co
   a.T = (int)seqlen; a.D = (int)d_inner; a.N = (int)d_state;
   a.K = (int)std::min<int64_t>(chunk, seqlen);
   a.nchunk = (int)mhs_num_chunks(seqlen, chunk);
+  a.ld_dt = (int)st.dt;
+  a.ld_bc = (int)st.bc;
   hipStream_t s = static_cast<hipStream_t>(stream);
   const FwdWs w = fwd_ws_layout(batch, seqlen, d_inner, d_state);
   if (workspace == nullptr || w.nseg == 1) return launch_fwd(p, a, (int)batch, s, g, e);
@@ -366,12 +392,15 @@ int scan_bwd(const void* x, const void* dt, const float* aneg, const void* B, co
              const void* dy, const float* dh_last, const float* ckpt, void* dx, void* ddt,
              float* daneg, void* dB, void* dC, void* workspace, size_t workspace_bytes,
              int64_t batch, int64_t seqlen, int64_t d_inner, int64_t d_state, int64_t chunk,
-             void* stream, const Gate& g, Elem e) {
+             void* stream, const Gate& g, Elem e, const Strides& st_in = Strides{}) {
   int rc = check_shape(batch, seqlen, d_inner, d_state, chunk);
   if (rc) return rc;
   if (!x || !dt || !aneg || !B || !C || !dy || !ckpt || !dx || !ddt || !daneg || !dB || !dC ||
       !workspace)
     return fail(MHS_EINVAL, "null pointer argument");
+  Strides st;
+  rc = resolve_strides(st_in, d_inner, d_state, st);
+  if (rc) return rc;
   const void* ptrs[] = {x, dt, aneg, B, C, dy, dh_last, ckpt, dx, ddt, daneg, dB, dC};
   for (const void* q : ptrs)
     if (q && !aligned16(q)) return fail(MHS_EINVAL, "device pointers must be 16-byte aligned");
@@ -399,6 +428,8 @@ int scan_bwd(const void* x, const void* dt, const float* aneg, const void* B, co
     f.ckpt = reinterpret_cast<float*>(ws + w.fine);
     f.h_last = nullptr;
     f.T = T; f.D = D; f.N = N; f.K = p.bwd_ki;
+    f.ld_dt = (int)st.dt;
+    f.ld_bc = (int)st.bc;
     f.nchunk = (int)mhs_num_chunks(T, p.bwd_ki);
     // Time segments that start on the caller's checkpoints (stride K): each
     // is a multiple of lcm(16, K) steps and starts from the exact state, so
@@ -432,6 +463,9 @@ int scan_bwd(const void* x, const void* dt, const float* aneg, const void* B, co
   a.cps = w.cps;
   a.carryL = w.nseg > 1 ? reinterpret_cast<float*>(ws + w.carryL) : nullptr;
   a.carrySdt = w.nseg > 1 ? reinterpret_cast<float*>(ws + w.carryS) : nullptr;
+  a.ld_dt = (int)st.dt;
+  a.ld_bc = (int)st.bc;
+  a.ld_ddt = (int)st.ddt;
   const unsigned nblk = (unsigned)((D + ch - 1) / ch);
   if (w.nseg > 1) {
     // Adjoint carries of segments 1..nseg-1 (segment 0 passes nothing on).
@@ -456,7 +490,7 @@ int scan_bwd(const void* x, const void* dt, const float* aneg, const void* B, co
   const int blocks = (int)std::min<long long>((total + 255) / 256, 4096);
   hipLaunchKernelGGL(p.k[e].reduce, dim3(blocks), dim3(256), 0, s, a.wsB, a.wsC, a.wsA,
                      g.on ? aneg : nullptr, dB, dC, daneg, (D + ch - 1) / ch,
-                     (int)batch * w.nseg, S, A);
+                     (int)batch * w.nseg, S, A, N, (long long)st.dbc);
   return check_launch("backward reduction kernel");
 }
 
@@ -540,13 +574,13 @@ int mhs_scan_gated_fwd_f32(const float* x, const float* dt_raw, const float* A, 
                            const float* C, float dt_min, float dt_max, float* y, float* ckpt,
                            float* h_last, void* workspace, size_t workspace_bytes, int64_t batch,
                            int64_t seqlen, int64_t d_inner, int64_t d_state, int64_t chunk,
-                           void* stream) {
+                           int64_t ld_dt, int64_t ld_bc, void* stream) {
   g_err[0] = '\0';
   Gate g;
   const int rc = check_gate(dt_min, dt_max, g);
   if (rc) return rc;
   return scan_fwd(x, dt_raw, A, B, C, y, ckpt, h_last, workspace, workspace_bytes, batch, seqlen,
-                  d_inner, d_state, chunk, stream, g, kF32);
+                  d_inner, d_state, chunk, stream, g, kF32, Strides{ld_dt, ld_bc, 0, 0});
 }
 
 int mhs_scan_gated_bwd_f32(const float* x, const float* dt_raw, const float* A, const float* B,
@@ -554,13 +588,15 @@ int mhs_scan_gated_bwd_f32(const float* x, const float* dt_raw, const float* A, 
                            const float* dh_last, const float* ckpt, float* dx, float* ddt_raw,
                            float* dA, float* dB, float* dC, void* workspace,
                            size_t workspace_bytes, int64_t batch, int64_t seqlen, int64_t d_inner,
-                           int64_t d_state, int64_t chunk, void* stream) {
+                           int64_t d_state, int64_t chunk, int64_t ld_dt, int64_t ld_bc,
+                           int64_t ld_ddt, int64_t ld_dbc, void* stream) {
   g_err[0] = '\0';
   Gate g;
   const int rc = check_gate(dt_min, dt_max, g);
   if (rc) return rc;
   return scan_bwd(x, dt_raw, A, B, C, dy, dh_last, ckpt, dx, ddt_raw, dA, dB, dC, workspace,
-                  workspace_bytes, batch, seqlen, d_inner, d_state, chunk, stream, g, kF32);
+                  workspace_bytes, batch, seqlen, d_inner, d_state, chunk, stream, g, kF32,
+                  Strides{ld_dt, ld_bc, ld_ddt, ld_dbc});
 }
 
 int mhs_scan_fwd_bf16(const uint16_t* x, const uint16_t* dt, const float* aneg, const uint16_t* B,
@@ -587,13 +623,14 @@ int mhs_scan_gated_fwd_bf16(const uint16_t* x, const uint16_t* dt_raw, const flo
                             const uint16_t* B, const uint16_t* C, float dt_min, float dt_max,
                             uint16_t* y, float* ckpt, float* h_last, void* workspace,
                             size_t workspace_bytes, int64_t batch, int64_t seqlen,
-                            int64_t d_inner, int64_t d_state, int64_t chunk, void* stream) {
+                            int64_t d_inner, int64_t d_state, int64_t chunk, int64_t ld_dt,
+                            int64_t ld_bc, void* stream) {
   g_err[0] = '\0';
   Gate g;
   const int rc = check_gate(dt_min, dt_max, g);
   if (rc) return rc;
   return scan_fwd(x, dt_raw, A, B, C, y, ckpt, h_last, workspace, workspace_bytes, batch, seqlen,
-                  d_inner, d_state, chunk, stream, g, kBF16);
+                  d_inner, d_state, chunk, stream, g, kBF16, Strides{ld_dt, ld_bc, 0, 0});
 }
 
 int mhs_scan_gated_bwd_bf16(const uint16_t* x, const uint16_t* dt_raw, const float* A,
@@ -602,13 +639,15 @@ int mhs_scan_gated_bwd_bf16(const uint16_t* x, const uint16_t* dt_raw, const flo
                             uint16_t* dx, uint16_t* ddt_raw, float* dA, uint16_t* dB,
                             uint16_t* dC, void* workspace, size_t workspace_bytes, int64_t batch,
                             int64_t seqlen, int64_t d_inner, int64_t d_state, int64_t chunk,
+                            int64_t ld_dt, int64_t ld_bc, int64_t ld_ddt, int64_t ld_dbc,
                             void* stream) {
   g_err[0] = '\0';
   Gate g;
   const int rc = check_gate(dt_min, dt_max, g);
   if (rc) return rc;
   return scan_bwd(x, dt_raw, A, B, C, dy, dh_last, ckpt, dx, ddt_raw, dA, dB, dC, workspace,
-                  workspace_bytes, batch, seqlen, d_inner, d_state, chunk, stream, g, kBF16);
+                  workspace_bytes, batch, seqlen, d_inner, d_state, chunk, stream, g, kBF16,
+                  Strides{ld_dt, ld_bc, ld_ddt, ld_dbc});
 }
 
 int mhs_scan_step_f32(float* h, const float* x, const float* dt, const float* aneg, const float* B,
@@ -679,10 +718,11 @@ void conv_fwd_launch(const float* x, long long x_rs, const float* w, const float
 }
 template <int K>
 void conv_bwd_launch(const float* x, long long x_rs, const float* w, const float* bias,
-                     const float* dout, float* dx, float* wsp, dim3 grid, int T, int D,
-                     hipStream_t s) {
+                     const float* dout, float* dx, long long dx_rs, float* wsp, dim3 grid, int T,
+                     int D, hipStream_t s) {
   hipLaunchKernelGGL((mhs::conv_silu_bwd_kernel<K, kConvTPT>), grid,
-                     dim3(mhs::kConvCh * mhs::kConvTG), 0, s, x, x_rs, w, bias, dout, dx, wsp, T, D);
+                     dim3(mhs::kConvCh * mhs::kConvTG), 0, s, x, x_rs, w, bias, dout, dx, dx_rs,
+                     wsp, T, D);
 }
 
 }  // namespace
@@ -720,13 +760,16 @@ size_t mhs_conv1d_silu_bwd_workspace_bytes(int64_t batch, int64_t seqlen, int64_
 }
 
 int mhs_conv1d_silu_bwd_f32(const float* x, int64_t x_row_stride, const float* w,
-                            const float* bias, const float* dout, float* dx, float* dw,
-                            float* dbias, void* workspace, size_t workspace_bytes,
+                            const float* bias, const float* dout, float* dx, int64_t dx_row_stride,
+                            float* dw, float* dbias, void* workspace, size_t workspace_bytes,
                             int64_t batch, int64_t seqlen, int64_t d_inner, int64_t kernel_size,
                             void* stream) {
   g_err[0] = '\0';
   int rc = check_conv(batch, seqlen, d_inner, kernel_size, x_row_stride);
   if (rc) return rc;
+  const long long dx_rs = dx_row_stride ? dx_row_stride : d_inner;
+  if (dx_rs < d_inner) return fail(MHS_EINVAL, "dx row stride %lld < d_inner %lld", dx_rs,
+                                   (long long)d_inner);
   if (!x || !w || !bias || !dout || !dx || !dw || !dbias || !workspace)
     return fail(MHS_EINVAL, "null pointer argument");
   const size_t need = mhs_conv1d_silu_bwd_workspace_bytes(batch, seqlen, d_inner, kernel_size);
@@ -739,14 +782,14 @@ int mhs_conv1d_silu_bwd_f32(const float* x, int64_t x_row_stride, const float* w
   const int T = (int)seqlen, D = (int)d_inner;
   float* wsp = static_cast<float*>(workspace);
   switch (kernel_size) {
-    case 1: conv_bwd_launch<1>(x, x_row_stride, w, bias, dout, dx, wsp, grid, T, D, s); break;
-    case 2: conv_bwd_launch<2>(x, x_row_stride, w, bias, dout, dx, wsp, grid, T, D, s); break;
-    case 3: conv_bwd_launch<3>(x, x_row_stride, w, bias, dout, dx, wsp, grid, T, D, s); break;
-    case 4: conv_bwd_launch<4>(x, x_row_stride, w, bias, dout, dx, wsp, grid, T, D, s); break;
-    case 5: conv_bwd_launch<5>(x, x_row_stride, w, bias, dout, dx, wsp, grid, T, D, s); break;
-    case 6: conv_bwd_launch<6>(x, x_row_stride, w, bias, dout, dx, wsp, grid, T, D, s); break;
-    case 7: conv_bwd_launch<7>(x, x_row_stride, w, bias, dout, dx, wsp, grid, T, D, s); break;
-    default: conv_bwd_launch<8>(x, x_row_stride, w, bias, dout, dx, wsp, grid, T, D, s); break;
+    case 1: conv_bwd_launch<1>(x, x_row_stride, w, bias, dout, dx, dx_rs, wsp, grid, T, D, s); break;
+    case 2: conv_bwd_launch<2>(x, x_row_stride, w, bias, dout, dx, dx_rs, wsp, grid, T, D, s); break;
+    case 3: conv_bwd_launch<3>(x, x_row_stride, w, bias, dout, dx, dx_rs, wsp, grid, T, D, s); break;
+    case 4: conv_bwd_launch<4>(x, x_row_stride, w, bias, dout, dx, dx_rs, wsp, grid, T, D, s); break;
+    case 5: conv_bwd_launch<5>(x, x_row_stride, w, bias, dout, dx, dx_rs, wsp, grid, T, D, s); break;
+    case 6: conv_bwd_launch<6>(x, x_row_stride, w, bias, dout, dx, dx_rs, wsp, grid, T, D, s); break;
+    case 7: conv_bwd_launch<7>(x, x_row_stride, w, bias, dout, dx, dx_rs, wsp, grid, T, D, s); break;
+    default: conv_bwd_launch<8>(x, x_row_stride, w, bias, dout, dx, dx_rs, wsp, grid, T, D, s); break;
   }
   rc = check_launch("conv1d+silu backward kernel");
   if (rc) return rc;
@@ -784,12 +827,15 @@ size_t mhs_out_gate_bwd_workspace_bytes(int64_t batch, int64_t seqlen, int64_t d
 }
 
 int mhs_out_gate_bwd_f32(const float* y, const float* d_skip, const float* z, int64_t z_row_stride,
-                         const float* dout, float* dy, float* dz, float* dd_skip, void* workspace,
-                         size_t workspace_bytes, int64_t batch, int64_t seqlen, int64_t d_inner,
-                         void* stream) {
+                         const float* dout, float* dy, float* dz, int64_t dz_row_stride,
+                         float* dd_skip, void* workspace, size_t workspace_bytes, int64_t batch,
+                         int64_t seqlen, int64_t d_inner, void* stream) {
   g_err[0] = '\0';
   int rc = check_conv(batch, seqlen, d_inner, 1, z_row_stride);
   if (rc) return rc;
+  const long long dz_rs = dz_row_stride ? dz_row_stride : d_inner;
+  if (dz_rs < d_inner) return fail(MHS_EINVAL, "dz row stride %lld < d_inner %lld", dz_rs,
+                                   (long long)d_inner);
   if (!y || !d_skip || !z || !dout || !dy || !dz || !dd_skip || !workspace)
     return fail(MHS_EINVAL, "null pointer argument");
   const size_t need = mhs_out_gate_bwd_workspace_bytes(batch, seqlen, d_inner);
@@ -802,8 +848,8 @@ int mhs_out_gate_bwd_f32(const float* y, const float* d_skip, const float* z, in
   float* wsp = static_cast<float*>(workspace);
   const int D = (int)d_inner;
   hipLaunchKernelGGL(mhs::out_gate_bwd_kernel<kConvTPT>, grid, dim3(mhs::kConvCh * mhs::kConvTG),
-                     0, s, y, d_skip, z, (long long)z_row_stride, dout, dy, dz, wsp, (int)seqlen,
-                     D);
+                     0, s, y, d_skip, z, (long long)z_row_stride, dout, dy, dz, dz_rs, wsp,
+                     (int)seqlen, D);
   rc = check_launch("output gate backward kernel");
   if (rc) return rc;
   hipLaunchKernelGGL(mhs::conv_reduce_kernel, dim3((unsigned)((D + 3) / 4)), dim3(256), 0, s, wsp,

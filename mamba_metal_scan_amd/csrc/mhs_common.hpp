@@ -380,15 +380,18 @@ template <int CH, int PER, int ES = 4>
 struct QuadLoader {
   static constexpr int TASKS = CH * kQuads;
   int tid, nthreads;
+  unsigned rs;          // row (time step) stride in bytes
   unsigned toff[PER];   // byte offset of step 4m of channel c from the sub-chunk base, or kOOB
-  __device__ __forceinline__ QuadLoader(int tid_, int nthreads_, int D, int d0)
-      : tid(tid_), nthreads(nthreads_) {
+  // D: channels; ld: elements between consecutive time steps (>= D; D for a
+  // contiguous (batch, T, D) tensor, more for a column slice of a wider one).
+  __device__ __forceinline__ QuadLoader(int tid_, int nthreads_, int D, int d0, int ld)
+      : tid(tid_), nthreads(nthreads_), rs((unsigned)ES * (unsigned)ld) {
 #pragma unroll
     for (int i = 0; i < PER; ++i) {
       const int e = tid + i * nthreads;
       const int c = e % CH, m = e / CH;
       toff[i] = (e < TASKS && d0 + c < D)
-                    ? (unsigned)ES * ((unsigned)(4 * m) * (unsigned)D + (unsigned)c)
+                    ? (unsigned)ES * ((unsigned)(4 * m) * (unsigned)ld + (unsigned)c)
                     : kOOB;
     }
   }
@@ -398,8 +401,7 @@ struct QuadLoader {
   // g covers (b, t0.., d0..) up to the end of the batch row (steps past T
   // are out of range).
   template <int POL = 0>
-  __device__ __forceinline__ void load(float4 (&v)[PER], const GBuf& g, int D) const {
-    const unsigned rs = (unsigned)ES * (unsigned)D;
+  __device__ __forceinline__ void load(float4 (&v)[PER], const GBuf& g) const {
 #pragma unroll
     for (int i = 0; i < PER; ++i) {
       const unsigned o = toff[i];
@@ -476,15 +478,16 @@ struct QuadLoader {
 // padded states and steps past T are zero.
 template <int PERS, int NPL, int ES = 4>
 struct RowLoader {
-  unsigned src[PERS];  // byte offset in the sub-chunk's global [16][N] block, or kOOB
+  unsigned src[PERS];  // byte offset in the sub-chunk's global [16][ld] block, or kOOB
   int dst[PERS];       // slot in the tile, or -1
-  __device__ __forceinline__ RowLoader(int tid, int nthreads, int N, int NP) {
+  // ld: elements between consecutive time steps (>= N).
+  __device__ __forceinline__ RowLoader(int tid, int nthreads, int N, int NP, int ld) {
 #pragma unroll
     for (int i = 0; i < PERS; ++i) {
       const int e = tid + i * nthreads;       // tile element (k, n), n fastest
       const int k = e / NP, n = e % NP;
       const bool in_tile = e < kSteps * NP;
-      src[i] = (in_tile && n < N) ? (unsigned)ES * (unsigned)(k * N + n) : kOOB;
+      src[i] = (in_tile && n < N) ? (unsigned)ES * (unsigned)(k * ld + n) : kOOB;
       dst[i] = in_tile ? (n / NPL) * (kSteps * NPL) + k * NPL + (n % NPL) : -1;
     }
   }

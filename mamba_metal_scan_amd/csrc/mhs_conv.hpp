@@ -66,7 +66,8 @@ template <int K, int TPT>
 __global__ void __launch_bounds__(kConvCh * kConvTG)
 conv_silu_bwd_kernel(const float* __restrict__ x, long long x_rs, const float* __restrict__ w,
                      const float* __restrict__ bias, const float* __restrict__ dout,
-                     float* __restrict__ dx, float* __restrict__ wsp, int T, int D) {
+                     float* __restrict__ dx, long long dx_rs, float* __restrict__ wsp, int T,
+                     int D) {
   __shared__ float part[kConvTG][K + 1][kConvCh];
   const int c = threadIdx.x % kConvCh;
   const int d = blockIdx.x * kConvCh + c;
@@ -84,7 +85,7 @@ conv_silu_bwd_kernel(const float* __restrict__ x, long long x_rs, const float* _
     const float bi = bias[d];
     const float* xb = x + (size_t)b * T * x_rs + d;
     const float* gb = dout + (size_t)b * T * D + d;
-    float* dxb = dx + (size_t)b * T * D + d;
+    float* dxb = dx + (size_t)b * T * dx_rs + d;   // rows dx_rs apart (>= D)
     // x[t0 - K + 1 .. t0 + TPT + K - 2]: inputs of pre over [t0, t0 + TPT + K - 1)
     constexpr int NX = TPT + 2 * (K - 1);
     float xw[NX];
@@ -112,7 +113,7 @@ conv_silu_bwd_kernel(const float* __restrict__ x, long long x_rs, const float* _
       float acc = 0.f;
 #pragma unroll
       for (int k = 0; k < K; ++k) acc = __builtin_fmaf(wk[k], sw[i + K - 1 - k], acc);
-      dxb[(size_t)(t0 + i) * D] = acc;
+      dxb[(size_t)(t0 + i) * dx_rs] = acc;
       // dw[k] += s[t] * x[t - K + 1 + k]; dbias += s[t]  (t = t0 + i < T)
 #pragma unroll
       for (int k = 0; k < K; ++k) pw[k] = __builtin_fmaf(sw[i], xw[i + k], pw[k]);

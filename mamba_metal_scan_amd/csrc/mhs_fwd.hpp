@@ -64,6 +64,10 @@ struct FwdArgs {
   // dt, to carrySdt (nseg, batch, D).
   float* carryH = nullptr;
   float* carrySdt = nullptr;
+  // Row strides (elements between consecutive time steps) of dt and of B,
+  // C: D and N for contiguous tensors, more for column slices of a wider
+  // projection output. x and y are contiguous.
+  int ld_dt = 0, ld_bc = 0;
 };
 
 constexpr int kCH = 32;   // channels per block
@@ -123,8 +127,9 @@ fwd_kernel(FwdArgs a) {
   }
 
   const size_t row0 = (size_t)b * T;
-  const QuadLoader<kCH, PER, ES> ql(tid, NT, D, d0);
-  const RowLoader<PERS, NPL, ES> rl(tid, NT, N, NP);
+  const QuadLoader<kCH, PER, ES> ql(tid, NT, D, d0, D);
+  const QuadLoader<kCH, PER, ES> qdt(tid, NT, D, d0, a.ld_dt);
+  const RowLoader<PERS, NPL, ES> rl(tid, NT, N, NP, a.ld_bc);
   float4 px[PER], pd[PER];
   float pb[PERS], pc[PERS];
   // Sub-chunk i of the segment (any i >= 0): first step and length (0 past
@@ -133,18 +138,21 @@ fwd_kernel(FwdArgs a) {
   auto sub_len = [&](int i) {
     return i < 0 ? 0 : max(0, min(kSteps, t_end - t_beg - i * kSteps));
   };
-  // Resource over one sub-chunk of a (batch, T, D) tensor from channel d0 on.
-  auto sub_buf = [&](const void* base, int i) {
+  // Resource over one sub-chunk of a (batch, T, D) tensor of row stride ld
+  // (channels d0 .. D-1 of its rows).
+  auto sub_buf = [&](const void* base, int i, int ld) {
     const int len = sub_len(i);
-    return GBuf(elem_at<ES>(base, (row0 + sub_t0(i)) * D + d0),
-                len > 0 ? (unsigned)ES * (unsigned)(len * D - d0) : 0u);
+    return GBuf(elem_at<ES>(base, (row0 + sub_t0(i)) * ld + d0),
+                len > 0 ? (unsigned)ES * (unsigned)((len - 1) * ld + D - d0) : 0u);
   };
   auto load_sub = [&](int i) {            // global -> staging registers
-    const unsigned sbytes = (unsigned)ES * (unsigned)(sub_len(i) * N);
-    ql.load(px, sub_buf(a.x, i), D);
-    ql.load(pd, sub_buf(a.dt, i), D);
-    rl.load(pb, GBuf(elem_at<ES>(a.B, (row0 + sub_t0(i)) * N), sbytes));
-    if constexpr (!FCARRY) rl.load(pc, GBuf(elem_at<ES>(a.C, (row0 + sub_t0(i)) * N), sbytes));
+    const int len = sub_len(i);
+    const unsigned sbytes = len > 0 ? (unsigned)ES * (unsigned)((len - 1) * a.ld_bc + N) : 0u;
+    ql.load(px, sub_buf(a.x, i, D));
+    qdt.load(pd, sub_buf(a.dt, i, a.ld_dt));
+    rl.load(pb, GBuf(elem_at<ES>(a.B, (row0 + sub_t0(i)) * a.ld_bc), sbytes));
+    if constexpr (!FCARRY)
+      rl.load(pc, GBuf(elem_at<ES>(a.C, (row0 + sub_t0(i)) * a.ld_bc), sbytes));
   };
   auto store_sub = [&](int i) {           // staging registers -> LDS buffer i&1
     float* buf = lds + (i & 1) * BUF;
@@ -177,7 +185,7 @@ fwd_kernel(FwdArgs a) {
     }
   };
   auto y_write = [&](int i) {
-    const GBuf yo = sub_buf(a.y != nullptr ? a.y : a.x, a.y != nullptr ? i : -1);
+    const GBuf yo = sub_buf(a.y != nullptr ? a.y : a.x, a.y != nullptr ? i : -1, D);
 #pragma unroll
     for (int f = 0; f < YT; ++f) {
       const int t0 = tid + f * NT;

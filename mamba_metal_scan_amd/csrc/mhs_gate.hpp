@@ -51,8 +51,8 @@ template <int TPT>
 __global__ void __launch_bounds__(kConvCh * kConvTG)
 out_gate_bwd_kernel(const float* __restrict__ y, const float* __restrict__ dskip,
                     const float* __restrict__ z, long long z_rs, const float* __restrict__ dout,
-                    float* __restrict__ dy, float* __restrict__ dz, float* __restrict__ wsp, int T,
-                    int D) {
+                    float* __restrict__ dy, float* __restrict__ dz, long long dz_rs,
+                    float* __restrict__ wsp, int T, int D) {
   __shared__ float part[kConvTG][kConvCh];
   const int c = threadIdx.x % kConvCh;
   const int d = blockIdx.x * kConvCh + c;
@@ -64,6 +64,7 @@ out_gate_bwd_kernel(const float* __restrict__ y, const float* __restrict__ dskip
     const float ds = dskip[d];
     const size_t row = (size_t)b * T * D + d;
     const float* zb = z + (size_t)b * T * z_rs + d;
+    float* dzb = dz + (size_t)b * T * dz_rs + d;   // rows dz_rs apart (>= D)
     const int n = min(TPT, T - t0);
     float yv[TPT], zv[TPT], gv[TPT];
 #pragma unroll
@@ -80,7 +81,7 @@ out_gate_bwd_kernel(const float* __restrict__ y, const float* __restrict__ dskip
       const float dyv = gv[i] * (zv[i] * s);
       const size_t o = row + (size_t)(t0 + i) * D;
       dy[o] = dyv;
-      dz[o] = gv[i] * (yv[i] + ds) * s * __builtin_fmaf(zv[i], 1.f - s, 1.f);
+      dzb[(size_t)(t0 + i) * dz_rs] = gv[i] * (yv[i] + ds) * s * __builtin_fmaf(zv[i], 1.f - s, 1.f);
       acc += dyv;
     }
   }

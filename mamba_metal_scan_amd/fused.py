@@ -126,3 +126,91 @@ def out_gate(y: torch.Tensor, d_skip: torch.Tensor, z: torch.Tensor) -> torch.Te
         raise ValueError(f"bad shapes: y {tuple(y.shape)}, d_skip {tuple(d_skip.shape)}, "
                          f"z {tuple(z.shape)}")
     return OutGateHIP.apply(y, d_skip, z)
+
+
+class MambaInnerHIP(torch.autograd.Function):
+    """The inner block between in_proj and out_proj, fused (fp32):
+    x, z = xz.chunk(2); xc = silu(conv(x)); [dt_raw | B | C] = xc W^T + b;
+    y = gated scan(xc, dt_raw, A, B, C); out = (y + D_skip) * silu(z).
+    The reference computes it as separate modules (mamba_metal/model.py:
+    197-200, :244-256). Fused, the three projections are one GEMM whose
+    output rows the scan reads in place; in the backward the scan writes its
+    dt_raw, B and C gradients into one projection gradient, the projections'
+    input gradient is accumulated onto the scan's dx by the GEMM itself, and
+    the conv and output gate write dx and dz straight into the two halves of
+    xz's gradient (no concatenation, no separate gradient sums)."""
+
+    @staticmethod
+    def forward(ctx, xz, conv_w, conv_b, w_dt, b_dt, w_b, w_c, a_raw, d_skip, dt_min, dt_max,
+                chunk):
+        bt, t_len, d2 = xz.shape
+        d, n = d2 // 2, a_raw.shape[1]
+        x, z = xz[..., :d], xz[..., d:]
+        w2 = conv_w.reshape(d, -1).contiguous()
+        cb = conv_b.contiguous()
+        xc = _native.dispatch("conv1d_silu_fwd")(x, w2, cb)
+        w_proj = torch.cat([w_dt, w_b, w_c], 0)
+        bias = torch.cat([b_dt, b_dt.new_zeros(2 * n)])
+        proj = torch.addmm(bias, xc.view(-1, d), w_proj.t()).view(bt, t_len, d + 2 * n)
+        need_grad = any(ctx.needs_input_grad)
+        y, ckpt, _ = _native.dispatch("scan_gated_fwd")(
+            xc, proj[..., :d], a_raw, proj[..., d:d + n], proj[..., d + n:], float(dt_min),
+            float(dt_max), chunk, need_grad)
+        out = _native.dispatch("out_gate_fwd")(y, d_skip, z)
+        ctx.gate = (float(dt_min), float(dt_max))
+        ctx.chunk = chunk
+        ctx.conv_shape = conv_w.shape
+        if need_grad:
+            ctx.save_for_backward(xz, w2, cb, w_proj, a_raw, d_skip, xc, proj, y, ckpt)
+        return out
+
+    @staticmethod
+    def backward(ctx, dout):
+        xz, w2, cb, w_proj, a_raw, d_skip, xc, proj, y, ckpt = ctx.saved_tensors
+        bt, t_len, d2 = xz.shape
+        d, n = d2 // 2, a_raw.shape[1]
+        dxz = torch.empty_like(xz)
+        dy, dd = _native.dispatch("out_gate_bwd_into")(y, d_skip, xz[..., d:],
+                                                       dout.contiguous(), dxz[..., d:])
+        dproj = torch.empty_like(proj)
+        dxc, da = _native.dispatch("scan_gated_bwd_into")(
+            xc, proj[..., :d], a_raw, proj[..., d:d + n], proj[..., d + n:], ctx.gate[0],
+            ctx.gate[1], dy, None, ckpt, ctx.chunk, dproj)
+        dp2 = dproj.view(-1, d + 2 * n)
+        dxc.view(-1, d).addmm_(dp2, w_proj)            # + the projections' input gradient
+        dw = dp2.t().mm(xc.view(-1, d))
+        db_dt = dp2[:, :d].sum(0)
+        dcw, dcb = _native.dispatch("conv1d_silu_bwd_into")(xz[..., :d], w2, cb, dxc,
+                                                            dxz[..., :d])
+        return (dxz, dcw.reshape(ctx.conv_shape), dcb, dw[:d], db_dt, dw[d:d + n],
+                dw[d + n:], da, dd, None, None, None)
+
+
+def mamba_inner(xz: torch.Tensor, conv_w: torch.Tensor, conv_b: torch.Tensor,
+                w_dt: torch.Tensor, b_dt: torch.Tensor, w_b: torch.Tensor, w_c: torch.Tensor,
+                a_raw: torch.Tensor, d_skip: torch.Tensor, dt_min: float, dt_max: float,
+                chunk: int = SSM_CHUNK) -> torch.Tensor:
+    """The fused inner block (see MambaInnerHIP): xz (B, T, 2 d_inner), conv
+    weight (d_inner, 1, K) / bias (d_inner), dt_proj weight (d_inner, d_inner)
+    and bias (d_inner), B_proj / C_proj weights (d_state, d_inner), A
+    (d_inner, d_state), D_skip (d_inner); fp32 on one ROCm device, d_inner and
+    d_state multiples of 4. Returns (B, T, d_inner), contiguous."""
+    tensors = (xz, conv_w, conv_b, w_dt, b_dt, w_b, w_c, a_raw, d_skip)
+    if not all(_hip_device(t) for t in tensors):
+        raise RuntimeError("mamba_inner needs every input on the ROCm device")
+    if not all(t.dtype == torch.float32 for t in tensors):
+        raise RuntimeError("mamba_inner is fp32-only")
+    if not (float(dt_min) < float(dt_max)):
+        raise ValueError(f"need dt_min < dt_max; got {dt_min}, {dt_max}")
+    if xz.dim() != 3 or xz.shape[2] % 2 or not xz.is_contiguous():
+        raise ValueError(f"xz must be a contiguous (B, T, 2 d_inner) tensor; got {tuple(xz.shape)}")
+    d, n = xz.shape[2] // 2, a_raw.shape[1]
+    if (a_raw.shape != (d, n) or w_dt.shape != (d, d) or b_dt.shape != (d,)
+            or w_b.shape != (n, d) or w_c.shape != (n, d) or d_skip.shape != (d,)
+            or conv_w.shape[0] != d or conv_b.shape != (d,)):
+        raise ValueError("mamba_inner: parameter shapes do not match d_inner "
+                         f"{d}, d_state {n}")
+    if d % 4 or n % 4:
+        raise ValueError(f"mamba_inner needs d_inner and d_state multiples of 4; got {d}, {n}")
+    return MambaInnerHIP.apply(xz, conv_w, conv_b, w_dt, b_dt, w_b, w_c, a_raw, d_skip, dt_min,
+                               dt_max, chunk)

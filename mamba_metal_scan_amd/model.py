@@ -13,7 +13,11 @@ plain torch; the selective scan is the only custom kernel:
   out_proj; residual. On a ROCm device the conv + SiLU is the fused
   ``conv1d_silu`` kernel, the dt gate and softplus(A) run inside the scan
   kernels (``selective_scan_gated``) and ``(y + D_skip) * silu(z)`` is the
-  fused ``out_gate`` kernel.
+  fused ``out_gate`` kernel. In fp32 without a cache, everything between
+  in_proj and out_proj is one autograd Function (``mamba_inner``): the dt, B
+  and C projections become one GEMM whose output the scan reads in place,
+  and the backward writes its gradients in place (no concatenations or
+  separate gradient sums).
 * ``TinyMamba`` (model.py:259-302): embedding, blocks, final RMSNorm, head tied
   to the embedding, cross entropy.
 * Recurrent cache: a prefill stores each block's conv tail and final state;
@@ -34,7 +38,7 @@ import torch.nn as nn
 import torch.nn.functional as F
 
 from .conv import conv1d_silu
-from .fused import out_gate, selective_scan_gated
+from .fused import mamba_inner, out_gate, selective_scan_gated
 from .scan import SSM_CHUNK, _hip_device, selective_scan, selective_state_step
 
 
@@ -255,9 +259,22 @@ class MambaBlock(nn.Module):
         xt = x.transpose(1, 2)                                           # (B, d_inner, T)
         return F.silu(self.conv(xt)[:, :, :xt.shape[2]]).transpose(1, 2)
 
+    def _inner(self, xz) -> bool:
+        """Whether the fused inner block (conv, projections, scan and output
+        gate in one autograd Function) applies: the HIP path in fp32, with
+        d_inner and d_state multiples of 4 and a conv of at most 8 taps."""
+        return (self._fused(xz) and self.d_inner % 4 == 0 and self.A.shape[1] % 4 == 0
+                and self.conv.kernel_size[0] <= 8)
+
     def forward(self, x, cache=None):
         residual = x
-        x, z = self.in_proj(self.norm(x)).chunk(2, dim=-1)
+        xz = self.in_proj(self.norm(x))
+        if cache is None and self._inner(xz):
+            out = mamba_inner(xz, self.conv.weight, self.conv.bias, self.dt_proj.weight,
+                              self.dt_proj.bias, self.B_proj.weight, self.C_proj.weight, self.A,
+                              self.D_skip, self.dt_min, self.dt_max, chunk=self.ckpt_chunk)
+            return residual + self.out_proj(out)
+        x, z = xz.chunk(2, dim=-1)
         k = self.conv.kernel_size[0]
         if cache is not None and cache.get("h") is not None and x.shape[1] == 1:
             y = self._step(x, cache)

@@ -135,18 +135,27 @@ def test_gated_scan_argument_errors():
     lib = _native.library()
     sizes = (2, 8, 32, 16, 16)
     outs = [A16] * 3 + [None, 0]          # y, ckpt, h_last; no workspace
-    rc = lib.mhs_scan_gated_fwd_f32(*([A16] * 5), 0.1, 0.1, *outs, *sizes, None)
+    rc = lib.mhs_scan_gated_fwd_f32(*([A16] * 5), 0.1, 0.1, *outs, *sizes, 0, 0, None)
     assert rc == MHS_EINVAL and "dt_min < dt_max" in _err(lib)
-    rc = lib.mhs_scan_gated_fwd_f32(*([A16] * 5), 0.001, float("nan"), *outs, *sizes, None)
+    rc = lib.mhs_scan_gated_fwd_f32(*([A16] * 5), 0.001, float("nan"), *outs, *sizes, 0, 0, None)
     assert rc == MHS_EINVAL and "dt_min < dt_max" in _err(lib)
-    rc = lib.mhs_scan_gated_fwd_f32(*([A16] * 5), 0.001, 0.1, *outs, 2, 8, 32, 65, 16, None)
+    rc = lib.mhs_scan_gated_fwd_f32(*([A16] * 5), 0.001, 0.1, *outs, 2, 8, 32, 65, 16, 0, 0, None)
     assert rc == MHS_EINVAL and "d_state" in _err(lib)
+    # row strides below d_inner (dt) or d_state (B, C) are rejected
+    rc = lib.mhs_scan_gated_fwd_f32(*([A16] * 5), 0.001, 0.1, *outs, *sizes, 31, 0, None)
+    assert rc == MHS_EINVAL and "row strides" in _err(lib)
+    rc = lib.mhs_scan_gated_fwd_f32(*([A16] * 5), 0.001, 0.1, *outs, *sizes, 64, 15, None)
+    assert rc == MHS_EINVAL and "row strides" in _err(lib)
     need = lib.mhs_scan_bwd_workspace_bytes(*sizes)
     rc = lib.mhs_scan_gated_bwd_f32(*([A16] * 5), 0.001, 0.1, *([A16] * 8), A16, need - 4,
-                                    *sizes, None)
+                                    *sizes, 0, 0, 0, 0, None)
     assert rc == MHS_EINVAL and "workspace too small" in _err(lib)
-    rc = lib.mhs_scan_gated_bwd_f32(*([A16] * 5), 1.0, 0.5, *([A16] * 8), A16, need, *sizes, None)
+    rc = lib.mhs_scan_gated_bwd_f32(*([A16] * 5), 1.0, 0.5, *([A16] * 8), A16, need, *sizes,
+                                    0, 0, 0, 0, None)
     assert rc == MHS_EINVAL and "dt_min < dt_max" in _err(lib)
+    rc = lib.mhs_scan_gated_bwd_f32(*([A16] * 5), 0.001, 0.1, *([A16] * 8), A16, need, *sizes,
+                                    0, 0, 0, 15, None)
+    assert rc == MHS_EINVAL and "row strides" in _err(lib)
 
 
 def test_out_gate_argument_errors():
@@ -157,9 +166,12 @@ def test_out_gate_argument_errors():
     rc = lib.mhs_out_gate_fwd_f32(A16, None, A16, 64, A16, 2, 8, 32, None)
     assert rc == MHS_EINVAL and "null" in _err(lib)
     need = lib.mhs_out_gate_bwd_workspace_bytes(2, 8, 32)
-    rc = lib.mhs_out_gate_bwd_f32(A16, A16, A16, 64, A16, A16, A16, A16, A16, need - 4, 2, 8, 32,
-                                  None)
+    rc = lib.mhs_out_gate_bwd_f32(A16, A16, A16, 64, A16, A16, A16, 0, A16, A16, need - 4, 2, 8,
+                                  32, None)
     assert rc == MHS_EINVAL and "workspace too small" in _err(lib)
+    rc = lib.mhs_out_gate_bwd_f32(A16, A16, A16, 64, A16, A16, A16, 31, A16, A16, need, 2, 8, 32,
+                                  None)
+    assert rc == MHS_EINVAL and "dz row stride" in _err(lib)
 
 
 def test_time_segments_knob_and_workspace():
@@ -210,3 +222,17 @@ def test_forward_workspace():
     assert rc == MHS_EINVAL and "workspace too small" in _err(lib)
     rc = lib.mhs_scan_fwd_ws_f32(*([A16] * 8), MIS, need, *sizes, None)
     assert rc == MHS_EINVAL and "256-byte" in _err(lib)
+
+
+def test_conv_argument_errors():
+    lib = _native.library()
+    need = lib.mhs_conv1d_silu_bwd_workspace_bytes(2, 8, 32, 4)
+    assert need > 0
+    rc = lib.mhs_conv1d_silu_fwd_f32(A16, 31, A16, A16, A16, 2, 8, 32, 4, None)
+    assert rc == MHS_EINVAL and "row stride" in _err(lib)
+    rc = lib.mhs_conv1d_silu_bwd_f32(A16, 64, A16, A16, A16, A16, 0, A16, A16, A16, need - 4,
+                                     2, 8, 32, 4, None)
+    assert rc == MHS_EINVAL and "workspace too small" in _err(lib)
+    rc = lib.mhs_conv1d_silu_bwd_f32(A16, 64, A16, A16, A16, A16, 31, A16, A16, A16, need,
+                                     2, 8, 32, 4, None)
+    assert rc == MHS_EINVAL and "dx row stride" in _err(lib)
