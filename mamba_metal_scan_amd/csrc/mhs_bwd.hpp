@@ -196,9 +196,14 @@ bwd_kernel(BwdArgs a) {
   float sdt_acc = 0.f;   // CARRY: sum of dt over the segment
 
   const size_t row0 = (size_t)b * T;
+  // Only the gated kernels read dt, B, C from (and write ddt into) column
+  // slices of wider tensors; the others keep compile-time-contiguous
+  // addressing.
+  const int ld_dt = GATED ? a.ld_dt : D, ld_bc = GATED ? a.ld_bc : N;
+  const int ld_ddt = GATED ? a.ld_ddt : D;
   const QuadLoader<kCH, PER, ES> ql(tid, NT, D, d0, D);
-  const QuadLoader<kCH, PER, ES> qdt(tid, NT, D, d0, a.ld_dt);
-  const RowLoader<PERS, NPL, ES> rl(tid, NT, N, NP, a.ld_bc);
+  const QuadLoader<kCH, PER, ES> qdt(tid, NT, D, d0, ld_dt);
+  const RowLoader<PERS, NPL, ES> rl(tid, NT, N, NP, ld_bc);
   float4 px[PER], pd[PER], py[PER];
   float pb[PERS], pc[PERS], ph[NPL];
 
@@ -212,16 +217,20 @@ bwd_kernel(BwdArgs a) {
   // (channels d0 .. D-1 of its rows).
   auto chunk_buf = [&](const void* base, int ci, int ld) {
     const int len = chunk_len(ci);
+    if constexpr (!GATED)   // contiguous (ld == D)
+      return GBuf(elem_at<ES>(base, (row0 + chunk_t0(ci)) * D + d0),
+                  len > 0 ? (unsigned)ES * (unsigned)(len * D - d0) : 0u);
     return GBuf(elem_at<ES>(base, (row0 + chunk_t0(ci)) * ld + d0),
                 len > 0 ? (unsigned)ES * (unsigned)((len - 1) * ld + D - d0) : 0u);
   };
   auto load_sub = [&](int ci) {           // global -> staging registers
     const int len = chunk_len(ci);
-    const unsigned sbytes = len > 0 ? (unsigned)ES * (unsigned)((len - 1) * a.ld_bc + N) : 0u;
-    const GBuf gs_b(elem_at<ES>(a.B, (row0 + chunk_t0(ci)) * a.ld_bc), sbytes);
-    const GBuf gs_c(elem_at<ES>(a.C, (row0 + chunk_t0(ci)) * a.ld_bc), sbytes);
+    const unsigned sbytes = !GATED ? (unsigned)ES * (unsigned)(len * N)
+                            : len > 0 ? (unsigned)ES * (unsigned)((len - 1) * ld_bc + N) : 0u;
+    const GBuf gs_b(elem_at<ES>(a.B, (row0 + chunk_t0(ci)) * ld_bc), sbytes);
+    const GBuf gs_c(elem_at<ES>(a.C, (row0 + chunk_t0(ci)) * ld_bc), sbytes);
     if constexpr (!CARRY) ql.load(px, chunk_buf(a.x, ci, D));
-    qdt.load(pd, chunk_buf(a.dt, ci, a.ld_dt));
+    qdt.load(pd, chunk_buf(a.dt, ci, ld_dt));
     ql.load(py, chunk_buf(a.dy, ci, D));
     if constexpr (!CARRY) rl.load(pb, gs_b);
     rl.load(pc, gs_c);
@@ -247,7 +256,7 @@ bwd_kernel(BwdArgs a) {
   auto finalize = [&](int ci, int j) {
     const float* sx = lds + j * BUF + oX;
     const float* sdt = lds + j * BUF;
-    const GBuf gdx = chunk_buf(a.dx, ci, D), gddt = chunk_buf(a.ddt, ci, a.ld_ddt);
+    const GBuf gdx = chunk_buf(a.dx, ci, D), gddt = chunk_buf(a.ddt, ci, ld_ddt);
 #pragma unroll
     for (int f = 0; f < FT; ++f) {
       const int task0 = tid + f * NT;
@@ -257,8 +266,8 @@ bwd_kernel(BwdArgs a) {
       const bool okc = ok && d0 + cc < D;
       const unsigned o0 = okc ? (unsigned)ES * ((unsigned)k * (unsigned)D + cc) : kOOB;
       const unsigned o1 = okc ? o0 + (unsigned)ES * (unsigned)D : kOOB;
-      const unsigned od0 = okc ? (unsigned)ES * ((unsigned)k * (unsigned)a.ld_ddt + cc) : kOOB;
-      const unsigned od1 = okc ? od0 + (unsigned)ES * (unsigned)a.ld_ddt : kOOB;
+      const unsigned od0 = okc ? (unsigned)ES * ((unsigned)k * (unsigned)ld_ddt + cc) : kOOB;
+      const unsigned od1 = okc ? od0 + (unsigned)ES * (unsigned)ld_ddt : kOOB;
       const float2 xv = lds2(sx + cm_elem(cc, k)), dtv = lds2(sdt + cm_elem(cc, k));
       const float x0 = xv.x, x1 = xv.y, t0v = dtv.x, t1v = dtv.y;
       float s1a = 0.f, s1b = 0.f, s2a = 0.f, s2b = 0.f;

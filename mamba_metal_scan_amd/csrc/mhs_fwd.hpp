@@ -127,9 +127,12 @@ fwd_kernel(FwdArgs a) {
   }
 
   const size_t row0 = (size_t)b * T;
+  // Only the gated kernels read dt, B, C from column slices of a wider
+  // tensor; the others keep compile-time-contiguous addressing.
+  const int ld_dt = GATED ? a.ld_dt : D, ld_bc = GATED ? a.ld_bc : N;
   const QuadLoader<kCH, PER, ES> ql(tid, NT, D, d0, D);
-  const QuadLoader<kCH, PER, ES> qdt(tid, NT, D, d0, a.ld_dt);
-  const RowLoader<PERS, NPL, ES> rl(tid, NT, N, NP, a.ld_bc);
+  const QuadLoader<kCH, PER, ES> qdt(tid, NT, D, d0, ld_dt);
+  const RowLoader<PERS, NPL, ES> rl(tid, NT, N, NP, ld_bc);
   float4 px[PER], pd[PER];
   float pb[PERS], pc[PERS];
   // Sub-chunk i of the segment (any i >= 0): first step and length (0 past
@@ -142,17 +145,21 @@ fwd_kernel(FwdArgs a) {
   // (channels d0 .. D-1 of its rows).
   auto sub_buf = [&](const void* base, int i, int ld) {
     const int len = sub_len(i);
+    if constexpr (!GATED)   // contiguous (ld == D)
+      return GBuf(elem_at<ES>(base, (row0 + sub_t0(i)) * D + d0),
+                  len > 0 ? (unsigned)ES * (unsigned)(len * D - d0) : 0u);
     return GBuf(elem_at<ES>(base, (row0 + sub_t0(i)) * ld + d0),
                 len > 0 ? (unsigned)ES * (unsigned)((len - 1) * ld + D - d0) : 0u);
   };
   auto load_sub = [&](int i) {            // global -> staging registers
     const int len = sub_len(i);
-    const unsigned sbytes = len > 0 ? (unsigned)ES * (unsigned)((len - 1) * a.ld_bc + N) : 0u;
+    const unsigned sbytes = !GATED ? (unsigned)ES * (unsigned)(len * N)
+                            : len > 0 ? (unsigned)ES * (unsigned)((len - 1) * ld_bc + N) : 0u;
     ql.load(px, sub_buf(a.x, i, D));
-    qdt.load(pd, sub_buf(a.dt, i, a.ld_dt));
-    rl.load(pb, GBuf(elem_at<ES>(a.B, (row0 + sub_t0(i)) * a.ld_bc), sbytes));
+    qdt.load(pd, sub_buf(a.dt, i, ld_dt));
+    rl.load(pb, GBuf(elem_at<ES>(a.B, (row0 + sub_t0(i)) * ld_bc), sbytes));
     if constexpr (!FCARRY)
-      rl.load(pc, GBuf(elem_at<ES>(a.C, (row0 + sub_t0(i)) * a.ld_bc), sbytes));
+      rl.load(pc, GBuf(elem_at<ES>(a.C, (row0 + sub_t0(i)) * ld_bc), sbytes));
   };
   auto store_sub = [&](int i) {           // staging registers -> LDS buffer i&1
     float* buf = lds + (i & 1) * BUF;
