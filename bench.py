@@ -258,6 +258,53 @@ def pmc_summary(args) -> None:
     print(f"\nwrote {path.relative_to(ROOT)} and {md.relative_to(ROOT)}")
 
 
+TRAIN_GROUPS = (  # (label, substrings of the kernel name), first match wins
+    ("fp32 GEMMs (rocBLAS / hipBLASLt)", ("Cijk_", "gemm", "Gemm")),
+    ("HIP scan (fwd, bwd, reduce)", ("mhs::fwd_kernel", "mhs::bwd_kernel", "mhs::bwd_reduce")),
+    ("HIP conv1d + SiLU", ("mhs::conv",)),
+    ("HIP output gate", ("mhs::out_gate",)),
+    ("softmax / cross-entropy", ("SoftMax", "nll_loss")),
+    ("AdamW (fused)", ("FusedOpti",)),
+    ("RMSNorm", ("layer_norm", "rms_norm", "RmsNorm")),
+)
+
+
+def trace_summary(args) -> None:
+    """Per-step kernel time of the train step from a rocprofv3 --kernel-trace
+    --stats run under args.trace_summary (kt/run_kernel_stats.csv), grouped
+    by kind; the run covered args.warmup + args.steps steps. Writes the
+    markdown under profiles/ and prints it."""
+    import csv
+    stats = os.path.join(args.trace_summary, "kt", "run_kernel_stats.csv")
+    rows = list(csv.DictReader(open(stats)))
+    n = args.warmup + args.steps
+    per = lambda r: float(r["TotalDurationNs"]) / n / 1e3   # us per step
+    groups: dict = {}
+    for r in rows:
+        label = next((g for g, keys in TRAIN_GROUPS if any(k in r["Name"] for k in keys)),
+                     "other framework ops")
+        groups[label] = groups.get(label, 0.0) + per(r)
+    total = sum(groups.values())
+    lines = ["# 80M TinyMamba train step (batch 16 x seq 512, fp32): kernel time per step", "",
+             "All commands run from /tmp with `TMPDIR=/tmp`; OUT is the output folder.", "",
+             "    rocprofv3 --kernel-trace --stats -d OUT/kt -o run --output-format csv -- \\",
+             f"        python3 bench.py --workload train --steps {args.steps} --warmup {args.warmup}",
+             f"    python3 bench.py --trace-summary OUT --steps {args.steps} --warmup {args.warmup}",
+             "", f"Kernel time summed over the {n} traced steps (warmup included) / {n}. "
+             "Under tracing each dispatch reads a few us longer than in a plain run.", "",
+             "| kind | ms / step | share |", "|---|---|---|"]
+    for label, us in sorted(groups.items(), key=lambda kv: -kv[1]):
+        lines.append(f"| {label} | {us / 1e3:.2f} | {us / total:.1%} |")
+    lines += [f"| total | {total / 1e3:.2f} | |", "", "Largest kernels:", "",
+              "| kernel | calls / step | us / step |", "|---|---|---|"]
+    for r in sorted(rows, key=lambda r: -float(r["TotalDurationNs"]))[:16]:
+        lines.append(f"| `{r['Name'][:72]}` | {int(r['Calls']) / n:g} | {per(r):.0f} |")
+    md = ROOT / "profiles" / "train_80m_16x512.md"
+    md.write_text("\n".join(lines) + "\n")
+    print("\n".join(lines))
+    print(f"\nwrote {md.relative_to(ROOT)}")
+
+
 def bench_train(steps: int = 10, warmup: int = 3) -> dict:
     """The 80M TinyMamba train step (fwd + bwd + AdamW lr 3e-4) with the HIP
     scan: vocab 32768, d_model 640, 12 layers, d_ff 2560 (d_inner 1432),
@@ -490,10 +537,15 @@ def main() -> int:
                     help="profiling driver: only N scan_fwd/scan_bwd launches + N copies")
     ap.add_argument("--pmc-summary", default=None, metavar="DIR",
                     help="summarise rocprofv3 FETCH_SIZE / WRITE_SIZE passes under DIR")
+    ap.add_argument("--trace-summary", default=None, metavar="DIR",
+                    help="summarise a kernel-trace run of --workload train under DIR")
     args = ap.parse_args()
 
     if args.pmc_summary:
         pmc_summary(args)
+        return 0
+    if args.trace_summary:
+        trace_summary(args)
         return 0
 
     if args.gpus != 1:
