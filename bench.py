@@ -11,8 +11,11 @@ Reported:
   value          whole-job tokens/s (batch*T per step / step time)
   ms_per_step    ms per fwd+bwd step (wall clock, synchronized)
   roofline       the dominant kernel launch (the backward: bwd kernel + its
-                 fixed-order reduction), timed live with HIP events on the
-                 launch stream: algorithmic bytes / average duration vs 8 TB/s
+                 fixed-order reduction), timed live with HIP events around
+                 it in every 4th timed step, on the launch stream: algorithmic
+                 bytes / average duration vs 8 TB/s
+  clock_settle   untimed steps run before the warmup until the GPU clock
+                 is steady (about 40 ms of load from idle)
   cpu_baseline   selective_scan(impl="torch") fwd+bwd on the host CPU, same
                  inputs, all threads of the process's CPU share
 
@@ -70,6 +73,29 @@ def make_inputs(bt, t_len, d, n, seed=2024):
     c_in = torch.randn(bt, t_len, n, generator=g)
     dy = torch.randn(bt, t_len, d, generator=g)
     return x, dt, aneg, b_in, c_in, dy
+
+
+SETTLE_MS = 100.0
+EVENT_EVERY = 4   # timed steps per step with per-launch HIP events
+
+
+def settle_clocks(fn, ms: float = SETTLE_MS) -> int:
+    """Run fn() back to back, untimed, until ms of wall time have passed, so
+    that what is timed next runs at the GPU's sustained clock. From idle,
+    MI355X takes about 40 ms of continuous load to get there: a 16x512x1536x16
+    scan fwd+bwd step takes 230 us at first and 187 us from then on. Returns
+    the number of calls (after a first one, which also pays one-time costs
+    such as loading the kernels and is not counted)."""
+    import torch
+    fn()
+    torch.cuda.synchronize()
+    t0, calls = time.perf_counter(), 0
+    while (time.perf_counter() - t0) * 1e3 < ms:
+        for _ in range(4):
+            fn()
+        calls += 4
+        torch.cuda.synchronize()
+    return calls
 
 
 def time_events(fn, reps: int) -> float:
@@ -223,19 +249,32 @@ def pmc_summary(args) -> None:
     lines = [f"# Scan kernels at {tag}, chunk {args.chunk} (fp32): kernel time and HBM traffic",
              "", "All commands run from /tmp with `TMPDIR=/tmp`; OUT is the output folder.", ""]
     stats = os.path.join(args.pmc_summary, "kt", "run_kernel_stats.csv")
+    trace = os.path.join(args.pmc_summary, "kt", "run_kernel_trace.csv")
     if os.path.exists(stats):
+        # The last `steps` dispatches of each scan kernel are those of
+        # bench.py's timed steps.
+        durs: dict = {}
+        if os.path.exists(trace):
+            for r in csv.DictReader(open(trace)):
+                durs.setdefault(r["Kernel_Name"], []).append(
+                    (int(r["End_Timestamp"]) - int(r["Start_Timestamp"])) / 1e3)
         lines += ["## Kernel trace", "",
                   "    rocprofv3 --kernel-trace --stats -d OUT/kt -o run --output-format csv -- \\",
-                  f"        python3 bench.py --steps 20 --warmup 5 --no-cpu-baseline --no-train {extra}", "",
-                  "| kernel | calls | avg us | min us | max us |", "|---|---|---|---|---|"]
+                  f"        python3 bench.py --steps {args.steps} --warmup {args.warmup} "
+                  f"--no-cpu-baseline --no-train {extra}", "",
+                  f"| kernel | calls | avg us | min us | max us | avg us, last {args.steps} |",
+                  "|---|---|---|---|---|---|"]
         for r in csv.DictReader(open(stats)):
+            last = durs.get(r["Name"], [])[-args.steps:]
+            tail = f"{sum(last) / len(last):.1f}" if len(last) == args.steps else ""
             lines.append(f"| `{r['Name'][:60]}` | {r['Calls']} | {float(r['AverageNs']) / 1e3:.1f} "
-                         f"| {float(r['MinNs']) / 1e3:.1f} | {float(r['MaxNs']) / 1e3:.1f} |")
+                         f"| {float(r['MinNs']) / 1e3:.1f} | {float(r['MaxNs']) / 1e3:.1f} | {tail} |")
         lines += ["", "The backward launch (the `scan_bwd` op) is `bwd_kernel` + "
-                  "`bwd_reduce_kernel`. Under kernel tracing each dispatch's duration reads "
-                  "about 7 us longer than the HIP-event average of the same launches run "
-                  "back to back without the profiler (bench.py's `avg_ms`): compare the "
-                  "`scan_fwd` and `roofline` figures of a plain `python bench.py` run.", ""]
+                  "`bwd_reduce_kernel`. The calls include bench.py's untimed clock-settle "
+                  "steps, which begin at the idle clock; the last column averages the "
+                  "timed steps' launches only, which bench.py's `scan_fwd.avg_ms` and "
+                  "`roofline.avg_ms` time with HIP events (those also include the short "
+                  "gap between the kernels of a launch).", ""]
     lines += ["## HBM traffic per launch", "",
               f"    rocprofv3 --pmc FETCH_SIZE -d OUT/fetch -o run --output-format csv -- "
               f"python3 bench.py --launches 5 {extra}",
@@ -367,6 +406,7 @@ def bench_longt(args) -> dict:
         _, ckpt, _ = fwd()
         bwd = lambda: torch.ops.mamba_hip.scan_bwd(x, dt, aneg, b_in, c_in, dy, None, ckpt, chunk)
         bwd()
+        settle_clocks(lambda: (fwd(), bwd()))
         f_ms, b_ms = time_events(fwd, 5), time_events(bwd, 5)
         rows.append({"chunk": chunk, "fwd_ms": f_ms, "bwd_ms": b_ms, "fwd_bwd_ms": f_ms + b_ms,
                      "fwd_bwd_GBs": nbytes["fwd_bwd"] / ((f_ms + b_ms) * 1e-3) / 1e9,
@@ -392,6 +432,7 @@ def bench_infer(args) -> dict:
     x, dt, aneg, b_in, c_in, _ = (t.to(dev) for t in make_inputs(bt, t_len, d, n))
     prefill = lambda: torch.ops.mamba_hip.scan_fwd(x, dt, aneg, b_in, c_in, t_len, False)
     prefill()
+    settle_clocks(prefill)
     p_ms = time_events(prefill, 5)
     p_bytes = 4 * (3 * bt * t_len * d + 2 * bt * t_len * n + d * n) + 4 * bt * d * n
     _, _, h = prefill()
@@ -450,30 +491,40 @@ def bench_scan(args) -> dict:
     x, dt, aneg, b_in, c_in, dy = (t.to(dev) for t in make_inputs(bt, t_len, d, n))
     leaves = [t.clone().requires_grad_(True) for t in (x, dt, aneg, b_in, c_in)]
 
-    def step():
+    # Every EVENT_EVERY-th timed step also records HIP events around its
+    # forward launch and its backward launch, on the stream the kernels run
+    # on (torch's current stream, which the autograd backward also uses): the
+    # per-launch averages come from the timed steps themselves. Each event is
+    # a marker packet that costs the GPU about 2.5 us; on every step the four
+    # of them would add 5% to the step time.
+    events = [[torch.cuda.Event(enable_timing=True) for _ in range(4)]
+              for _ in range((args.steps + EVENT_EVERY - 1) // EVENT_EVERY)]
+
+    def step(ev=None):
         for t in leaves:
             t.grad = None
+        if ev is not None:
+            ev[0].record()
         y = selective_scan_hip(*leaves, chunk=chunk)
+        if ev is not None:
+            ev[1].record()
+            ev[2].record()
         y.backward(dy)
+        if ev is not None:
+            ev[3].record()
 
+    settled = settle_clocks(step)
     for _ in range(args.warmup):
         step()
     torch.cuda.synchronize()
     t0 = time.perf_counter()
-    for _ in range(args.steps):
-        step()
+    for i in range(args.steps):
+        step(events[i // EVENT_EVERY] if i % EVENT_EVERY == 0 else None)
     torch.cuda.synchronize()
     elapsed = time.perf_counter() - t0
     ms = elapsed * 1e3 / args.steps
-
-    # Per-launch timing of the forward and backward ops on the launch stream.
-    xc, dtc, ac, bc, cc = (t.detach() for t in leaves)
-    _, ckpt, _ = torch.ops.mamba_hip.scan_fwd(xc, dtc, ac, bc, cc, chunk, True)
-    reps = max(args.steps, 10)
-    fwd_ms = time_events(lambda: torch.ops.mamba_hip.scan_fwd(xc, dtc, ac, bc, cc, chunk, True),
-                         reps)
-    bwd_ms = time_events(lambda: torch.ops.mamba_hip.scan_bwd(xc, dtc, ac, bc, cc, dy, None,
-                                                              ckpt, chunk), reps)
+    fwd_ms = sum(e[0].elapsed_time(e[1]) for e in events) / len(events)
+    bwd_ms = sum(e[2].elapsed_time(e[3]) for e in events) / len(events)
     nbytes = scan_bytes(bt, t_len, d, n)
     bwd_gbs = nbytes["bwd"] / (bwd_ms * 1e-3) / 1e9
     fwd_gbs = nbytes["fwd"] / (fwd_ms * 1e-3) / 1e9
@@ -504,13 +555,16 @@ def bench_scan(args) -> dict:
         "roofline": {"bound": "hbm", "achieved": bwd_gbs, "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": bwd_gbs / HBM_PEAK_GBS, "traffic": traffic,
                      "kernel": "scan backward launch (bwd_kernel + bwd_reduce_kernel)",
-                     "avg_ms": bwd_ms, "algorithmic_bytes": nbytes["bwd"]},
+                     "avg_ms": bwd_ms, "algorithmic_bytes": nbytes["bwd"],
+                     "timed_launches": len(events)},
         "scan_fwd": {"avg_ms": fwd_ms, "achieved_GBs": fwd_gbs,
                      "algorithmic_bytes": nbytes["fwd"]},
         "scan_fwd_bwd": {"avg_ms": fwd_ms + bwd_ms, "achieved_GBs": pair_gbs,
                          "frac": pair_gbs / HBM_PEAK_GBS,
                          "algorithmic_bytes": nbytes["fwd_bwd"]},
         "library_version": hex(_native.library().mhs_version()),
+        "clock_settle": {"ms": SETTLE_MS, "steps": settled,
+                         "note": "untimed steps before the warmup, until the GPU clock is steady"},
     }
     if not args.no_train:
         out["train_80m"] = bench_train()
@@ -523,8 +577,8 @@ def main() -> int:
     ap = argparse.ArgumentParser(description=__doc__,
                                  formatter_class=argparse.RawDescriptionHelpFormatter)
     ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=50)
-    ap.add_argument("--warmup", type=int, default=10)
+    ap.add_argument("--steps", type=int, default=200)
+    ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--workload", default="scan", choices=["scan", "train", "longt", "infer"])
     ap.add_argument("--no-train", action="store_true", help="skip the 80M train-step figure")
     ap.add_argument("--batch", type=int, default=16)
