@@ -152,6 +152,9 @@ int mhs_scan_bwd_f32(const float* x, const float* dt, const float* aneg,
  * recurrence of mhs_scan_fwd_ws_f32 on (x, dt, Aneg, B, C). Needs finite
  * dt_min < dt_max. Same outputs, layouts, checkpoints and workspace (may be
  * NULL) as mhs_scan_fwd_ws_f32.
+ * dt_bias: NULL, or the dt projection's bias (d_inner fp32, any alignment),
+ * added to dt_raw before the sigmoid: then dt_raw may be the projection's
+ * output without its bias (`dt_proj(x) = x W^T + b`, model.py:197).
  * ld_dt, ld_bc: elements between consecutive time steps of dt_raw and of B,
  * C (0: contiguous, i.e. d_inner and d_state). Larger strides read column
  * slices of one wider tensor, e.g. a single projection whose rows hold
@@ -160,7 +163,7 @@ int mhs_scan_bwd_f32(const float* x, const float* dt, const float* aneg,
  */
 int mhs_scan_gated_fwd_f32(const float* x, const float* dt_raw, const float* A,
                            const float* B, const float* C, float dt_min, float dt_max,
-                           float* y, float* ckpt, float* h_last,
+                           const float* dt_bias, float* y, float* ckpt, float* h_last,
                            void* workspace, size_t workspace_bytes,
                            int64_t batch, int64_t seqlen, int64_t d_inner, int64_t d_state,
                            int64_t chunk, int64_t ld_dt, int64_t ld_bc, void* stream);
@@ -176,12 +179,15 @@ int mhs_scan_gated_fwd_f32(const float* x, const float* dt_raw, const float* A,
  * ld_dbc: row strides of the outputs ddt_raw and dB, dC (0: contiguous), so
  * that they can be written into the column slices of one gradient tensor of
  * the projection. dx is contiguous.
+ * dt_bias: as in the forward. ddt_bias: NULL, or d_inner fp32 that receive
+ * the gradient of the bias, sum over batch and time of ddt_raw (a fixed-order
+ * reduction: also bit-for-bit reproducible).
  */
 int mhs_scan_gated_bwd_f32(const float* x, const float* dt_raw, const float* A,
                            const float* B, const float* C, float dt_min, float dt_max,
-                           const float* dy, const float* dh_last, const float* ckpt,
-                           float* dx, float* ddt_raw, float* dA, float* dB, float* dC,
-                           void* workspace, size_t workspace_bytes,
+                           const float* dt_bias, const float* dy, const float* dh_last,
+                           const float* ckpt, float* dx, float* ddt_raw, float* dA, float* dB,
+                           float* dC, float* ddt_bias, void* workspace, size_t workspace_bytes,
                            int64_t batch, int64_t seqlen, int64_t d_inner, int64_t d_state,
                            int64_t chunk, int64_t ld_dt, int64_t ld_bc, int64_t ld_ddt,
                            int64_t ld_dbc, void* stream);
@@ -190,7 +196,7 @@ int mhs_scan_gated_bwd_f32(const float* x, const float* dt_raw, const float* A,
  * bf16 activations with fp32 state. The same four scan entry points with x,
  * dt (or dt_raw), B, C, y, dy, dx, ddt (or ddt_raw), dB and dC as bf16
  * (uint16_t bit patterns, the upper half of an fp32); aneg / A, daneg / dA,
- * dh_last, ckpt and h_last stay fp32. Loads widen exactly; all arithmetic,
+ * dt_bias, ddt_bias, dh_last, ckpt and h_last stay fp32. Loads widen exactly; all arithmetic,
  * the recurrent state and the reductions are fp32; each bf16 output is its
  * fp32 value rounded to nearest even. Same layouts, workspaces and
  * determinism as the fp32 entry points. No counterpart in the reference
@@ -211,15 +217,15 @@ int mhs_scan_bwd_bf16(const uint16_t* x, const uint16_t* dt, const float* aneg,
                       int64_t chunk, void* stream);
 int mhs_scan_gated_fwd_bf16(const uint16_t* x, const uint16_t* dt_raw, const float* A,
                             const uint16_t* B, const uint16_t* C, float dt_min, float dt_max,
-                            uint16_t* y, float* ckpt, float* h_last,
+                            const float* dt_bias, uint16_t* y, float* ckpt, float* h_last,
                             void* workspace, size_t workspace_bytes,
                             int64_t batch, int64_t seqlen, int64_t d_inner, int64_t d_state,
                             int64_t chunk, int64_t ld_dt, int64_t ld_bc, void* stream);
 int mhs_scan_gated_bwd_bf16(const uint16_t* x, const uint16_t* dt_raw, const float* A,
                             const uint16_t* B, const uint16_t* C, float dt_min, float dt_max,
-                            const uint16_t* dy, const float* dh_last, const float* ckpt,
-                            uint16_t* dx, uint16_t* ddt_raw, float* dA, uint16_t* dB,
-                            uint16_t* dC, void* workspace, size_t workspace_bytes,
+                            const float* dt_bias, const uint16_t* dy, const float* dh_last,
+                            const float* ckpt, uint16_t* dx, uint16_t* ddt_raw, float* dA,
+                            uint16_t* dB, uint16_t* dC, float* ddt_bias, void* workspace, size_t workspace_bytes,
                             int64_t batch, int64_t seqlen, int64_t d_inner, int64_t d_state,
                             int64_t chunk, int64_t ld_dt, int64_t ld_bc, int64_t ld_ddt,
                             int64_t ld_dbc, void* stream);

@@ -89,10 +89,10 @@ def library() -> ctypes.CDLL:
             lib.mhs_conv1d_silu_bwd_f32.argtypes = ([_P, _I64] + [_P] * 4 + [_I64] + [_P] * 3
                                                     + [ctypes.c_size_t] + [_I64] * 4 + [_P])
             lib.mhs_scan_gated_fwd_f32.restype = ctypes.c_int
-            lib.mhs_scan_gated_fwd_f32.argtypes = ([_P] * 5 + [_F32] * 2 + [_P] * 4
+            lib.mhs_scan_gated_fwd_f32.argtypes = ([_P] * 5 + [_F32] * 2 + [_P] * 5
                                                    + [ctypes.c_size_t] + [_I64] * 7 + [_P])
             lib.mhs_scan_gated_bwd_f32.restype = ctypes.c_int
-            lib.mhs_scan_gated_bwd_f32.argtypes = ([_P] * 5 + [_F32] * 2 + [_P] * 9
+            lib.mhs_scan_gated_bwd_f32.argtypes = ([_P] * 5 + [_F32] * 2 + [_P] * 11
                                                    + [ctypes.c_size_t] + [_I64] * 9 + [_P])
             lib.mhs_out_gate_fwd_f32.restype = ctypes.c_int
             lib.mhs_out_gate_fwd_f32.argtypes = [_P] * 3 + [_I64, _P] + [_I64] * 3 + [_P]
@@ -385,15 +385,26 @@ def _conv1d_silu_bwd_into_fake(x, w, bias, dout, dx):
     return torch.empty_like(w), torch.empty_like(bias)
 
 
+def _dt_bias(dt_bias: Optional[torch.Tensor], x: torch.Tensor) -> None:
+    """The dt projection's bias: None, or fp32 (d_inner,) contiguous on x's device."""
+    d = x.shape[2]
+    if dt_bias is not None and (dt_bias.dtype != torch.float32 or dt_bias.shape != (d,)
+                                or not dt_bias.is_contiguous() or dt_bias.device != x.device):
+        raise HipScanError(f"dt_bias must be a contiguous fp32 ({d},) tensor on {x.device}; got "
+                           f"{dt_bias.dtype} {tuple(dt_bias.shape)} on {dt_bias.device}")
+
+
 def _scan_gated_fwd_impl(x: torch.Tensor, dt_raw: torch.Tensor, a_raw: torch.Tensor,
                    b_in: torch.Tensor, c_in: torch.Tensor, dt_min: float, dt_max: float,
-                   chunk: int, with_ckpt: bool
+                   chunk: int, with_ckpt: bool, dt_bias: Optional[torch.Tensor] = None
                    ) -> tuple[torch.Tensor, torch.Tensor, torch.Tensor]:
-    """scan_fwd with dt = dt_min + (dt_max - dt_min) * sigmoid(dt_raw) and
-    Aneg = softplus(a_raw) formed inside the kernels. dt_raw, B and C may be
-    column slices of a wider tensor (dense rows; B and C with one row stride)."""
+    """scan_fwd with dt = dt_min + (dt_max - dt_min) * sigmoid(dt_raw + dt_bias)
+    and Aneg = softplus(a_raw) formed inside the kernels (dt_bias: the dt
+    projection's bias, or None). dt_raw, B and C may be column slices of a
+    wider tensor (dense rows; B and C with one row stride)."""
     bt, t_len, d = x.shape
     n = a_raw.shape[1]
+    _dt_bias(dt_bias, x)
     ld_dt, ld_bc = _rows(dt_raw), _bc_rows(b_in, c_in)
     y, ckpt, h_last = _fwd_outputs(x, n, chunk, with_ckpt)
     ws, ws_bytes = _fwd_workspace(x, n)
@@ -401,8 +412,8 @@ def _scan_gated_fwd_impl(x: torch.Tensor, dt_raw: torch.Tensor, a_raw: torch.Ten
     fn = lib.mhs_scan_gated_fwd_bf16 if x.dtype == torch.bfloat16 else lib.mhs_scan_gated_fwd_f32
     with _on(x.device):
         rc = fn(_ptr(x), _ptr(dt_raw), _ptr(a_raw), _ptr(b_in), _ptr(c_in), dt_min, dt_max,
-                _ptr(y), _ptr(ckpt) if with_ckpt else None, _ptr(h_last), _ptr(ws), ws_bytes,
-                bt, t_len, d, n, chunk, ld_dt, ld_bc, _stream(x.device))
+                _ptr(dt_bias), _ptr(y), _ptr(ckpt) if with_ckpt else None, _ptr(h_last),
+                _ptr(ws), ws_bytes, bt, t_len, d, n, chunk, ld_dt, ld_bc, _stream(x.device))
     _check(rc, "gated scan forward")
     return y, ckpt, h_last
 
@@ -411,19 +422,24 @@ scan_gated_fwd = _register("scan_gated_fwd", _scan_gated_fwd_impl, ())
 
 
 @scan_gated_fwd.register_fake
-def _scan_gated_fwd_fake(x, dt_raw, a_raw, b_in, c_in, dt_min, dt_max, chunk, with_ckpt):
+def _scan_gated_fwd_fake(x, dt_raw, a_raw, b_in, c_in, dt_min, dt_max, chunk, with_ckpt,
+                         dt_bias=None):
     return _scan_fwd_fake(x, dt_raw, a_raw, b_in, c_in, chunk, with_ckpt)
 
 
 def _scan_gated_bwd_impl(x: torch.Tensor, dt_raw: torch.Tensor, a_raw: torch.Tensor,
                    b_in: torch.Tensor, c_in: torch.Tensor, dt_min: float, dt_max: float,
                    dy: torch.Tensor, dh_last: Optional[torch.Tensor], ckpt: torch.Tensor,
-                   chunk: int
-                   ) -> tuple[torch.Tensor, torch.Tensor, torch.Tensor, torch.Tensor, torch.Tensor]:
-    """(dx, d dt_raw, d a_raw, dB, dC) for the gated forward that produced
-    `ckpt`; the gradients are contiguous (inputs as scan_gated_fwd)."""
+                   chunk: int, dt_bias: Optional[torch.Tensor] = None
+                   ) -> tuple[torch.Tensor, torch.Tensor, torch.Tensor, torch.Tensor, torch.Tensor,
+                              torch.Tensor]:
+    """(dx, d dt_raw, d a_raw, dB, dC, d dt_bias) for the gated forward that
+    produced `ckpt` (same dt_bias); the gradients are contiguous (inputs as
+    scan_gated_fwd). d dt_bias, the sum of d dt_raw over batch and time, is
+    fp32 (d_inner,) also when dt_bias is None."""
     bt, t_len, d = x.shape
     n = a_raw.shape[1]
+    _dt_bias(dt_bias, x)
     ld_dt, ld_bc = _rows(dt_raw), _bc_rows(b_in, c_in)
     lib = library()
     dx = torch.empty_like(x)
@@ -431,6 +447,7 @@ def _scan_gated_bwd_impl(x: torch.Tensor, dt_raw: torch.Tensor, a_raw: torch.Ten
     da = torch.empty_like(a_raw)
     db = x.new_empty((bt, t_len, n))
     dc = x.new_empty((bt, t_len, n))
+    dbias = a_raw.new_empty((d,))
     ws_bytes = int(lib.mhs_scan_bwd_workspace_bytes(bt, t_len, d, n, chunk))
     if ws_bytes == 0:
         raise HipScanError(f"no backward workspace size for shape {(bt, t_len, d, n)} chunk {chunk}")
@@ -438,11 +455,11 @@ def _scan_gated_bwd_impl(x: torch.Tensor, dt_raw: torch.Tensor, a_raw: torch.Ten
     fn = lib.mhs_scan_gated_bwd_bf16 if x.dtype == torch.bfloat16 else lib.mhs_scan_gated_bwd_f32
     with _on(x.device):
         rc = fn(_ptr(x), _ptr(dt_raw), _ptr(a_raw), _ptr(b_in), _ptr(c_in), dt_min, dt_max,
-                _ptr(dy), _ptr(dh_last), _ptr(ckpt), _ptr(dx), _ptr(ddt), _ptr(da), _ptr(db),
-                _ptr(dc), _ptr(ws), ws_bytes, bt, t_len, d, n, chunk, ld_dt, ld_bc, 0, 0,
-                _stream(x.device))
+                _ptr(dt_bias), _ptr(dy), _ptr(dh_last), _ptr(ckpt), _ptr(dx), _ptr(ddt),
+                _ptr(da), _ptr(db), _ptr(dc), _ptr(dbias), _ptr(ws), ws_bytes, bt, t_len, d, n,
+                chunk, ld_dt, ld_bc, 0, 0, _stream(x.device))
     _check(rc, "gated scan backward")
-    return dx, ddt, da, db, dc
+    return dx, ddt, da, db, dc, dbias
 
 
 scan_gated_bwd = _register("scan_gated_bwd", _scan_gated_bwd_impl, ())
@@ -451,14 +468,16 @@ scan_gated_bwd = _register("scan_gated_bwd", _scan_gated_bwd_impl, ())
 def _scan_gated_bwd_into_impl(x: torch.Tensor, dt_raw: torch.Tensor, a_raw: torch.Tensor,
                               b_in: torch.Tensor, c_in: torch.Tensor, dt_min: float,
                               dt_max: float, dy: torch.Tensor, dh_last: Optional[torch.Tensor],
-                              ckpt: torch.Tensor, chunk: int, dproj: torch.Tensor
-                              ) -> tuple[torch.Tensor, torch.Tensor]:
+                              ckpt: torch.Tensor, chunk: int, dproj: torch.Tensor,
+                              dt_bias: Optional[torch.Tensor] = None
+                              ) -> tuple[torch.Tensor, torch.Tensor, torch.Tensor]:
     """scan_gated_bwd writing d dt_raw, dB and dC into the column slices
     [0, D), [D, D+N), [D+N, D+2N) of dproj (B, T, D+2N, contiguous): the
     gradient of one projection whose output rows are [dt_raw | B | C].
-    Returns (dx, d a_raw)."""
+    Returns (dx, d a_raw, d dt_bias)."""
     bt, t_len, d = x.shape
     n = a_raw.shape[1]
+    _dt_bias(dt_bias, x)
     if dproj.shape != (bt, t_len, d + 2 * n) or not dproj.is_contiguous():
         raise HipScanError(f"dproj must be a contiguous {(bt, t_len, d + 2 * n)} tensor; got "
                            f"{tuple(dproj.shape)} strides {dproj.stride()}")
@@ -466,6 +485,7 @@ def _scan_gated_bwd_into_impl(x: torch.Tensor, dt_raw: torch.Tensor, a_raw: torc
     lib = library()
     dx = torch.empty_like(x)
     da = torch.empty_like(a_raw)
+    dbias = a_raw.new_empty((d,))
     ws_bytes = int(lib.mhs_scan_bwd_workspace_bytes(bt, t_len, d, n, chunk))
     if ws_bytes == 0:
         raise HipScanError(f"no backward workspace size for shape {(bt, t_len, d, n)} chunk {chunk}")
@@ -476,11 +496,11 @@ def _scan_gated_bwd_into_impl(x: torch.Tensor, dt_raw: torch.Tensor, a_raw: torc
     w = d + 2 * n
     with _on(x.device):
         rc = fn(_ptr(x), _ptr(dt_raw), _ptr(a_raw), _ptr(b_in), _ptr(c_in), dt_min, dt_max,
-                _ptr(dy), _ptr(dh_last), _ptr(ckpt), _ptr(dx), base, _ptr(da), base + d * es,
-                base + (d + n) * es, _ptr(ws), ws_bytes, bt, t_len, d, n, chunk, ld_dt, ld_bc, w,
-                w, _stream(x.device))
+                _ptr(dt_bias), _ptr(dy), _ptr(dh_last), _ptr(ckpt), _ptr(dx), base, _ptr(da),
+                base + d * es, base + (d + n) * es, _ptr(dbias), _ptr(ws), ws_bytes, bt, t_len,
+                d, n, chunk, ld_dt, ld_bc, w, w, _stream(x.device))
     _check(rc, "gated scan backward")
-    return dx, da
+    return dx, da, dbias
 
 
 scan_gated_bwd_into = _register("scan_gated_bwd_into", _scan_gated_bwd_into_impl, ("dproj",))
@@ -488,14 +508,17 @@ scan_gated_bwd_into = _register("scan_gated_bwd_into", _scan_gated_bwd_into_impl
 
 @scan_gated_bwd_into.register_fake
 def _scan_gated_bwd_into_fake(x, dt_raw, a_raw, b_in, c_in, dt_min, dt_max, dy, dh_last, ckpt,
-                              chunk, dproj):
-    return torch.empty_like(x), torch.empty_like(a_raw)
+                              chunk, dproj, dt_bias=None):
+    return torch.empty_like(x), torch.empty_like(a_raw), a_raw.new_empty((x.shape[2],))
 
 
 @scan_gated_bwd.register_fake
-def _scan_gated_bwd_fake(x, dt_raw, a_raw, b_in, c_in, dt_min, dt_max, dy, dh_last, ckpt, chunk):
-    return (torch.empty_like(x), torch.empty_like(dt_raw), torch.empty_like(a_raw),
-            torch.empty_like(b_in), torch.empty_like(c_in))
+def _scan_gated_bwd_fake(x, dt_raw, a_raw, b_in, c_in, dt_min, dt_max, dy, dh_last, ckpt, chunk,
+                         dt_bias=None):
+    bt, t_len, d = x.shape
+    n = a_raw.shape[1]
+    return (torch.empty_like(x), x.new_empty((bt, t_len, d)), torch.empty_like(a_raw),
+            x.new_empty((bt, t_len, n)), x.new_empty((bt, t_len, n)), a_raw.new_empty((d,)))
 
 
 def _out_gate_fwd_impl(y: torch.Tensor, d_skip: torch.Tensor, z: torch.Tensor) -> torch.Tensor:

@@ -72,9 +72,14 @@ struct BwdArgs {
   float* wsA;            // (batch, D, N)
   int batch, T, D, N, K, nchunk;
   // Gated kernels only (GATED): dt holds the raw gate input and aneg holds A
-  // (dt = dt_lo + dt_span * sigmoid(raw), Aneg = softplus(A); mamba_metal/
-  // model.py:197, :200), and ddt receives the gradient of the raw input.
+  // (dt = dt_lo + dt_span * sigmoid(raw + dt_bias[d]), Aneg = softplus(A);
+  // mamba_metal/model.py:197, :200), and ddt receives the gradient of the raw
+  // input. dt_bias may be null. wsDB (nseg, batch, D), if not null, receives
+  // per block the sum over its steps of that gradient: the bias gradient's
+  // partials.
   float dt_lo, dt_span, dt_inv_span;
+  const float* dt_bias;
+  float* wsDB;
   // Time segments (the chunk-parallel-over-time variant): the chunks split
   // into nseg segments of cps chunks, one block per (channel block, batch
   // row, segment), blockIdx.y = seg * batch + b. With nseg > 1:
@@ -206,6 +211,9 @@ bwd_kernel(BwdArgs a) {
   const RowLoader<PERS, NPL, ES> rl(tid, NT, N, NP, ld_bc);
   float4 px[PER], pd[PER], py[PER];
   float pb[PERS], pc[PERS], ph[NPL];
+  float gbias[PER];   // GATED: the dt bias of each staging task's channel
+  if constexpr (GATED) qdt.load_channel(gbias, a.dt_bias, d0);
+  float dbias_acc = 0.f;   // GATED: this thread's sum of the raw dt gradient (channel tid % 32)
 
   // Chunk ci (any integer): first step and length (0 outside this block's
   // segment, so that every load and store of a chunk outside it is empty).
@@ -242,7 +250,7 @@ bwd_kernel(BwdArgs a) {
   };
   auto store_sub = [&](int j, int ci) {   // staging registers (chunk ci) -> buffer j
     float* s0 = lds + j * BUF;
-    if constexpr (GATED) ql.gate(pd, chunk_len(ci), a.dt_lo, a.dt_span);
+    if constexpr (GATED) qdt.gate(pd, chunk_len(ci), a.dt_lo, a.dt_span, gbias);
     ql.store_cm(s0, pd);
     ql.store_cm(s0 + oDY, py);
     if constexpr (!CARRY) ql.store_cm(s0 + oX, px);
@@ -257,6 +265,7 @@ bwd_kernel(BwdArgs a) {
     const float* sx = lds + j * BUF + oX;
     const float* sdt = lds + j * BUF;
     const GBuf gdx = chunk_buf(a.dx, ci, D), gddt = chunk_buf(a.ddt, ci, ld_ddt);
+    const int len = chunk_len(ci);
 #pragma unroll
     for (int f = 0; f < FT; ++f) {
       const int task0 = tid + f * NT;
@@ -286,11 +295,12 @@ bwd_kernel(BwdArgs a) {
         const float u0 = t0v - a.dt_lo, u1 = t1v - a.dt_lo;   // span * s
         g0 *= u0 * (a.dt_span - u0) * a.dt_inv_span;
         g1 *= u1 * (a.dt_span - u1) * a.dt_inv_span;
+        // Task f's channel is tid % 32 for every f (NT is a multiple of 32).
+        dbias_acc += (okc && k < len ? g0 : 0.f) + (okc && k + 1 < len ? g1 : 0.f);
       }
       st_elem<ES, kStream>(gddt, g0, od0);
       st_elem<ES, kStream>(gddt, g1, od1);
     }
-    const int len = chunk_len(ci);
     const size_t wrow = ((size_t)blockIdx.x * a.batch + b) * T + chunk_t0(ci);
     const unsigned sbytes = 4u * (unsigned)(len * N);
     const GBuf gwb(a.wsB + wrow * N, sbytes), gwc(a.wsC + wrow * N, sbytes);
@@ -447,6 +457,22 @@ bwd_kernel(BwdArgs a) {
 #pragma unroll
   for (int j = 0; j < NPL; ++j) out[j] = -acc[j];
   store_states<NPL>(GBuf(a.wsA + slot * slice, slice_bytes), st_lane, nvalid, out);
+  if constexpr (GATED) {
+    if (a.wsDB != nullptr) {
+      // The block's sum of the raw dt gradient per channel: the NT / 32
+      // threads of channel cc (tid = cc + 32 r) added in a fixed order.
+      static_assert(NT % kCH == 0, "finalize tasks keep their channel");
+      __syncthreads();   // every finalize read of LDS is done
+      lds[tid] = dbias_acc;
+      __syncthreads();
+      if (tid < kCH && d0 + tid < D) {
+        float sum = 0.f;
+#pragma unroll
+        for (int r = 0; r < NT / kCH; ++r) sum += lds[r * kCH + tid];
+        a.wsDB[slot * D + d0 + tid] = sum;
+      }
+    }
+  }
 }
 
 // dB, dC: sum the per-block partials over the nblk channel blocks;
@@ -477,15 +503,19 @@ __device__ __forceinline__ void ordered_sum2(const float* __restrict__ p, const 
 
 // a_raw: null, or A for the gated backward: then daneg receives dAneg *
 // softplus'(A) = dAneg * sigmoid(A), the gradient of A. dB, dC: ES-byte
-// elements (fp32 or bf16), rows of N elements ld_dbc apart.
+// elements (fp32 or bf16), rows of N elements ld_dbc apart. Dn: 0, or D for
+// the gated backward's dt-bias gradient: dbias[d] = the sum of wsDB's
+// `batch` rows (of Dn) in a fixed order.
 template <int ES = 4>
 __global__ void __launch_bounds__(256)
 bwd_reduce_kernel(const float* __restrict__ wsB, const float* __restrict__ wsC,
                   const float* __restrict__ wsA, const float* __restrict__ a_raw,
                   void* __restrict__ dB, void* __restrict__ dC, float* __restrict__ daneg,
-                  int nblk, int batch, long long S, long long A, int N, long long ld_dbc) {
+                  int nblk, int batch, long long S, long long A, int N, long long ld_dbc,
+                  const float* __restrict__ wsDB, float* __restrict__ dbias, int Dn) {
   const long long stride = (long long)gridDim.x * blockDim.x;
-  for (long long i = (long long)blockIdx.x * blockDim.x + threadIdx.x; i < S + A; i += stride) {
+  for (long long i = (long long)blockIdx.x * blockDim.x + threadIdx.x; i < S + A + Dn;
+       i += stride) {
     if (i < S) {
       float sb = 0.f, sc = 0.f;
       ordered_sum2(wsB + i, wsC + i, (size_t)S, nblk, sb, sc);
@@ -497,11 +527,16 @@ bwd_reduce_kernel(const float* __restrict__ wsB, const float* __restrict__ wsC,
         static_cast<unsigned short*>(dB)[o] = f32_to_bf16(sb);
         static_cast<unsigned short*>(dC)[o] = f32_to_bf16(sc);
       }
-    } else {
+    } else if (i < S + A) {
       const long long j = i - S;
       float s = 0.f;
       for (int bb = 0; bb < batch; ++bb) s += wsA[(size_t)bb * A + j];
       daneg[j] = a_raw != nullptr ? s / (1.f + expf(-a_raw[j])) : s;
+    } else {
+      const long long j = i - S - A;
+      float s = 0.f;
+      for (int bb = 0; bb < batch; ++bb) s += wsDB[(size_t)bb * Dn + j];
+      dbias[j] = s;
     }
   }
 }

@@ -100,7 +100,8 @@ struct Kernels {
   BwdFn carry = nullptr;    // adjoint-carry pass of the time segments
   BwdFn carry_g = nullptr;  // gated
   void (*reduce)(const float*, const float*, const float*, const float*, void*, void*, float*,
-                 int, int, long long, long long, int, long long) = nullptr;
+                 int, int, long long, long long, int, long long, const float*, float*,
+                 int) = nullptr;
 };
 
 // Activation element types: x, dt, B, C, y, dy, dx, ddt, dB, dC in fp32 or
@@ -220,7 +221,8 @@ int check_shape(int64_t batch, int64_t seqlen, int64_t d_inner, int64_t d_state,
 size_t round_up(size_t n, size_t m) { return (n + m - 1) / m * m; }
 
 struct WsLayout {
-  size_t partB = 0, partC = 0, partA = 0, carryL = 0, carryS = 0, fine = 0, total = 0;
+  size_t partB = 0, partC = 0, partA = 0, partDB = 0, carryL = 0, carryS = 0, fine = 0,
+         total = 0;
   int nseg = 1, cps = 1;
 };
 
@@ -237,6 +239,8 @@ WsLayout ws_layout(int64_t batch, int64_t T, int64_t D, int64_t N, int64_t chunk
   off += round_up(nblk * S * 4, 256);
   w.partA = off;
   off += round_up((size_t)w.nseg * batch * D * N * 4, 256);
+  w.partDB = off;   // the gated backward's dt-bias partials
+  off += round_up((size_t)w.nseg * batch * D * 4, 256);
   if (w.nseg > 1) {
     w.carryL = off;
     off += round_up((size_t)w.nseg * batch * D * N * 4, 256);
@@ -249,10 +253,14 @@ WsLayout ws_layout(int64_t batch, int64_t T, int64_t D, int64_t N, int64_t chunk
   return w;
 }
 
-// The block's dt gate (mamba_metal/model.py:197): dt = lo + span * sigmoid(raw).
+// The block's dt gate (mamba_metal/model.py:197): dt = lo + span *
+// sigmoid(raw + bias), bias the dt projection's (null: none); dbias, if not
+// null, receives the backward's gradient of the bias.
 struct Gate {
   bool on = false;
   float lo = 0.f, span = 0.f;
+  const float* bias = nullptr;
+  float* dbias = nullptr;
 };
 
 int check_gate(float dt_min, float dt_max, Gate& g) {
@@ -276,6 +284,7 @@ int launch_fwd(const Plan& p, mhs::FwdArgs a, int batch, hipStream_t s, const Ga
   const FwdFn fn = aligned ? (g.on ? kk.fwd_g : kk.fwd) : (g.on ? kk.fwd_any_g : kk.fwd_any);
   a.dt_lo = g.lo;
   a.dt_span = g.span;
+  a.dt_bias = g.bias;
   a.batch = batch;
   if (nseg == 1) {
     a.seg_len = a.T;
@@ -367,6 +376,7 @@ int scan_fwd(const void* x, const void* dt, const float* aneg, const void* B, co
   a.carrySdt = reinterpret_cast<float*>(ws + w.carryS);
   a.dt_lo = g.lo;
   a.dt_span = g.span;
+  a.dt_bias = g.bias;
   const unsigned nblk = (unsigned)((d_inner + mhs::kCH - 1) / mhs::kCH);
   mhs::FwdArgs c = a;
   c.y = nullptr;
@@ -459,6 +469,8 @@ int scan_bwd(const void* x, const void* dt, const float* aneg, const void* B, co
   a.dt_lo = g.lo;
   a.dt_span = g.span;
   a.dt_inv_span = g.on ? 1.f / g.span : 0.f;
+  a.dt_bias = g.bias;
+  a.wsDB = g.dbias != nullptr ? reinterpret_cast<float*>(ws + w.partDB) : nullptr;
   a.nseg = w.nseg;
   a.cps = w.cps;
   a.carryL = w.nseg > 1 ? reinterpret_cast<float*>(ws + w.carryL) : nullptr;
@@ -486,11 +498,12 @@ int scan_bwd(const void* x, const void* dt, const float* aneg, const void* B, co
 
   const long long S = (long long)batch * T * N;
   const long long A = (long long)D * N;
-  const long long total = S + A;
+  const int Dn = g.dbias != nullptr ? D : 0;
+  const long long total = S + A + Dn;
   const int blocks = (int)std::min<long long>((total + 255) / 256, 4096);
   hipLaunchKernelGGL(p.k[e].reduce, dim3(blocks), dim3(256), 0, s, a.wsB, a.wsC, a.wsA,
                      g.on ? aneg : nullptr, dB, dC, daneg, (D + ch - 1) / ch,
-                     (int)batch * w.nseg, S, A, N, (long long)st.dbc);
+                     (int)batch * w.nseg, S, A, N, (long long)st.dbc, a.wsDB, g.dbias, Dn);
   return check_launch("backward reduction kernel");
 }
 
@@ -571,7 +584,8 @@ int mhs_scan_bwd_f32(const float* x, const float* dt, const float* aneg, const f
 }
 
 int mhs_scan_gated_fwd_f32(const float* x, const float* dt_raw, const float* A, const float* B,
-                           const float* C, float dt_min, float dt_max, float* y, float* ckpt,
+                           const float* C, float dt_min, float dt_max, const float* dt_bias,
+                           float* y, float* ckpt,
                            float* h_last, void* workspace, size_t workspace_bytes, int64_t batch,
                            int64_t seqlen, int64_t d_inner, int64_t d_state, int64_t chunk,
                            int64_t ld_dt, int64_t ld_bc, void* stream) {
@@ -579,14 +593,16 @@ int mhs_scan_gated_fwd_f32(const float* x, const float* dt_raw, const float* A, 
   Gate g;
   const int rc = check_gate(dt_min, dt_max, g);
   if (rc) return rc;
+  g.bias = dt_bias;
   return scan_fwd(x, dt_raw, A, B, C, y, ckpt, h_last, workspace, workspace_bytes, batch, seqlen,
                   d_inner, d_state, chunk, stream, g, kF32, Strides{ld_dt, ld_bc, 0, 0});
 }
 
 int mhs_scan_gated_bwd_f32(const float* x, const float* dt_raw, const float* A, const float* B,
-                           const float* C, float dt_min, float dt_max, const float* dy,
-                           const float* dh_last, const float* ckpt, float* dx, float* ddt_raw,
-                           float* dA, float* dB, float* dC, void* workspace,
+                           const float* C, float dt_min, float dt_max, const float* dt_bias,
+                           const float* dy, const float* dh_last, const float* ckpt, float* dx,
+                           float* ddt_raw, float* dA, float* dB, float* dC, float* ddt_bias,
+                           void* workspace,
                            size_t workspace_bytes, int64_t batch, int64_t seqlen, int64_t d_inner,
                            int64_t d_state, int64_t chunk, int64_t ld_dt, int64_t ld_bc,
                            int64_t ld_ddt, int64_t ld_dbc, void* stream) {
@@ -594,6 +610,8 @@ int mhs_scan_gated_bwd_f32(const float* x, const float* dt_raw, const float* A, 
   Gate g;
   const int rc = check_gate(dt_min, dt_max, g);
   if (rc) return rc;
+  g.bias = dt_bias;
+  g.dbias = ddt_bias;
   return scan_bwd(x, dt_raw, A, B, C, dy, dh_last, ckpt, dx, ddt_raw, dA, dB, dC, workspace,
                   workspace_bytes, batch, seqlen, d_inner, d_state, chunk, stream, g, kF32,
                   Strides{ld_dt, ld_bc, ld_ddt, ld_dbc});
@@ -621,7 +639,7 @@ int mhs_scan_bwd_bf16(const uint16_t* x, const uint16_t* dt, const float* aneg, 
 
 int mhs_scan_gated_fwd_bf16(const uint16_t* x, const uint16_t* dt_raw, const float* A,
                             const uint16_t* B, const uint16_t* C, float dt_min, float dt_max,
-                            uint16_t* y, float* ckpt, float* h_last, void* workspace,
+                            const float* dt_bias, uint16_t* y, float* ckpt, float* h_last, void* workspace,
                             size_t workspace_bytes, int64_t batch, int64_t seqlen,
                             int64_t d_inner, int64_t d_state, int64_t chunk, int64_t ld_dt,
                             int64_t ld_bc, void* stream) {
@@ -629,15 +647,16 @@ int mhs_scan_gated_fwd_bf16(const uint16_t* x, const uint16_t* dt_raw, const flo
   Gate g;
   const int rc = check_gate(dt_min, dt_max, g);
   if (rc) return rc;
+  g.bias = dt_bias;
   return scan_fwd(x, dt_raw, A, B, C, y, ckpt, h_last, workspace, workspace_bytes, batch, seqlen,
                   d_inner, d_state, chunk, stream, g, kBF16, Strides{ld_dt, ld_bc, 0, 0});
 }
 
 int mhs_scan_gated_bwd_bf16(const uint16_t* x, const uint16_t* dt_raw, const float* A,
                             const uint16_t* B, const uint16_t* C, float dt_min, float dt_max,
-                            const uint16_t* dy, const float* dh_last, const float* ckpt,
-                            uint16_t* dx, uint16_t* ddt_raw, float* dA, uint16_t* dB,
-                            uint16_t* dC, void* workspace, size_t workspace_bytes, int64_t batch,
+                            const float* dt_bias, const uint16_t* dy, const float* dh_last,
+                            const float* ckpt, uint16_t* dx, uint16_t* ddt_raw, float* dA,
+                            uint16_t* dB, uint16_t* dC, float* ddt_bias, void* workspace, size_t workspace_bytes, int64_t batch,
                             int64_t seqlen, int64_t d_inner, int64_t d_state, int64_t chunk,
                             int64_t ld_dt, int64_t ld_bc, int64_t ld_ddt, int64_t ld_dbc,
                             void* stream) {
@@ -645,6 +664,8 @@ int mhs_scan_gated_bwd_bf16(const uint16_t* x, const uint16_t* dt_raw, const flo
   Gate g;
   const int rc = check_gate(dt_min, dt_max, g);
   if (rc) return rc;
+  g.bias = dt_bias;
+  g.dbias = ddt_bias;
   return scan_bwd(x, dt_raw, A, B, C, dy, dh_last, ckpt, dx, ddt_raw, dA, dB, dC, workspace,
                   workspace_bytes, batch, seqlen, d_inner, d_state, chunk, stream, g, kBF16,
                   Strides{ld_dt, ld_bc, ld_ddt, ld_dbc});

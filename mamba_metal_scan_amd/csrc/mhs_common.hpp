@@ -412,18 +412,28 @@ struct QuadLoader {
       v[i].w = ld_elem<ES, POL>(g, ok ? o + 3 * rs : kOOB);
     }
   }
-  // Gate staged dt values in place: dt = lo + span * sigmoid(raw) for the
-  // steps below len; steps at or past len (and channels past d_inner) get
-  // dt = 0, which makes them identity steps of the recurrence, as the zeros
-  // an ungated load returns there.
-  __device__ __forceinline__ void gate(float4 (&v)[PER], int len, float lo, float span) const {
+  // Per task, the element of a per-channel vector (the dt gate's bias) for
+  // its channel d0 + chan(i); 0 for tasks past the tile, channels past
+  // d_inner, or no vector.
+  __device__ __forceinline__ void load_channel(float (&v)[PER], const float* vec, int d0) const {
+#pragma unroll
+    for (int i = 0; i < PER; ++i)
+      v[i] = (vec != nullptr && toff[i] != kOOB) ? vec[d0 + chan(i)] : 0.f;
+  }
+  // Gate staged dt values in place: dt = lo + span * sigmoid(raw + bias) for
+  // the steps below len (bias: the task's channel bias, see load_channel);
+  // steps at or past len (and channels past d_inner) get dt = 0, which makes
+  // them identity steps of the recurrence, as the zeros an ungated load
+  // returns there.
+  __device__ __forceinline__ void gate(float4 (&v)[PER], int len, float lo, float span,
+                                       const float (&bias)[PER]) const {
 #pragma unroll
     for (int i = 0; i < PER; ++i) {
       const int s0 = toff[i] != kOOB ? 4 * quad(i) : kSteps;
-      v[i].x = s0 < len ? gate_dt(v[i].x, lo, span) : 0.f;
-      v[i].y = s0 + 1 < len ? gate_dt(v[i].y, lo, span) : 0.f;
-      v[i].z = s0 + 2 < len ? gate_dt(v[i].z, lo, span) : 0.f;
-      v[i].w = s0 + 3 < len ? gate_dt(v[i].w, lo, span) : 0.f;
+      v[i].x = s0 < len ? gate_dt(v[i].x + bias[i], lo, span) : 0.f;
+      v[i].y = s0 + 1 < len ? gate_dt(v[i].y + bias[i], lo, span) : 0.f;
+      v[i].z = s0 + 2 < len ? gate_dt(v[i].z + bias[i], lo, span) : 0.f;
+      v[i].w = s0 + 3 < len ? gate_dt(v[i].w + bias[i], lo, span) : 0.f;
     }
   }
   // Channel-major swizzled tile [CH][16].

@@ -44,9 +44,11 @@ struct FwdArgs {
   float* h_last;   // may be null
   int T, D, N, K, nchunk;
   // Gated kernels only (GATED): dt holds the raw gate input and aneg holds A;
-  // dt = dt_lo + dt_span * sigmoid(raw) and Aneg = softplus(A) are formed in
-  // the kernel (mamba_metal/model.py:197, :200).
+  // dt = dt_lo + dt_span * sigmoid(raw + dt_bias[d]) and Aneg = softplus(A)
+  // are formed in the kernel (mamba_metal/model.py:197, :200; dt_bias, the
+  // dt projection's bias, may be null).
   float dt_lo, dt_span;
+  const float* dt_bias = nullptr;
   // Time segments: blockIdx.y = seg * batch + b; segment seg covers steps
   // [seg * seg_len, min(T, (seg + 1) * seg_len)), seg_len a multiple of 16
   // (nseg = 1, seg_len >= T: the whole sequence). A segment other than the
@@ -135,6 +137,8 @@ fwd_kernel(FwdArgs a) {
   const RowLoader<PERS, NPL, ES> rl(tid, NT, N, NP, ld_bc);
   float4 px[PER], pd[PER];
   float pb[PERS], pc[PERS];
+  float gbias[PER];   // GATED: the dt bias of each staging task's channel
+  if constexpr (GATED) qdt.load_channel(gbias, a.dt_bias, d0);
   // Sub-chunk i of the segment (any i >= 0): first step and length (0 past
   // the segment).
   auto sub_t0 = [&](int i) { return min(t_beg + max(i, 0) * kSteps, T - 1); };
@@ -163,7 +167,7 @@ fwd_kernel(FwdArgs a) {
   };
   auto store_sub = [&](int i) {           // staging registers -> LDS buffer i&1
     float* buf = lds + (i & 1) * BUF;
-    if constexpr (GATED) ql.gate(pd, sub_len(i), a.dt_lo, a.dt_span);
+    if constexpr (GATED) qdt.gate(pd, sub_len(i), a.dt_lo, a.dt_span, gbias);
     ql.store_cm(buf, pd);
     ql.store_cm_product(buf + kCH * kSteps, pd, px);
     rl.store(buf + 2 * kCH * kSteps, pb);

@@ -32,9 +32,15 @@ class SelectiveScanGatedHIP(torch.autograd.Function):
 
     @staticmethod
     def forward(ctx, x, dt_raw, a_raw, b_in, c_in, dt_min, dt_max, chunk=SSM_CHUNK,
-                return_state=False):
+                return_state=False, dt_bias=None):
         _validate(x, dt_raw, a_raw, b_in, c_in, chunk)
         x, dt_raw, a_raw, b_in, c_in = (t.contiguous() for t in (x, dt_raw, a_raw, b_in, c_in))
+        if dt_bias is not None:
+            if dt_bias.shape != (x.shape[2],) or dt_bias.dtype != torch.float32:
+                raise ValueError(f"dt_bias must be fp32 of shape ({x.shape[2]},); got "
+                                 f"{dt_bias.dtype} {tuple(dt_bias.shape)}")
+            dt_bias = dt_bias.contiguous()
+        ctx.has_bias = dt_bias is not None
         ctx.set_materialize_grads(False)
         ctx.chunk = chunk
         ctx.gate = (float(dt_min), float(dt_max))
@@ -44,12 +50,12 @@ class SelectiveScanGatedHIP(torch.autograd.Function):
             bt, t_len, d = x.shape
             y = x.new_zeros((bt, t_len, d))
             h_last = x.new_zeros((bt, d, a_raw.shape[1]))
-            ctx.save_for_backward(x, dt_raw, a_raw, b_in, c_in)
+            ctx.save_for_backward(x, dt_raw, a_raw, b_in, c_in, dt_bias)
         else:
-            need_grad = any(ctx.needs_input_grad[:5])
+            need_grad = any(ctx.needs_input_grad[:5]) or ctx.needs_input_grad[9]
             y, ckpt, h_last = _native.dispatch("scan_gated_fwd")(
-                x, dt_raw, a_raw, b_in, c_in, ctx.gate[0], ctx.gate[1], chunk, need_grad)
-            ctx.save_for_backward(x, dt_raw, a_raw, b_in, c_in, ckpt)
+                x, dt_raw, a_raw, b_in, c_in, ctx.gate[0], ctx.gate[1], chunk, need_grad, dt_bias)
+            ctx.save_for_backward(x, dt_raw, a_raw, b_in, c_in, dt_bias, ckpt)
         if return_state:
             return y, h_last
         return y
@@ -59,31 +65,37 @@ class SelectiveScanGatedHIP(torch.autograd.Function):
         dy = grads[0]
         dh_last = grads[1] if ctx.return_state and len(grads) > 1 else None
         if ctx.empty:
-            x, dt_raw, a_raw, b_in, c_in = ctx.saved_tensors
+            x, dt_raw, a_raw, b_in, c_in, dt_bias = ctx.saved_tensors
             return (torch.zeros_like(x), torch.zeros_like(dt_raw), torch.zeros_like(a_raw),
-                    torch.zeros_like(b_in), torch.zeros_like(c_in), None, None, None, None)
-        x, dt_raw, a_raw, b_in, c_in, ckpt = ctx.saved_tensors
+                    torch.zeros_like(b_in), torch.zeros_like(c_in), None, None, None, None,
+                    torch.zeros_like(dt_bias) if ctx.has_bias else None)
+        x, dt_raw, a_raw, b_in, c_in, dt_bias, ckpt = ctx.saved_tensors
         if dy is None:
             dy = torch.zeros_like(x)
         dy = dy.contiguous()
         if dh_last is not None:
             dh_last = dh_last.contiguous()
-        dx, ddt, da, db, dc = _native.dispatch("scan_gated_bwd")(
-            x, dt_raw, a_raw, b_in, c_in, ctx.gate[0], ctx.gate[1], dy, dh_last, ckpt, ctx.chunk)
-        return dx, ddt, da, db, dc, None, None, None, None
+        dx, ddt, da, db, dc, dbias = _native.dispatch("scan_gated_bwd")(
+            x, dt_raw, a_raw, b_in, c_in, ctx.gate[0], ctx.gate[1], dy, dh_last, ckpt, ctx.chunk,
+            dt_bias)
+        return dx, ddt, da, db, dc, None, None, None, None, dbias if ctx.has_bias else None
 
 
 def selective_scan_gated(x: torch.Tensor, dt_raw: torch.Tensor, a_raw: torch.Tensor,
                          b_in: torch.Tensor, c_in: torch.Tensor, dt_min: float, dt_max: float,
-                         chunk: int = SSM_CHUNK, return_state: bool = False):
-    """``selective_scan(x, dt_min + (dt_max - dt_min) * sigmoid(dt_raw), softplus(a_raw),
-    B, C)`` in the fused gfx950 kernels (the reference's MambaBlock._proj +
-    _scan, mamba_metal/model.py:197-200, :213-215). Inputs on one ROCm device,
-    fp32; needs dt_min < dt_max."""
+                         chunk: int = SSM_CHUNK, return_state: bool = False,
+                         dt_bias: torch.Tensor | None = None):
+    """``selective_scan(x, dt_min + (dt_max - dt_min) * sigmoid(dt_raw + dt_bias),
+    softplus(a_raw), B, C)`` in the fused gfx950 kernels (the reference's
+    MambaBlock._proj + _scan, mamba_metal/model.py:197-200, :213-215). dt_bias
+    (optional, (d_inner,)) is the dt projection's bias, so that dt_raw may be
+    the projection without it; its gradient is reduced inside the backward.
+    Inputs on one ROCm device, fp32 (x, dt_raw, B, C may be bf16); needs
+    dt_min < dt_max."""
     if not (float(dt_min) < float(dt_max)):
         raise ValueError(f"need dt_min < dt_max; got {dt_min}, {dt_max}")
     return SelectiveScanGatedHIP.apply(x, dt_raw, a_raw, b_in, c_in, dt_min, dt_max, chunk,
-                                       return_state)
+                                       return_state, dt_bias)
 
 
 class OutGateHIP(torch.autograd.Function):
@@ -130,15 +142,17 @@ def out_gate(y: torch.Tensor, d_skip: torch.Tensor, z: torch.Tensor) -> torch.Te
 
 class MambaInnerHIP(torch.autograd.Function):
     """The inner block between in_proj and out_proj, fused (fp32):
-    x, z = xz.chunk(2); xc = silu(conv(x)); [dt_raw | B | C] = xc W^T + b;
-    y = gated scan(xc, dt_raw, A, B, C); out = (y + D_skip) * silu(z).
+    x, z = xz.chunk(2); xc = silu(conv(x)); [dt_raw | B | C] = xc W^T;
+    y = gated scan(xc, dt_raw + b_dt, A, B, C); out = (y + D_skip) * silu(z).
     The reference computes it as separate modules (mamba_metal/model.py:
-    197-200, :244-256). Fused, the three projections are one GEMM whose
-    output rows the scan reads in place; in the backward the scan writes its
-    dt_raw, B and C gradients into one projection gradient, the projections'
-    input gradient is accumulated onto the scan's dx by the GEMM itself, and
-    the conv and output gate write dx and dz straight into the two halves of
-    xz's gradient (no concatenation, no separate gradient sums)."""
+    197-200, :244-256). Fused, the three projections are one GEMM (no bias:
+    the dt projection's bias is added by the scan kernels as they gate dt)
+    whose output rows the scan reads in place; in the backward the scan writes
+    its dt_raw, B and C gradients into one projection gradient and reduces the
+    bias gradient itself, the projections' input gradient is accumulated onto
+    the scan's dx by the GEMM, and the conv and output gate write dx and dz
+    straight into the two halves of xz's gradient (no concatenation, no
+    separate gradient sums)."""
 
     @staticmethod
     def forward(ctx, xz, conv_w, conv_b, w_dt, b_dt, w_b, w_c, a_raw, d_skip, dt_min, dt_max,
@@ -150,36 +164,35 @@ class MambaInnerHIP(torch.autograd.Function):
         cb = conv_b.contiguous()
         xc = _native.dispatch("conv1d_silu_fwd")(x, w2, cb)
         w_proj = torch.cat([w_dt, w_b, w_c], 0)
-        bias = torch.cat([b_dt, b_dt.new_zeros(2 * n)])
-        proj = torch.addmm(bias, xc.view(-1, d), w_proj.t()).view(bt, t_len, d + 2 * n)
+        bias = b_dt.contiguous()
+        proj = torch.mm(xc.view(-1, d), w_proj.t()).view(bt, t_len, d + 2 * n)
         need_grad = any(ctx.needs_input_grad)
         y, ckpt, _ = _native.dispatch("scan_gated_fwd")(
             xc, proj[..., :d], a_raw, proj[..., d:d + n], proj[..., d + n:], float(dt_min),
-            float(dt_max), chunk, need_grad)
+            float(dt_max), chunk, need_grad, bias)
         out = _native.dispatch("out_gate_fwd")(y, d_skip, z)
         ctx.gate = (float(dt_min), float(dt_max))
         ctx.chunk = chunk
         ctx.conv_shape = conv_w.shape
         if need_grad:
-            ctx.save_for_backward(xz, w2, cb, w_proj, a_raw, d_skip, xc, proj, y, ckpt)
+            ctx.save_for_backward(xz, w2, cb, w_proj, bias, a_raw, d_skip, xc, proj, y, ckpt)
         return out
 
     @staticmethod
     def backward(ctx, dout):
-        xz, w2, cb, w_proj, a_raw, d_skip, xc, proj, y, ckpt = ctx.saved_tensors
+        xz, w2, cb, w_proj, bias, a_raw, d_skip, xc, proj, y, ckpt = ctx.saved_tensors
         bt, t_len, d2 = xz.shape
         d, n = d2 // 2, a_raw.shape[1]
         dxz = torch.empty_like(xz)
         dy, dd = _native.dispatch("out_gate_bwd_into")(y, d_skip, xz[..., d:],
                                                        dout.contiguous(), dxz[..., d:])
         dproj = torch.empty_like(proj)
-        dxc, da = _native.dispatch("scan_gated_bwd_into")(
+        dxc, da, db_dt = _native.dispatch("scan_gated_bwd_into")(
             xc, proj[..., :d], a_raw, proj[..., d:d + n], proj[..., d + n:], ctx.gate[0],
-            ctx.gate[1], dy, None, ckpt, ctx.chunk, dproj)
+            ctx.gate[1], dy, None, ckpt, ctx.chunk, dproj, bias)
         dp2 = dproj.view(-1, d + 2 * n)
         dxc.view(-1, d).addmm_(dp2, w_proj)            # + the projections' input gradient
         dw = dp2.t().mm(xc.view(-1, d))
-        db_dt = dp2[:, :d].sum(0)
         dcw, dcb = _native.dispatch("conv1d_silu_bwd_into")(xz[..., :d], w2, cb, dxc,
                                                             dxz[..., :d])
         return (dxz, dcw.reshape(ctx.conv_shape), dcb, dw[:d], db_dt, dw[d:d + n],

@@ -64,6 +64,48 @@ def test_gated_scan_matches_the_oracle(bt, t_len, d, n, chunk):
         assert_close(name, g, r)
 
 
+# With the dt projection's bias inside the kernels: grids small enough to run
+# in time segments (the carry passes stage the biased gate too, and every
+# segment leaves its own bias partials), a stride above the backward's window
+# (fine checkpoints recomputed through the biased gate), channels off the
+# 32-channel blocks, and the 80M block's shape.
+BIAS_CASES = [(1, 600, 64, 16, 16), (2, 333, 40, 16, 16), (2, 77, 64, 16, 64),
+              (3, 130, 70, 5, 7), (16, 512, 1432, 16, 16)]
+
+
+@pytest.mark.parametrize("bt,t_len,d,n,chunk", BIAS_CASES)
+def test_gated_scan_with_dt_bias_matches_the_oracle(bt, t_len, d, n, chunk):
+    """dt = lo + span * sigmoid(raw + bias): the oracle on raw + bias, and the
+    bias gradient equal to the oracle's raw gradient summed over batch and
+    time (raw + bias depends on the bias with derivative one); the bias
+    gradient is also bitwise reproducible."""
+    print(f"[case] gated scan with dt bias {bt}x{t_len}x{d}x{n} chunk {chunk}", flush=True)
+    arrs = _gated_inputs(bt, t_len, d, n, seed=3 * d + n)
+    rng = np.random.default_rng(11)
+    bias = (0.7 * rng.standard_normal(d)).astype(np.float32)
+    dy = rng.standard_normal((bt, t_len, d), dtype=np.float32)
+    ref_in = list(arrs)
+    ref_in[1] = (arrs[1].astype(np.float64) + bias.astype(np.float64)).astype(np.float64)
+    y_ref, _, _ = oracle.scan_gated_fwd(*ref_in, LO, HI)
+    g_ref = list(oracle.scan_gated_bwd(*ref_in, LO, HI, dy))
+    g_ref.append(np.asarray(g_ref[1]).sum(axis=(0, 1)))
+
+    runs = []
+    for _ in range(2):
+        leaves = [torch.from_numpy(a).to(DEV).requires_grad_(True) for a in arrs]
+        tb = torch.from_numpy(bias).to(DEV).requires_grad_(True)
+        y = selective_scan_gated(*leaves, LO, HI, chunk=chunk, dt_bias=tb)
+        grads = torch.autograd.grad(y, leaves + [tb], torch.from_numpy(dy).to(DEV))
+        runs.append((y.detach(), grads))
+    torch.cuda.synchronize()
+    y, grads = runs[0]
+    assert_close("y", y, y_ref)
+    for name, g, r in zip(("dx", "ddt_raw", "dA", "dB", "dC", "dbias"), grads, g_ref):
+        assert g.shape == np.asarray(r).shape, name
+        assert_close(name, g, r)
+    assert torch.equal(runs[0][1][5], runs[1][1][5])
+
+
 def test_gated_scan_equals_the_scan_on_torch_gated_inputs():
     """Gate fused in the kernels == the framework's gate followed by the plain
     HIP scan, values and gradients (within fp32 rounding of dt)."""

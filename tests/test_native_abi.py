@@ -59,11 +59,12 @@ def test_chunk_arithmetic():
 
 
 def test_workspace_size_formula():
-    """dB/dC block partials (48 blocks of 32 channels) + dAneg batch partials,
-    + fine checkpoints when the stride exceeds the 16-step window."""
+    """dB/dC block partials (48 blocks of 32 channels) + dAneg batch partials
+    + the gated dt-bias batch partials, + fine checkpoints when the stride
+    exceeds the 16-step window."""
     lib = _native.library()
     nblk, s, a = 48, 16 * 512 * 16, 16 * 1536 * 16
-    base = 2 * nblk * s * 4 + a * 4
+    base = 2 * nblk * s * 4 + a * 4 + 16 * 1536 * 4
     assert lib.mhs_scan_bwd_workspace_bytes(16, 512, 1536, 16, 16) == base
     assert lib.mhs_scan_bwd_workspace_bytes(16, 512, 1536, 16, 64) == base + 32 * a * 4
     assert lib.mhs_scan_bwd_workspace_bytes(16, 512, 1536, 0, 16) == 0
@@ -135,25 +136,25 @@ def test_gated_scan_argument_errors():
     lib = _native.library()
     sizes = (2, 8, 32, 16, 16)
     outs = [A16] * 3 + [None, 0]          # y, ckpt, h_last; no workspace
-    rc = lib.mhs_scan_gated_fwd_f32(*([A16] * 5), 0.1, 0.1, *outs, *sizes, 0, 0, None)
+    rc = lib.mhs_scan_gated_fwd_f32(*([A16] * 5), 0.1, 0.1, None, *outs, *sizes, 0, 0, None)
     assert rc == MHS_EINVAL and "dt_min < dt_max" in _err(lib)
-    rc = lib.mhs_scan_gated_fwd_f32(*([A16] * 5), 0.001, float("nan"), *outs, *sizes, 0, 0, None)
+    rc = lib.mhs_scan_gated_fwd_f32(*([A16] * 5), 0.001, float("nan"), None, *outs, *sizes, 0, 0, None)
     assert rc == MHS_EINVAL and "dt_min < dt_max" in _err(lib)
-    rc = lib.mhs_scan_gated_fwd_f32(*([A16] * 5), 0.001, 0.1, *outs, 2, 8, 32, 65, 16, 0, 0, None)
+    rc = lib.mhs_scan_gated_fwd_f32(*([A16] * 5), 0.001, 0.1, None, *outs, 2, 8, 32, 65, 16, 0, 0, None)
     assert rc == MHS_EINVAL and "d_state" in _err(lib)
     # row strides below d_inner (dt) or d_state (B, C) are rejected
-    rc = lib.mhs_scan_gated_fwd_f32(*([A16] * 5), 0.001, 0.1, *outs, *sizes, 31, 0, None)
+    rc = lib.mhs_scan_gated_fwd_f32(*([A16] * 5), 0.001, 0.1, None, *outs, *sizes, 31, 0, None)
     assert rc == MHS_EINVAL and "row strides" in _err(lib)
-    rc = lib.mhs_scan_gated_fwd_f32(*([A16] * 5), 0.001, 0.1, *outs, *sizes, 64, 15, None)
+    rc = lib.mhs_scan_gated_fwd_f32(*([A16] * 5), 0.001, 0.1, None, *outs, *sizes, 64, 15, None)
     assert rc == MHS_EINVAL and "row strides" in _err(lib)
     need = lib.mhs_scan_bwd_workspace_bytes(*sizes)
-    rc = lib.mhs_scan_gated_bwd_f32(*([A16] * 5), 0.001, 0.1, *([A16] * 8), A16, need - 4,
+    rc = lib.mhs_scan_gated_bwd_f32(*([A16] * 5), 0.001, 0.1, None, *([A16] * 8), None, A16, need - 4,
                                     *sizes, 0, 0, 0, 0, None)
     assert rc == MHS_EINVAL and "workspace too small" in _err(lib)
-    rc = lib.mhs_scan_gated_bwd_f32(*([A16] * 5), 1.0, 0.5, *([A16] * 8), A16, need, *sizes,
+    rc = lib.mhs_scan_gated_bwd_f32(*([A16] * 5), 1.0, 0.5, None, *([A16] * 8), None, A16, need, *sizes,
                                     0, 0, 0, 0, None)
     assert rc == MHS_EINVAL and "dt_min < dt_max" in _err(lib)
-    rc = lib.mhs_scan_gated_bwd_f32(*([A16] * 5), 0.001, 0.1, *([A16] * 8), A16, need, *sizes,
+    rc = lib.mhs_scan_gated_bwd_f32(*([A16] * 5), 0.001, 0.1, None, *([A16] * 8), None, A16, need, *sizes,
                                     0, 0, 0, 15, None)
     assert rc == MHS_EINVAL and "row strides" in _err(lib)
 
@@ -177,7 +178,8 @@ def test_out_gate_argument_errors():
 def test_time_segments_knob_and_workspace():
     """Automatic split: one segment at 16x512x1536x16 (768 blocks), three at
     4x16384x2048x16 (256 blocks); forced splits add the per-segment dAneg
-    partials and the carries (L: segments x batch x D x N, sum dt: x batch x D)."""
+    and dt-bias partials and the carries (L: segments x batch x D x N, sum dt:
+    x batch x D)."""
     lib = _native.library()
     with pytest.raises(_native.HipScanError, match="time segments"):
         _native.set_time_segments(9)
@@ -190,7 +192,7 @@ def test_time_segments_knob_and_workspace():
         nblk = (d + 31) // 32
         s_ = bt * t * n
         a = bt * d * n
-        base = 2 * ru(nblk * s_ * 4) + ru(segs * a * 4)
+        base = 2 * ru(nblk * s_ * 4) + ru(segs * a * 4) + ru(segs * bt * d * 4)
         if segs > 1:
             base += ru(segs * a * 4) + ru(segs * bt * d * 4)
         return base
