@@ -61,10 +61,16 @@ def test_bf16_scan_matches_the_oracle(bt, t_len, d, n, chunk):
         assert_close(name, g, r, TOL_F32 if name == "dAneg" else TOL_BF16)
 
 
-@pytest.mark.parametrize("bt,t_len,d,n,segs", [(2, 130, 70, 16, 0), (16, 512, 1432, 16, 0),
-                                               (1, 300, 64, 16, 3)])
-def test_bf16_gated_scan_matches_the_oracle(bt, t_len, d, n, segs):
-    print(f"[case] bf16 gated scan {bt}x{t_len}x{d}x{n} segments {segs}", flush=True)
+@pytest.mark.parametrize("bt,t_len,d,n,segs,bias", [(2, 130, 70, 16, 0, False),
+                                                    (16, 512, 1432, 16, 0, False),
+                                                    (1, 300, 64, 16, 3, False),
+                                                    (2, 130, 70, 16, 0, True),
+                                                    (1, 300, 64, 16, 3, True)])
+def test_bf16_gated_scan_matches_the_oracle(bt, t_len, d, n, segs, bias):
+    """bf16 activations through the gate; with an fp32 dt bias, whose
+    gradient (the fp32 sum of the raw dt gradient, before its rounding to
+    bf16) meets the fp32 bar."""
+    print(f"[case] bf16 gated scan {bt}x{t_len}x{d}x{n} segments {segs} bias {bias}", flush=True)
     rng = np.random.default_rng(d)
     x = rng.standard_normal((bt, t_len, d), dtype=np.float32)
     raw = (2.0 * rng.standard_normal((bt, t_len, d))).astype(np.float32)
@@ -75,23 +81,33 @@ def test_bf16_gated_scan_matches_the_oracle(bt, t_len, d, n, segs):
     dy = rng.standard_normal((bt, t_len, d), dtype=np.float32)
     acts = [_bf16(v) for v in (x, raw, b_in, c_in)]
     dyb = _bf16(dy)
+    dt_bias = (0.5 * rng.standard_normal(d)).astype(np.float32) if bias else None
     ref_in = [_f64(acts[0]), _f64(acts[1]), a, _f64(acts[2]), _f64(acts[3])]
+    if bias:
+        ref_in[1] = ref_in[1] + dt_bias.astype(np.float64)
     y_ref, _, _ = oracle.scan_gated_fwd(*ref_in, LO, HI)
-    g_ref = oracle.scan_gated_bwd(*ref_in, LO, HI, _f64(dyb))
+    g_ref = list(oracle.scan_gated_bwd(*ref_in, LO, HI, _f64(dyb)))
 
     leaves = [acts[0].to(DEV), acts[1].to(DEV), torch.from_numpy(a).to(DEV), acts[2].to(DEV),
               acts[3].to(DEV)]
     leaves = [t.requires_grad_(True) for t in leaves]
+    names = ["dx", "ddt_raw", "dA", "dB", "dC"]
+    tb = None
+    if bias:
+        tb = torch.from_numpy(dt_bias).to(DEV).requires_grad_(True)
+        leaves.append(tb)
+        names.append("dbias")
+        g_ref.append(np.asarray(g_ref[1]).sum(axis=(0, 1)))
     _native.set_time_segments(segs)
     try:
-        y = selective_scan_gated(*leaves, LO, HI, chunk=16)
+        y = selective_scan_gated(*leaves[:5], LO, HI, chunk=16, dt_bias=tb)
         grads = torch.autograd.grad(y, leaves, dyb.to(DEV))
         torch.cuda.synchronize()
     finally:
         _native.set_time_segments(0)
     assert_close("y", y, y_ref, TOL_BF16)
-    for name, g, r in zip(("dx", "ddt_raw", "dA", "dB", "dC"), grads, g_ref):
-        assert_close(name, g, r, TOL_F32 if name == "dA" else TOL_BF16)
+    for name, g, r in zip(names, grads, g_ref):
+        assert_close(name, g, r, TOL_F32 if name in ("dA", "dbias") else TOL_BF16)
 
 
 def test_bf16_matches_fp32_kernels_on_the_same_values():

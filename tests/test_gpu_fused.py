@@ -106,6 +106,15 @@ def test_gated_scan_with_dt_bias_matches_the_oracle(bt, t_len, d, n, chunk):
     assert torch.equal(runs[0][1][5], runs[1][1][5])
 
 
+def test_gated_scan_rejects_a_bad_dt_bias():
+    arrs = [torch.from_numpy(a).to(DEV) for a in _gated_inputs(1, 8, 32, 16, seed=1)]
+    with pytest.raises(ValueError, match="dt_bias"):
+        selective_scan_gated(*arrs, LO, HI, dt_bias=torch.zeros(31, device=DEV))
+    with pytest.raises(ValueError, match="dt_bias"):
+        selective_scan_gated(*arrs, LO, HI, dt_bias=torch.zeros(32, device=DEV,
+                                                                 dtype=torch.float64))
+
+
 def test_gated_scan_equals_the_scan_on_torch_gated_inputs():
     """Gate fused in the kernels == the framework's gate followed by the plain
     HIP scan, values and gradients (within fp32 rounding of dt)."""
