@@ -98,6 +98,20 @@ def settle_clocks(fn, ms: float = SETTLE_MS) -> int:
     return calls
 
 
+def copy_bandwidth(nbytes: int = 256 << 20) -> dict:
+    """A device-to-device copy of nbytes (read + write: 2 nbytes of traffic),
+    timed with HIP events after a clock settle: the practical HBM rate next to
+    the 8 TB/s spec. The copy is large enough that its kernel, not the host's
+    per-call cost, sets the pace."""
+    import torch
+    src = torch.empty(nbytes // 4, device="cuda")
+    dst = torch.empty_like(src)
+    settle_clocks(lambda: dst.copy_(src), ms=30.0)
+    ms = time_events(lambda: dst.copy_(src), 50)
+    del src, dst
+    return {"bytes": 2 * nbytes, "avg_ms": ms, "GBs": 2 * nbytes / (ms * 1e-3) / 1e9}
+
+
 def time_events(fn, reps: int) -> float:
     """Average GPU duration (ms) of fn() over reps, HIP events on the current stream."""
     import torch
@@ -111,19 +125,27 @@ def time_events(fn, reps: int) -> float:
     return sum(s.elapsed_time(e) for s, e in zip(start, stop)) / reps
 
 
-def cpu_baseline_scan(bt, t_len, d, n) -> dict:
-    """selective_scan(impl='torch') fwd+bwd on the CPU, full workload, one rep."""
+def cpu_baseline_scan(bt, t_len, d, n, reps: int = 3) -> dict:
+    """selective_scan(impl='torch') fwd+bwd on the CPU, full workload: one
+    warm-up, then the median of `reps` timed reps."""
+    import statistics
     import torch
     from mamba_metal_scan_amd import selective_scan
     threads = cpu_threads()
     torch.set_num_threads(threads)
     x, dt, aneg, b_in, c_in, dy = make_inputs(bt, t_len, d, n)
-    leaves = [t.clone().requires_grad_(True) for t in (x, dt, aneg, b_in, c_in)]
-    try:
+
+    def one() -> float:
+        leaves = [t.clone().requires_grad_(True) for t in (x, dt, aneg, b_in, c_in)]
         t0 = time.perf_counter()
         y = selective_scan(*leaves, impl="torch")
         y.backward(dy)
-        el = time.perf_counter() - t0
+        return time.perf_counter() - t0
+
+    try:
+        one()
+        times = [one() for _ in range(reps)]
+        el = statistics.median(times)
     except (RuntimeError, MemoryError) as exc:   # e.g. out of host memory
         return {"value": None, "unit": "tokens/s", "cores": threads, "kind": "port",
                 "sample": f"selective_scan(impl='torch') fwd+bwd {bt}x{t_len}x{d}x{n}: "
@@ -138,8 +160,10 @@ def cpu_baseline_scan(bt, t_len, d, n) -> dict:
         pass
     return {"value": bt * t_len / el, "unit": "tokens/s", "cores": threads, "kind": "port",
             "ms_per_step": el * 1e3, "cpu": cpu_model,
+            "rep_ms": [round(t * 1e3, 1) for t in times],
             "sample": f"selective_scan(impl='torch') fwd+bwd, full {bt}x{t_len}x{d}x{n} "
-                      f"workload, 1 rep, torch CPU threads={threads}"}
+                      f"workload, 1 warm-up + median of {reps} reps, torch CPU "
+                      f"threads={threads}"}
 
 
 def run_launches(args) -> None:
@@ -565,6 +589,7 @@ def bench_scan(args) -> dict:
         "library_version": hex(_native.library().mhs_version()),
         "clock_settle": {"ms": SETTLE_MS, "steps": settled,
                          "note": "untimed steps before the warmup, until the GPU clock is steady"},
+        "hbm_copy": copy_bandwidth(),
     }
     if not args.no_train:
         out["train_80m"] = bench_train()
