@@ -145,8 +145,12 @@ def num_chunks(seqlen: int, chunk: int) -> int:
     return (seqlen + chunk - 1) // chunk
 
 
+@torch.compiler.assume_constant_result
 def preferred_chunk(d_state: int) -> int:
-    """Largest checkpoint stride the backward kernel walks without recomputing."""
+    """Largest checkpoint stride the backward kernel walks without recomputing
+    (0: d_state unsupported). A constant for a given d_state and variant
+    setting, so torch.compile evaluates it once while tracing instead of
+    tracing the library call."""
     return int(library().mhs_preferred_chunk(d_state))
 
 
