@@ -172,3 +172,76 @@ def test_compiled_tinymamba_train_step_matches_eager():
     assert_close("loss", l1, l2, 1e-6)
     for (name, _), a, b in zip(model.named_parameters(), g1, g2):
         assert_close(name, a, b, 1e-5)
+
+
+def _capture(fn):
+    """fn() warmed up on a side stream, then captured in a HIP graph; returns
+    (graph, the captured outputs)."""
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        fn()
+    torch.cuda.current_stream().wait_stream(side)
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        outs = fn()
+    return graph, outs
+
+
+@pytest.mark.parametrize("shape", [(4, 256, 512, 16), (1, 1024, 128, 16)])
+def test_scan_fwd_bwd_replays_from_a_hip_graph(shape):
+    """Forward + backward launches captured once and replayed three times,
+    with other eager scans and synchronizations between the replays: every
+    replay equals the eager result bit for bit. The second shape is small
+    enough to run in time segments (forward workspace, carry kernels)."""
+    bt, t_len, d, n = shape
+    print(f"[case] HIP graph scan fwd+bwd {shape}", flush=True)
+    x, dt, aneg, b_in, c_in, dy = _scan_args(bt, t_len, d, n, seed=7)
+
+    def step(x=x):
+        y, ckpt, h_last = OPS.scan_fwd(x, dt, aneg, b_in, c_in, 16, True)
+        return (y, h_last) + tuple(OPS.scan_bwd(x, dt, aneg, b_in, c_in, dy, None, ckpt, 16))
+
+    ref = [t.clone() for t in step()]
+    graph, outs = _capture(step)
+    for rep in range(3):
+        other = step(x * (0.5 + rep))     # eager work on other inputs between replays
+        torch.cuda.synchronize()
+        graph.replay()
+        torch.cuda.synchronize()
+        for name, a, b in zip(("y", "h_last", "dx", "ddt", "dAneg", "dB", "dC"), outs, ref):
+            assert torch.equal(a, b), f"replay {rep}: {name} differs"
+        del other
+
+
+def test_inner_block_fwd_bwd_replays_from_a_hip_graph():
+    """The fused inner block's forward and autograd backward (conv, GEMMs,
+    gated scan with its bias, output gate) captured and replayed."""
+    print("[case] HIP graph mamba_inner fwd+bwd", flush=True)
+    bt, t_len, d, n = 4, 128, 256, 16
+    g = _gen(8)
+    params = [torch.randn(bt, t_len, 2 * d, generator=g), 0.3 * torch.randn(d, 1, 4, generator=g),
+              0.1 * torch.randn(d, generator=g), 0.05 * torch.randn(d, d, generator=g),
+              0.5 * torch.randn(d, generator=g), 0.1 * torch.randn(n, d, generator=g),
+              0.1 * torch.randn(n, d, generator=g),
+              torch.log(torch.arange(1, n + 1, dtype=torch.float32)).expand(d, n).contiguous(),
+              torch.randn(d, generator=g)]
+    dout = torch.randn(bt, t_len, d, generator=g).to(DEV)
+
+    def step(leaves):
+        out = mamba_inner(*leaves, 0.001, 0.1, chunk=16)
+        return (out,) + tuple(torch.autograd.grad(out, leaves, dout))
+
+    # The eager runs use their own leaf tensors: the captured leaves' autograd
+    # nodes then belong to the capture's streams only.
+    eager = [p.to(DEV).requires_grad_(True) for p in params]
+    leaves = [p.to(DEV).requires_grad_(True) for p in params]
+    ref = [t.detach().clone() for t in step(eager)]
+    graph, outs = _capture(lambda: step(leaves))
+    for rep in range(3):
+        step(eager)                       # eager work between replays
+        torch.cuda.synchronize()
+        graph.replay()
+        torch.cuda.synchronize()
+        for i, (a, b) in enumerate(zip(outs, ref)):
+            assert torch.equal(a, b), f"replay {rep}: output {i} differs"
