@@ -1,8 +1,8 @@
 /*
  * scan_oracle.c -- TEST INFRASTRUCTURE ONLY: a plain-C, float64 restatement of
  * the reference's selective scan, used as the checker for the gfx950 kernels.
- * Only tests/, __graft_entry__.smoke() and bench.py's cpu_baseline leg may
- * load it; the product path never does.
+ * Only tests/ and __graft_entry__.smoke() load it; the product path never
+ * does.
  *
  * Follows mamba_metal/scan.py of the reference:
  *   forward  -- the recurrence of scan.py:13-15 (and README.md:35-39), with
