@@ -125,30 +125,39 @@ def time_events(fn, reps: int) -> float:
     return sum(s.elapsed_time(e) for s, e in zip(start, stop)) / reps
 
 
-def cpu_baseline_scan(bt, t_len, d, n, reps: int = 3) -> dict:
-    """selective_scan(impl='torch') fwd+bwd on the CPU, full workload: one
-    warm-up, then the median of `reps` timed reps."""
+def cpu_baseline_scan(bt, t_len, d, n, reps: int = 3, warmup: int = 1, grad: bool = True,
+                      what: str = "the full workload") -> dict:
+    """selective_scan(impl='torch') on the host CPU: fwd+bwd (grad) or the
+    forward under no_grad, on a (bt, t_len, d, n) workload; `warmup` untimed
+    reps, then the median of `reps` timed ones. `what` says how the shape
+    relates to the benchmarked workload."""
     import statistics
     import torch
     from mamba_metal_scan_amd import selective_scan
     threads = cpu_threads()
     torch.set_num_threads(threads)
     x, dt, aneg, b_in, c_in, dy = make_inputs(bt, t_len, d, n)
+    kind = "fwd+bwd" if grad else "fwd (no_grad)"
 
     def one() -> float:
-        leaves = [t.clone().requires_grad_(True) for t in (x, dt, aneg, b_in, c_in)]
+        leaves = [t.clone().requires_grad_(grad) for t in (x, dt, aneg, b_in, c_in)]
         t0 = time.perf_counter()
-        y = selective_scan(*leaves, impl="torch")
-        y.backward(dy)
+        if grad:
+            y = selective_scan(*leaves, impl="torch")
+            y.backward(dy)
+        else:
+            with torch.no_grad():
+                selective_scan(*leaves, impl="torch")
         return time.perf_counter() - t0
 
     try:
-        one()
+        for _ in range(warmup):
+            one()
         times = [one() for _ in range(reps)]
         el = statistics.median(times)
     except (RuntimeError, MemoryError) as exc:   # e.g. out of host memory
         return {"value": None, "unit": "tokens/s", "cores": threads, "kind": "port",
-                "sample": f"selective_scan(impl='torch') fwd+bwd {bt}x{t_len}x{d}x{n}: "
+                "sample": f"selective_scan(impl='torch') {kind} {bt}x{t_len}x{d}x{n}: "
                           f"failed ({type(exc).__name__})"}
     cpu_model = ""
     try:
@@ -161,9 +170,8 @@ def cpu_baseline_scan(bt, t_len, d, n, reps: int = 3) -> dict:
     return {"value": bt * t_len / el, "unit": "tokens/s", "cores": threads, "kind": "port",
             "ms_per_step": el * 1e3, "cpu": cpu_model,
             "rep_ms": [round(t * 1e3, 1) for t in times],
-            "sample": f"selective_scan(impl='torch') fwd+bwd, full {bt}x{t_len}x{d}x{n} "
-                      f"workload, 1 warm-up + median of {reps} reps, torch CPU "
-                      f"threads={threads}"}
+            "sample": f"selective_scan(impl='torch') {kind} on {bt}x{t_len}x{d}x{n} ({what}), "
+                      f"{warmup} warm-up + median of {reps} reps, torch CPU threads={threads}"}
 
 
 def run_launches(args) -> None:
@@ -438,12 +446,17 @@ def bench_longt(args) -> dict:
         print(f"longt chunk {chunk}: fwd {f_ms:.3f} ms bwd {b_ms:.3f} ms", file=sys.stderr,
               flush=True)
     best = min(rows, key=lambda r: r["fwd_bwd_ms"])
+    # The CPU path on the first 1024 of the 16384 steps (the full sequence
+    # would take minutes): the same per-token work.
+    cpu = cpu_baseline_scan(bt, 1024, d, n, reps=1, warmup=0,
+                            what=f"the first 1024 of the workload's {t_len} steps")
     return {"metric": "long-sequence scan fwd+bwd GB/s (4x16384x2048x16 fp32)",
             "value": best["fwd_bwd_GBs"], "unit": "GB/s", "n_gpus": 1,
             "ms_per_step": best["fwd_bwd_ms"], "higher_is_better": True, "dtype": "f32",
             "data": "synthetic", "algorithmic_bytes": nbytes["fwd_bwd"],
             "config": {"workload": "selective_scan fwd+bwd 4x16384x2048x16, stride sweep"},
-            "strides": rows}
+            "strides": rows, "gpu_tokens_per_s": bt * t_len / (best["fwd_bwd_ms"] * 1e-3),
+            "cpu_baseline": cpu}
 
 
 def bench_infer(args) -> dict:
@@ -497,13 +510,15 @@ def bench_infer(args) -> dict:
     torch.cuda.synchronize()
     graph_us = start.elapsed_time(stop) * 1e3 / (3 * steps)
     s_bytes = 4 * (2 * bt * d * n + 3 * bt * d + 2 * bt * n + d * n)
+    cpu = cpu_baseline_scan(bt, t_len, d, n, reps=1, warmup=0, grad=False)
     return {"metric": "prefill GB/s and decode us/step (32x2048x4096x16 fp32)",
             "value": p_bytes / (p_ms * 1e-3) / 1e9, "unit": "GB/s", "n_gpus": 1,
             "ms_per_step": p_ms, "higher_is_better": True, "dtype": "f32", "data": "synthetic",
             "config": {"workload": "prefill 32x2048x4096x16 + 256 decode steps"},
             "decode_us_per_step": graph_us, "decode_GBs": s_bytes / (graph_us * 1e-6) / 1e9,
             "decode_us_per_step_eager": eager_us,
-            "prefill_algorithmic_bytes": p_bytes, "decode_algorithmic_bytes": s_bytes}
+            "prefill_algorithmic_bytes": p_bytes, "decode_algorithmic_bytes": s_bytes,
+            "prefill_tokens_per_s": bt * t_len / (p_ms * 1e-3), "cpu_baseline": cpu}
 
 
 def bench_scan(args) -> dict:
