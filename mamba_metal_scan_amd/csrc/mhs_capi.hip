@@ -32,7 +32,7 @@ MHS_FOR_PLANS(MHS_BWD_INST, extern, 2)
 
 namespace {
 
-constexpr int kVersion = (0 << 16) | (1 << 8) | 0;
+constexpr int kVersion = (0 << 16) | (2 << 8) | 0;   // 0.2: gated row strides and dt bias
 
 thread_local char g_err[512] = "";
 
