@@ -343,11 +343,15 @@ TRAIN_GROUPS = (  # (label, substrings of the kernel name), first match wins
 def trace_summary(args) -> None:
     """Per-step kernel time of the train step from a rocprofv3 --kernel-trace
     --stats run under args.trace_summary (kt/run_kernel_stats.csv), grouped
-    by kind; the run covered args.warmup + args.steps steps. Writes the
+    by kind; the run covered args.warmup + args.steps steps. For the longt
+    and infer workloads, the per-kernel table of such a run. Writes the
     markdown under profiles/ and prints it."""
     import csv
     stats = os.path.join(args.trace_summary, "kt", "run_kernel_stats.csv")
     rows = list(csv.DictReader(open(stats)))
+    if args.workload in ("longt", "infer"):
+        workload_trace_summary(args, rows)
+        return
     n = args.warmup + args.steps
     per = lambda r: float(r["TotalDurationNs"]) / n / 1e3   # us per step
     groups: dict = {}
@@ -371,6 +375,35 @@ def trace_summary(args) -> None:
     for r in sorted(rows, key=lambda r: -float(r["TotalDurationNs"]))[:16]:
         lines.append(f"| `{r['Name'][:72]}` | {int(r['Calls']) / n:g} | {per(r):.0f} |")
     md = ROOT / "profiles" / "train_80m_16x512.md"
+    md.write_text("\n".join(lines) + "\n")
+    print("\n".join(lines))
+    print(f"\nwrote {md.relative_to(ROOT)}")
+
+
+def workload_trace_summary(args, rows) -> None:
+    """Markdown of a kernel-trace run of --workload longt (at the strides of
+    args.strides) or --workload infer: every kernel with its calls and
+    durations."""
+    if args.workload == "longt":
+        title = f"Long-sequence scan 4x16384x2048x16 fwd+bwd, stride {args.strides}"
+        run = f"python3 bench.py --workload longt --strides {args.strides}"
+        md = ROOT / "profiles" / f"longt_4x16384x2048x16_stride{args.strides.replace(',', '_')}.md"
+    else:
+        title = "Prefill 32x2048x4096x16 (forward + final state) and 256 decode steps"
+        run = "python3 bench.py --workload infer"
+        md = ROOT / "profiles" / "infer_32x2048x4096x16.md"
+    lines = [f"# {title}: kernel time", "",
+             "All commands run from /tmp with `TMPDIR=/tmp`; OUT is the output folder.", "",
+             "    rocprofv3 --kernel-trace --stats -d OUT/kt -o run --output-format csv -- \\",
+             f"        {run}",
+             f"    python3 bench.py --trace-summary OUT --workload {args.workload}"
+             + (f" --strides {args.strides}" if args.workload == "longt" else ""), "",
+             "The calls include bench.py's untimed clock-settle calls and the warm-up "
+             "before each timing.", "",
+             "| kernel | calls | avg us | min us | max us |", "|---|---|---|---|---|"]
+    for r in sorted(rows, key=lambda r: -float(r["TotalDurationNs"])):
+        lines.append(f"| `{r['Name'][:72]}` | {r['Calls']} | {float(r['AverageNs']) / 1e3:.1f} "
+                     f"| {float(r['MinNs']) / 1e3:.1f} | {float(r['MaxNs']) / 1e3:.1f} |")
     md.write_text("\n".join(lines) + "\n")
     print("\n".join(lines))
     print(f"\nwrote {md.relative_to(ROOT)}")
@@ -433,7 +466,7 @@ def bench_longt(args) -> dict:
     x, dt, aneg, b_in, c_in, dy = (t.to(dev) for t in make_inputs(bt, t_len, d, n))
     nbytes = scan_bytes(bt, t_len, d, n)
     rows = []
-    for chunk in (16, 32, 64, 128):
+    for chunk in (int(v) for v in args.strides.split(",")):
         fwd = lambda: torch.ops.mamba_hip.scan_fwd(x, dt, aneg, b_in, c_in, chunk, True)
         _, ckpt, _ = fwd()
         bwd = lambda: torch.ops.mamba_hip.scan_bwd(x, dt, aneg, b_in, c_in, dy, None, ckpt, chunk)
@@ -631,6 +664,8 @@ def main() -> int:
                     help="profiling driver: only N scan_fwd/scan_bwd launches + N copies")
     ap.add_argument("--pmc-summary", default=None, metavar="DIR",
                     help="summarise rocprofv3 FETCH_SIZE / WRITE_SIZE passes under DIR")
+    ap.add_argument("--strides", default="16,32,64,128",
+                    help="checkpoint strides of --workload longt (comma-separated)")
     ap.add_argument("--trace-summary", default=None, metavar="DIR",
                     help="summarise a kernel-trace run of --workload train under DIR")
     args = ap.parse_args()
