@@ -1,0 +1,43 @@
+"""bench.py's contract on the CPU: the one-GPU rule, the failure without a GPU,
+and the algorithmic byte counts its roofline figures divide by."""
+from __future__ import annotations
+
+import subprocess
+import sys
+from pathlib import Path
+
+import torch
+
+ROOT = Path(__file__).resolve().parents[1]
+sys.path.insert(0, str(ROOT))
+import bench  # noqa: E402
+
+
+def _run(*args):
+    return subprocess.run([sys.executable, str(ROOT / "bench.py"), *args], capture_output=True,
+                          text=True, timeout=300)
+
+
+def test_more_than_one_gpu_exits_with_a_message():
+    r = _run("--gpus", "2")
+    assert r.returncode != 0
+    assert "single MI355X" in r.stderr and "--gpus 2" in r.stderr
+    assert r.stdout.strip() == ""            # no JSON line
+
+
+def test_without_a_gpu_it_fails_cleanly():
+    if torch.cuda.is_available():
+        return
+    r = _run("--steps", "1", "--warmup", "0")
+    assert r.returncode == 1 and "needs a ROCm GPU" in r.stderr
+
+
+def test_algorithmic_bytes():
+    """fwd = 4(3E + 2S + A), bwd = 4(5E + 4S + 2A) with E = B T D, S = B T N,
+    A = D N: 406,093,824 B for the fwd+bwd pair at 16x512x1536x16 (50.76 us at
+    8 TB/s), and 378.8 MB per layer at the 80M model's d_inner of 1432."""
+    b = bench.scan_bytes(16, 512, 1536, 16)
+    assert b["fwd_bwd"] == 406_093_824 == b["fwd"] + b["bwd"]
+    assert b["fwd"] == 4 * (3 * 12_582_912 + 2 * 131_072 + 24_576)
+    assert abs(b["fwd_bwd"] / 8e12 * 1e6 - 50.76) < 0.01
+    assert round(bench.scan_bytes(16, 512, 1432, 16)["fwd_bwd"] / 1e6, 1) == 378.8
