@@ -23,7 +23,7 @@ from oracle import oracle
 pytestmark = pytest.mark.gpu
 DEV = "cuda"
 LO, HI = 0.001, 0.1
-NCASES = 24
+NCASES = 40
 
 
 def _case(i):
