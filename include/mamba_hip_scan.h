@@ -77,6 +77,15 @@ int mhs_set_variant(int states_per_lane);
  * channel's whole sequence in one thread, scan.py:78-127, :132-261). */
 int mhs_set_time_segments(int segments);
 
+/* The compute-unit count the automatic time-segment choice plans for: the
+ * current device's (hipDeviceAttributeMultiprocessorCount, queried once per
+ * device; 256, MI355X's count, when no device can be queried), unless forced.
+ * mhs_set_cu_count forces it process-wide (1..65536; 0 restores the query),
+ * for tests and tuning; like the other knobs it is read when a call is made,
+ * and the workspace sizes depend on it. No counterpart in the reference. */
+int mhs_set_cu_count(int cus);
+int mhs_cu_count(void);
+
 /*
  * Forward scan. Replaces the reference's `lib.ssm_fwd(x, dt, Aneg, Bm, Cm, y,
  * ckpt, Bt, T, D, Kc)` launch (mamba_metal/scan.py:78-127, launched at :377-378).

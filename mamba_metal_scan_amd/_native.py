@@ -31,6 +31,7 @@ EXPORTED_SYMBOLS = (
     "mhs_out_gate_bwd_workspace_bytes", "mhs_out_gate_bwd_f32", "mhs_set_time_segments",
     "mhs_scan_fwd_workspace_bytes", "mhs_scan_fwd_ws_f32", "mhs_scan_fwd_bf16",
     "mhs_scan_bwd_bf16", "mhs_scan_gated_fwd_bf16", "mhs_scan_gated_bwd_bf16",
+    "mhs_set_cu_count", "mhs_cu_count",
 )
 
 _lib: Optional[ctypes.CDLL] = None
@@ -69,6 +70,10 @@ def library() -> ctypes.CDLL:
             lib.mhs_set_variant.argtypes = [ctypes.c_int]
             lib.mhs_set_time_segments.restype = ctypes.c_int
             lib.mhs_set_time_segments.argtypes = [ctypes.c_int]
+            lib.mhs_set_cu_count.restype = ctypes.c_int
+            lib.mhs_set_cu_count.argtypes = [ctypes.c_int]
+            lib.mhs_cu_count.restype = ctypes.c_int
+            lib.mhs_cu_count.argtypes = []
             lib.mhs_scan_fwd_f32.restype = ctypes.c_int
             lib.mhs_scan_fwd_f32.argtypes = [_P] * 8 + [_I64] * 5 + [_P]
             lib.mhs_scan_fwd_workspace_bytes.restype = ctypes.c_size_t
@@ -162,6 +167,12 @@ def set_variant(states_per_lane: int) -> None:
 def set_time_segments(segments: int) -> None:
     """Force the backward's number of time segments (1..8; 0 = automatic), process-wide."""
     _check(library().mhs_set_time_segments(int(segments)), "mhs_set_time_segments")
+
+
+def set_cu_count(cus: int) -> None:
+    """Force the compute-unit count the automatic time-segment split plans for
+    (0 = query the current device), process-wide."""
+    _check(library().mhs_set_cu_count(int(cus)), "mhs_set_cu_count")
 
 
 # --------------------------------------------------------------- custom ops

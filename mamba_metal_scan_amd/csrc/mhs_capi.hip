@@ -57,9 +57,39 @@ std::atomic<int> g_npl_override{0};
 // Forced number of backward time segments (0 = automatic); see mhs_set_time_segments.
 std::atomic<int> g_seg_override{0};
 
-constexpr int kCUs = 256;        // MI355X compute units
+constexpr int kDefaultCUs = 256; // MI355X compute units (used when no device can be queried)
+constexpr int kMaxDevices = 64;
 constexpr int kMaxSegments = 8;
 constexpr int kMinSegChunks = 8; // automatic split: at least 8 chunks per segment
+
+// Forced compute-unit count (0 = query the device); see mhs_set_cu_count.
+std::atomic<int> g_cu_override{0};
+std::atomic<int> g_cu_cache[kMaxDevices];   // per device, 0 until queried
+
+// Compute units of the current device, queried once per device and cached
+// (a partitioned MI355X exposes fewer than 256). Without a usable device the
+// MI355X count, so that the host-side size queries still answer.
+int device_cus() {
+  const int forced = g_cu_override.load(std::memory_order_relaxed);
+  if (forced > 0) return forced;
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess) {
+    (void)hipGetLastError();
+    return kDefaultCUs;
+  }
+  if (dev >= 0 && dev < kMaxDevices) {
+    const int cached = g_cu_cache[dev].load(std::memory_order_relaxed);
+    if (cached > 0) return cached;
+  }
+  int n = 0;
+  if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
+      n <= 0) {
+    (void)hipGetLastError();
+    n = kDefaultCUs;
+  }
+  if (dev >= 0 && dev < kMaxDevices) g_cu_cache[dev].store(n, std::memory_order_relaxed);
+  return n;
+}
 
 // Time segments of the backward for this shape (see BwdArgs in mhs_bwd.hpp).
 // Automatic: one segment while the grid has at least two blocks per CU;
@@ -70,8 +100,9 @@ void segments_for(int64_t batch, int64_t D, int nch, int& nseg, int& cps) {
   int want = g_seg_override.load(std::memory_order_relaxed);
   if (want == 0) {
     want = 1;
-    if (blocks < 2 * kCUs) {
-      want = (int)std::min<int64_t>(kMaxSegments, (3 * kCUs + blocks - 1) / blocks);
+    const int cus = device_cus();
+    if (blocks < 2 * (int64_t)cus) {
+      want = (int)std::min<int64_t>(kMaxSegments, (3 * (int64_t)cus + blocks - 1) / blocks);
       want = std::max(1, std::min(want, nch / kMinSegChunks));
     }
   }
@@ -534,6 +565,16 @@ int mhs_set_time_segments(int segments) {
   g_seg_override.store(segments, std::memory_order_relaxed);
   return MHS_OK;
 }
+
+int mhs_set_cu_count(int cus) {
+  if (cus < 0 || cus > 65536)
+    return fail(MHS_EINVAL, "compute-unit count must be 0 (query the device) .. 65536; got %d",
+                cus);
+  g_cu_override.store(cus, std::memory_order_relaxed);
+  return MHS_OK;
+}
+
+int mhs_cu_count(void) { return device_cus(); }
 
 int64_t mhs_preferred_chunk(int64_t d_state) {
   Plan p;

@@ -238,3 +238,28 @@ def test_conv_argument_errors():
     rc = lib.mhs_conv1d_silu_bwd_f32(A16, 64, A16, A16, A16, A16, 31, A16, A16, A16, need,
                                      2, 8, 32, 4, None)
     assert rc == MHS_EINVAL and "dx row stride" in _err(lib)
+
+
+def test_segment_split_follows_the_compute_unit_count():
+    """The automatic split plans for the device's compute units: 256 blocks
+    (4 x 16384 x 2048 x 16) get three segments at 256 CUs, one at 128 (two
+    blocks per CU already) and eight (the maximum) at 1024; the forward's
+    workspace follows. Without a device the count is MI355X's 256."""
+    lib = _native.library()
+    assert lib.mhs_cu_count() == 256
+    ru = lambda v: (v + 255) // 256 * 256
+    fwd_ws = lambda segs: ru(segs * 4 * 2048 * 16 * 4) + ru(segs * 4 * 2048 * 4)
+    shape = (4, 16384, 2048, 16)
+    try:
+        _native.set_cu_count(128)
+        assert lib.mhs_cu_count() == 128
+        assert lib.mhs_scan_fwd_workspace_bytes(*shape) == 0
+        _native.set_cu_count(1024)
+        assert lib.mhs_scan_fwd_workspace_bytes(*shape) == fwd_ws(8)
+        _native.set_cu_count(256)
+        assert lib.mhs_scan_fwd_workspace_bytes(*shape) == fwd_ws(3)
+        with pytest.raises(_native.HipScanError, match="compute-unit count"):
+            _native.set_cu_count(-1)
+    finally:
+        _native.set_cu_count(0)
+    assert lib.mhs_cu_count() == 256
