@@ -21,7 +21,8 @@
  * `stream` (a hipStream_t; NULL = the legacy default stream). Functions return 0
  * or an MHS_E* code; mhs_last_error() gives a message for the calling thread.
  * Entry points may be called concurrently from several threads / streams: no
- * buffer is shared between calls.
+ * buffer is shared between calls (except the static scratch of
+ * mhs_scan_fwd_noalloc_f32, see there).
  */
 #ifndef MAMBA_HIP_SCAN_H
 #define MAMBA_HIP_SCAN_H
@@ -123,6 +124,31 @@ int mhs_scan_fwd_ws_f32(const float* x, const float* dt, const float* aneg,
                         void* workspace, size_t workspace_bytes,
                         int64_t batch, int64_t seqlen, int64_t d_inner, int64_t d_state,
                         int64_t chunk, void* stream);
+
+/*
+ * mhs_scan_fwd_ws_f32 without a workspace argument and without any
+ * allocation: the time segments' carries live in a static device array of
+ * MHS_NOALLOC_SCRATCH_BYTES (16 MiB) that every GPU the library runs on holds
+ * from module load until the process ends. No counterpart in the reference:
+ * it is for callers that cannot allocate device memory (code under HIP graph
+ * capture, tight serving loops, harnesses that forbid hipMalloc). It calls no
+ * hipMalloc / hipFree. Same arguments (minus the workspace), outputs and
+ * kernels as mhs_scan_fwd_ws_f32. Shapes whose carries need more than the
+ * static scratch (mhs_scan_fwd_workspace_bytes > MHS_NOALLOC_SCRATCH_BYTES)
+ * fail with MHS_EINVAL before any launch; on MI355X (256 CUs) no automatic
+ * split needs more than 8.5 MB (d_state 64); forced splits may. The stream
+ * (if not NULL) must belong to the current device. All calls on one GPU
+ * share its scratch, which keeps the last call's contents (each call writes
+ * every slot it reads first, so nothing needs clearing): calls that overlap
+ * in time on one GPU (concurrent streams) race and give wrong results;
+ * serialize them.
+ */
+#define MHS_NOALLOC_SCRATCH_BYTES 16777216u
+int mhs_scan_fwd_noalloc_f32(const float* x, const float* dt, const float* aneg,
+                             const float* B, const float* C,
+                             float* y, float* ckpt, float* h_last,
+                             int64_t batch, int64_t seqlen, int64_t d_inner, int64_t d_state,
+                             int64_t chunk, void* stream);
 
 /* Bytes of device workspace mhs_scan_bwd_f32 needs for this shape. */
 size_t mhs_scan_bwd_workspace_bytes(int64_t batch, int64_t seqlen, int64_t d_inner,

@@ -31,8 +31,12 @@ EXPORTED_SYMBOLS = (
     "mhs_out_gate_bwd_workspace_bytes", "mhs_out_gate_bwd_f32", "mhs_set_time_segments",
     "mhs_scan_fwd_workspace_bytes", "mhs_scan_fwd_ws_f32", "mhs_scan_fwd_bf16",
     "mhs_scan_bwd_bf16", "mhs_scan_gated_fwd_bf16", "mhs_scan_gated_bwd_bf16",
-    "mhs_set_cu_count", "mhs_cu_count",
+    "mhs_set_cu_count", "mhs_cu_count", "mhs_scan_fwd_noalloc_f32",
 )
+
+# Size of the static device scratch of mhs_scan_fwd_noalloc_f32 (the header's
+# MHS_NOALLOC_SCRATCH_BYTES).
+NOALLOC_SCRATCH_BYTES = 16 << 20
 
 _lib: Optional[ctypes.CDLL] = None
 _lock = threading.Lock()
@@ -76,6 +80,8 @@ def library() -> ctypes.CDLL:
             lib.mhs_cu_count.argtypes = []
             lib.mhs_scan_fwd_f32.restype = ctypes.c_int
             lib.mhs_scan_fwd_f32.argtypes = [_P] * 8 + [_I64] * 5 + [_P]
+            lib.mhs_scan_fwd_noalloc_f32.restype = ctypes.c_int
+            lib.mhs_scan_fwd_noalloc_f32.argtypes = [_P] * 8 + [_I64] * 5 + [_P]
             lib.mhs_scan_fwd_workspace_bytes.restype = ctypes.c_size_t
             lib.mhs_scan_fwd_workspace_bytes.argtypes = [_I64] * 4
             lib.mhs_scan_fwd_ws_f32.restype = ctypes.c_int

@@ -429,6 +429,52 @@ int scan_fwd(const void* x, const void* dt, const float* aneg, const void* B, co
   return check_launch("forward scan kernel");
 }
 
+}  // namespace
+
+// ------------------------------------------------- allocation-free forward
+//
+// The device scratch of mhs_scan_fwd_noalloc_f32: what mhs_scan_fwd_ws_f32's
+// workspace holds, the time segments' carried end states and dt sums. Every
+// GPU the library runs on holds its own copy from module load until the
+// process ends. In host code `scratch` names a host-side shadow, never device
+// memory: launches take the address hipGetSymbolAddress returns for the
+// current device (scratch_address), looked up once per device.
+static __device__ __align__(256) unsigned char scratch[MHS_NOALLOC_SCRATCH_BYTES];
+
+namespace {
+
+std::mutex g_scratch_mu;
+void* g_scratch_dev[kMaxDevices] = {};
+
+// The current device's copy of `scratch`; the stream (if not NULL) must
+// belong to that device.
+int scratch_address(void* stream, void** out) {
+  int dev = 0;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) return fail(MHS_EHIP, "hipGetDevice: %s", hipGetErrorString(e));
+  if (dev < 0 || dev >= kMaxDevices)
+    return fail(MHS_EINVAL, "device %d: at most %d devices are supported", dev, kMaxDevices);
+  if (stream != nullptr) {
+    hipDevice_t sdev = -1;
+    e = hipStreamGetDevice(static_cast<hipStream_t>(stream), &sdev);
+    if (e != hipSuccess) return fail(MHS_EHIP, "hipStreamGetDevice: %s", hipGetErrorString(e));
+    if (sdev != dev)
+      return fail(MHS_EINVAL, "the stream belongs to device %d but device %d is current", sdev,
+                  dev);
+  }
+  std::lock_guard<std::mutex> lk(g_scratch_mu);
+  if (g_scratch_dev[dev] == nullptr) {
+    void* p = nullptr;
+    e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (e != hipSuccess || p == nullptr)
+      return fail(MHS_EHIP, "hipGetSymbolAddress(scratch) on device %d: %s", dev,
+                  hipGetErrorString(e));
+    g_scratch_dev[dev] = p;
+  }
+  *out = g_scratch_dev[dev];
+  return MHS_OK;
+}
+
 int scan_bwd(const void* x, const void* dt, const float* aneg, const void* B, const void* C,
              const void* dy, const float* dh_last, const float* ckpt, void* dx, void* ddt,
              float* daneg, void* dB, void* dC, void* workspace, size_t workspace_bytes,
@@ -612,6 +658,30 @@ int mhs_scan_fwd_ws_f32(const float* x, const float* dt, const float* aneg, cons
   g_err[0] = '\0';
   return scan_fwd(x, dt, aneg, B, C, y, ckpt, h_last, workspace, workspace_bytes, batch, seqlen,
                   d_inner, d_state, chunk, stream, Gate{}, kF32);
+}
+
+int mhs_scan_fwd_noalloc_f32(const float* x, const float* dt, const float* aneg, const float* B,
+                             const float* C, float* y, float* ckpt, float* h_last, int64_t batch,
+                             int64_t seqlen, int64_t d_inner, int64_t d_state, int64_t chunk,
+                             void* stream) {
+  g_err[0] = '\0';
+  int rc = check_shape(batch, seqlen, d_inner, d_state, chunk);
+  if (rc) return rc;
+  const FwdWs w = fwd_ws_layout(batch, seqlen, d_inner, d_state);
+  if (w.total > (size_t)MHS_NOALLOC_SCRATCH_BYTES)
+    return fail(MHS_EINVAL, "the time segments of this shape need %zu bytes of scratch, more than "
+                "the %zu-byte static scratch of mhs_scan_fwd_noalloc_f32; call "
+                "mhs_scan_fwd_ws_f32 with a workspace", w.total,
+                (size_t)MHS_NOALLOC_SCRATCH_BYTES);
+  void* ws = nullptr;
+  if (w.total > 0) {
+    rc = scratch_address(stream, &ws);
+    if (rc) return rc;
+  }
+  // Every slot the segmented passes read is written by the carry pass of the
+  // same call first: nothing in the scratch needs clearing.
+  return scan_fwd(x, dt, aneg, B, C, y, ckpt, h_last, ws, w.total, batch, seqlen, d_inner,
+                  d_state, chunk, stream, Gate{}, kF32);
 }
 
 int mhs_scan_bwd_f32(const float* x, const float* dt, const float* aneg, const float* B,
