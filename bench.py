@@ -54,12 +54,39 @@ def scan_bytes(bt: int, t_len: int, d: int, n: int) -> dict:
             "fwd_bwd": 4 * (8 * e + 6 * s + 3 * a)}
 
 
-def cpu_threads() -> int:
+CPU_THREAD_CAP = 16   # the host CPU share of one GPU on the benchmark machines
+
+
+def affinity_cpus() -> int:
     try:
-        n = len(os.sched_getaffinity(0))
+        return len(os.sched_getaffinity(0))
     except AttributeError:
-        n = os.cpu_count() or 1
-    return max(1, min(n, 16))
+        return os.cpu_count() or 1
+
+
+def cpu_threads() -> int:
+    """Threads for the CPU baseline: the process's CPU affinity, at most the
+    host share of one GPU (CPU_THREAD_CAP; the affinity mask of a one-GPU job
+    can name every core of the host while its fair share is 16)."""
+    return max(1, min(affinity_cpus(), CPU_THREAD_CAP))
+
+
+def keep_heap() -> str:
+    """glibc: serve the CPU path's blocks from one heap (one arena, no mmap)
+    and never trim it, so that later reps reuse the pages the first one
+    faulted in instead of mapping and faulting fresh ones (mallopt
+    M_ARENA_MAX 1, M_MMAP_MAX 0, M_TRIM_THRESHOLD off). Measured: the reps
+    that hit millions of minor page faults took 4.6-5.5 s against 0.61 s for
+    those that did not. Returns what was set."""
+    import ctypes
+    try:
+        libc = ctypes.CDLL("libc.so.6")
+        m_trim_threshold, m_mmap_max, m_arena_max = -1, -4, -8
+        ok = (libc.mallopt(m_arena_max, 1) and libc.mallopt(m_mmap_max, 0)
+              and libc.mallopt(m_trim_threshold, -1))
+        return "glibc mallopt: one arena, no mmap, no trim" if ok else "glibc mallopt refused"
+    except OSError:
+        return "default allocator"
 
 
 def make_inputs(bt, t_len, d, n, seed=2024):
@@ -125,22 +152,26 @@ def time_events(fn, reps: int) -> float:
     return sum(s.elapsed_time(e) for s, e in zip(start, stop)) / reps
 
 
-def cpu_baseline_scan(bt, t_len, d, n, reps: int = 3, warmup: int = 1, grad: bool = True,
+def cpu_baseline_scan(bt, t_len, d, n, reps: int = 3, warmup: int = 2, grad: bool = True,
                       what: str = "the full workload") -> dict:
     """selective_scan(impl='torch') on the host CPU: fwd+bwd (grad) or the
     forward under no_grad, on a (bt, t_len, d, n) workload; `warmup` untimed
-    reps, then the median of `reps` timed ones. `what` says how the shape
-    relates to the benchmarked workload."""
+    reps, then `reps` timed ones (value: their median). Every rep's time and
+    minor page faults are reported. `what` says how the shape relates to the
+    benchmarked workload."""
+    import resource
     import statistics
     import torch
     from mamba_metal_scan_amd import selective_scan
     threads = cpu_threads()
     torch.set_num_threads(threads)
+    heap = keep_heap()
     x, dt, aneg, b_in, c_in, dy = make_inputs(bt, t_len, d, n)
     kind = "fwd+bwd" if grad else "fwd (no_grad)"
 
-    def one() -> float:
+    def one():
         leaves = [t.clone().requires_grad_(grad) for t in (x, dt, aneg, b_in, c_in)]
+        f0 = resource.getrusage(resource.RUSAGE_SELF).ru_minflt
         t0 = time.perf_counter()
         if grad:
             y = selective_scan(*leaves, impl="torch")
@@ -148,17 +179,18 @@ def cpu_baseline_scan(bt, t_len, d, n, reps: int = 3, warmup: int = 1, grad: boo
         else:
             with torch.no_grad():
                 selective_scan(*leaves, impl="torch")
-        return time.perf_counter() - t0
+        el = time.perf_counter() - t0
+        return el, resource.getrusage(resource.RUSAGE_SELF).ru_minflt - f0
 
     try:
-        for _ in range(warmup):
-            one()
-        times = [one() for _ in range(reps)]
-        el = statistics.median(times)
+        warm = [one() for _ in range(warmup)]
+        timed = [one() for _ in range(reps)]
     except (RuntimeError, MemoryError) as exc:   # e.g. out of host memory
         return {"value": None, "unit": "tokens/s", "cores": threads, "kind": "port",
                 "sample": f"selective_scan(impl='torch') {kind} {bt}x{t_len}x{d}x{n}: "
                           f"failed ({type(exc).__name__})"}
+    times = [t for t, _ in timed]
+    el = statistics.median(times)
     cpu_model = ""
     try:
         for line in open("/proc/cpuinfo"):
@@ -168,8 +200,12 @@ def cpu_baseline_scan(bt, t_len, d, n, reps: int = 3, warmup: int = 1, grad: boo
     except OSError:
         pass
     return {"value": bt * t_len / el, "unit": "tokens/s", "cores": threads, "kind": "port",
-            "ms_per_step": el * 1e3, "cpu": cpu_model,
+            "ms_per_step": el * 1e3, "min_ms": min(times) * 1e3, "cpu": cpu_model,
+            "affinity_cpus": affinity_cpus(), "thread_cap": CPU_THREAD_CAP, "heap": heap,
             "rep_ms": [round(t * 1e3, 1) for t in times],
+            "warmup_ms": [round(t * 1e3, 1) for t, _ in warm],
+            "rep_minor_faults": [f for _, f in timed],
+            "warmup_minor_faults": [f for _, f in warm],
             "sample": f"selective_scan(impl='torch') {kind} on {bt}x{t_len}x{d}x{n} ({what}), "
                       f"{warmup} warm-up + median of {reps} reps, torch CPU threads={threads}"}
 
@@ -209,15 +245,13 @@ ISSUE_COUNTERS = ("GRBM_GUI_ACTIVE SQ_WAVES SQ_ACTIVE_INST_VALU SQ_ACTIVE_INST_V
 N_XCD, N_CU = 8, 256   # MI355X: GRBM_GUI_ACTIVE is summed over its 8 XCDs
 
 
-def issue_counter_lines(mean: dict, extra: str) -> list:
+def issue_counter_lines(mean: dict) -> list:
     """Markdown for the third pmc pass: per scan kernel, its GPU-clock cycles
     and the shares of them the CUs spent issuing VALU instructions, with two
     VALU instructions issued together (a transcendental beside another), with
     resident waves, and stalled on LDS bank conflicts. SQ_* cycle counters
     are in quad-cycles summed over the SIMDs of each CU."""
     out = ["", "## Issue counters", "",
-           f"    rocprofv3 --pmc {ISSUE_COUNTERS} -d OUT/valu -o run --output-format csv -- "
-           f"python3 bench.py --launches 5 {extra}", "",
            f"Kernel cycles = GRBM_GUI_ACTIVE / {N_XCD} (the counter is summed over the XCDs). "
            f"VALU busy = SQ_ACTIVE_INST_VALU / ({N_CU} CUs x cycles); dual issue = "
            "SQ_ACTIVE_INST_VALU2 / SQ_ACTIVE_INST_VALU; resident waves per CU = "
@@ -237,92 +271,175 @@ def issue_counter_lines(mean: dict, extra: str) -> list:
     return out
 
 
-def pmc_summary(args) -> None:
-    """Per-launch HBM traffic from two rocprofv3 --pmc passes (FETCH_SIZE, then
-    WRITE_SIZE, KiB per dispatch) under args.pmc_summary, each scaled by what
-    the counter reads for the calibration copy of COPY_BYTES; writes the
-    traffic file bench.py reports from and prints a markdown table."""
+COUNTERS_NAME = "scan_{shape}_counters.json"
+N_SIMD = 4 * N_CU
+
+
+def shape_tag(bt, t_len, d, n) -> str:
+    return f"{bt}x{t_len}x{d}x{n}"
+
+
+def load_counters(bt, t_len, d, n, chunk):
+    """The committed counter summary of this workload (None if there is none,
+    or it was taken at another checkpoint stride or reduction)."""
+    from mamba_metal_scan_amd import _native
+    path = ROOT / "profiles" / COUNTERS_NAME.format(shape=shape_tag(bt, t_len, d, n))
+    try:
+        c = json.loads(path.read_text())
+    except (OSError, ValueError):
+        return None
+    red = "fixed" if _native.library().mhs_deterministic() else "atomic"
+    if c.get("chunk") != chunk or c.get("reduction") != red:
+        return None
+    return c
+
+
+def valu_block(c):
+    """VALU issue of the scan kernels from the committed counters: the lane
+    operations per second of SQ_INSTS_VALU (wave instructions x 64 lanes)
+    over the kernel-trace duration, against 1024 SIMDs x 16 lanes per clock
+    (non-packed fp32; the clock is GRBM_GUI_ACTIVE over the duration), and the
+    share of cycles the VALUs were busy (SQ_ACTIVE_INST_VALU)."""
+    if not c:
+        return None
+    out = {"bound": "valu", "unit": "G lane-op/s",
+           "source": f"profiles/{COUNTERS_NAME.format(shape=c['shape'])}"}
+    for name in ("bwd_kernel", "fwd_kernel"):
+        k = c["kernels"].get(name)
+        if not k or "valu_insts" not in k:
+            return None
+        sec = k["duration_us"] * 1e-6
+        clk = k["cycles"] / sec
+        achieved = k["valu_insts"] * 64 / sec
+        peak = N_SIMD * 16 * clk
+        entry = {"achieved": achieved / 1e9, "peak": peak / 1e9, "frac": achieved / peak,
+                 "busy": k["valu_busy"], "clock_GHz": clk / 1e9,
+                 "valu_insts_per_wave": k["valu_insts"] / k["waves"],
+                 "duration_us": k["duration_us"]}
+        if name == "bwd_kernel":
+            out.update({"kernel": name, **entry})
+        else:
+            out["fwd_kernel"] = entry
+    return out
+
+
+def _read_pmc(root: str) -> dict:
+    """Mean counter value per (kernel, counter) over every counter-collection
+    CSV under root."""
     import csv
     import glob
     vals: dict = {}
-    for f in glob.glob(os.path.join(args.pmc_summary, "**", "*counter_collection.csv"),
-                       recursive=True):
+    for f in glob.glob(os.path.join(root, "**", "*counter_collection.csv"), recursive=True):
         for r in csv.DictReader(open(f)):
             k = (_short_kernel(r["Kernel_Name"]), r["Counter_Name"])
             vals.setdefault(k, []).append(float(r["Counter_Value"]))
-    mean = {k: sum(v) / len(v) for k, v in vals.items()}
+    return {k: sum(v) / len(v) for k, v in vals.items()}
+
+
+def pmc_summary(args) -> None:
+    """Per-launch HBM traffic from two rocprofv3 --pmc passes (FETCH_SIZE, then
+    WRITE_SIZE, KiB per dispatch), each scaled by what the counter reads for
+    the calibration copy of COPY_BYTES; VALU issue counters from a third pass;
+    kernel durations from a --kernel-trace --stats run (kt/). Writes
+    profiles/scan_<shape>_counters.json (what bench.py reports from) and
+    profiles/scan_<shape>.md, and prints the markdown."""
+    import csv
+    from mamba_metal_scan_amd import _native
+    mean = _read_pmc(args.pmc_summary)
     fetch_factor = COPY_BYTES / (mean[("copy", "FETCH_SIZE")] * 1024)
     write_factor = COPY_BYTES / (mean[("copy", "WRITE_SIZE")] * 1024)
     shape = (args.batch, args.seqlen, args.d_inner, args.d_state)
+    tag = shape_tag(*shape)
     nbytes = scan_bytes(*shape)
-    rows = {}
+    # Kernel-trace durations: the last `steps` dispatches of each kernel are
+    # those of bench.py's timed steps.
+    durs: dict = {}
+    trace = os.path.join(args.pmc_summary, "kt", "run_kernel_trace.csv")
+    if os.path.exists(trace):
+        for r in csv.DictReader(open(trace)):
+            durs.setdefault(_short_kernel(r["Kernel_Name"]), []).append(
+                (int(r["End_Timestamp"]) - int(r["Start_Timestamp"])) / 1e3)
+    kernels = {}
     for kern in ("fwd_kernel", "bwd_kernel", "bwd_reduce_kernel"):
+        if (kern, "FETCH_SIZE") not in mean:
+            continue
         rd = mean[(kern, "FETCH_SIZE")] * 1024 * fetch_factor
         wr = mean[(kern, "WRITE_SIZE")] * 1024 * write_factor
-        rows[kern] = {"read_bytes": rd, "write_bytes": wr, "hbm_bytes": rd + wr}
-    bwd_total = rows["bwd_kernel"]["hbm_bytes"] + rows["bwd_reduce_kernel"]["hbm_bytes"]
-    tag = "x".join(map(str, shape))
-    out = {
-        "workload": f"selective_scan {tag} chunk {args.chunk}",
-        "hbm_bytes_per_launch": bwd_total,
-        "launch": "scan backward (bwd_kernel + bwd_reduce_kernel)",
-        "algorithmic_bytes": nbytes["bwd"],
-        "fwd_hbm_bytes_per_launch": rows["fwd_kernel"]["hbm_bytes"],
-        "fwd_algorithmic_bytes": nbytes["fwd"],
-        "kernels": rows,
-        "calibration": {"copy_bytes": COPY_BYTES, "fetch_factor": fetch_factor,
-                        "write_factor": write_factor},
-    }
-    path = ROOT / "profiles" / f"scan_bwd_{tag}_traffic.json"
-    path.write_text(json.dumps(out, indent=1) + "\n")
+        k = {"read_bytes": rd, "write_bytes": wr, "hbm_bytes": rd + wr}
+        last = durs.get(kern, [])[-args.steps:]
+        if last:
+            k["duration_us"] = sum(last) / len(last)
+        if (kern, "SQ_INSTS_VALU") in mean:
+            cyc = mean[(kern, "GRBM_GUI_ACTIVE")] / N_XCD
+            k.update({"cycles": cyc, "valu_insts": mean[(kern, "SQ_INSTS_VALU")],
+                      "waves": mean[(kern, "SQ_WAVES")],
+                      "valu_busy": mean[(kern, "SQ_ACTIVE_INST_VALU")] / (N_CU * cyc),
+                      "valu_dual_issue": mean[(kern, "SQ_ACTIVE_INST_VALU2")]
+                      / max(mean[(kern, "SQ_ACTIVE_INST_VALU")], 1.0),
+                      "exp_insts": mean[(kern, "SQ_INSTS_VALU_TRANS_F32")],
+                      "lds_bank_conflict": mean[(kern, "SQ_LDS_BANK_CONFLICT")] / (N_CU * cyc)})
+        kernels[kern] = k
+    bwd_total = sum(kernels[k]["hbm_bytes"] for k in ("bwd_kernel", "bwd_reduce_kernel")
+                    if k in kernels)
     extra = " ".join(f"--{k.replace('_', '-')} {getattr(args, k)}"
                      for k, dflt in (("batch", 16), ("seqlen", 512), ("d_inner", 1536),
                                      ("d_state", 16), ("chunk", 16)) if getattr(args, k) != dflt)
-    lines = [f"# Scan kernels at {tag}, chunk {args.chunk} (fp32): kernel time and HBM traffic",
-             "", "All commands run from /tmp with `TMPDIR=/tmp`; OUT is the output folder.", ""]
+    out = {
+        "shape": tag, "chunk": args.chunk,
+        "reduction": "fixed" if _native.library().mhs_deterministic() else "atomic",
+        "workload": f"selective_scan {tag} chunk {args.chunk}",
+        "bwd_launch": {"hbm_bytes": bwd_total, "algorithmic_bytes": nbytes["bwd"],
+                       "kernels": "bwd_kernel + bwd_reduce_kernel"},
+        "fwd_launch": {"hbm_bytes": kernels["fwd_kernel"]["hbm_bytes"],
+                       "algorithmic_bytes": nbytes["fwd"]},
+        "kernels": kernels,
+        "calibration": {"copy_bytes": COPY_BYTES, "fetch_factor": fetch_factor,
+                        "write_factor": write_factor},
+        "commands": {
+            "kernel_trace": "rocprofv3 --kernel-trace --stats -d OUT/kt -o run --output-format csv "
+                            f"-- python3 bench.py --steps {args.steps} --warmup {args.warmup} "
+                            f"--no-cpu-baseline --no-train --no-extra {extra}".strip(),
+            "fetch": f"rocprofv3 --pmc FETCH_SIZE -d OUT/fetch -o run --output-format csv -- "
+                     f"python3 bench.py --launches 5 {extra}".strip(),
+            "write": f"rocprofv3 --pmc WRITE_SIZE -d OUT/write -o run --output-format csv -- "
+                     f"python3 bench.py --launches 5 {extra}".strip(),
+            "valu": f"rocprofv3 --pmc {ISSUE_COUNTERS} -d OUT/valu -o run --output-format csv "
+                    f"-- python3 bench.py --launches 5 {extra}".strip(),
+            "summary": f"python3 bench.py --pmc-summary OUT {extra}".strip()},
+    }
+    path = ROOT / "profiles" / COUNTERS_NAME.format(shape=tag)
+    path.write_text(json.dumps(out, indent=1) + "\n")
+    lines = [f"# Scan kernels at {tag}, chunk {args.chunk} (fp32, {out['reduction']}-order "
+             "reduction): kernel time, HBM traffic, VALU issue", "",
+             "All commands run from /tmp with `TMPDIR=/tmp`; OUT is the output folder.", "",
+             "    " + out["commands"]["kernel_trace"], "    " + out["commands"]["fetch"],
+             "    " + out["commands"]["write"], "    " + out["commands"]["valu"],
+             "    " + out["commands"]["summary"], ""]
     stats = os.path.join(args.pmc_summary, "kt", "run_kernel_stats.csv")
-    trace = os.path.join(args.pmc_summary, "kt", "run_kernel_trace.csv")
     if os.path.exists(stats):
-        # The last `steps` dispatches of each scan kernel are those of
-        # bench.py's timed steps.
-        durs: dict = {}
-        if os.path.exists(trace):
-            for r in csv.DictReader(open(trace)):
-                durs.setdefault(r["Kernel_Name"], []).append(
-                    (int(r["End_Timestamp"]) - int(r["Start_Timestamp"])) / 1e3)
         lines += ["## Kernel trace", "",
-                  "    rocprofv3 --kernel-trace --stats -d OUT/kt -o run --output-format csv -- \\",
-                  f"        python3 bench.py --steps {args.steps} --warmup {args.warmup} "
-                  f"--no-cpu-baseline --no-train {extra}", "",
                   f"| kernel | calls | avg us | min us | max us | avg us, last {args.steps} |",
                   "|---|---|---|---|---|---|"]
         for r in csv.DictReader(open(stats)):
-            last = durs.get(r["Name"], [])[-args.steps:]
+            last = durs.get(_short_kernel(r["Name"]), [])[-args.steps:]
             tail = f"{sum(last) / len(last):.1f}" if len(last) == args.steps else ""
             lines.append(f"| `{r['Name'][:60]}` | {r['Calls']} | {float(r['AverageNs']) / 1e3:.1f} "
                          f"| {float(r['MinNs']) / 1e3:.1f} | {float(r['MaxNs']) / 1e3:.1f} | {tail} |")
         lines += ["", "The backward launch (the `scan_bwd` op) is `bwd_kernel` + "
                   "`bwd_reduce_kernel`. The calls include bench.py's untimed clock-settle "
                   "steps, which begin at the idle clock; the last column averages the "
-                  "timed steps' launches only, which bench.py's `scan_fwd.avg_ms` and "
-                  "`roofline.avg_ms` time with HIP events (those also include the short "
-                  "gap between the kernels of a launch).", ""]
+                  "timed steps' launches only.", ""]
     lines += ["## HBM traffic per launch", "",
-              f"    rocprofv3 --pmc FETCH_SIZE -d OUT/fetch -o run --output-format csv -- "
-              f"python3 bench.py --launches 5 {extra}",
-              f"    rocprofv3 --pmc WRITE_SIZE -d OUT/write -o run --output-format csv -- "
-              f"python3 bench.py --launches 5 {extra}",
-              f"    python3 bench.py --pmc-summary OUT {extra}", "",
               f"Calibration: a {COPY_BYTES} B device copy reads FETCH_SIZE x{fetch_factor:.3f} and "
               f"WRITE_SIZE x{write_factor:.3f} of its true bytes; the figures below are scaled by "
               f"those factors (KiB counters x 1024 x factor).", "",
               "| kernel | read MB | write MB | HBM MB | algorithmic MB |", "|---|---|---|---|---|"]
-    for kern, r in rows.items():
+    for kern, r in kernels.items():
         alg = {"fwd_kernel": nbytes["fwd"], "bwd_kernel": nbytes["bwd"]}.get(kern)
         lines.append(f"| {kern} | {r['read_bytes'] / 1e6:.1f} | {r['write_bytes'] / 1e6:.1f} | "
                      f"{r['hbm_bytes'] / 1e6:.1f} | {'' if alg is None else f'{alg / 1e6:.1f}'} |")
     if ("bwd_kernel", "SQ_ACTIVE_INST_VALU") in mean:
-        lines += issue_counter_lines(mean, extra)
+        lines += issue_counter_lines(mean)
     md = ROOT / "profiles" / f"scan_{tag}.md"
     md.write_text("\n".join(lines) + "\n")
     print("\n".join(lines))
@@ -456,17 +573,22 @@ def bench_train(steps: int = 10, warmup: int = 3) -> dict:
     return out
 
 
-def bench_longt(args) -> dict:
-    """Long-sequence scan 4 x 16384 x 2048 x 16 fwd+bwd, checkpoint strides 16/32/64/128."""
+LONGT = (4, 16384, 2048, 16)
+
+
+def longt_measure(strides) -> list:
+    """The long-sequence scan 4 x 16384 x 2048 x 16 fwd+bwd at each checkpoint
+    stride: HIP-event times of the forward and backward launches (5 each,
+    after a clock settle), algorithmic GB/s, checkpoint bytes."""
     import torch
     from mamba_metal_scan_amd import _native
     _native.library()
-    bt, t_len, d, n = 4, 16384, 2048, 16
+    bt, t_len, d, n = LONGT
     dev = torch.device("cuda", 0)
     x, dt, aneg, b_in, c_in, dy = (t.to(dev) for t in make_inputs(bt, t_len, d, n))
     nbytes = scan_bytes(bt, t_len, d, n)
     rows = []
-    for chunk in (int(v) for v in args.strides.split(",")):
+    for chunk in strides:
         fwd = lambda: torch.ops.mamba_hip.scan_fwd(x, dt, aneg, b_in, c_in, chunk, True)
         _, ckpt, _ = fwd()
         bwd = lambda: torch.ops.mamba_hip.scan_bwd(x, dt, aneg, b_in, c_in, dy, None, ckpt, chunk)
@@ -478,7 +600,18 @@ def bench_longt(args) -> dict:
                      "ckpt_bytes": ckpt.numel() * 4})
         print(f"longt chunk {chunk}: fwd {f_ms:.3f} ms bwd {b_ms:.3f} ms", file=sys.stderr,
               flush=True)
+        del ckpt
+    del x, dt, aneg, b_in, c_in, dy
+    torch.cuda.empty_cache()
+    return rows
+
+
+def bench_longt(args) -> dict:
+    """Long-sequence scan 4 x 16384 x 2048 x 16 fwd+bwd, checkpoint strides 16/32/64/128."""
+    bt, t_len, d, n = LONGT
+    rows = longt_measure([int(v) for v in args.strides.split(",")])
     best = min(rows, key=lambda r: r["fwd_bwd_ms"])
+    nbytes = scan_bytes(bt, t_len, d, n)
     # The CPU path on the first 1024 of the 16384 steps (the full sequence
     # would take minutes): the same per-token work.
     cpu = cpu_baseline_scan(bt, 1024, d, n, reps=1, warmup=0,
@@ -492,12 +625,17 @@ def bench_longt(args) -> dict:
             "cpu_baseline": cpu}
 
 
-def bench_infer(args) -> dict:
-    """Prefill 32 x 2048 x 4096 x 16 (forward + final state), then 256 decode steps."""
+INFER = (32, 2048, 4096, 16)
+
+
+def infer_measure() -> dict:
+    """Prefill 32 x 2048 x 4096 x 16 (forward + final state; HIP events, 5
+    launches after a clock settle), then 256 recurrent decode steps, eager
+    and replayed from one HIP graph."""
     import torch
     from mamba_metal_scan_amd import _native, selective_state_step
     _native.library()
-    bt, t_len, d, n = 32, 2048, 4096, 16
+    bt, t_len, d, n = INFER
     dev = torch.device("cuda", 0)
     x, dt, aneg, b_in, c_in, _ = (t.to(dev) for t in make_inputs(bt, t_len, d, n))
     prefill = lambda: torch.ops.mamba_hip.scan_fwd(x, dt, aneg, b_in, c_in, t_len, False)
@@ -512,6 +650,7 @@ def bench_infer(args) -> dict:
     dts = torch.nn.functional.softplus(torch.randn(steps, bt, d, generator=g) - 4.0).to(dev)
     bs = torch.randn(steps, bt, n, generator=g).to(dev)
     cs = torch.randn(steps, bt, n, generator=g).to(dev)
+
     def decode():
         for i in range(steps):
             selective_state_step(h, xs[i], dts[i], aneg, bs[i], cs[i])
@@ -543,15 +682,25 @@ def bench_infer(args) -> dict:
     torch.cuda.synchronize()
     graph_us = start.elapsed_time(stop) * 1e3 / (3 * steps)
     s_bytes = 4 * (2 * bt * d * n + 3 * bt * d + 2 * bt * n + d * n)
+    del graph, x, dt, aneg, b_in, c_in, h, xs, dts, bs, cs
+    torch.cuda.empty_cache()
+    return {"prefill_ms": p_ms, "prefill_GBs": p_bytes / (p_ms * 1e-3) / 1e9,
+            "prefill_algorithmic_bytes": p_bytes,
+            "prefill_tokens_per_s": bt * t_len / (p_ms * 1e-3),
+            "decode_us_per_step": graph_us, "decode_GBs": s_bytes / (graph_us * 1e-6) / 1e9,
+            "decode_us_per_step_eager": eager_us, "decode_algorithmic_bytes": s_bytes}
+
+
+def bench_infer(args) -> dict:
+    """Prefill 32 x 2048 x 4096 x 16 (forward + final state), then 256 decode steps."""
+    bt, t_len, d, n = INFER
+    m = infer_measure()
     cpu = cpu_baseline_scan(bt, t_len, d, n, reps=1, warmup=0, grad=False)
     return {"metric": "prefill GB/s and decode us/step (32x2048x4096x16 fp32)",
-            "value": p_bytes / (p_ms * 1e-3) / 1e9, "unit": "GB/s", "n_gpus": 1,
-            "ms_per_step": p_ms, "higher_is_better": True, "dtype": "f32", "data": "synthetic",
-            "config": {"workload": "prefill 32x2048x4096x16 + 256 decode steps"},
-            "decode_us_per_step": graph_us, "decode_GBs": s_bytes / (graph_us * 1e-6) / 1e9,
-            "decode_us_per_step_eager": eager_us,
-            "prefill_algorithmic_bytes": p_bytes, "decode_algorithmic_bytes": s_bytes,
-            "prefill_tokens_per_s": bt * t_len / (p_ms * 1e-3), "cpu_baseline": cpu}
+            "value": m["prefill_GBs"], "unit": "GB/s", "n_gpus": 1,
+            "ms_per_step": m["prefill_ms"], "higher_is_better": True, "dtype": "f32",
+            "data": "synthetic", "config": {"workload": "prefill 32x2048x4096x16 + 256 decode steps"},
+            **m, "cpu_baseline": cpu}
 
 
 def bench_scan(args) -> dict:
@@ -601,13 +750,11 @@ def bench_scan(args) -> dict:
     bwd_gbs = nbytes["bwd"] / (bwd_ms * 1e-3) / 1e9
     fwd_gbs = nbytes["fwd"] / (fwd_ms * 1e-3) / 1e9
     pair_gbs = nbytes["fwd_bwd"] / ((fwd_ms + bwd_ms) * 1e-3) / 1e9
-    traffic = None
-    tfile = ROOT / "profiles" / "scan_bwd_16x512x1536x16_traffic.json"
-    if tfile.exists() and chunk == 16 and (bt, t_len, d, n) == (16, 512, 1536, 16):
-        try:
-            traffic = json.loads(tfile.read_text()).get("hbm_bytes_per_launch")
-        except (OSError, ValueError):
-            traffic = None
+    # HBM traffic and VALU counters of this workload's kernels, from the
+    # committed rocprofv3 summary (written by --pmc-summary; the counters
+    # cannot be read from inside a timed run).
+    counters = load_counters(bt, t_len, d, n, chunk)
+    traffic = counters["bwd_launch"]["hbm_bytes"] if counters else None
     out = {
         "metric": METRIC,
         "value": bt * t_len / (ms * 1e-3),
@@ -626,9 +773,13 @@ def bench_scan(args) -> dict:
                    "parallelism": "single GPU"},
         "roofline": {"bound": "hbm", "achieved": bwd_gbs, "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": bwd_gbs / HBM_PEAK_GBS, "traffic": traffic,
+                     "traffic_source": (f"profiles/{COUNTERS_NAME.format(shape=shape_tag(bt, t_len, d, n))}"
+                                        " (rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE, copy-calibrated)"
+                                        if counters else None),
                      "kernel": "scan backward launch (bwd_kernel + bwd_reduce_kernel)",
                      "avg_ms": bwd_ms, "algorithmic_bytes": nbytes["bwd"],
                      "timed_launches": len(events)},
+        "valu": valu_block(counters),
         "scan_fwd": {"avg_ms": fwd_ms, "achieved_GBs": fwd_gbs,
                      "algorithmic_bytes": nbytes["fwd"]},
         "scan_fwd_bwd": {"avg_ms": fwd_ms + bwd_ms, "achieved_GBs": pair_gbs,
@@ -639,11 +790,47 @@ def bench_scan(args) -> dict:
                          "note": "untimed steps before the warmup, until the GPU clock is steady"},
         "hbm_copy": copy_bandwidth(),
     }
+    if not args.no_extra:
+        # The same shape at the reference's default checkpoint stride (64),
+        # and the backward with fp32 atomics instead of the fixed-order
+        # reduction.
+        out["scan_fwd_bwd_chunk64"] = pair_events(x, dt, aneg, b_in, c_in, dy, 64)
+        _native.set_reduction(_native.REDUCTION_ATOMIC)
+        try:
+            out["scan_bwd_atomic"] = {k: v for k, v in pair_events(
+                x, dt, aneg, b_in, c_in, dy, chunk).items() if k.startswith("bwd")}
+        finally:
+            _native.set_reduction(_native.REDUCTION_AUTO)
+    del x, dt, aneg, b_in, c_in, dy, leaves
+    torch.cuda.empty_cache()
+    if not args.no_extra:
+        out["longt_4x16384x2048x16"] = {
+            "strides": longt_measure([16, 64]),
+            "algorithmic_bytes": scan_bytes(*LONGT)["fwd_bwd"]}
+        out["infer_32x2048x4096x16"] = infer_measure()
     if not args.no_train:
         out["train_80m"] = bench_train()
     if not args.no_cpu_baseline:
         out["cpu_baseline"] = cpu_baseline_scan(bt, t_len, d, n)
     return out
+
+
+def pair_events(x, dt, aneg, b_in, c_in, dy, chunk: int, reps: int = 20) -> dict:
+    """The scan's forward and backward launches (the registered ops) at one
+    checkpoint stride: HIP-event averages over `reps` each, after a short
+    clock settle."""
+    import torch
+    ops = torch.ops.mamba_hip
+    fwd = lambda: ops.scan_fwd(x, dt, aneg, b_in, c_in, chunk, True)
+    _, ckpt, _ = fwd()
+    bwd = lambda: ops.scan_bwd(x, dt, aneg, b_in, c_in, dy, None, ckpt, chunk)
+    settle_clocks(lambda: (fwd(), bwd()), ms=30.0)
+    f_ms, b_ms = time_events(fwd, reps), time_events(bwd, reps)
+    nbytes = scan_bytes(*x.shape, aneg.shape[1])
+    return {"chunk": chunk, "fwd_ms": f_ms, "bwd_ms": b_ms, "fwd_bwd_ms": f_ms + b_ms,
+            "bwd_GBs": nbytes["bwd"] / (b_ms * 1e-3) / 1e9,
+            "fwd_bwd_GBs": nbytes["fwd_bwd"] / ((f_ms + b_ms) * 1e-3) / 1e9,
+            "ckpt_bytes": ckpt.numel() * 4}
 
 
 def main() -> int:
@@ -660,6 +847,11 @@ def main() -> int:
     ap.add_argument("--d-state", dest="d_state", type=int, default=16)
     ap.add_argument("--chunk", type=int, default=16)
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--no-extra", action="store_true",
+                    help="only the headline workload (no chunk-64, atomic, long-sequence and "
+                         "inference figures)")
+    ap.add_argument("--reduction", default="auto", choices=["auto", "fixed", "atomic"],
+                    help="the backward's reduction of dB, dC, dAneg (default: the library's)")
     ap.add_argument("--launches", type=int, default=0,
                     help="profiling driver: only N scan_fwd/scan_bwd launches + N copies")
     ap.add_argument("--pmc-summary", default=None, metavar="DIR",
@@ -670,6 +862,9 @@ def main() -> int:
                     help="summarise a kernel-trace run of --workload train under DIR")
     args = ap.parse_args()
 
+    from mamba_metal_scan_amd import _native
+    _native.set_reduction({"auto": _native.REDUCTION_AUTO, "fixed": _native.REDUCTION_FIXED,
+                           "atomic": _native.REDUCTION_ATOMIC}[args.reduction])
     if args.pmc_summary:
         pmc_summary(args)
         return 0

@@ -87,6 +87,22 @@ int mhs_set_time_segments(int segments);
 int mhs_set_cu_count(int cus);
 int mhs_cu_count(void);
 
+/* How the backward reduces its sums over channels (dB, dC) and over batch and
+ * time (dAneg, the gated dt-bias gradient), process-wide, read when a call is
+ * made (the workspace size depends on it):
+ *   1  fixed order: per-block partials in the workspace, added by a reduction
+ *      kernel in a fixed order; bit-for-bit reproducible run to run.
+ *   2  fp32 atomics: each block adds its (wave64 DPP/permlane + LDS reduced)
+ *      sums into the zeroed gradients with device-scope fp32 atomics, as the
+ *      reference's kernel does (mamba_metal/scan.py:237-245); no partials and
+ *      no reduction kernel, a far smaller workspace, and a rounding that
+ *      varies with the order the additions land in (about 1e-7 relative of
+ *      each sum: far inside the 1e-4 parity bar).
+ *   0  automatic (1: measured faster on MI355X, see mhs_capi.hip).
+ * mhs_deterministic() is 1 when the current setting reproduces bit for bit. */
+int mhs_set_reduction(int mode);
+int mhs_deterministic(void);
+
 /*
  * Forward scan. Replaces the reference's `lib.ssm_fwd(x, dt, Aneg, Bm, Cm, y,
  * ckpt, Bt, T, D, Kc)` launch (mamba_metal/scan.py:78-127, launched at :377-378).
@@ -163,9 +179,10 @@ size_t mhs_scan_bwd_workspace_bytes(int64_t batch, int64_t seqlen, int64_t d_inn
  *   dh_last  : gradient of the returned final state, or NULL (= zero; the
  *              reference drops it, scan.py:390-393)
  *   dx, ddt, daneg, dB, dC : fully written (no pre-zeroing needed). dB, dC and
- *              daneg are sums over channels / (batch, time); they are reduced
- *              through the workspace in a fixed order, so results are
- *              bit-for-bit reproducible run to run.
+ *              daneg are sums over channels / (batch, time), reduced as
+ *              mhs_set_reduction selects (fixed order, the default: bit-for-bit
+ *              reproducible; atomics: reproducible to rounding). dx and ddt are
+ *              reproducible bit for bit either way.
  *   workspace: >= mhs_scan_bwd_workspace_bytes(...) bytes of device memory,
  *              256-byte aligned; its contents on entry do not matter.
  */

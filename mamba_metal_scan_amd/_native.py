@@ -13,6 +13,7 @@ from __future__ import annotations
 
 import contextlib
 import ctypes
+import functools
 import threading
 from pathlib import Path
 from typing import Optional
@@ -31,7 +32,8 @@ EXPORTED_SYMBOLS = (
     "mhs_out_gate_bwd_workspace_bytes", "mhs_out_gate_bwd_f32", "mhs_set_time_segments",
     "mhs_scan_fwd_workspace_bytes", "mhs_scan_fwd_ws_f32", "mhs_scan_fwd_bf16",
     "mhs_scan_bwd_bf16", "mhs_scan_gated_fwd_bf16", "mhs_scan_gated_bwd_bf16",
-    "mhs_set_cu_count", "mhs_cu_count", "mhs_scan_fwd_noalloc_f32",
+    "mhs_set_cu_count", "mhs_cu_count", "mhs_scan_fwd_noalloc_f32", "mhs_set_reduction",
+    "mhs_deterministic",
 )
 
 # Size of the static device scratch of mhs_scan_fwd_noalloc_f32 (the header's
@@ -78,6 +80,10 @@ def library() -> ctypes.CDLL:
             lib.mhs_set_cu_count.argtypes = [ctypes.c_int]
             lib.mhs_cu_count.restype = ctypes.c_int
             lib.mhs_cu_count.argtypes = []
+            lib.mhs_set_reduction.restype = ctypes.c_int
+            lib.mhs_set_reduction.argtypes = [ctypes.c_int]
+            lib.mhs_deterministic.restype = ctypes.c_int
+            lib.mhs_deterministic.argtypes = []
             lib.mhs_scan_fwd_f32.restype = ctypes.c_int
             lib.mhs_scan_fwd_f32.argtypes = [_P] * 8 + [_I64] * 5 + [_P]
             lib.mhs_scan_fwd_noalloc_f32.restype = ctypes.c_int
@@ -175,10 +181,125 @@ def set_time_segments(segments: int) -> None:
     _check(library().mhs_set_time_segments(int(segments)), "mhs_set_time_segments")
 
 
+REDUCTION_AUTO, REDUCTION_FIXED, REDUCTION_ATOMIC = 0, 1, 2
+_reduction = REDUCTION_AUTO      # the mode last set through set_reduction
+_reduction_lock = threading.Lock()
+
+
+def set_reduction(mode: int) -> None:
+    """How the backward reduces dB, dC, dAneg (and the gated dt-bias gradient),
+    process-wide: REDUCTION_FIXED (fixed-order partials, bit-for-bit
+    reproducible), REDUCTION_ATOMIC (fp32 atomics into the zeroed gradients)
+    or REDUCTION_AUTO (the library's choice: the fixed order, measured faster
+    on MI355X). While torch's deterministic algorithms are enabled
+    (torch.use_deterministic_algorithms) the backward ops use the fixed order
+    whatever this says."""
+    global _reduction
+    with _reduction_lock:
+        _check(library().mhs_set_reduction(int(mode)), "mhs_set_reduction")
+        _reduction = int(mode)
+
+
+@contextlib.contextmanager
+def _bwd_reduction():
+    """Around one backward call (workspace query and launch): the fixed-order
+    reduction while torch's deterministic algorithms are enabled, else the
+    process-wide mode."""
+    if not torch.are_deterministic_algorithms_enabled():
+        yield
+        return
+    with _reduction_lock:
+        lib = library()
+        lib.mhs_set_reduction(REDUCTION_FIXED)
+        try:
+            yield
+        finally:
+            lib.mhs_set_reduction(_reduction)
+
+
 def set_cu_count(cus: int) -> None:
     """Force the compute-unit count the automatic time-segment split plans for
     (0 = query the current device), process-wide."""
     _check(library().mhs_set_cu_count(int(cus)), "mhs_set_cu_count")
+
+
+# ------------------------------------------------------- host-side checks
+#
+# The registered ops are public (torch.ops.mamba_hip.*), so each checks what
+# its kernels assume before anything is launched: one ROCm device, the dtypes
+# the kernels read, shapes, dense layouts (or the row strides the kernel
+# takes), and the checkpoint buffer's shape for the stride. A mismatch raises
+# HipScanError; nothing reaches the device.
+
+_ACT = (torch.float32, torch.bfloat16)
+
+
+def _need(ok: bool, what: str, msg: str) -> None:
+    if not ok:
+        raise HipScanError(f"{what}: {msg}")
+
+
+def _on_one_device(what: str, *ts: Optional[torch.Tensor]) -> None:
+    ts = [t for t in ts if t is not None]
+    dev = ts[0].device
+    _need(dev.type == "cuda" and all(t.device == dev for t in ts), what,
+          "every tensor must be on one ROCm device; got " + ", ".join(str(t.device) for t in ts))
+
+
+def _dense(what: str, **ts: Optional[torch.Tensor]) -> None:
+    for name, t in ts.items():
+        if t is not None and not t.is_contiguous():
+            raise HipScanError(f"{what}: {name} must be contiguous; got strides {t.stride()} "
+                               f"for shape {tuple(t.shape)}")
+
+
+def _fp32(what: str, **ts: Optional[torch.Tensor]) -> None:
+    for name, t in ts.items():
+        if t is not None and t.dtype != torch.float32:
+            raise HipScanError(f"{what}: {name} must be float32; got {t.dtype}")
+
+
+def _shaped(what: str, name: str, t: Optional[torch.Tensor], shape) -> None:
+    if t is not None and tuple(t.shape) != tuple(shape):
+        raise HipScanError(f"{what}: {name} must have shape {tuple(shape)}; got "
+                           f"{tuple(t.shape)}")
+
+
+def _check_scan(what: str, x, dt, aneg, b_in, c_in, chunk: int, dense_dt_bc: bool = True) -> None:
+    """Common checks of the scan ops: x (B,T,D); dt (B,T,D); Aneg / A (D,N)
+    fp32; B, C (B,T,N); x, dt, B, C all fp32 or all bf16; x (and unless the
+    op takes row strides, dt, B, C) contiguous; chunk >= 1."""
+    _on_one_device(what, x, dt, aneg, b_in, c_in)
+    _need(x.dim() == 3 and aneg.dim() == 2, what,
+          f"x must be (B,T,D) and Aneg (D,N); got {tuple(x.shape)}, {tuple(aneg.shape)}")
+    bt, t_len, d = x.shape
+    n = aneg.shape[1]
+    _shaped(what, "dt", dt, (bt, t_len, d))
+    _shaped(what, "Aneg", aneg, (d, n))
+    _shaped(what, "B", b_in, (bt, t_len, n))
+    _shaped(what, "C", c_in, (bt, t_len, n))
+    _need(x.dtype in _ACT and all(t.dtype == x.dtype for t in (dt, b_in, c_in)), what,
+          "x, dt, B, C must all be float32 or all bfloat16; got "
+          + ", ".join(str(t.dtype) for t in (x, dt, b_in, c_in)))
+    _fp32(what, Aneg=aneg)
+    _dense(what, x=x, Aneg=aneg)
+    if dense_dt_bc:
+        _dense(what, dt=dt, B=b_in, C=c_in)
+    _need(isinstance(chunk, int) and chunk >= 1, what, f"chunk must be an int >= 1; got {chunk!r}")
+
+
+def _check_bwd(what: str, x, aneg, dy, dh_last, ckpt, chunk: int) -> None:
+    """The backward's extra operands: dy like x; dh_last None or (B,D,N)
+    fp32; ckpt the forward's (B, ceil(T/chunk), D, N) fp32 checkpoints."""
+    bt, t_len, d = x.shape
+    n = aneg.shape[1]
+    _on_one_device(what, x, dy, dh_last, ckpt)
+    _shaped(what, "dy", dy, (bt, t_len, d))
+    _need(dy.dtype == x.dtype, what, f"dy must have x's dtype {x.dtype}; got {dy.dtype}")
+    _shaped(what, "dh_last", dh_last, (bt, d, n))
+    _shaped(what, f"ckpt (chunk {chunk})", ckpt, (bt, num_chunks(t_len, chunk), d, n))
+    _fp32(what, dh_last=dh_last, ckpt=ckpt)
+    _dense(what, dy=dy, dh_last=dh_last, ckpt=ckpt)
 
 
 # --------------------------------------------------------------- custom ops
@@ -201,21 +322,41 @@ def _fwd_workspace(x: torch.Tensor, n: int):
     return torch.empty(nbytes, dtype=torch.uint8, device=x.device), nbytes
 
 
+def _bwd_workspace(x: torch.Tensor, n: int, chunk: int):
+    """(workspace tensor, bytes) for a backward on (B,T,D) x with d_state n
+    and checkpoint stride chunk, under the current reduction mode."""
+    bt, t_len, d = x.shape
+    nbytes = int(library().mhs_scan_bwd_workspace_bytes(bt, t_len, d, n, chunk))
+    if nbytes == 0:
+        raise HipScanError(f"no backward workspace size for shape {(bt, t_len, d, n)} "
+                           f"chunk {chunk}")
+    return torch.empty(nbytes, dtype=torch.uint8, device=x.device), nbytes
+
+
 _IMPLS: dict = {}
 
 
-def _register(name: str, impl, mutates_args):
-    """Register impl as the custom op mamba_hip::<name> (for torch.compile and
-    torch.ops callers) and keep the plain function for dispatch()."""
+def _register(name: str, impl, mutates_args, check):
+    """Register impl, preceded by the host-side argument checks `check` (same
+    arguments), as the custom op mamba_hip::<name> (for torch.compile and
+    torch.ops callers); keep the plain impl for dispatch()."""
     _IMPLS[name] = impl
-    return torch.library.custom_op(f"mamba_hip::{name}", impl, mutates_args=mutates_args)
+
+    @functools.wraps(impl)
+    def checked(*args, **kwargs):
+        check(*args, **kwargs)
+        return impl(*args, **kwargs)
+
+    return torch.library.custom_op(f"mamba_hip::{name}", checked, mutates_args=mutates_args)
 
 
 def dispatch(name: str):
     """The op the autograd Functions call: the registered torch.ops.mamba_hip
     op while torch.compile traces, else its plain implementation (the same
-    code without the dispatcher's per-call overhead, about as long as the
-    C-ABI call itself at the training shape)."""
+    code without the dispatcher's per-call overhead and without the op's
+    argument checks, which the Functions' own validation and .contiguous()
+    calls already cover; together these are as long as the kernels' GPU time
+    at the training shape, and the GPU would wait for them)."""
     if torch.compiler.is_compiling():
         return getattr(torch.ops.mamba_hip, name)
     return _IMPLS[name]
@@ -239,7 +380,10 @@ def _scan_fwd_impl(x: torch.Tensor, dt: torch.Tensor, aneg: torch.Tensor, b_in: 
     return y, ckpt, h_last
 
 
-scan_fwd = _register("scan_fwd", _scan_fwd_impl, ())
+scan_fwd = _register(
+    "scan_fwd", _scan_fwd_impl, (),
+    lambda x, dt, aneg, b_in, c_in, chunk, with_ckpt:
+        _check_scan("scan_fwd", x, dt, aneg, b_in, c_in, chunk))
 
 
 @scan_fwd.register_fake
@@ -260,12 +404,9 @@ def _scan_bwd_impl(x: torch.Tensor, dt: torch.Tensor, aneg: torch.Tensor, b_in: 
     daneg = torch.empty_like(aneg)
     db = torch.empty_like(b_in)
     dc = torch.empty_like(c_in)
-    ws_bytes = int(lib.mhs_scan_bwd_workspace_bytes(bt, t_len, d, n, chunk))
-    if ws_bytes == 0:
-        raise HipScanError(f"no backward workspace size for shape {(bt, t_len, d, n)} chunk {chunk}")
-    ws = torch.empty(ws_bytes, dtype=torch.uint8, device=x.device)
     fn = lib.mhs_scan_bwd_bf16 if x.dtype == torch.bfloat16 else lib.mhs_scan_bwd_f32
-    with _on(x.device):
+    with _bwd_reduction(), _on(x.device):
+        ws, ws_bytes = _bwd_workspace(x, n, chunk)
         rc = fn(_ptr(x), _ptr(dt), _ptr(aneg), _ptr(b_in), _ptr(c_in), _ptr(dy),
                 _ptr(dh_last), _ptr(ckpt), _ptr(dx), _ptr(ddt), _ptr(daneg), _ptr(db), _ptr(dc),
                 _ptr(ws), ws_bytes, bt, t_len, d, n, chunk, _stream(x.device))
@@ -273,7 +414,12 @@ def _scan_bwd_impl(x: torch.Tensor, dt: torch.Tensor, aneg: torch.Tensor, b_in: 
     return dx, ddt, daneg, db, dc
 
 
-scan_bwd = _register("scan_bwd", _scan_bwd_impl, ())
+def _check_scan_bwd(x, dt, aneg, b_in, c_in, dy, dh_last, ckpt, chunk):
+    _check_scan("scan_bwd", x, dt, aneg, b_in, c_in, chunk)
+    _check_bwd("scan_bwd", x, aneg, dy, dh_last, ckpt, chunk)
+
+
+scan_bwd = _register("scan_bwd", _scan_bwd_impl, (), _check_scan_bwd)
 
 
 @scan_bwd.register_fake
@@ -295,7 +441,19 @@ def _scan_step_impl(h: torch.Tensor, x: torch.Tensor, dt: torch.Tensor, aneg: to
     return y
 
 
-scan_step = _register("scan_step", _scan_step_impl, ("h",))
+def _check_scan_step(h, x, dt, aneg, b_in, c_in):
+    what = "scan_step"
+    _on_one_device(what, h, x, dt, aneg, b_in, c_in)
+    _need(h.dim() == 3, what, f"h must be (B,D,N); got {tuple(h.shape)}")
+    bt, d, n = h.shape
+    for name, t, shape in (("x", x, (bt, d)), ("dt", dt, (bt, d)), ("Aneg", aneg, (d, n)),
+                           ("B", b_in, (bt, n)), ("C", c_in, (bt, n))):
+        _shaped(what, name, t, shape)
+    _fp32(what, h=h, x=x, dt=dt, Aneg=aneg, B=b_in, C=c_in)
+    _dense(what, h=h, x=x, dt=dt, Aneg=aneg, B=b_in, C=c_in)
+
+
+scan_step = _register("scan_step", _scan_step_impl, ("h",), _check_scan_step)
 
 
 @scan_step.register_fake
@@ -315,6 +473,40 @@ def _rows(x: torch.Tensor) -> int:
 
 
 _conv_rows = _rows
+
+
+def _check_conv(what: str, x, w, bias, dout=None, dx=None) -> None:
+    """conv1d + SiLU: fp32 x (B,T,D) with dense rows (row stride allowed), w
+    (D,K) and bias (D,) contiguous, dout (B,T,D) contiguous, dx (B,T,D) with
+    dense rows."""
+    _on_one_device(what, x, w, bias, dout, dx)
+    _need(x.dim() == 3 and w.dim() == 2, what,
+          f"x must be (B,T,D) and w (D,K); got {tuple(x.shape)}, {tuple(w.shape)}")
+    _shaped(what, "w", w, (x.shape[2], w.shape[1]))
+    _shaped(what, "bias", bias, (x.shape[2],))
+    _shaped(what, "dout", dout, x.shape)
+    _shaped(what, "dx", dx, x.shape)
+    _fp32(what, x=x, w=w, bias=bias, dout=dout, dx=dx)
+    _dense(what, w=w, bias=bias, dout=dout)
+    _rows(x)
+    if dx is not None:
+        _rows(dx)
+
+
+def _check_gate(what: str, y, d_skip, z, dout=None, dz=None) -> None:
+    """Output gate: fp32 y (B,T,D) and dout contiguous, d_skip (D,)
+    contiguous, z and dz (B,T,D) with dense rows."""
+    _on_one_device(what, y, d_skip, z, dout, dz)
+    _need(y.dim() == 3, what, f"y must be (B,T,D); got {tuple(y.shape)}")
+    _shaped(what, "d_skip", d_skip, (y.shape[2],))
+    _shaped(what, "z", z, y.shape)
+    _shaped(what, "dout", dout, y.shape)
+    _shaped(what, "dz", dz, y.shape)
+    _fp32(what, y=y, d_skip=d_skip, z=z, dout=dout, dz=dz)
+    _dense(what, y=y, d_skip=d_skip, dout=dout)
+    _rows(z)
+    if dz is not None:
+        _rows(dz)
 
 
 def _bc_rows(b_in: torch.Tensor, c_in: torch.Tensor) -> int:
@@ -338,7 +530,8 @@ def _conv1d_silu_fwd_impl(x: torch.Tensor, w: torch.Tensor, bias: torch.Tensor) 
     return out
 
 
-conv1d_silu_fwd = _register("conv1d_silu_fwd", _conv1d_silu_fwd_impl, ())
+conv1d_silu_fwd = _register("conv1d_silu_fwd", _conv1d_silu_fwd_impl, (),
+                            lambda x, w, bias: _check_conv("conv1d_silu_fwd", x, w, bias))
 
 
 @conv1d_silu_fwd.register_fake
@@ -367,7 +560,9 @@ def _conv1d_silu_bwd_impl(x: torch.Tensor, w: torch.Tensor, bias: torch.Tensor, 
     return dx, dw, dbias
 
 
-conv1d_silu_bwd = _register("conv1d_silu_bwd", _conv1d_silu_bwd_impl, ())
+conv1d_silu_bwd = _register(
+    "conv1d_silu_bwd", _conv1d_silu_bwd_impl, (),
+    lambda x, w, bias, dout: _check_conv("conv1d_silu_bwd", x, w, bias, dout))
 
 
 @conv1d_silu_bwd.register_fake
@@ -398,7 +593,9 @@ def _conv1d_silu_bwd_into_impl(x: torch.Tensor, w: torch.Tensor, bias: torch.Ten
     return dw, dbias
 
 
-conv1d_silu_bwd_into = _register("conv1d_silu_bwd_into", _conv1d_silu_bwd_into_impl, ("dx",))
+conv1d_silu_bwd_into = _register(
+    "conv1d_silu_bwd_into", _conv1d_silu_bwd_into_impl, ("dx",),
+    lambda x, w, bias, dout, dx: _check_conv("conv1d_silu_bwd_into", x, w, bias, dout, dx))
 
 
 @conv1d_silu_bwd_into.register_fake
@@ -439,7 +636,10 @@ def _scan_gated_fwd_impl(x: torch.Tensor, dt_raw: torch.Tensor, a_raw: torch.Ten
     return y, ckpt, h_last
 
 
-scan_gated_fwd = _register("scan_gated_fwd", _scan_gated_fwd_impl, ())
+scan_gated_fwd = _register(
+    "scan_gated_fwd", _scan_gated_fwd_impl, (),
+    lambda x, dt_raw, a_raw, b_in, c_in, dt_min, dt_max, chunk, with_ckpt, dt_bias=None:
+        _check_scan("scan_gated_fwd", x, dt_raw, a_raw, b_in, c_in, chunk, dense_dt_bc=False))
 
 
 @scan_gated_fwd.register_fake
@@ -469,12 +669,9 @@ def _scan_gated_bwd_impl(x: torch.Tensor, dt_raw: torch.Tensor, a_raw: torch.Ten
     db = x.new_empty((bt, t_len, n))
     dc = x.new_empty((bt, t_len, n))
     dbias = a_raw.new_empty((d,))
-    ws_bytes = int(lib.mhs_scan_bwd_workspace_bytes(bt, t_len, d, n, chunk))
-    if ws_bytes == 0:
-        raise HipScanError(f"no backward workspace size for shape {(bt, t_len, d, n)} chunk {chunk}")
-    ws = torch.empty(ws_bytes, dtype=torch.uint8, device=x.device)
     fn = lib.mhs_scan_gated_bwd_bf16 if x.dtype == torch.bfloat16 else lib.mhs_scan_gated_bwd_f32
-    with _on(x.device):
+    with _bwd_reduction(), _on(x.device):
+        ws, ws_bytes = _bwd_workspace(x, n, chunk)
         rc = fn(_ptr(x), _ptr(dt_raw), _ptr(a_raw), _ptr(b_in), _ptr(c_in), dt_min, dt_max,
                 _ptr(dt_bias), _ptr(dy), _ptr(dh_last), _ptr(ckpt), _ptr(dx), _ptr(ddt),
                 _ptr(da), _ptr(db), _ptr(dc), _ptr(dbias), _ptr(ws), ws_bytes, bt, t_len, d, n,
@@ -483,7 +680,13 @@ def _scan_gated_bwd_impl(x: torch.Tensor, dt_raw: torch.Tensor, a_raw: torch.Ten
     return dx, ddt, da, db, dc, dbias
 
 
-scan_gated_bwd = _register("scan_gated_bwd", _scan_gated_bwd_impl, ())
+def _check_scan_gated_bwd(x, dt_raw, a_raw, b_in, c_in, dt_min, dt_max, dy, dh_last, ckpt,
+                          chunk, dt_bias=None):
+    _check_scan("scan_gated_bwd", x, dt_raw, a_raw, b_in, c_in, chunk, dense_dt_bc=False)
+    _check_bwd("scan_gated_bwd", x, a_raw, dy, dh_last, ckpt, chunk)
+
+
+scan_gated_bwd = _register("scan_gated_bwd", _scan_gated_bwd_impl, (), _check_scan_gated_bwd)
 
 
 def _scan_gated_bwd_into_impl(x: torch.Tensor, dt_raw: torch.Tensor, a_raw: torch.Tensor,
@@ -507,15 +710,12 @@ def _scan_gated_bwd_into_impl(x: torch.Tensor, dt_raw: torch.Tensor, a_raw: torc
     dx = torch.empty_like(x)
     da = torch.empty_like(a_raw)
     dbias = a_raw.new_empty((d,))
-    ws_bytes = int(lib.mhs_scan_bwd_workspace_bytes(bt, t_len, d, n, chunk))
-    if ws_bytes == 0:
-        raise HipScanError(f"no backward workspace size for shape {(bt, t_len, d, n)} chunk {chunk}")
-    ws = torch.empty(ws_bytes, dtype=torch.uint8, device=x.device)
     fn = lib.mhs_scan_gated_bwd_bf16 if x.dtype == torch.bfloat16 else lib.mhs_scan_gated_bwd_f32
     es = dproj.element_size()
     base = dproj.data_ptr()
     w = d + 2 * n
-    with _on(x.device):
+    with _bwd_reduction(), _on(x.device):
+        ws, ws_bytes = _bwd_workspace(x, n, chunk)
         rc = fn(_ptr(x), _ptr(dt_raw), _ptr(a_raw), _ptr(b_in), _ptr(c_in), dt_min, dt_max,
                 _ptr(dt_bias), _ptr(dy), _ptr(dh_last), _ptr(ckpt), _ptr(dx), base, _ptr(da),
                 base + d * es, base + (d + n) * es, _ptr(dbias), _ptr(ws), ws_bytes, bt, t_len,
@@ -524,7 +724,17 @@ def _scan_gated_bwd_into_impl(x: torch.Tensor, dt_raw: torch.Tensor, a_raw: torc
     return dx, da, dbias
 
 
-scan_gated_bwd_into = _register("scan_gated_bwd_into", _scan_gated_bwd_into_impl, ("dproj",))
+def _check_scan_gated_bwd_into(x, dt_raw, a_raw, b_in, c_in, dt_min, dt_max, dy, dh_last, ckpt,
+                               chunk, dproj, dt_bias=None):
+    what = "scan_gated_bwd_into"
+    _check_scan(what, x, dt_raw, a_raw, b_in, c_in, chunk, dense_dt_bc=False)
+    _check_bwd(what, x, a_raw, dy, dh_last, ckpt, chunk)
+    _on_one_device(what, x, dproj)
+    _need(dproj.dtype == x.dtype, what, f"dproj must have x's dtype {x.dtype}; got {dproj.dtype}")
+
+
+scan_gated_bwd_into = _register("scan_gated_bwd_into", _scan_gated_bwd_into_impl, ("dproj",),
+                                _check_scan_gated_bwd_into)
 
 
 @scan_gated_bwd_into.register_fake
@@ -554,7 +764,8 @@ def _out_gate_fwd_impl(y: torch.Tensor, d_skip: torch.Tensor, z: torch.Tensor) -
     return out
 
 
-out_gate_fwd = _register("out_gate_fwd", _out_gate_fwd_impl, ())
+out_gate_fwd = _register("out_gate_fwd", _out_gate_fwd_impl, (),
+                         lambda y, d_skip, z: _check_gate("out_gate_fwd", y, d_skip, z))
 
 
 @out_gate_fwd.register_fake
@@ -582,7 +793,9 @@ def _out_gate_bwd_impl(y: torch.Tensor, d_skip: torch.Tensor, z: torch.Tensor, d
     return dy, dd, dz
 
 
-out_gate_bwd = _register("out_gate_bwd", _out_gate_bwd_impl, ())
+out_gate_bwd = _register(
+    "out_gate_bwd", _out_gate_bwd_impl, (),
+    lambda y, d_skip, z, dout: _check_gate("out_gate_bwd", y, d_skip, z, dout))
 
 
 @out_gate_bwd.register_fake
@@ -612,7 +825,9 @@ def _out_gate_bwd_into_impl(y: torch.Tensor, d_skip: torch.Tensor, z: torch.Tens
     return dy, dd
 
 
-out_gate_bwd_into = _register("out_gate_bwd_into", _out_gate_bwd_into_impl, ("dz",))
+out_gate_bwd_into = _register(
+    "out_gate_bwd_into", _out_gate_bwd_into_impl, ("dz",),
+    lambda y, d_skip, z, dout, dz: _check_gate("out_gate_bwd_into", y, d_skip, z, dout, dz))
 
 
 @out_gate_bwd_into.register_fake

@@ -22,9 +22,11 @@ LIB_PATH = PKG_DIR / LIB_NAME
 ARCH = "gfx950"
 
 # The host code and small kernels, and the scan kernels' instantiations in
-# four units (forward / backward x fp32 / bf16) compiled in parallel.
+# five units (forward / backward x fp32 / bf16, and the fp32 backward with
+# atomics) compiled in parallel.
 SOURCES = ["mhs_capi.hip", "mhs_kern_fwd_f32.hip", "mhs_kern_fwd_bf16.hip",
-           "mhs_kern_bwd_f32.hip", "mhs_kern_bwd_bf16.hip"]
+           "mhs_kern_bwd_f32.hip", "mhs_kern_bwd_bf16.hip", "mhs_kern_bwd_atom.hip",
+           "mhs_kern_bwd_atom_bf16.hip"]
 HEADERS = ["mhs_common.hpp", "mhs_fwd.hpp", "mhs_bwd.hpp", "mhs_step.hpp", "mhs_conv.hpp",
            "mhs_gate.hpp", "mhs_instances.hpp"]
 

@@ -96,6 +96,15 @@ struct BwdArgs {
   // and of ddt: D, N and D for contiguous tensors, more for column slices of
   // a wider projection output (and its gradient). x, dy, dx are contiguous.
   int ld_dt, ld_bc, ld_ddt;
+  // Atomic kernels only (ATOM): the fp32 gradients the blocks add into with
+  // fp32 atomics instead of writing partials (wsB, wsC, wsA, wsDB unused),
+  // zeroed beforehand: dB, dC (rows ld_dbc apart), dAneg (or the gated
+  // kernels' dA), the gated kernels' dt-bias gradient (may be null).
+  float* dB = nullptr;
+  float* dC = nullptr;
+  float* daneg = nullptr;
+  float* dbias = nullptr;
+  int ld_dbc = 0;
 };
 
 // One staging buffer (the kernel keeps two) and the single-buffered rest.
@@ -117,7 +126,12 @@ __host__ __device__ constexpr int bwd_lds_floats(int G, int NPL) {
 // (dA and G, no state, no gradients, no x or B traffic) and write L_s and
 // the segment's sum of dt.
 // ES: bytes per element of x, dt, B, C, dy, dx, ddt (4: fp32, 2: bf16).
-template <int NPL, int G, int MINW, bool GATED, bool CARRY, int ES = 4>
+// ATOM: the block sums of dB and dC, each lane's dAneg and the block's
+// dt-bias sums are added into zeroed fp32 gradients with fp32 atomics (no
+// partials, no reduction kernel; the order of the additions, and so the
+// rounding, varies from run to run). For bf16 activations dB and dC go to
+// fp32 buffers that a later pass rounds to bf16.
+template <int NPL, int G, int MINW, bool GATED, bool CARRY, int ES = 4, bool ATOM = false>
 __global__ void __launch_bounds__(64 * G, MINW)
 bwd_kernel(BwdArgs a) {
   constexpr int NT = 64 * G;
@@ -130,6 +144,7 @@ bwd_kernel(BwdArgs a) {
   constexpr int M = 4 * NPL;            // dB/dC products per lane per two steps
   static_assert(NPL == 2 || NPL == 4, "two or four states per lane");
   static_assert(FK * NT == kSteps * NP, "dB/dC copy-out must tile the block");
+  static_assert(!ATOM || !CARRY, "atomics: gradient pass only");
 
   extern __shared__ float lds[];
   const int N = a.N;
@@ -215,39 +230,57 @@ bwd_kernel(BwdArgs a) {
   if constexpr (GATED) qdt.load_channel(gbias, a.dt_bias, d0);
   float dbias_acc = 0.f;   // GATED: this thread's sum of the raw dt gradient (channel tid % 32)
 
-  // Chunk ci (any integer): first step and length (0 outside this block's
-  // segment, so that every load and store of a chunk outside it is empty).
-  auto chunk_t0 = [&](int ci) { return min(max(ci, 0) * K, T - 1); };
+  // Chunk ci (any integer): its length (0 outside this block's segment, so
+  // that every load and store of a chunk outside it is empty).
+  const int last_len = T - (nch - 1) * K;
   auto chunk_len = [&](int ci) {
-    return (ci < c_lo || ci >= c_hi) ? 0 : max(0, min(K, T - ci * K));
+    return (ci < c_lo || ci >= c_hi) ? 0 : ci == nch - 1 ? last_len : K;
   };
-  // Resource over one chunk of a (batch, T, D) tensor of row stride ld
-  // (channels d0 .. D-1 of its rows).
-  auto chunk_buf = [&](const void* base, int ci, int ld) {
-    const int len = chunk_len(ci);
-    if constexpr (!GATED)   // contiguous (ld == D)
-      return GBuf(elem_at<ES>(base, (row0 + chunk_t0(ci)) * D + d0),
-                  len > 0 ? (unsigned)ES * (unsigned)(len * D - d0) : 0u);
-    return GBuf(elem_at<ES>(base, (row0 + chunk_t0(ci)) * ld + d0),
-                len > 0 ? (unsigned)ES * (unsigned)((len - 1) * ld + D - d0) : 0u);
+  // Resources over chunk ci of the operands (channels d0 .. D-1 of the
+  // (batch, T, D) ones, all N states of B, C and of the dB / dC rows; see
+  // SubStream): empty outside [c_lo, c_hi).
+  auto stream = [&](const void* base, int ld, int c0, int width) {
+    return SubStream<ES>(base, row0, ld, c0, width, K, c_lo, c_hi, nch - 1, last_len);
   };
-  auto load_sub = [&](int ci) {           // global -> staging registers
-    const int len = chunk_len(ci);
-    const unsigned sbytes = !GATED ? (unsigned)ES * (unsigned)(len * N)
-                            : len > 0 ? (unsigned)ES * (unsigned)((len - 1) * ld_bc + N) : 0u;
-    const GBuf gs_b(elem_at<ES>(a.B, (row0 + chunk_t0(ci)) * ld_bc), sbytes);
-    const GBuf gs_c(elem_at<ES>(a.C, (row0 + chunk_t0(ci)) * ld_bc), sbytes);
-    if constexpr (!CARRY) ql.load(px, chunk_buf(a.x, ci, D));
-    qdt.load(pd, chunk_buf(a.dt, ci, ld_dt));
-    ql.load(py, chunk_buf(a.dy, ci, D));
-    if constexpr (!CARRY) rl.load(pb, gs_b);
-    rl.load(pc, gs_c);
+  const SubStream<ES> sx = stream(a.x, D, d0, D), sdt = stream(a.dt, ld_dt, d0, D),
+                      sdy = stream(a.dy, D, d0, D), sB = stream(a.B, ld_bc, 0, N),
+                      sC = stream(a.C, ld_bc, 0, N), sdx = stream(a.dx, D, d0, D),
+                      sddt = stream(a.ddt, ld_ddt, d0, D);
+  // global -> staging registers: chunk ci (the prologue), or the chunk of
+  // the loop's load cursors (two below the chunk walked).
+  auto load_sub = [&](int ci) {
+    if constexpr (!CARRY) ql.load(px, sx.at(ci));
+    qdt.load(pd, sdt.at(ci));
+    ql.load(py, sdy.at(ci));
+    if constexpr (!CARRY) rl.load(pb, sB.at(ci));
+    rl.load(pc, sC.at(ci));
   };
-  // h at the start of chunk ci: checkpoint ci-1, or 0 for the first chunk.
+  StreamCursor<ES> lx(sx, c_hi - 3), ldt(sdt, c_hi - 3), ldy(sdy, c_hi - 3), lB(sB, c_hi - 3),
+      lC(sC, c_hi - 3);
+  auto load_next = [&]() {
+    if constexpr (!CARRY) ql.load(px, lx.get(sx));
+    qdt.load(pd, ldt.get(sdt));
+    ql.load(py, ldy.get(sdy));
+    if constexpr (!CARRY) rl.load(pb, lB.get(sB));
+    rl.load(pc, lC.get(sC));
+  };
+  auto load_down = [&]() {
+    lx.down(sx);
+    ldt.down(sdt);
+    ldy.down(sdy);
+    lB.down(sB);
+    lC.down(sC);
+  };
+  // h at the start of chunk ci: checkpoint ci-1, or 0 for the first chunk
+  // (empty for ci <= 0). The loop walks it with a pointer moved down by one
+  // (D, N) slice per chunk.
+  const float* ck_row = a.ckpt + ((size_t)b * nch - 1) * slice;
   auto load_h0 = [&](int ci) {
-    load_states<NPL>(ph, GBuf(a.ckpt + ((size_t)b * nch + max(ci - 1, 0)) * slice,
-                              ci > 0 ? slice_bytes : 0u), st_lane, nvalid);
+    load_states<NPL>(ph, GBuf(ck_row + (ptrdiff_t)ci * (ptrdiff_t)slice, ci > 0 ? slice_bytes : 0u),
+                     st_lane, nvalid);
   };
+  const float* ck_next = ck_row + (ptrdiff_t)(c_hi - 3) * (ptrdiff_t)slice;
+  int ck_i = c_hi - 3;
   auto store_sub = [&](int j, int ci) {   // staging registers (chunk ci) -> buffer j
     float* s0 = lds + j * BUF;
     if constexpr (GATED) qdt.gate(pd, chunk_len(ci), a.dt_lo, a.dt_span, gbias);
@@ -258,14 +291,24 @@ bwd_kernel(BwdArgs a) {
     if constexpr (!CARRY) rl.store(s0 + oB, pb);
     rl.store(s0 + oC, pc);
   };
-  // dx, ddt and the dB, dC block sums of chunk ci, staged in buffer j: from
-  // tS and tDBC (which hold them until the next reverse phase) and the
-  // chunk's x and dt tiles.
-  auto finalize = [&](int ci, int j) {
-    const float* sx = lds + j * BUF + oX;
-    const float* sdt = lds + j * BUF;
-    const GBuf gdx = chunk_buf(a.dx, ci, D), gddt = chunk_buf(a.ddt, ci, ld_ddt);
-    const int len = chunk_len(ci);
+  // The fp32 rows of the dB / dC block sums of chunk ci: this block's
+  // partials (rows of N), or with ATOM the gradients themselves (rows ld_dbc
+  // apart).
+  const size_t prow = ((size_t)blockIdx.x * a.batch + b) * T;
+  const SubStream<4> swB(a.wsB, prow, N, 0, N, K, c_lo, c_hi, nch - 1, last_len),
+                     swC(a.wsC, prow, N, 0, N, K, c_lo, c_hi, nch - 1, last_len),
+                     sdB(a.dB, row0, a.ld_dbc, 0, N, K, c_lo, c_hi, nch - 1, last_len),
+                     sdC(a.dC, row0, a.ld_dbc, 0, N, K, c_lo, c_hi, nch - 1, last_len);
+  const SubStream<4>& sBsum = ATOM ? sdB : swB;
+  const SubStream<4>& sCsum = ATOM ? sdC : swC;
+  // dx, ddt and the dB, dC block sums of chunk ci (len steps), staged in
+  // buffer j, into gdx, gddt and the dB / dC rows gbs, gcs: from tS and tDBC
+  // (which hold them until the next reverse phase) and the chunk's x and dt
+  // tiles.
+  auto finalize = [&](int j, int len, const GBuf& gdx, const GBuf& gddt, const GBuf& gbs,
+                      const GBuf& gcs) {
+    const float* tx = lds + j * BUF + oX;
+    const float* tdt = lds + j * BUF;
 #pragma unroll
     for (int f = 0; f < FT; ++f) {
       const int task0 = tid + f * NT;
@@ -277,7 +320,7 @@ bwd_kernel(BwdArgs a) {
       const unsigned o1 = okc ? o0 + (unsigned)ES * (unsigned)D : kOOB;
       const unsigned od0 = okc ? (unsigned)ES * ((unsigned)k * (unsigned)ld_ddt + cc) : kOOB;
       const unsigned od1 = okc ? od0 + (unsigned)ES * (unsigned)ld_ddt : kOOB;
-      const float2 xv = lds2(sx + cm_elem(cc, k)), dtv = lds2(sdt + cm_elem(cc, k));
+      const float2 xv = lds2(tx + cm_elem(cc, k)), dtv = lds2(tdt + cm_elem(cc, k));
       const float x0 = xv.x, x1 = xv.y, t0v = dtv.x, t1v = dtv.y;
       float s1a = 0.f, s1b = 0.f, s2a = 0.f, s2b = 0.f;
 #pragma unroll
@@ -301,18 +344,27 @@ bwd_kernel(BwdArgs a) {
       st_elem<ES, kStream>(gddt, g0, od0);
       st_elem<ES, kStream>(gddt, g1, od1);
     }
-    const size_t wrow = ((size_t)blockIdx.x * a.batch + b) * T + chunk_t0(ci);
-    const unsigned sbytes = 4u * (unsigned)(len * N);
-    const GBuf gwb(a.wsB + wrow * N, sbytes), gwc(a.wsC + wrow * N, sbytes);
+    // The block's sums: partials (rows of N), or with ATOM added into rows
+    // (b, t) of dB and dC (ld_dbc apart). The resources end after the
+    // chunk's last row.
+    const int ldr = ATOM ? a.ld_dbc : N;
 #pragma unroll
     for (int f = 0; f < FK; ++f) {
       const int r = tid + f * NT;                 // (k, n) of the tile, n fastest
       const int k = r / NP, n = r % NP;
-      const unsigned o = n < N ? 4u * (unsigned)(k * N + n) : kOOB;
-      gwb.st<kStream>(tDBC[r], o);
-      gwc.st<kStream>(tDBC[kSteps * NP + r], o);
+      const unsigned o = n < N ? 4u * (unsigned)(k * ldr + n) : kOOB;
+      if constexpr (ATOM) {
+        gbs.atomic_add(tDBC[r], o);
+        gcs.atomic_add(tDBC[kSteps * NP + r], o);
+      } else {
+        gbs.st<kStream>(tDBC[r], o);
+        gcs.st<kStream>(tDBC[kSteps * NP + r], o);
+      }
     }
   };
+  // finalize's output resources walked down with the loop (chunk ci + 1).
+  StreamCursor<ES> fdx(sdx, c_hi), fddt(sddt, c_hi);
+  StreamCursor<4> fbs(sBsum, c_hi), fcs(sCsum, c_hi);
 
   // Prologue: the segment's last chunk staged in LDS buffer 0, the one
   // before it in the staging registers.
@@ -329,8 +381,9 @@ bwd_kernel(BwdArgs a) {
   __syncthreads();
 
   const int nit = c_hi - c_lo;
+  ProgressPriority prio(nit);
   for (int i = 0; i < nit; ++i) {
-    progress_priority(i, nit);
+    prio.step(i);
     const int ci = c_hi - 1 - i;
     const float* s0 = lds + (i & 1) * BUF;
     const float* gB = s0 + oB + q * kSteps * NPL;
@@ -353,8 +406,9 @@ bwd_kernel(BwdArgs a) {
             u[j] = exp2_hw(dts[s] * a2[j]) * __builtin_fmaf(dys[s], Cq[s][j], u[j]);
         }
         if (m == 2) store_sub((i + 1) & 1, ci - 1);
-        if (m == 1) load_sub(ci - 2);
+        if (m == 1) load_next();
       }
+      load_down();
       __syncthreads();   // chunk ci-1 staged
       continue;
     }
@@ -375,7 +429,9 @@ bwd_kernel(BwdArgs a) {
           hs[4 * m + s][j] = Bq[s][j] * dtxs[s];       // b_k, turned into h_k below
         }
       }
-      if (m == 0) finalize(ci + 1, (i + 1) & 1);   // no-op stores past the sequence end
+      if (m == 0)   // no-op stores past the sequence end
+        finalize((i + 1) & 1, chunk_len(ci + 1), fdx.get(sdx), fddt.get(sddt), fbs.get(sBsum),
+                 fcs.get(sCsum));
     }
 #pragma unroll
     for (int k = 0; k < kSteps; ++k)
@@ -432,7 +488,7 @@ bwd_kernel(BwdArgs a) {
       *reinterpret_cast<float2*>(ts + (2 * m * 64 + lane) * 2) = make_float2(o[0], o[1]);
       *reinterpret_cast<float2*>(ts + ((2 * m + 1) * 64 + lane) * 2) = make_float2(o[2], o[3]);
       if (m == 2) store_sub((i + 1) & 1, ci - 1);  // unused when ci == 0
-      if (m == 1) load_sub(ci - 2);        // loads nothing when ci < 2
+      if (m == 1) load_next();             // chunk ci - 2: loads nothing when ci < 2
     }
     // h at the start of chunk ci-1, copied here and now (an opaque copy the
     // compiler cannot sink): ph's registers are then free for the next
@@ -441,7 +497,14 @@ bwd_kernel(BwdArgs a) {
     // store still in flight: a full memory drain per chunk.
 #pragma unroll
     for (int j = 0; j < NPL; ++j) hc[j] = opaque_copy(ph[j]);
-    load_h0(ci - 2);
+    load_states<NPL>(ph, GBuf(ck_next, ck_i > 0 ? slice_bytes : 0u), st_lane, nvalid);   // h0(ci-2)
+    ck_next -= slice;
+    --ck_i;
+    load_down();
+    fdx.down(sdx);
+    fddt.down(sddt);
+    fbs.down(sBsum);
+    fcs.down(sCsum);
     __syncthreads();   // tS / tDBC complete; chunk ci-1 staged
   }
   const size_t slot = (size_t)seg * a.batch + b;
@@ -451,14 +514,27 @@ bwd_kernel(BwdArgs a) {
     if (q == 0 && act) a.carrySdt[slot * D + d] = sdt_acc;
     return;
   }
-  finalize(c_lo, (nit - 1) & 1);
+  finalize((nit - 1) & 1, chunk_len(c_lo), sdx.at(c_lo), sddt.at(c_lo), sBsum.at(c_lo),
+           sCsum.at(c_lo));
 
   float out[NPL];
 #pragma unroll
   for (int j = 0; j < NPL; ++j) out[j] = -acc[j];
-  store_states<NPL>(GBuf(a.wsA + slot * slice, slice_bytes), st_lane, nvalid, out);
+  if constexpr (ATOM) {
+    // dAneg, or for the gated kernel dA = dAneg * softplus'(A) = dAneg * sigmoid(A).
+    const GBuf gda(a.daneg, slice_bytes);
+#pragma unroll
+    for (int j = 0; j < NPL; ++j) {
+      float v = out[j];
+      if constexpr (GATED)
+        v *= (act && j < nvalid) ? sigmoid_f(a.aneg[(size_t)d * N + n0 + j]) : 0.f;
+      gda.atomic_add(v, (st_lane != kOOB && j < nvalid) ? st_lane + 4u * j : kOOB);
+    }
+  } else {
+    store_states<NPL>(GBuf(a.wsA + slot * slice, slice_bytes), st_lane, nvalid, out);
+  }
   if constexpr (GATED) {
-    if (a.wsDB != nullptr) {
+    if (ATOM ? a.dbias != nullptr : a.wsDB != nullptr) {
       // The block's sum of the raw dt gradient per channel: the NT / 32
       // threads of channel cc (tid = cc + 32 r) added in a fixed order.
       static_assert(NT % kCH == 0, "finalize tasks keep their channel");
@@ -469,7 +545,10 @@ bwd_kernel(BwdArgs a) {
         float sum = 0.f;
 #pragma unroll
         for (int r = 0; r < NT / kCH; ++r) sum += lds[r * kCH + tid];
-        a.wsDB[slot * D + d0 + tid] = sum;
+        if constexpr (ATOM)
+          GBuf(a.dbias, 4u * (unsigned)D).atomic_add(sum, 4u * (unsigned)(d0 + tid));
+        else
+          a.wsDB[slot * D + d0 + tid] = sum;
       }
     }
   }
@@ -537,6 +616,31 @@ bwd_reduce_kernel(const float* __restrict__ wsB, const float* __restrict__ wsC,
       float s = 0.f;
       for (int bb = 0; bb < batch; ++bb) s += wsDB[(size_t)bb * Dn + j];
       dbias[j] = s;
+    }
+  }
+}
+
+// Zero the gradients the atomic backward adds into: dB and dC (rows x N,
+// rows ld apart), dAneg (A floats) and the dt-bias gradient (Dn floats; null
+// when Dn is 0). A kernel rather than hipMemsetAsync, so that the launch
+// sequence stays capturable in a HIP graph without memset nodes.
+template <int UNUSED = 0>
+__global__ void __launch_bounds__(256)
+zero_grads_kernel(float* __restrict__ dB, float* __restrict__ dC, long long rows, int N,
+                  long long ld, float* __restrict__ daneg, long long A, float* __restrict__ dbias,
+                  int Dn) {
+  const long long S = rows * N;
+  const long long stride = (long long)gridDim.x * blockDim.x;
+  for (long long i = (long long)blockIdx.x * blockDim.x + threadIdx.x; i < S + A + Dn;
+       i += stride) {
+    if (i < S) {
+      const long long o = ld == N ? i : (i / N) * ld + i % N;
+      dB[o] = 0.f;
+      dC[o] = 0.f;
+    } else if (i < S + A) {
+      daneg[i - S] = 0.f;
+    } else {
+      dbias[i - S - A] = 0.f;
     }
   }
 }

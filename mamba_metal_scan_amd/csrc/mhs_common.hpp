@@ -191,13 +191,33 @@ __device__ __forceinline__ void wave_lds_sync() {
 // longer hidden by other waves. A block ahead of the others drops below them
 // and yields its issue slots until they catch up. (The wave's own
 // arbitration priority only.)
-__device__ __forceinline__ void progress_priority(int i, int n) {
-  const int q = (10 * i) / max(n, 1);
-  if (q < 4) __builtin_amdgcn_s_setprio(3);
-  else if (q < 7) __builtin_amdgcn_s_setprio(2);
-  else if (q < 9) __builtin_amdgcn_s_setprio(1);
-  else __builtin_amdgcn_s_setprio(0);
-}
+//
+// The levels change only at three iterations, computed once before the walk
+// (iteration i has level 3 - #{k : i >= ceil(k n / 10), k = 4, 7, 9}): per
+// iteration the walk pays one scalar compare, not a division and a chain of
+// branches (scalar instructions take issue slots from the wave's VALU work).
+struct ProgressPriority {
+  int th[3];   // first iterations of levels 2, 1, 0
+  int next;    // the next iteration at which the level changes
+  __device__ __forceinline__ explicit ProgressPriority(int n) {
+    n = max(n, 1);
+    th[0] = (4 * n + 9) / 10;
+    th[1] = (7 * n + 9) / 10;
+    th[2] = (9 * n + 9) / 10;
+    next = 0;
+  }
+  __device__ __forceinline__ void step(int i) {
+    if (i != next) return;
+    const int lvl = 3 - (i >= th[0]) - (i >= th[1]) - (i >= th[2]);
+    switch (lvl) {
+      case 3: __builtin_amdgcn_s_setprio(3); break;
+      case 2: __builtin_amdgcn_s_setprio(2); break;
+      case 1: __builtin_amdgcn_s_setprio(1); break;
+      default: __builtin_amdgcn_s_setprio(0); break;
+    }
+    next = i < th[0] ? th[0] : i < th[1] ? th[1] : i < th[2] ? th[2] : 0x7FFFFFFF;
+  }
+};
 
 // An opaque register copy. A loop-carried value that comes from a global
 // load on some path into the loop (a state or parameter read before it) is
@@ -307,6 +327,13 @@ struct GBuf {
   __device__ __forceinline__ void st(float v, unsigned byte_off) const {
     __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(v), r, byte_off, 0, POL);
   }
+  // fp32 atomic add at device (agent) scope, no return value
+  // (buffer_atomic_add_f32 without glc; no cache-policy bits, as the compiler
+  // emits for an agent-scope atomicrmw on gfx950). Out of range offsets are
+  // dropped like stores.
+  __device__ __forceinline__ void atomic_add(float v, unsigned byte_off) const {
+    __builtin_amdgcn_raw_ptr_buffer_atomic_fadd_f32(v, r, byte_off, 0, 0);
+  }
 };
 
 // Element storage of the (batch, T, D) and (batch, T, N) activations: fp32
@@ -342,6 +369,56 @@ template <int ES>
 __device__ __forceinline__ const float* elem_at(const void* base, size_t idx) {
   return reinterpret_cast<const float*>(static_cast<const char*>(base) + idx * ES);
 }
+
+// One (batch, T, ·) operand walked a chunk of `steps` steps at a time. The
+// resource over chunk i covers its rows from column c0 (row stride ld, width
+// columns): [p0 + i * step, + bytes(i)), with bytes the full chunk's, the
+// short last chunk's (index ilast, last_len rows) or 0 for indices outside
+// [lo, hi). The base is linear in i (no clamping: outside the range the
+// resource is empty and never dereferenced), so that the compiler turns
+// i * step into one 64-bit scalar add per operand and iteration instead of
+// the 64-bit product (row0 + t0) * ld (scalar instructions take issue slots
+// from the wave's VALU work).
+template <int ES>
+struct SubStream {
+  const char* p0;
+  size_t step;
+  unsigned full, last;
+  int lo, hi, ilast;
+  __device__ __forceinline__ SubStream(const void* base, size_t row, int ld, int c0, int width,
+                                       int steps, int lo_, int hi_, int ilast_, int last_len)
+      : p0(static_cast<const char*>(base) + ((size_t)row * ld + c0) * ES),
+        step((size_t)steps * ld * ES),
+        full((unsigned)ES * (unsigned)((steps - 1) * ld + width - c0)),
+        last((unsigned)ES * (unsigned)((last_len - 1) * ld + width - c0)),
+        lo(lo_), hi(hi_), ilast(ilast_) {}
+  __device__ __forceinline__ unsigned bytes(int i) const {
+    return i < lo || i >= hi ? 0u : i == ilast ? last : full;
+  }
+  __device__ __forceinline__ const char* base(int i) const {
+    return p0 + (ptrdiff_t)i * (ptrdiff_t)step;
+  }
+  __device__ __forceinline__ GBuf at(int i) const {
+    return GBuf(reinterpret_cast<const float*>(base(i)), bytes(i));
+  }
+};
+
+// A SubStream walked backwards one chunk per loop iteration: the current
+// chunk's pointer, moved down by one step (a 64-bit scalar subtract) instead
+// of recomputed from the index.
+template <int ES>
+struct StreamCursor {
+  const char* p;
+  int i;
+  __device__ __forceinline__ StreamCursor(const SubStream<ES>& s, int i0) : p(s.base(i0)), i(i0) {}
+  __device__ __forceinline__ GBuf get(const SubStream<ES>& s) const {
+    return GBuf(reinterpret_cast<const float*>(p), s.bytes(i));
+  }
+  __device__ __forceinline__ void down(const SubStream<ES>& s) {
+    p -= s.step;
+    --i;
+  }
+};
 
 // NPL consecutive states of one lane at byte offset `off` (kOOB: none);
 // states at or beyond `nvalid` are padding and are not stored.

@@ -88,13 +88,21 @@ __host__ __device__ constexpr int fwd_lds_floats(int G, int NPL) {
 // on sub-chunk ends (and the last one on the final state): no per-step tests.
 // GATED: dt and Aneg come from the block's raw projections (see FwdArgs); the
 // staging threads gate each dt once per block as they move it to LDS.
-// FCARRY: the carry pass of the time segments (see FwdArgs): blocks of
-// segments 0..nseg-2 scan their segment from zero and write only its end
-// state and sum of dt (no C, no y, no checkpoints).
+// PASS: what the kernel produces.
+//   kPassFull:  y, checkpoints, final state.
+//   kPassCarry: the carry pass of the time segments (see FwdArgs): blocks of
+//               segments 0..nseg-2 scan their segment from zero and write
+//               only its end state and sum of dt (no C, no y, no checkpoints).
+//   kPassCkpt:  checkpoints only (no C, no y): the backward's recompute of
+//               finer checkpoints for strides above its register window.
 // ES: bytes per element of x, dt, B, C and y (4: fp32, 2: bf16).
-template <int NPL, int G, int MINW, bool KALIGNED, bool GATED, bool FCARRY = false, int ES = 4>
+constexpr int kPassFull = 0, kPassCarry = 1, kPassCkpt = 2;
+
+template <int NPL, int G, int MINW, bool KALIGNED, bool GATED, int PASS = kPassFull, int ES = 4>
 __global__ void __launch_bounds__(64 * G, MINW)
 fwd_kernel(FwdArgs a) {
+  constexpr bool FCARRY = PASS == kPassCarry;
+  constexpr bool NOY = PASS != kPassFull;   // no C operand, no y
   constexpr int NT = 64 * G;                    // threads
   constexpr int NP = 2 * G * NPL;               // padded states
   constexpr int BUF = fwd_buf_floats(G, NPL);
@@ -139,31 +147,24 @@ fwd_kernel(FwdArgs a) {
   float pb[PERS], pc[PERS];
   float gbias[PER];   // GATED: the dt bias of each staging task's channel
   if constexpr (GATED) qdt.load_channel(gbias, a.dt_bias, d0);
-  // Sub-chunk i of the segment (any i >= 0): first step and length (0 past
-  // the segment).
-  auto sub_t0 = [&](int i) { return min(t_beg + max(i, 0) * kSteps, T - 1); };
-  auto sub_len = [&](int i) {
-    return i < 0 ? 0 : max(0, min(kSteps, t_end - t_beg - i * kSteps));
-  };
-  // Resource over one sub-chunk of a (batch, T, D) tensor of row stride ld
-  // (channels d0 .. D-1 of its rows).
-  auto sub_buf = [&](const void* base, int i, int ld) {
-    const int len = sub_len(i);
-    if constexpr (!GATED)   // contiguous (ld == D)
-      return GBuf(elem_at<ES>(base, (row0 + sub_t0(i)) * D + d0),
-                  len > 0 ? (unsigned)ES * (unsigned)(len * D - d0) : 0u);
-    return GBuf(elem_at<ES>(base, (row0 + sub_t0(i)) * ld + d0),
-                len > 0 ? (unsigned)ES * (unsigned)((len - 1) * ld + D - d0) : 0u);
-  };
+  // Sub-chunk i of the segment (any i >= 0): its length (0 past the segment).
+  const int last_len = t_end - t_beg - (nsub - 1) * kSteps;
+  auto sub_len = [&](int i) { return i < nsub - 1 ? kSteps : i == nsub - 1 ? last_len : 0; };
+  // Resources over sub-chunk i of the operands (channels d0 .. D-1 of the
+  // (batch, T, D) ones, all N states of B and C; see SubStream).
+  const size_t r0 = row0 + t_beg;
+  const int il = nsub - 1;
+  const SubStream<ES> sx(a.x, r0, D, d0, D, kSteps, 0, nsub, il, last_len);
+  const SubStream<ES> sdt(a.dt, r0, ld_dt, d0, D, kSteps, 0, nsub, il, last_len);
+  const SubStream<ES> sB(a.B, r0, ld_bc, 0, N, kSteps, 0, nsub, il, last_len);
+  const SubStream<ES> sC(a.C, r0, ld_bc, 0, N, kSteps, 0, nsub, il, last_len);
+  const SubStream<ES> sy(a.y != nullptr ? a.y : a.x, r0, D, d0, D, kSteps, 0,
+                         a.y != nullptr ? nsub : 0, il, last_len);
   auto load_sub = [&](int i) {            // global -> staging registers
-    const int len = sub_len(i);
-    const unsigned sbytes = !GATED ? (unsigned)ES * (unsigned)(len * N)
-                            : len > 0 ? (unsigned)ES * (unsigned)((len - 1) * ld_bc + N) : 0u;
-    ql.load(px, sub_buf(a.x, i, D));
-    qdt.load(pd, sub_buf(a.dt, i, ld_dt));
-    rl.load(pb, GBuf(elem_at<ES>(a.B, (row0 + sub_t0(i)) * ld_bc), sbytes));
-    if constexpr (!FCARRY)
-      rl.load(pc, GBuf(elem_at<ES>(a.C, (row0 + sub_t0(i)) * ld_bc), sbytes));
+    ql.load(px, sx.at(i));
+    qdt.load(pd, sdt.at(i));
+    rl.load(pb, sB.at(i));
+    if constexpr (!NOY) rl.load(pc, sC.at(i));
   };
   auto store_sub = [&](int i) {           // staging registers -> LDS buffer i&1
     float* buf = lds + (i & 1) * BUF;
@@ -171,7 +172,7 @@ fwd_kernel(FwdArgs a) {
     ql.store_cm(buf, pd);
     ql.store_cm_product(buf + kCH * kSteps, pd, px);
     rl.store(buf + 2 * kCH * kSteps, pb);
-    if constexpr (!FCARRY) rl.store(buf + 2 * kCH * kSteps + kSteps * NP, pc);
+    if constexpr (!NOY) rl.store(buf + 2 * kCH * kSteps + kSteps * NP, pc);
   };
   // y of sub-chunk i: every wave leaves, per channel and step, the sum over
   // its two half-waves (added in registers), in a step-pair-major tile
@@ -196,7 +197,7 @@ fwd_kernel(FwdArgs a) {
     }
   };
   auto y_write = [&](int i) {
-    const GBuf yo = sub_buf(a.y != nullptr ? a.y : a.x, a.y != nullptr ? i : -1, D);
+    const GBuf yo = sy.at(i);
 #pragma unroll
     for (int f = 0; f < YT; ++f) {
       const int t0 = tid + f * NT;
@@ -252,8 +253,9 @@ fwd_kernel(FwdArgs a) {
   int next_ck = a.ckpt != nullptr ? min((t_beg / a.K + 1) * a.K, T) : kDone;
   const float* ck_base = a.ckpt != nullptr ? a.ckpt + (size_t)b * a.nchunk * ck_stride : a.aneg;
   const float* ck_ptr = ck_base + (size_t)(t_beg / a.K) * ck_stride;
+  ProgressPriority prio(nsub);
   for (int i = 0; i < nsub; ++i) {
-    progress_priority(i, nsub);
+    prio.step(i);
     const int t0 = t_beg + i * kSteps;
     const float* buf = lds + (i & 1) * BUF;
     const float* cDT = buf;
@@ -270,7 +272,7 @@ fwd_kernel(FwdArgs a) {
 #pragma unroll
       for (int j = 0; j < NPL; ++j) {
         qB[j] = lds4(gB + 4 * m * NPL + 4 * j);
-        if constexpr (!FCARRY) qC[j] = lds4(gC + 4 * m * NPL + 4 * j);
+        if constexpr (!NOY) qC[j] = lds4(gC + 4 * m * NPL + 4 * j);
       }
     };
     read_quad(0);
@@ -284,7 +286,7 @@ fwd_kernel(FwdArgs a) {
       f4_to(bxs, qbx);
 #pragma unroll
       for (int e = 0; e < 4 * NPL; ++e) {
-        const float4 tb = qB[e / 4], tc = FCARRY ? tb : qC[e / 4];
+        const float4 tb = qB[e / 4], tc = NOY ? tb : qC[e / 4];
         const float vb[4] = {tb.x, tb.y, tb.z, tb.w}, vc[4] = {tc.x, tc.y, tc.z, tc.w};
         Bq[e / NPL][e % NPL] = vb[e % 4];
         Cq[e / NPL][e % NPL] = vc[e % 4];
@@ -307,12 +309,12 @@ fwd_kernel(FwdArgs a) {
 #pragma unroll
         for (int j = 0; j < NPL; ++j) {
           h[j] = __builtin_fmaf(da[s][j], h[j], u[s][j]);
-          if constexpr (!FCARRY) acc = __builtin_fmaf(Cq[s][j], h[j], acc);
+          if constexpr (!NOY) acc = __builtin_fmaf(Cq[s][j], h[j], acc);
           hq[s][j] = h[j];
         }
         yq[s] = acc;
       }
-      if constexpr (!FCARRY) {
+      if constexpr (!NOY) {
         // Add the two half-waves (same channels, different states): lanes
         // 0-31 end with steps 0, 1 of the quad, lanes 32-63 with steps 2, 3.
         const auto s02 = __builtin_amdgcn_permlane32_swap(__float_as_uint(yq[0]),
@@ -328,8 +330,8 @@ fwd_kernel(FwdArgs a) {
       // scheduling region. Unconditional: past either end of the sequence the
       // resources are empty (loads return 0, stores are dropped) and the LDS
       // buffer written is not read again.
-      if (!FCARRY && m == 0) y_read(i - 1);
-      if (!FCARRY && m == 1) y_write(i - 1);
+      if (!NOY && m == 0) y_read(i - 1);
+      if (!NOY && m == 1) y_write(i - 1);
       if (m == 1) store_sub(i + 1);
       if (m == 2) load_sub(i + 2);
 
@@ -368,8 +370,10 @@ fwd_kernel(FwdArgs a) {
   if (KALIGNED && a.ckpt != nullptr && last_seg)
     store_states<NPL>(GBuf(ck_base + (size_t)(a.nchunk - 1) * ck_stride, slice_bytes), ck_lane,
                       nvalid, h);
-  y_read(nsub - 1);
-  y_write(nsub - 1);
+  if constexpr (!NOY) {
+    y_read(nsub - 1);
+    y_write(nsub - 1);
+  }
 
   if (a.h_last != nullptr && last_seg)
     store_states<NPL>(GBuf(a.h_last + (size_t)b * ck_stride, slice_bytes), ck_lane, nvalid, h);

@@ -18,15 +18,17 @@
   X(PREFIX, 4, 4, 2, ES) X(PREFIX, 4, 5, 2, ES) X(PREFIX, 4, 6, 2, ES)                 \
   X(PREFIX, 4, 7, 2, ES) X(PREFIX, 4, 8, 2, ES)
 
-// Forward: checkpoint stride aligned / any, ungated / gated, and the carry
-// pass of the time segments (ungated / gated).
-#define MHS_FWD_INST(PREFIX, NPL, G, MINW, ES)                                                 \
-  PREFIX template __global__ void fwd_kernel<NPL, G, MINW, true, false, false, ES>(FwdArgs);   \
-  PREFIX template __global__ void fwd_kernel<NPL, G, MINW, false, false, false, ES>(FwdArgs);  \
-  PREFIX template __global__ void fwd_kernel<NPL, G, MINW, true, true, false, ES>(FwdArgs);    \
-  PREFIX template __global__ void fwd_kernel<NPL, G, MINW, false, true, false, ES>(FwdArgs);   \
-  PREFIX template __global__ void fwd_kernel<NPL, G, MINW, true, false, true, ES>(FwdArgs);    \
-  PREFIX template __global__ void fwd_kernel<NPL, G, MINW, true, true, true, ES>(FwdArgs);
+// Forward: checkpoint stride aligned / any, ungated / gated; the carry pass
+// of the time segments and the checkpoint-only pass (ungated / gated).
+#define MHS_FWD_INST(PREFIX, NPL, G, MINW, ES)                                                   \
+  PREFIX template __global__ void fwd_kernel<NPL, G, MINW, true, false, kPassFull, ES>(FwdArgs);  \
+  PREFIX template __global__ void fwd_kernel<NPL, G, MINW, false, false, kPassFull, ES>(FwdArgs); \
+  PREFIX template __global__ void fwd_kernel<NPL, G, MINW, true, true, kPassFull, ES>(FwdArgs);   \
+  PREFIX template __global__ void fwd_kernel<NPL, G, MINW, false, true, kPassFull, ES>(FwdArgs);  \
+  PREFIX template __global__ void fwd_kernel<NPL, G, MINW, true, false, kPassCarry, ES>(FwdArgs); \
+  PREFIX template __global__ void fwd_kernel<NPL, G, MINW, true, true, kPassCarry, ES>(FwdArgs);  \
+  PREFIX template __global__ void fwd_kernel<NPL, G, MINW, true, false, kPassCkpt, ES>(FwdArgs);  \
+  PREFIX template __global__ void fwd_kernel<NPL, G, MINW, true, true, kPassCkpt, ES>(FwdArgs);
 
 // Backward: ungated / gated, gradient pass / adjoint-carry pass.
 #define MHS_BWD_INST(PREFIX, NPL, G, MINW, ES)                                    \
@@ -34,3 +36,9 @@
   PREFIX template __global__ void bwd_kernel<NPL, G, MINW, true, false, ES>(BwdArgs);  \
   PREFIX template __global__ void bwd_kernel<NPL, G, MINW, false, true, ES>(BwdArgs);  \
   PREFIX template __global__ void bwd_kernel<NPL, G, MINW, true, true, ES>(BwdArgs);
+
+// Backward with fp32 atomics for dB, dC, dAneg and the dt bias: ungated /
+// gated.
+#define MHS_BWD_ATOM_INST(PREFIX, NPL, G, MINW, ES)                                    \
+  PREFIX template __global__ void bwd_kernel<NPL, G, MINW, false, false, ES, true>(BwdArgs); \
+  PREFIX template __global__ void bwd_kernel<NPL, G, MINW, true, false, ES, true>(BwdArgs);

@@ -13,8 +13,8 @@ import pytest
 import torch
 import torch.nn.functional as F
 
-from helpers import assert_close
-from mamba_metal_scan_amd import mamba_inner, selective_scan_gated, selective_scan_hip
+from helpers import assert_close, assert_same, reduction
+from mamba_metal_scan_amd import _native, mamba_inner, selective_scan_gated, selective_scan_hip
 
 pytestmark = pytest.mark.gpu
 DEV = "cuda"
@@ -188,30 +188,35 @@ def _capture(fn):
     return graph, outs
 
 
+@pytest.mark.parametrize("mode", ["fixed", "atomic"])
 @pytest.mark.parametrize("shape", [(4, 256, 512, 16), (1, 1024, 128, 16)])
-def test_scan_fwd_bwd_replays_from_a_hip_graph(shape):
+def test_scan_fwd_bwd_replays_from_a_hip_graph(shape, mode):
     """Forward + backward launches captured once and replayed three times,
     with other eager scans and synchronizations between the replays: every
-    replay equals the eager result bit for bit. The second shape is small
-    enough to run in time segments (forward workspace, carry kernels)."""
+    replay equals the eager result bit for bit (with the atomic reduction:
+    the atomically reduced sums within RED_TOL; their zero-fill is a kernel,
+    captured with the rest). The second shape is small enough to run in time
+    segments (forward workspace, carry kernels)."""
     bt, t_len, d, n = shape
-    print(f"[case] HIP graph scan fwd+bwd {shape}", flush=True)
+    atomic = mode == "atomic"
+    print(f"[case] HIP graph scan fwd+bwd {shape} {mode}", flush=True)
     x, dt, aneg, b_in, c_in, dy = _scan_args(bt, t_len, d, n, seed=7)
 
     def step(x=x):
         y, ckpt, h_last = OPS.scan_fwd(x, dt, aneg, b_in, c_in, 16, True)
         return (y, h_last) + tuple(OPS.scan_bwd(x, dt, aneg, b_in, c_in, dy, None, ckpt, 16))
 
-    ref = [t.clone() for t in step()]
-    graph, outs = _capture(step)
-    for rep in range(3):
-        other = step(x * (0.5 + rep))     # eager work on other inputs between replays
-        torch.cuda.synchronize()
-        graph.replay()
-        torch.cuda.synchronize()
-        for name, a, b in zip(("y", "h_last", "dx", "ddt", "dAneg", "dB", "dC"), outs, ref):
-            assert torch.equal(a, b), f"replay {rep}: {name} differs"
-        del other
+    with reduction(_native.REDUCTION_ATOMIC if atomic else _native.REDUCTION_FIXED):
+        ref = [t.clone() for t in step()]
+        graph, outs = _capture(step)
+        for rep in range(3):
+            other = step(x * (0.5 + rep))     # eager work on other inputs between replays
+            torch.cuda.synchronize()
+            graph.replay()
+            torch.cuda.synchronize()
+            for name, a, b in zip(("y", "h_last", "dx", "ddt", "dAneg", "dB", "dC"), outs, ref):
+                assert_same(name, a, b, atomic)
+            del other
 
 
 def test_inner_block_fwd_bwd_replays_from_a_hip_graph():
@@ -233,15 +238,18 @@ def test_inner_block_fwd_bwd_replays_from_a_hip_graph():
         return (out,) + tuple(torch.autograd.grad(out, leaves, dout))
 
     # The eager runs use their own leaf tensors: the captured leaves' autograd
-    # nodes then belong to the capture's streams only.
+    # nodes then belong to the capture's streams only. Fixed-order reduction:
+    # the atomically reduced dB, dC feed the weight GEMMs, so with atomics
+    # nearly every output would carry their rounding.
     eager = [p.to(DEV).requires_grad_(True) for p in params]
     leaves = [p.to(DEV).requires_grad_(True) for p in params]
-    ref = [t.detach().clone() for t in step(eager)]
-    graph, outs = _capture(lambda: step(leaves))
-    for rep in range(3):
-        step(eager)                       # eager work between replays
-        torch.cuda.synchronize()
-        graph.replay()
-        torch.cuda.synchronize()
-        for i, (a, b) in enumerate(zip(outs, ref)):
-            assert torch.equal(a, b), f"replay {rep}: output {i} differs"
+    with reduction(_native.REDUCTION_FIXED):
+        ref = [t.detach().clone() for t in step(eager)]
+        graph, outs = _capture(lambda: step(leaves))
+        for rep in range(3):
+            step(eager)                       # eager work between replays
+            torch.cuda.synchronize()
+            graph.replay()
+            torch.cuda.synchronize()
+            for i, (a, b) in enumerate(zip(outs, ref)):
+                assert torch.equal(a, b), f"replay {rep}: output {i} differs"

@@ -11,7 +11,7 @@ import numpy as np
 import pytest
 import torch
 
-from helpers import ATOL, RTOL, TOL, assert_close, rel_err, to_np
+from helpers import ATOL, RED_TOL, RTOL, TOL, assert_close, assert_same, reduction, rel_err, to_np
 from mamba_metal_scan_amd import _native, selective_scan, selective_scan_hip, selective_scan_ref
 from oracle import oracle
 
@@ -37,6 +37,19 @@ GROUPED_SHAPES = [(16, 96, 1500, 16), (12, 64, 2048, 16), (6, 50, 3000, 16)]
 
 def _to_dev(arrs):
     return [torch.from_numpy(a).to(DEV) for a in arrs]
+
+
+def _bench_inputs(bt, t_len, d, n, seed):
+    """The benchmark's seeded inputs (torch generator on the CPU, then moved):
+    x, B, C, dy ~ N(0,1), dt = softplus(N(-4,1)), Aneg[d,n] = n+1."""
+    g = torch.Generator().manual_seed(seed)
+    x = torch.randn(bt, t_len, d, generator=g)
+    dt = torch.nn.functional.softplus(torch.randn(bt, t_len, d, generator=g) - 4.0)
+    aneg = torch.arange(1, n + 1, dtype=torch.float32).repeat(d, 1)
+    b_in = torch.randn(bt, t_len, n, generator=g)
+    c_in = torch.randn(bt, t_len, n, generator=g)
+    dy = torch.randn(bt, t_len, d, generator=g)
+    return [t.to(DEV) for t in (x, dt, aneg, b_in, c_in, dy)]
 
 
 def _run_hip(inp, dy, chunk=None, dh_last=None):
@@ -153,14 +166,87 @@ def test_training_shape_fwd_bwd_matches_the_oracle():
     print("[errors vs fp64]", {k: f"{v:.2e}" for k, v in errs.items()}, flush=True)
 
 
-def test_backward_is_bitwise_deterministic():
+def test_training_shape_matches_the_torch_reference_in_fp32():
+    """16x512x1536x16: the HIP scan against selective_scan(impl="torch") in
+    fp32 on the same device and the same seeded inputs, y and all five
+    gradients within max relative error 1e-4 (max|hip - torch| / max|torch|)."""
+    bt, t_len, d, n = 16, 512, 1536, 16
+    print("[case] torch-ref parity 16x512x1536x16", flush=True)
+    inp = _bench_inputs(bt, t_len, d, n, seed=31)
+    dy = inp.pop()
+    y, _, g_hip = _run_hip(inp, dy)
+    leaves = [t.clone().requires_grad_(True) for t in inp]
+    ref = selective_scan(*leaves, impl="torch")
+    g_ref = torch.autograd.grad(ref, leaves, grad_outputs=dy)
+    torch.cuda.synchronize()
+    errs = {"y": assert_close("y", y, ref)}
+    for name, g, r in zip(("dx", "ddt", "dAneg", "dB", "dC"), g_hip, g_ref):
+        errs[name] = assert_close(name, g, r)
+    print("[errors vs torch fp32]", {k: f"{v:.2e}" for k, v in errs.items()}, flush=True)
+
+
+@pytest.mark.parametrize("chunk", [1, 7, 64, 511, 512])
+def test_training_shape_stride_sweep(chunk):
+    """16x512x1536x16 at checkpoint strides 1, 7, 64, 511, 512 against
+    stride 16 (fixed-order reduction): y, the state and every gradient agree
+    to fp32 rounding (the backward recomputes the same states from the
+    checkpoints, whatever their stride)."""
+    bt, t_len, d, n = 16, 512, 1536, 16
+    print(f"[case] 16x512x1536x16 chunk {chunk} vs 16", flush=True)
+    x, dt, aneg, b_in, c_in, dy = _bench_inputs(bt, t_len, d, n, seed=7)
+
+    def run(k):
+        y, ckpt, h_last = torch.ops.mamba_hip.scan_fwd(x, dt, aneg, b_in, c_in, k, True)
+        assert ckpt.shape == (bt, (t_len + k - 1) // k, d, n)
+        grads = torch.ops.mamba_hip.scan_bwd(x, dt, aneg, b_in, c_in, dy, None, ckpt, k)
+        return (y, h_last) + tuple(grads)
+
+    with reduction(_native.REDUCTION_FIXED):
+        base, other = run(16), run(chunk)
+    torch.cuda.synchronize()
+    for name, a, b in zip(("y", "h_last", "dx", "ddt", "dAneg", "dB", "dC"), other, base):
+        assert_close(name, a, b, 1e-6)
+
+
+@pytest.mark.parametrize("mode", ["fixed", "atomic"])
+def test_backward_determinism(mode):
+    """Fixed-order reduction: every gradient bit for bit equal run to run.
+    Atomic reduction: dx and ddt still bit for bit; dB, dC, dAneg within
+    RED_TOL (their rounding depends on the order the atomics land in)."""
+    atomic = mode == "atomic"
     arrs = oracle.make_inputs(4, 200, 300, 16, seed=77, style="bench")
     inp = _to_dev(arrs)
     dy = torch.randn(4, 200, 300, device=DEV, generator=torch.Generator(DEV).manual_seed(0))
-    g1 = _run_hip(inp, dy)[2]
-    g2 = _run_hip(inp, dy)[2]
-    for a, b in zip(g1, g2):
-        assert torch.equal(a, b)
+    with reduction(_native.REDUCTION_ATOMIC if atomic else _native.REDUCTION_FIXED):
+        g1 = _run_hip(inp, dy)[2]
+        g2 = _run_hip(inp, dy)[2]
+    for name, a, b in zip(("dx", "ddt", "dAneg", "dB", "dC"), g1, g2):
+        assert_same(name, a, b, atomic)
+
+
+def test_atomic_and_fixed_order_reductions_agree_at_the_training_shape():
+    """16x512x1536x16: the atomic backward against the fixed-order one (dx,
+    ddt bit for bit; the reduced sums within RED_TOL), and the atomic path's
+    run-to-run spread over five backward calls, printed."""
+    bt, t_len, d, n = 16, 512, 1536, 16
+    print("[case] reductions at 16x512x1536x16", flush=True)
+    x, dt, aneg, b_in, c_in, dy = _bench_inputs(bt, t_len, d, n, seed=2024)
+    _, ckpt, _ = torch.ops.mamba_hip.scan_fwd(x, dt, aneg, b_in, c_in, 16, True)
+    bwd = lambda: torch.ops.mamba_hip.scan_bwd(x, dt, aneg, b_in, c_in, dy, None, ckpt, 16)
+    with reduction(_native.REDUCTION_FIXED):
+        fixed = bwd()
+    with reduction(_native.REDUCTION_ATOMIC):
+        runs = [bwd() for _ in range(5)]
+    torch.cuda.synchronize()
+    names = ("dx", "ddt", "dAneg", "dB", "dC")
+    for name, a, b in zip(names, runs[0], fixed):
+        assert_same(name, a, b, atomic=True)
+    spread = {name: max(rel_err(r[i], runs[0][i]) for r in runs[1:])
+              for i, name in enumerate(names)}
+    print("[atomic run-to-run max rel diff]", {k: f"{v:.1e}" for k, v in spread.items()},
+          flush=True)
+    assert spread["dx"] == 0.0 and spread["ddt"] == 0.0
+    assert max(spread.values()) <= RED_TOL
 
 
 @pytest.mark.parametrize("npl,n", [(2, 16), (4, 16), (2, 7), (4, 7), (4, 24), (2, 32)])

@@ -59,15 +59,28 @@ def test_chunk_arithmetic():
 
 
 def test_workspace_size_formula():
-    """dB/dC block partials (48 blocks of 32 channels) + dAneg batch partials
-    + the gated dt-bias batch partials, + fine checkpoints when the stride
-    exceeds the 16-step window."""
+    """Fixed-order reduction: dB/dC block partials (48 blocks of 32 channels)
+    + dAneg batch partials + the gated dt-bias batch partials. Atomic
+    reduction: only the fp32 dB/dC sums a bf16 backward rounds from. Either
+    way + fine checkpoints when the stride exceeds the 16-step window."""
     lib = _native.library()
     nblk, s, a = 48, 16 * 512 * 16, 16 * 1536 * 16
-    base = 2 * nblk * s * 4 + a * 4 + 16 * 1536 * 4
-    assert lib.mhs_scan_bwd_workspace_bytes(16, 512, 1536, 16, 16) == base
-    assert lib.mhs_scan_bwd_workspace_bytes(16, 512, 1536, 16, 64) == base + 32 * a * 4
-    assert lib.mhs_scan_bwd_workspace_bytes(16, 512, 1536, 0, 16) == 0
+    try:
+        _native.set_reduction(_native.REDUCTION_FIXED)
+        assert lib.mhs_deterministic() == 1
+        base = 2 * nblk * s * 4 + a * 4 + 16 * 1536 * 4
+        assert lib.mhs_scan_bwd_workspace_bytes(16, 512, 1536, 16, 16) == base
+        assert lib.mhs_scan_bwd_workspace_bytes(16, 512, 1536, 16, 64) == base + 32 * a * 4
+        assert lib.mhs_scan_bwd_workspace_bytes(16, 512, 1536, 0, 16) == 0
+        _native.set_reduction(_native.REDUCTION_ATOMIC)
+        assert lib.mhs_deterministic() == 0
+        assert lib.mhs_scan_bwd_workspace_bytes(16, 512, 1536, 16, 16) == 2 * s * 4
+        assert lib.mhs_scan_bwd_workspace_bytes(16, 512, 1536, 16, 64) == 2 * s * 4 + 32 * a * 4
+    finally:
+        _native.set_reduction(_native.REDUCTION_AUTO)
+    assert lib.mhs_deterministic() == 1      # automatic: the fixed order
+    with pytest.raises(_native.HipScanError, match="reduction mode"):
+        _native.set_reduction(3)
 
 
 def test_set_variant_rejects_unknown_splits():
@@ -188,25 +201,31 @@ def test_time_segments_knob_and_workspace():
     def ru(v):
         return (v + 255) // 256 * 256
 
-    def expect(bt, t, d, n, segs):
-        nblk = (d + 31) // 32
+    def expect(bt, t, d, n, segs, atomic):
+        nblk = 1 if atomic else (d + 31) // 32
         s_ = bt * t * n
         a = bt * d * n
-        base = 2 * ru(nblk * s_ * 4) + ru(segs * a * 4) + ru(segs * bt * d * 4)
+        base = 2 * ru(nblk * s_ * 4)
+        if not atomic:
+            base += ru(segs * a * 4) + ru(segs * bt * d * 4)
         if segs > 1:
             base += ru(segs * a * 4) + ru(segs * bt * d * 4)
         return base
 
-    assert lib.mhs_scan_bwd_workspace_bytes(16, 512, 1536, 16, 16) == expect(16, 512, 1536, 16, 1)
-    assert lib.mhs_scan_bwd_workspace_bytes(4, 16384, 2048, 16, 16) == expect(4, 16384, 2048, 16, 3)
-    try:
-        _native.set_time_segments(3)
-        assert lib.mhs_scan_bwd_workspace_bytes(16, 512, 1536, 16, 16) == expect(16, 512, 1536, 16, 3)
-        # 5 chunks at most: 5 segments of one chunk
-        _native.set_time_segments(8)
-        assert lib.mhs_scan_bwd_workspace_bytes(1, 80, 64, 16, 16) == expect(1, 80, 64, 16, 5)
-    finally:
-        _native.set_time_segments(0)
+    for mode, atomic in ((_native.REDUCTION_FIXED, False), (_native.REDUCTION_ATOMIC, True)):
+        try:
+            _native.set_reduction(mode)
+            ws = lib.mhs_scan_bwd_workspace_bytes
+            assert ws(16, 512, 1536, 16, 16) == expect(16, 512, 1536, 16, 1, atomic)
+            assert ws(4, 16384, 2048, 16, 16) == expect(4, 16384, 2048, 16, 3, atomic)
+            _native.set_time_segments(3)
+            assert ws(16, 512, 1536, 16, 16) == expect(16, 512, 1536, 16, 3, atomic)
+            # 5 chunks at most: 5 segments of one chunk
+            _native.set_time_segments(8)
+            assert ws(1, 80, 64, 16, 16) == expect(1, 80, 64, 16, 5, atomic)
+        finally:
+            _native.set_time_segments(0)
+            _native.set_reduction(_native.REDUCTION_AUTO)
 
 
 def test_forward_workspace():
