@@ -82,16 +82,21 @@ struct BwdArgs {
   float* wsDB;
   // Time segments (the chunk-parallel-over-time variant): the chunks split
   // into nseg segments of cps chunks, one block per (channel block, batch
-  // row, segment), blockIdx.y = seg * batch + b. With nseg > 1:
-  //   carryL   (nseg, batch, D, N): slot s >= 1 holds L_s = dA_a * G_a of
-  //            segment s walked from a zero adjoint (a = its first step);
-  //   carrySdt (nseg, batch, D):    slot s >= 1 holds sum dt over segment s.
-  // The adjoint entering segment s from the later ones is then
-  //   K_{nseg-1} = dh_last (or 0),  K_{s-1} = L_s + exp(-Aneg * Sdt_s) * K_s,
-  // which each block of the gradient pass folds from the slots it needs.
+  // row, segment), blockIdx.y = seg * batch + b. The carry pass (CARRY) runs
+  // over carry units of cps / cunits chunks (cunits per segment: a grid with
+  // enough blocks to hide its dependent chains), launched with cps = the
+  // unit's chunks and one block per unit of segments 1..nseg-1. With
+  // nseg > 1:
+  //   carryL   (nunits, batch, D, N): slot u >= cunits holds L_u = dA_a * G_a
+  //            of unit u walked from a zero adjoint (a = its first step);
+  //   carrySdt (nunits, batch, D):    slot u >= cunits holds sum dt over unit u.
+  // The adjoint entering segment s from the later ones is then folded from
+  // the last unit down to the first unit after segment s:
+  //   K = dh_last (or 0);  K <- L_u + exp(-Aneg * Sdt_u) * K.
   int nseg, cps;
   float* carryL;
   float* carrySdt;
+  int cunits = 1, nunits = 0;
   // Row strides (elements between consecutive time steps) of dt, of B and C,
   // and of ddt: D, N and D for contiguous tensors, more for column slices of
   // a wider projection output (and its gradient). x, dy, dx are contiguous.
@@ -156,7 +161,7 @@ bwd_kernel(BwdArgs a) {
   const int q = wave * 2 + hh;
   const int n0 = q * NPL;
   const int b = blockIdx.y % a.batch;
-  const int seg = blockIdx.y / a.batch + (CARRY ? 1 : 0);
+  const int seg = blockIdx.y / a.batch + (CARRY ? a.cunits : 0);   // CARRY: the unit
   const int d0 = blockIdx.x * kCH;
   const int d = d0 + c;
   const bool act = d < a.D;
@@ -198,7 +203,7 @@ bwd_kernel(BwdArgs a) {
     // with the carries of the later segments for the others.
     const float* dhl = a.dh_last != nullptr ? a.dh_last + (size_t)b * slice : a.aneg;
     load_states<NPL>(u, GBuf(dhl, a.dh_last != nullptr ? slice_bytes : 0u), st_lane, nvalid);
-    for (int s2 = a.nseg - 1; s2 > seg; --s2) {
+    for (int s2 = a.nunits - 1; s2 >= (seg + 1) * a.cunits; --s2) {
       float lv[NPL];
       const size_t slot = (size_t)s2 * a.batch + b;
       load_states<NPL>(lv, GBuf(a.carryL + slot * slice, slice_bytes), st_lane, nvalid);

@@ -107,24 +107,58 @@ int device_cus() {
   return n;
 }
 
-// Time segments of the backward for this shape (see BwdArgs in mhs_bwd.hpp).
-// Automatic: one segment while the grid has at least two blocks per CU;
-// below that, enough segments for about three blocks per CU, each at least
-// kMinSegChunks chunks long. Returns (segments, chunks per segment).
-void segments_for(int64_t batch, int64_t D, int nch, int& nseg, int& cps) {
+// Time segments for this shape (see FwdArgs in mhs_fwd.hpp and BwdArgs in
+// mhs_bwd.hpp), in units of nch chunks (16-step sub-chunks in the forward,
+// the backward's chunks in the backward). Automatic: one segment while the
+// grid has at least two blocks per CU; below that, enough segments for about
+// three blocks per CU, each at least kMinSegChunks chunks long. The carry
+// passes run over carry units, cunits per segment, chosen so that their grid
+// has about kCarryBlocksPerCU blocks per CU (a carry pass is a chain of
+// dependent steps per state: it needs the waves to hide them), each at least
+// kMinUnitChunks chunks long. Segments that start from exact states
+// (carries = false) have no carry pass and a single unit each.
+constexpr int kCarryBlocksPerCU = 4;
+constexpr int kMinUnitChunks = 2;
+
+struct Segments {
+  int nseg = 1;    // segments
+  int cps = 1;     // chunks per segment (the last may be shorter)
+  int cunits = 1;  // carry units per segment
+  int ups = 1;     // chunks per carry unit (cps = cunits * ups)
+  int nunits = 1;  // carry units over the whole sequence
+};
+
+Segments segments_for(int64_t batch, int64_t D, int nch, bool carries = true) {
+  Segments r;
   const int64_t blocks = batch * ((D + mhs::kCH - 1) / mhs::kCH);
+  const int cus = device_cus();
   int want = g_seg_override.load(std::memory_order_relaxed);
   if (want == 0) {
     want = 1;
-    const int cus = device_cus();
     if (blocks < 2 * (int64_t)cus) {
       want = (int)std::min<int64_t>(kMaxSegments, (3 * (int64_t)cus + blocks - 1) / blocks);
       want = std::max(1, std::min(want, nch / kMinSegChunks));
     }
   }
   want = std::max(1, std::min(want, nch));
-  cps = (nch + want - 1) / want;
-  nseg = (nch + cps - 1) / cps;    // no empty segment
+  int cps = (nch + want - 1) / want;
+  int nseg = (nch + cps - 1) / cps;    // no empty segment
+  int f = 1;
+  if (carries && nseg > 1) {
+    f = (int)std::max<int64_t>(1, (int64_t)kCarryBlocksPerCU * cus / (blocks * (nseg - 1)));
+    f = std::max(1, std::min(f, cps / kMinUnitChunks));
+  }
+  r.ups = (cps + f - 1) / f;
+  r.cunits = f;
+  r.cps = r.ups * f;
+  r.nseg = (nch + r.cps - 1) / r.cps;
+  r.nunits = (nch + r.ups - 1) / r.ups;
+  if (r.nseg == 1) {   // no carries
+    r.cunits = 1;
+    r.ups = r.cps;
+    r.nunits = 1;
+  }
+  return r;
 }
 
 using FwdFn = void (*)(mhs::FwdArgs);
@@ -283,7 +317,8 @@ size_t round_up(size_t n, size_t m) { return (n + m - 1) / m * m; }
 struct WsLayout {
   size_t partB = 0, partC = 0, partA = 0, partDB = 0, carryL = 0, carryS = 0, fine = 0,
          total = 0;
-  int nseg = 1, cps = 1;
+  Segments sg;
+  int nseg = 1;
   bool atomic = false;
 };
 
@@ -293,7 +328,8 @@ WsLayout ws_layout(int64_t batch, int64_t T, int64_t D, int64_t N, int64_t chunk
   const size_t nblk = (size_t)((D + mhs::kCH - 1) / mhs::kCH);
   const size_t S = (size_t)batch * T * N;
   const int kb = (int)std::min<int64_t>(chunk, T) > bwd_ki ? bwd_ki : (int)std::min<int64_t>(chunk, T);
-  segments_for(batch, D, (int)((T + kb - 1) / kb), w.nseg, w.cps);
+  w.sg = segments_for(batch, D, (int)((T + kb - 1) / kb));
+  w.nseg = w.sg.nseg;
   size_t off = 0;
   const size_t parts = w.atomic ? 1 : nblk;
   w.partB = off;
@@ -306,11 +342,11 @@ WsLayout ws_layout(int64_t batch, int64_t T, int64_t D, int64_t N, int64_t chunk
     w.partDB = off;   // the gated backward's dt-bias partials
     off += round_up((size_t)w.nseg * batch * D * 4, 256);
   }
-  if (w.nseg > 1) {
+  if (w.nseg > 1) {   // carries per unit
     w.carryL = off;
-    off += round_up((size_t)w.nseg * batch * D * N * 4, 256);
+    off += round_up((size_t)w.sg.nunits * batch * D * N * 4, 256);
     w.carryS = off;
-    off += round_up((size_t)w.nseg * batch * D * 4, 256);
+    off += round_up((size_t)w.sg.nunits * batch * D * 4, 256);
   }
   w.fine = off;
   if (chunk > bwd_ki) off += round_up((size_t)batch * ((T + bwd_ki - 1) / bwd_ki) * D * N * 4, 256);
@@ -369,16 +405,17 @@ int launch_fwd(const Plan& p, mhs::FwdArgs a, int batch, hipStream_t s, const Ga
 // (see FwdArgs in mhs_fwd.hpp); total 0 when the shape runs unsegmented.
 struct FwdWs {
   size_t carryH = 0, carryS = 0, total = 0;
-  int nseg = 1, cps = 1;   // segments, sub-chunks of 16 steps per segment
+  Segments sg;   // in sub-chunks of 16 steps
 };
 
 FwdWs fwd_ws_layout(int64_t batch, int64_t T, int64_t D, int64_t N) {
   FwdWs w;
-  segments_for(batch, D, (int)((T + mhs::kSteps - 1) / mhs::kSteps), w.nseg, w.cps);
-  if (w.nseg > 1) {
+  w.sg = segments_for(batch, D, (int)((T + mhs::kSteps - 1) / mhs::kSteps));
+  if (w.sg.nseg > 1) {   // carries of the units of segments 0..nseg-2
+    const size_t units = (size_t)(w.sg.nseg - 1) * w.sg.cunits;
     w.carryH = 0;
-    w.carryS = round_up((size_t)w.nseg * batch * D * N * 4, 256);
-    w.total = w.carryS + round_up((size_t)w.nseg * batch * D * 4, 256);
+    w.carryS = round_up(units * batch * D * N * 4, 256);
+    w.total = w.carryS + round_up(units * batch * D * 4, 256);
   }
   return w;
 }
@@ -429,7 +466,7 @@ int scan_fwd(const void* x, const void* dt, const float* aneg, const void* B, co
   a.ld_bc = (int)st.bc;
   hipStream_t s = static_cast<hipStream_t>(stream);
   const FwdWs w = fwd_ws_layout(batch, seqlen, d_inner, d_state);
-  if (workspace == nullptr || w.nseg == 1) return launch_fwd(p, a, (int)batch, s, g, e);
+  if (workspace == nullptr || w.sg.nseg == 1) return launch_fwd(p, a, (int)batch, s, g, e);
   if (workspace_bytes < w.total)
     return fail(MHS_EINVAL, "workspace too small: %zu < %zu bytes", workspace_bytes, w.total);
   if (reinterpret_cast<uintptr_t>(workspace) & 255u)
@@ -438,7 +475,8 @@ int scan_fwd(const void* x, const void* dt, const float* aneg, const void* B, co
   // segment from its folded start state.
   char* ws = static_cast<char*>(workspace);
   a.batch = (int)batch;
-  a.seg_len = w.cps * mhs::kSteps;
+  a.seg_len = w.sg.cps * mhs::kSteps;
+  a.cunits = w.sg.cunits;
   a.h_init = nullptr;
   a.carryH = reinterpret_cast<float*>(ws + w.carryH);
   a.carrySdt = reinterpret_cast<float*>(ws + w.carryS);
@@ -446,23 +484,25 @@ int scan_fwd(const void* x, const void* dt, const float* aneg, const void* B, co
   a.dt_span = g.span;
   a.dt_bias = g.bias;
   const unsigned nblk = (unsigned)((d_inner + mhs::kCH - 1) / mhs::kCH);
-  mhs::FwdArgs c = a;
+  mhs::FwdArgs c = a;   // the carry pass: one "segment" per carry unit
   c.y = nullptr;
   c.ckpt = nullptr;
   c.h_last = nullptr;
+  c.seg_len = w.sg.ups * mhs::kSteps;
   const Kernels& kk = p.k[e];
   const FwdFn cfn = g.on ? kk.fcarry_g : kk.fcarry;
   rc = ensure_lds(reinterpret_cast<const void*>(cfn), p.fwd_lds);
   if (rc) return rc;
-  hipLaunchKernelGGL(cfn, dim3(nblk, (unsigned)(batch * (w.nseg - 1))), dim3(64 * p.G), p.fwd_lds,
-                     s, c);
+  hipLaunchKernelGGL(cfn, dim3(nblk, (unsigned)(batch * (w.sg.nseg - 1) * w.sg.cunits)),
+                     dim3(64 * p.G), p.fwd_lds, s, c);
   rc = check_launch("forward carry kernel");
   if (rc) return rc;
   const bool aligned = a.K % mhs::kSteps == 0 || a.K >= a.T;
   const FwdFn fn = aligned ? (g.on ? kk.fwd_g : kk.fwd) : (g.on ? kk.fwd_any_g : kk.fwd_any);
   rc = ensure_lds(reinterpret_cast<const void*>(fn), p.fwd_lds);
   if (rc) return rc;
-  hipLaunchKernelGGL(fn, dim3(nblk, (unsigned)(batch * w.nseg)), dim3(64 * p.G), p.fwd_lds, s, a);
+  hipLaunchKernelGGL(fn, dim3(nblk, (unsigned)(batch * w.sg.nseg)), dim3(64 * p.G), p.fwd_lds, s,
+                     a);
   return check_launch("forward scan kernel");
 }
 
@@ -559,9 +599,9 @@ int scan_bwd(const void* x, const void* dt, const float* aneg, const void* B, co
     // is a multiple of lcm(16, K) steps and starts from the exact state, so
     // they run in parallel where the grid alone would leave CUs idle.
     const int64_t unit = std::lcm<int64_t>(mhs::kSteps, K);
-    int nseg = 1, ups = 1;
-    segments_for(batch, D, (int)((T + unit - 1) / unit), nseg, ups);
-    f.seg_len = (int)std::min<int64_t>((int64_t)ups * unit, T);
+    const Segments sg = segments_for(batch, D, (int)((T + unit - 1) / unit), /*carries=*/false);
+    const int nseg = sg.nseg;
+    f.seg_len = (int)std::min<int64_t>((int64_t)sg.cps * unit, T);
     f.h_init = ckpt;
     f.init_K = K;
     f.init_nchunk = (int)mhs_num_chunks(T, K);
@@ -586,7 +626,9 @@ int scan_bwd(const void* x, const void* dt, const float* aneg, const void* B, co
   a.dt_bias = g.bias;
   a.wsDB = g.dbias != nullptr ? reinterpret_cast<float*>(ws + w.partDB) : nullptr;
   a.nseg = w.nseg;
-  a.cps = w.cps;
+  a.cps = w.sg.cps;
+  a.cunits = w.sg.cunits;
+  a.nunits = w.sg.nunits;
   a.carryL = w.nseg > 1 ? reinterpret_cast<float*>(ws + w.carryL) : nullptr;
   a.carrySdt = w.nseg > 1 ? reinterpret_cast<float*>(ws + w.carryS) : nullptr;
   a.ld_dt = (int)st.dt;
@@ -612,12 +654,15 @@ int scan_bwd(const void* x, const void* dt, const float* aneg, const void* B, co
     if (rc) return rc;
   }
   if (w.nseg > 1) {
-    // Adjoint carries of segments 1..nseg-1 (segment 0 passes nothing on).
+    // Adjoint carries of the units of segments 1..nseg-1 (segment 0 passes
+    // nothing on): one block per unit.
     const BwdFn cfn = g.on ? p.k[e].carry_g : p.k[e].carry;
     rc = ensure_lds(reinterpret_cast<const void*>(cfn), p.bwd_lds);
     if (rc) return rc;
-    hipLaunchKernelGGL(cfn, dim3(nblk, (unsigned)(batch * (w.nseg - 1))), dim3(64 * p.G),
-                       p.bwd_lds, s, a);
+    mhs::BwdArgs c = a;
+    c.cps = w.sg.ups;
+    hipLaunchKernelGGL(cfn, dim3(nblk, (unsigned)(batch * (w.sg.nunits - w.sg.cunits))),
+                       dim3(64 * p.G), p.bwd_lds, s, c);
     rc = check_launch("backward carry kernel");
     if (rc) return rc;
   }

@@ -59,13 +59,16 @@ struct FwdArgs {
   const float* h_init = nullptr;
   int init_K = 1, init_nchunk = 1;
   // Carried segments (no h_init): segment s >= 1 starts from the state folded
-  // from the earlier segments' carries, H_0 = 0 and
-  //   H_{s+1} = exp(-Aneg * Sdt_s) * H_s + hend_s,
-  // where the carry pass (FCARRY) wrote hend_s, the state after segment s
-  // scanned from zero, to carryH (nseg, batch, D, N) and Sdt_s, its sum of
-  // dt, to carrySdt (nseg, batch, D).
+  // from the carries of everything before it. The carry pass (FCARRY) runs
+  // over carry units of seg_len / cunits steps (cunits per segment, so that
+  // its grid has enough blocks to hide its dependent chains) and writes, for
+  // unit u, hend_u, the state after unit u scanned from zero, to carryH
+  // (units, batch, D, N) and Sdt_u, its sum of dt, to carrySdt (units,
+  // batch, D). Segment s folds units 0 .. s*cunits - 1: H_0 = 0 and
+  //   H_{u+1} = exp(-Aneg * Sdt_u) * H_u + hend_u.
   float* carryH = nullptr;
   float* carrySdt = nullptr;
+  int cunits = 1;
   // Row strides (elements between consecutive time steps) of dt and of B,
   // C: D and N for contiguous tensors, more for column slices of a wider
   // projection output. x and y are contiguous.
@@ -236,7 +239,7 @@ fwd_kernel(FwdArgs a) {
     load_states<NPL>(h, GBuf(a.h_init + ((size_t)b * a.init_nchunk + t_beg / a.init_K - 1) *
                                             ck_stride, slice_bytes), ck_lane, nvalid);
   } else if (!FCARRY && seg > 0 && a.carryH != nullptr) {
-    for (int s2 = 0; s2 < seg; ++s2) {
+    for (int s2 = 0; s2 < seg * a.cunits; ++s2) {
       const size_t slot = (size_t)s2 * a.batch + b;
       float hv[NPL];
       load_states<NPL>(hv, GBuf(a.carryH + slot * ck_stride, slice_bytes), ck_lane, nvalid);

@@ -190,9 +190,12 @@ def test_out_gate_argument_errors():
 
 def test_time_segments_knob_and_workspace():
     """Automatic split: one segment at 16x512x1536x16 (768 blocks), three at
-    4x16384x2048x16 (256 blocks); forced splits add the per-segment dAneg
-    and dt-bias partials and the carries (L: segments x batch x D x N, sum dt:
-    x batch x D)."""
+    4x16384x2048x16 (256 blocks: 3 blocks per CU); forced splits add the
+    per-segment dAneg and dt-bias partials and the carries of the carry
+    units (L: units x batch x D x N, sum dt: units x batch x D). At
+    4x16384x2048x16 each segment of 342 chunks splits into 2 carry units of
+    171, so that the carry pass has 4 blocks per CU: 6 units over the 1024
+    chunks."""
     lib = _native.library()
     with pytest.raises(_native.HipScanError, match="time segments"):
         _native.set_time_segments(9)
@@ -201,7 +204,7 @@ def test_time_segments_knob_and_workspace():
     def ru(v):
         return (v + 255) // 256 * 256
 
-    def expect(bt, t, d, n, segs, atomic):
+    def expect(bt, t, d, n, segs, units, atomic):
         nblk = 1 if atomic else (d + 31) // 32
         s_ = bt * t * n
         a = bt * d * n
@@ -209,20 +212,22 @@ def test_time_segments_knob_and_workspace():
         if not atomic:
             base += ru(segs * a * 4) + ru(segs * bt * d * 4)
         if segs > 1:
-            base += ru(segs * a * 4) + ru(segs * bt * d * 4)
+            base += ru(units * a * 4) + ru(units * bt * d * 4)
         return base
 
     for mode, atomic in ((_native.REDUCTION_FIXED, False), (_native.REDUCTION_ATOMIC, True)):
         try:
             _native.set_reduction(mode)
             ws = lib.mhs_scan_bwd_workspace_bytes
-            assert ws(16, 512, 1536, 16, 16) == expect(16, 512, 1536, 16, 1, atomic)
-            assert ws(4, 16384, 2048, 16, 16) == expect(4, 16384, 2048, 16, 3, atomic)
+            assert ws(16, 512, 1536, 16, 16) == expect(16, 512, 1536, 16, 1, 1, atomic)
+            assert ws(4, 16384, 2048, 16, 16) == expect(4, 16384, 2048, 16, 3, 6, atomic)
+            # 768 blocks: the carry pass (1536 blocks) needs no finer units
             _native.set_time_segments(3)
-            assert ws(16, 512, 1536, 16, 16) == expect(16, 512, 1536, 16, 3, atomic)
-            # 5 chunks at most: 5 segments of one chunk
+            assert ws(16, 512, 1536, 16, 16) == expect(16, 512, 1536, 16, 3, 3, atomic)
+            # 5 chunks at most: 5 segments of one chunk, units of at least 2
+            # chunks do not fit
             _native.set_time_segments(8)
-            assert ws(1, 80, 64, 16, 16) == expect(1, 80, 64, 16, 5, atomic)
+            assert ws(1, 80, 64, 16, 16) == expect(1, 80, 64, 16, 5, 5, atomic)
         finally:
             _native.set_time_segments(0)
             _native.set_reduction(_native.REDUCTION_AUTO)
@@ -230,13 +235,15 @@ def test_time_segments_knob_and_workspace():
 
 def test_forward_workspace():
     """The forward needs no workspace where the grid fills the GPU; below two
-    blocks per CU it holds the segments' carried states and dt sums."""
+    blocks per CU it holds the carried states and dt sums of the carry units
+    before the last segment."""
     lib = _native.library()
     assert lib.mhs_scan_fwd_workspace_bytes(16, 512, 1536, 16) == 0
-    # 4 x 16384 x 2048 x 16: 256 blocks -> 3 segments
+    # 4 x 16384 x 2048 x 16: 256 blocks -> 3 segments of 342 sub-chunks, 2
+    # carry units each (4 blocks per CU in the carry pass): 4 units carried
     ru = lambda v: (v + 255) // 256 * 256
     assert lib.mhs_scan_fwd_workspace_bytes(4, 16384, 2048, 16) == \
-        ru(3 * 4 * 2048 * 16 * 4) + ru(3 * 4 * 2048 * 4)
+        ru(4 * 4 * 2048 * 16 * 4) + ru(4 * 4 * 2048 * 4)
     sizes = (4, 16384, 2048, 16, 16)
     need = lib.mhs_scan_fwd_workspace_bytes(*sizes[:4])
     rc = lib.mhs_scan_fwd_ws_f32(*([A16] * 8), A16, need - 4, *sizes, None)
@@ -262,21 +269,22 @@ def test_conv_argument_errors():
 def test_segment_split_follows_the_compute_unit_count():
     """The automatic split plans for the device's compute units: 256 blocks
     (4 x 16384 x 2048 x 16) get three segments at 256 CUs, one at 128 (two
-    blocks per CU already) and eight (the maximum) at 1024; the forward's
-    workspace follows. Without a device the count is MI355X's 256."""
+    blocks per CU already) and eight (the maximum) at 1024; the carry units
+    and the forward's workspace follow (1024 CUs: 7 carried segments x 2
+    units; 256 CUs: 2 x 2). Without a device the count is MI355X's 256."""
     lib = _native.library()
     assert lib.mhs_cu_count() == 256
     ru = lambda v: (v + 255) // 256 * 256
-    fwd_ws = lambda segs: ru(segs * 4 * 2048 * 16 * 4) + ru(segs * 4 * 2048 * 4)
+    fwd_ws = lambda units: ru(units * 4 * 2048 * 16 * 4) + ru(units * 4 * 2048 * 4)
     shape = (4, 16384, 2048, 16)
     try:
         _native.set_cu_count(128)
         assert lib.mhs_cu_count() == 128
         assert lib.mhs_scan_fwd_workspace_bytes(*shape) == 0
         _native.set_cu_count(1024)
-        assert lib.mhs_scan_fwd_workspace_bytes(*shape) == fwd_ws(8)
+        assert lib.mhs_scan_fwd_workspace_bytes(*shape) == fwd_ws(14)
         _native.set_cu_count(256)
-        assert lib.mhs_scan_fwd_workspace_bytes(*shape) == fwd_ws(3)
+        assert lib.mhs_scan_fwd_workspace_bytes(*shape) == fwd_ws(4)
         with pytest.raises(_native.HipScanError, match="compute-unit count"):
             _native.set_cu_count(-1)
     finally:

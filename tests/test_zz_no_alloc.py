@@ -81,7 +81,7 @@ def test_noalloc_forward_rejects_shapes_beyond_its_scratch():
     """A forced split whose carries exceed the static scratch fails on the
     host, before any launch, with a message naming the way out."""
     lib = _native.library()
-    bt, t_len, d, n = 16, 256, 16384, 16     # 8 segments: 8 x 16 x 16384 x 17 x 4 B > 16 MiB
+    bt, t_len, d, n = 16, 256, 16384, 16     # 8 segments, 7 carried: 7 x 16 x 16384 x 17 x 4 B > 16 MiB
     x = torch.zeros(16, device=DEV)
     try:
         _native.set_time_segments(8)
