@@ -11,7 +11,7 @@ Reported:
   value          whole-job tokens/s (batch*T per step / step time)
   ms_per_step    ms per fwd+bwd step (wall clock, synchronized)
   roofline       the dominant kernel launch (the backward: bwd kernel + its
-                 fixed-order reduction), timed live with HIP events around
+                 reduction; the fixed order at this shape), timed live with HIP events around
                  it in every 4th timed step, on the launch stream: algorithmic
                  bytes / average duration vs 8 TB/s
   clock_settle   untimed steps run before the warmup until the GPU clock
@@ -22,10 +22,10 @@ Reported:
   train_80m      the 80M TinyMamba train step (fwd + bwd + AdamW) with the HIP
                  scan at batch 16 x seq 512: tokens/s and peak HBM
 
-Other workloads (--workload): "train" (the 80M train step alone), "longt"
-(4 x 16384 x 2048 x 16 fwd+bwd,
-checkpoint-stride sweep), "infer" (prefill 32 x 2048 x 4096 x 16 + 256
-recurrent decode steps).
+Other workloads (--workload): "train" (the 80M train step alone; --size 18M
+for the reference bench's smaller size, --ref to add the torch scan at its
+small size), "longt" (4 x 16384 x 2048 x 16 fwd+bwd, checkpoint-stride
+sweep), "infer" (prefill 32 x 2048 x 4096 x 16 + 256 recurrent decode steps).
 
 Only one GPU is used: --gpus N > 1 exits with a message.
 """
@@ -279,6 +279,13 @@ def shape_tag(bt, t_len, d, n) -> str:
     return f"{bt}x{t_len}x{d}x{n}"
 
 
+def reduction_name(bt, t_len, d, n, chunk):
+    """'fixed' or 'atomic': the reduction the backward uses at this shape."""
+    from mamba_metal_scan_amd import _native
+    mode = _native.bwd_reduction(bt, t_len, d, n, chunk)
+    return "atomic" if mode == _native.REDUCTION_ATOMIC else "fixed"
+
+
 def load_counters(bt, t_len, d, n, chunk):
     """The committed counter summary of this workload (None if there is none,
     or it was taken at another checkpoint stride or reduction)."""
@@ -288,7 +295,7 @@ def load_counters(bt, t_len, d, n, chunk):
         c = json.loads(path.read_text())
     except (OSError, ValueError):
         return None
-    red = "fixed" if _native.library().mhs_deterministic() else "atomic"
+    red = reduction_name(bt, t_len, d, n, chunk)
     if c.get("chunk") != chunk or c.get("reduction") != red:
         return None
     return c
@@ -386,7 +393,7 @@ def pmc_summary(args) -> None:
                                      ("d_state", 16), ("chunk", 16)) if getattr(args, k) != dflt)
     out = {
         "shape": tag, "chunk": args.chunk,
-        "reduction": "fixed" if _native.library().mhs_deterministic() else "atomic",
+        "reduction": reduction_name(*shape, args.chunk),
         "workload": f"selective_scan {tag} chunk {args.chunk}",
         "bwd_launch": {"hbm_bytes": bwd_total, "algorithmic_bytes": nbytes["bwd"],
                        "kernels": "bwd_kernel + bwd_reduce_kernel"},
@@ -526,23 +533,41 @@ def workload_trace_summary(args, rows) -> None:
     print(f"\nwrote {md.relative_to(ROOT)}")
 
 
-def bench_train(steps: int = 10, warmup: int = 3) -> dict:
-    """The 80M TinyMamba train step (fwd + bwd + AdamW lr 3e-4) with the HIP
-    scan: vocab 32768, d_model 640, 12 layers, d_ff 2560 (d_inner 1432),
-    d_state 16, batch 16 x seq 512, random init, tokens uniform in [0, 32768)."""
+# The reference bench's model sizes (bench/bench.py:37-40), named for the
+# transformer budget each Mamba is matched to; "60M" counts 79.5M parameters
+# with its 32768 x 640 embedding (the headline "80M" train step). "ref" is the
+# small size the reference also runs with the torch scan (--ref).
+TRAIN_SIZES = {
+    "18M": dict(d_model=384, n_layers=10, d_ff=1536, batch=16, seq=512),
+    "60M": dict(d_model=640, n_layers=12, d_ff=2560, batch=16, seq=512),
+    "ref": dict(d_model=128, n_layers=2, d_ff=512, batch=4, seq=128),
+}
+
+
+def bench_train(steps: int = 10, warmup: int = 3, size: str = "60M",
+                scan_impl: str = "hip") -> dict:
+    """A TinyMamba train step (fwd + bwd + AdamW lr 3e-4) of one of the
+    reference bench's sizes: vocab 32768, d_state 16, d_conv 4, random init,
+    tokens uniform in [0, 32768). Peak HBM is torch's allocator peak over the
+    timed steps (the reference's gate: under 16 GB at 18M, where its torch
+    scan needed 47.7 GB)."""
     import torch
     from mamba_metal_scan_amd import MambaConfig, TinyMamba
     from mamba_metal_scan_amd.gemm_tuning import TABLE, use_tuned_gemms
     tuned = use_tuned_gemms()
     torch.manual_seed(1337)
     dev = torch.device("cuda", 0)
-    cfg = MambaConfig(vocab_size=32768, d_model=640, n_layers=12, d_ff=2560, max_seq_len=512,
-                      d_state=16, d_conv=4, scan_impl="hip")
+    sz = TRAIN_SIZES[size]
+    bt, seq = sz["batch"], sz["seq"]
+    cfg = MambaConfig(vocab_size=32768, d_model=sz["d_model"], n_layers=sz["n_layers"],
+                      d_ff=sz["d_ff"], max_seq_len=seq, d_state=16, d_conv=4,
+                      scan_impl=scan_impl)
     model = TinyMamba(cfg).to(dev)
     # The reference's optimizer (AdamW, lr 3e-4, bench/bench.py:90); torch's
     # fused implementation of the same update runs it in one pass per step.
     opt = torch.optim.AdamW(model.parameters(), lr=3e-4, fused=True)
-    idx = torch.randint(0, 32768, (16, 513), generator=torch.Generator().manual_seed(1337)).to(dev)
+    idx = torch.randint(0, 32768, (bt, seq + 1),
+                        generator=torch.Generator().manual_seed(1337)).to(dev)
     x, y = idx[:, :-1], idx[:, 1:]
 
     def step():
@@ -561,12 +586,13 @@ def bench_train(steps: int = 10, warmup: int = 3) -> dict:
         loss = step()
     torch.cuda.synchronize()
     el = time.perf_counter() - t0
-    out = {"tokens_per_s": 16 * 512 * steps / el, "ms_per_step": el * 1e3 / steps,
+    out = {"tokens_per_s": bt * seq * steps / el, "ms_per_step": el * 1e3 / steps,
            "steps": steps, "warmup": warmup, "loss": float(loss.item()),
            "params": model.count_params(), "d_inner": model.d_inner,
            "peak_hbm_GB": torch.cuda.max_memory_allocated(dev) / 1e9,
-           "config": "TinyMamba 80M (vocab 32768, d_model 640, 12 layers, d_state 16), "
-                     "batch 16 x seq 512, fp32, AdamW (fused), scan_impl=hip",
+           "config": f"TinyMamba {size} class ({model.count_params() / 1e6:.1f}M parameters: "
+                     f"vocab 32768, d_model {sz['d_model']}, {sz['n_layers']} layers, d_state "
+                     f"16), batch {bt} x seq {seq}, fp32, AdamW (fused), scan_impl={scan_impl}",
            "gemm_solutions": TABLE.name if tuned else "library default"}
     del model, opt
     torch.cuda.empty_cache()
@@ -597,7 +623,8 @@ def longt_measure(strides) -> list:
         f_ms, b_ms = time_events(fwd, 5), time_events(bwd, 5)
         rows.append({"chunk": chunk, "fwd_ms": f_ms, "bwd_ms": b_ms, "fwd_bwd_ms": f_ms + b_ms,
                      "fwd_bwd_GBs": nbytes["fwd_bwd"] / ((f_ms + b_ms) * 1e-3) / 1e9,
-                     "ckpt_bytes": ckpt.numel() * 4})
+                     "ckpt_bytes": ckpt.numel() * 4,
+                     "reduction": reduction_name(bt, t_len, d, n, chunk)})
         print(f"longt chunk {chunk}: fwd {f_ms:.3f} ms bwd {b_ms:.3f} ms", file=sys.stderr,
               flush=True)
         del ckpt
@@ -841,6 +868,12 @@ def main() -> int:
     ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--workload", default="scan", choices=["scan", "train", "longt", "infer"])
     ap.add_argument("--no-train", action="store_true", help="skip the 80M train-step figure")
+    ap.add_argument("--size", default="60M", choices=["18M", "60M"],
+                    help="--workload train: the reference bench's model size (60M: the 79.5M-"
+                         "parameter headline step)")
+    ap.add_argument("--ref", action="store_true",
+                    help="--workload train: also the torch scan at the reference bench's "
+                         "small size")
     ap.add_argument("--batch", type=int, default=16)
     ap.add_argument("--seqlen", type=int, default=512)
     ap.add_argument("--d-inner", dest="d_inner", type=int, default=1536)
@@ -884,13 +917,20 @@ def main() -> int:
         run_launches(args)
         return 0
     if args.workload == "train":
-        t = bench_train(steps=args.steps, warmup=args.warmup)
-        out = {"metric": "80M TinyMamba fp32 train step tok/s (batch 16 x seq 512)",
+        t = bench_train(steps=args.steps, warmup=args.warmup, size=args.size)
+        name = "80M" if args.size == "60M" else args.size
+        out = {"metric": f"{name} TinyMamba fp32 train step tok/s (batch 16 x seq 512)",
                "value": t["tokens_per_s"], "unit": "tokens/s", "n_gpus": 1,
                "steps": args.steps, "warmup": args.warmup, "ms_per_step": t["ms_per_step"],
                "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "f32",
                "data": "synthetic tokens U[0, 32768)", "config": {"workload": t["config"]},
-               "train_80m": t}
+               f"train_{name.lower()}": t}
+        if args.ref:
+            # The torch scan (a Python loop over time) at the reference's
+            # small size, with the HIP scan at the same size beside it.
+            out["ref_torch"] = bench_train(steps=args.steps, warmup=1, size="ref",
+                                           scan_impl="torch")
+            out["ref_hip"] = bench_train(steps=args.steps, warmup=1, size="ref")
     else:
         out = {"scan": bench_scan, "longt": bench_longt, "infer": bench_infer}[args.workload](args)
     print(json.dumps(out), flush=True)

@@ -98,10 +98,17 @@ int mhs_cu_count(void);
  *      no reduction kernel, a far smaller workspace, and a rounding that
  *      varies with the order the additions land in (about 1e-7 relative of
  *      each sum: far inside the 1e-4 parity bar).
- *   0  automatic (1: measured faster on MI355X, see mhs_capi.hip).
- * mhs_deterministic() is 1 when the current setting reproduces bit for bit. */
+ *   0  automatic, per shape: 1 where the backward runs in one time segment
+ *      (the grid fills the GPU), 2 where it runs in several; each measured
+ *      the faster there on MI355X.
+ * mhs_deterministic() is 1 when the current setting reproduces bit for bit
+ * at every shape (mode 1). mhs_scan_bwd_reduction() returns the mode (1 or
+ * 2) a backward of this shape uses under the current setting, 0 for a shape
+ * the backward rejects. */
 int mhs_set_reduction(int mode);
 int mhs_deterministic(void);
+int mhs_scan_bwd_reduction(int64_t batch, int64_t seqlen, int64_t d_inner, int64_t d_state,
+                           int64_t chunk);
 
 /*
  * Forward scan. Replaces the reference's `lib.ssm_fwd(x, dt, Aneg, Bm, Cm, y,

@@ -34,6 +34,7 @@ EXPORTED_SYMBOLS = (
     "mhs_scan_bwd_bf16", "mhs_scan_gated_fwd_bf16", "mhs_scan_gated_bwd_bf16",
     "mhs_set_cu_count", "mhs_cu_count", "mhs_scan_fwd_noalloc_f32", "mhs_set_reduction",
     "mhs_deterministic",
+    "mhs_scan_bwd_reduction",
 )
 
 # Size of the static device scratch of mhs_scan_fwd_noalloc_f32 (the header's
@@ -84,6 +85,8 @@ def library() -> ctypes.CDLL:
             lib.mhs_set_reduction.argtypes = [ctypes.c_int]
             lib.mhs_deterministic.restype = ctypes.c_int
             lib.mhs_deterministic.argtypes = []
+            lib.mhs_scan_bwd_reduction.restype = ctypes.c_int
+            lib.mhs_scan_bwd_reduction.argtypes = [_I64] * 5
             lib.mhs_scan_fwd_f32.restype = ctypes.c_int
             lib.mhs_scan_fwd_f32.argtypes = [_P] * 8 + [_I64] * 5 + [_P]
             lib.mhs_scan_fwd_noalloc_f32.restype = ctypes.c_int
@@ -190,14 +193,26 @@ def set_reduction(mode: int) -> None:
     """How the backward reduces dB, dC, dAneg (and the gated dt-bias gradient),
     process-wide: REDUCTION_FIXED (fixed-order partials, bit-for-bit
     reproducible), REDUCTION_ATOMIC (fp32 atomics into the zeroed gradients)
-    or REDUCTION_AUTO (the library's choice: the fixed order, measured faster
-    on MI355X). While torch's deterministic algorithms are enabled
+    or REDUCTION_AUTO (the library's choice per shape: the fixed order where
+    the backward's grid fills the GPU, atomics where it runs in time segments;
+    each measured the faster there on MI355X; bwd_reduction() tells which a
+    shape gets). While torch's deterministic algorithms are enabled
     (torch.use_deterministic_algorithms) the backward ops use the fixed order
     whatever this says."""
     global _reduction
     with _reduction_lock:
         _check(library().mhs_set_reduction(int(mode)), "mhs_set_reduction")
         _reduction = int(mode)
+
+
+def bwd_reduction(batch: int, seqlen: int, d_inner: int, d_state: int, chunk: int) -> int:
+    """The reduction (REDUCTION_FIXED or REDUCTION_ATOMIC) a backward of this
+    shape uses under the process-wide mode (not counting torch's
+    deterministic mode, which forces the fixed order)."""
+    mode = library().mhs_scan_bwd_reduction(batch, seqlen, d_inner, d_state, chunk)
+    if mode == 0:
+        raise HipScanError(f"mhs_scan_bwd_reduction: {library().mhs_last_error().decode()}")
+    return mode
 
 
 @contextlib.contextmanager

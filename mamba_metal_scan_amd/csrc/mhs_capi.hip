@@ -62,15 +62,18 @@ std::atomic<int> g_seg_override{0};
 // mhs_set_reduction (0 = automatic).
 std::atomic<int> g_reduction{0};
 constexpr int kRedFixed = 1, kRedAtomic = 2;
-// The automatic choice: the fixed order. Measured on MI355X at
-// 16x512x1536x16, the backward launch takes 133 us with it and 145 us with
-// atomics (the atomics' round trips hold up the kernel's in-order memory
-// counter, which outweighs the reduction kernel they replace).
-constexpr int kRedAuto = kRedFixed;
-
-bool atomic_reduction() {
+// The automatic choice, per shape: the fixed order where the backward runs in
+// one time segment (the grid fills the GPU), atomics where it runs in several.
+// Measured on MI355X (backward launch, same box):
+//   16x512x1536x16, one segment:        fixed 126.1 us, atomics 145.4 us;
+//   4x16384x2048x16, three segments:    fixed 1597 us,  atomics 1511 us.
+// At the first the atomics cost more kernel time than the reduction kernel
+// they replace (12 us); at the second the reduction kernel reads 64 channel
+// blocks' partials of every (b, t, n), 537 MB in 116 us, more than the
+// atomics cost.
+bool atomic_reduction(bool segmented) {
   const int m = g_reduction.load(std::memory_order_relaxed);
-  return (m == 0 ? kRedAuto : m) == kRedAtomic;
+  return m == 0 ? segmented : m == kRedAtomic;
 }
 
 constexpr int kDefaultCUs = 256; // MI355X compute units (used when no device can be queried)
@@ -111,7 +114,12 @@ int device_cus() {
 // mhs_bwd.hpp), in units of nch chunks (16-step sub-chunks in the forward,
 // the backward's chunks in the backward). Automatic: one segment while the
 // grid has at least two blocks per CU; below that, enough segments for about
-// three blocks per CU, each at least kMinSegChunks chunks long. The carry
+// per_cu blocks per CU, each at least kMinSegChunks chunks long: the
+// forward's carry pass costs more of its main pass than the backward's does,
+// and the forward plans for kFwdBlocksPerCU, the backward for
+// kBwdBlocksPerCU (measured on MI355X at 4x16384x2048x16, 256 blocks:
+// forward 821 / 880 / 945 us and backward 1679 / 1597 / 1846 us with 2 / 3 /
+// 4 segments). The carry
 // passes run over carry units, cunits per segment, chosen so that their grid
 // has about kCarryBlocksPerCU blocks per CU (a carry pass is a chain of
 // dependent steps per state: it needs the waves to hide them), each at least
@@ -119,6 +127,7 @@ int device_cus() {
 // (carries = false) have no carry pass and a single unit each.
 constexpr int kCarryBlocksPerCU = 4;
 constexpr int kMinUnitChunks = 2;
+constexpr int kFwdBlocksPerCU = 2, kBwdBlocksPerCU = 3;
 
 struct Segments {
   int nseg = 1;    // segments
@@ -128,7 +137,7 @@ struct Segments {
   int nunits = 1;  // carry units over the whole sequence
 };
 
-Segments segments_for(int64_t batch, int64_t D, int nch, bool carries = true) {
+Segments segments_for(int64_t batch, int64_t D, int nch, int per_cu, bool carries = true) {
   Segments r;
   const int64_t blocks = batch * ((D + mhs::kCH - 1) / mhs::kCH);
   const int cus = device_cus();
@@ -136,7 +145,7 @@ Segments segments_for(int64_t batch, int64_t D, int nch, bool carries = true) {
   if (want == 0) {
     want = 1;
     if (blocks < 2 * (int64_t)cus) {
-      want = (int)std::min<int64_t>(kMaxSegments, (3 * (int64_t)cus + blocks - 1) / blocks);
+      want = (int)std::min<int64_t>(kMaxSegments, (per_cu * (int64_t)cus + blocks - 1) / blocks);
       want = std::max(1, std::min(want, nch / kMinSegChunks));
     }
   }
@@ -324,12 +333,12 @@ struct WsLayout {
 
 WsLayout ws_layout(int64_t batch, int64_t T, int64_t D, int64_t N, int64_t chunk, int bwd_ki) {
   WsLayout w;
-  w.atomic = atomic_reduction();
   const size_t nblk = (size_t)((D + mhs::kCH - 1) / mhs::kCH);
   const size_t S = (size_t)batch * T * N;
   const int kb = (int)std::min<int64_t>(chunk, T) > bwd_ki ? bwd_ki : (int)std::min<int64_t>(chunk, T);
-  w.sg = segments_for(batch, D, (int)((T + kb - 1) / kb));
+  w.sg = segments_for(batch, D, (int)((T + kb - 1) / kb), kBwdBlocksPerCU);
   w.nseg = w.sg.nseg;
+  w.atomic = atomic_reduction(w.nseg > 1);
   size_t off = 0;
   const size_t parts = w.atomic ? 1 : nblk;
   w.partB = off;
@@ -410,7 +419,7 @@ struct FwdWs {
 
 FwdWs fwd_ws_layout(int64_t batch, int64_t T, int64_t D, int64_t N) {
   FwdWs w;
-  w.sg = segments_for(batch, D, (int)((T + mhs::kSteps - 1) / mhs::kSteps));
+  w.sg = segments_for(batch, D, (int)((T + mhs::kSteps - 1) / mhs::kSteps), kFwdBlocksPerCU);
   if (w.sg.nseg > 1) {   // carries of the units of segments 0..nseg-2
     const size_t units = (size_t)(w.sg.nseg - 1) * w.sg.cunits;
     w.carryH = 0;
@@ -599,7 +608,8 @@ int scan_bwd(const void* x, const void* dt, const float* aneg, const void* B, co
     // is a multiple of lcm(16, K) steps and starts from the exact state, so
     // they run in parallel where the grid alone would leave CUs idle.
     const int64_t unit = std::lcm<int64_t>(mhs::kSteps, K);
-    const Segments sg = segments_for(batch, D, (int)((T + unit - 1) / unit), /*carries=*/false);
+    const Segments sg =
+        segments_for(batch, D, (int)((T + unit - 1) / unit), kBwdBlocksPerCU, /*carries=*/false);
     const int nseg = sg.nseg;
     f.seg_len = (int)std::min<int64_t>((int64_t)sg.cps * unit, T);
     f.h_init = ckpt;
@@ -727,7 +737,18 @@ int mhs_set_reduction(int mode) {
   return MHS_OK;
 }
 
-int mhs_deterministic(void) { return atomic_reduction() ? 0 : 1; }
+int mhs_deterministic(void) {
+  return g_reduction.load(std::memory_order_relaxed) == kRedFixed ? 1 : 0;
+}
+
+int mhs_scan_bwd_reduction(int64_t batch, int64_t seqlen, int64_t d_inner, int64_t d_state,
+                           int64_t chunk) {
+  if (check_shape(batch, seqlen, d_inner, d_state, chunk)) return 0;
+  Plan p;
+  if (!make_plan((int)d_state, p)) return 0;
+  return ws_layout(batch, seqlen, d_inner, d_state, chunk, p.bwd_ki).atomic ? kRedAtomic
+                                                                            : kRedFixed;
+}
 
 int mhs_set_cu_count(int cus) {
   if (cus < 0 || cus > 65536)

@@ -78,7 +78,8 @@ def test_gated_scan_with_dt_bias_matches_the_oracle(bt, t_len, d, n, chunk):
     """dt = lo + span * sigmoid(raw + bias): the oracle on raw + bias, and the
     bias gradient equal to the oracle's raw gradient summed over batch and
     time (raw + bias depends on the bias with derivative one); the bias
-    gradient is also bitwise reproducible."""
+    gradient is also reproducible run to run (bit for bit under the
+    fixed-order reduction, to rounding under atomics)."""
     print(f"[case] gated scan with dt bias {bt}x{t_len}x{d}x{n} chunk {chunk}", flush=True)
     arrs = _gated_inputs(bt, t_len, d, n, seed=3 * d + n)
     rng = np.random.default_rng(11)
@@ -103,7 +104,7 @@ def test_gated_scan_with_dt_bias_matches_the_oracle(bt, t_len, d, n, chunk):
     for name, g, r in zip(("dx", "ddt_raw", "dA", "dB", "dC", "dbias"), grads, g_ref):
         assert g.shape == np.asarray(r).shape, name
         assert_close(name, g, r)
-    atomic = not _native.library().mhs_deterministic()
+    atomic = _native.bwd_reduction(bt, t_len, d, n, chunk) == _native.REDUCTION_ATOMIC
     assert_same("dbias", runs[0][1][5], runs[1][1][5], atomic)
 
 

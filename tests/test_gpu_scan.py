@@ -331,9 +331,12 @@ SEGMENT_CASES = [(2, 100, 64, 16, 16, 2), (1, 300, 96, 16, 16, 3), (2, 257, 40, 
                  (1, 2048, 64, 16, 64, 0)]
 
 
+@pytest.mark.parametrize("mode", ["auto", "fixed"])
 @pytest.mark.parametrize("bt,t_len,d,n,chunk,segs", SEGMENT_CASES)
-def test_time_segments_match_the_oracle(bt, t_len, d, n, chunk, segs):
-    print(f"[case] time segments {segs}: {bt}x{t_len}x{d}x{n} chunk {chunk}", flush=True)
+def test_time_segments_match_the_oracle(bt, t_len, d, n, chunk, segs, mode):
+    """Split backwards reduce with atomics under the automatic choice; the
+    fixed order is forced as well."""
+    print(f"[case] time segments {segs}: {bt}x{t_len}x{d}x{n} chunk {chunk} {mode}", flush=True)
     arrs = oracle.make_inputs(bt, t_len, d, n, seed=77 + d, style="bench")
     rng = np.random.default_rng(78)
     dy = rng.standard_normal((bt, t_len, d), dtype=np.float32)
@@ -342,10 +345,11 @@ def test_time_segments_match_the_oracle(bt, t_len, d, n, chunk, segs):
     g_ref = oracle.scan_bwd(*arrs, dy, dh_last=dh)
     _native.set_time_segments(segs)
     try:
-        y, h_last, grads = _run_hip(_to_dev(arrs), torch.from_numpy(dy).to(DEV), chunk=chunk,
-                                    dh_last=torch.from_numpy(dh).to(DEV))
-        _, ckpt, _ = torch.ops.mamba_hip.scan_fwd(*_to_dev(arrs), chunk, True)
-        torch.cuda.synchronize()
+        with reduction(_native.REDUCTION_FIXED if mode == "fixed" else _native.REDUCTION_AUTO):
+            y, h_last, grads = _run_hip(_to_dev(arrs), torch.from_numpy(dy).to(DEV), chunk=chunk,
+                                        dh_last=torch.from_numpy(dh).to(DEV))
+            _, ckpt, _ = torch.ops.mamba_hip.scan_fwd(*_to_dev(arrs), chunk, True)
+            torch.cuda.synchronize()
     finally:
         _native.set_time_segments(0)
     assert_close("y", y, y_ref)
@@ -356,8 +360,9 @@ def test_time_segments_match_the_oracle(bt, t_len, d, n, chunk, segs):
 
 
 def test_time_segments_auto_split_at_the_long_sequence_shape():
-    """4 x 16384 x 2048 x 16 (256 blocks): the automatic split (3 segments)
-    against the single-segment backward on the same inputs."""
+    """4 x 16384 x 2048 x 16 (256 blocks): the automatic split (2 forward
+    segments, 3 backward segments with the atomic reduction) against the
+    single-segment passes (fixed-order reduction) on the same inputs."""
     bt, t_len, d, n = 4, 16384, 2048, 16
     print(f"[case] auto time segments {bt}x{t_len}x{d}x{n}", flush=True)
     g = torch.Generator().manual_seed(5)

@@ -78,9 +78,40 @@ def test_workspace_size_formula():
         assert lib.mhs_scan_bwd_workspace_bytes(16, 512, 1536, 16, 64) == 2 * s * 4 + 32 * a * 4
     finally:
         _native.set_reduction(_native.REDUCTION_AUTO)
-    assert lib.mhs_deterministic() == 1      # automatic: the fixed order
+    # automatic: per shape, so not bit for bit at every shape
+    assert lib.mhs_deterministic() == 0
     with pytest.raises(_native.HipScanError, match="reduction mode"):
         _native.set_reduction(3)
+
+
+def test_automatic_reduction_follows_the_time_segments():
+    """Automatic: the fixed order where the backward runs in one time segment
+    (16x512x1536x16: 768 blocks, three per CU), atomics where it runs in
+    several (4x16384x2048x16: 256 blocks); forced modes hold at every shape,
+    and the workspace follows the mode the shape gets."""
+    lib = _native.library()
+    one, several = (16, 512, 1536, 16, 16), (4, 16384, 2048, 16, 16)
+    assert _native.bwd_reduction(*one) == _native.REDUCTION_FIXED
+    assert _native.bwd_reduction(*several) == _native.REDUCTION_ATOMIC
+    auto_ws = lib.mhs_scan_bwd_workspace_bytes(*several)
+    try:
+        for mode in (_native.REDUCTION_FIXED, _native.REDUCTION_ATOMIC):
+            _native.set_reduction(mode)
+            assert _native.bwd_reduction(*one) == mode
+            assert _native.bwd_reduction(*several) == mode
+            if mode == _native.REDUCTION_ATOMIC:
+                assert lib.mhs_scan_bwd_workspace_bytes(*several) == auto_ws
+            else:
+                assert lib.mhs_scan_bwd_workspace_bytes(*several) > auto_ws
+        # a forced split turns the automatic choice to atomics
+        _native.set_reduction(_native.REDUCTION_AUTO)
+        _native.set_time_segments(2)
+        assert _native.bwd_reduction(*one) == _native.REDUCTION_ATOMIC
+    finally:
+        _native.set_time_segments(0)
+        _native.set_reduction(_native.REDUCTION_AUTO)
+    with pytest.raises(_native.HipScanError, match="d_state"):
+        _native.bwd_reduction(16, 512, 1536, 0, 16)
 
 
 def test_set_variant_rejects_unknown_splits():
@@ -239,8 +270,9 @@ def test_forward_workspace():
     before the last segment."""
     lib = _native.library()
     assert lib.mhs_scan_fwd_workspace_bytes(16, 512, 1536, 16) == 0
-    # 4 x 16384 x 2048 x 16: 256 blocks -> 3 segments of 342 sub-chunks, 2
-    # carry units each (4 blocks per CU in the carry pass): 4 units carried
+    # 4 x 16384 x 2048 x 16: 256 blocks -> 2 segments (the forward plans for
+    # two blocks per CU) of 512 sub-chunks, 4 carry units each (4 blocks per
+    # CU in the carry pass): the 4 units of the first segment carried
     ru = lambda v: (v + 255) // 256 * 256
     assert lib.mhs_scan_fwd_workspace_bytes(4, 16384, 2048, 16) == \
         ru(4 * 4 * 2048 * 16 * 4) + ru(4 * 4 * 2048 * 4)
@@ -268,10 +300,10 @@ def test_conv_argument_errors():
 
 def test_segment_split_follows_the_compute_unit_count():
     """The automatic split plans for the device's compute units: 256 blocks
-    (4 x 16384 x 2048 x 16) get three segments at 256 CUs, one at 128 (two
-    blocks per CU already) and eight (the maximum) at 1024; the carry units
-    and the forward's workspace follow (1024 CUs: 7 carried segments x 2
-    units; 256 CUs: 2 x 2). Without a device the count is MI355X's 256."""
+    (4 x 16384 x 2048 x 16) get two forward segments at 256 CUs, one at 128
+    (two blocks per CU already) and eight (the maximum) at 1024; the carry
+    units and the forward's workspace follow (1024 CUs: 7 carried segments x
+    2 units; 256 CUs: 1 x 4). Without a device the count is MI355X's 256."""
     lib = _native.library()
     assert lib.mhs_cu_count() == 256
     ru = lambda v: (v + 255) // 256 * 256
