@@ -104,6 +104,72 @@ def make_inputs(bt, t_len, d, n, seed=2024):
 
 SETTLE_MS = 100.0
 EVENT_EVERY = 4   # timed steps per step with per-launch HIP events
+HIP_EVENT_DISABLE_SYSTEM_FENCE = 0x20000000
+USE_TORCH_EVENTS = False   # --torch-events: torch.cuda.Event instead of TimingEvent
+
+
+class TimingEvent:
+    """A HIP event for GPU timing only, recorded on torch's current stream and
+    created with hipEventDisableSystemFence: recording it skips the
+    system-scope cache writeback and invalidate that a default event (torch's
+    torch.cuda.Event) performs, which costs the GPU several us per marker and
+    slows the work right after it. Its timestamps are read after a device
+    synchronize. The runtime is the one torch loaded (same soname)."""
+    _hip = None
+
+    @classmethod
+    def _lib(cls):
+        import ctypes
+        if cls._hip is None:
+            lib = ctypes.CDLL("libamdhip64.so.7")
+            lib.hipEventCreateWithFlags.argtypes = [ctypes.POINTER(ctypes.c_void_p), ctypes.c_uint]
+            lib.hipEventRecord.argtypes = [ctypes.c_void_p, ctypes.c_void_p]
+            lib.hipEventElapsedTime.argtypes = [ctypes.POINTER(ctypes.c_float), ctypes.c_void_p,
+                                                ctypes.c_void_p]
+            lib.hipEventDestroy.argtypes = [ctypes.c_void_p]
+            cls._hip = lib
+        return cls._hip
+
+    def __init__(self):
+        import ctypes
+        self.ev = ctypes.c_void_p()
+        rc = self._lib().hipEventCreateWithFlags(ctypes.byref(self.ev),
+                                                 HIP_EVENT_DISABLE_SYSTEM_FENCE)
+        if rc != 0:
+            raise RuntimeError(f"hipEventCreateWithFlags failed ({rc})")
+
+    def record(self):
+        import ctypes
+        import torch
+        rc = self._lib().hipEventRecord(self.ev,
+                                        ctypes.c_void_p(torch.cuda.current_stream().cuda_stream))
+        if rc != 0:
+            raise RuntimeError(f"hipEventRecord failed ({rc})")
+
+    def elapsed_time(self, end: "TimingEvent") -> float:
+        """Milliseconds from this event to `end`."""
+        import ctypes
+        ms = ctypes.c_float()
+        rc = self._lib().hipEventElapsedTime(ctypes.byref(ms), self.ev, end.ev)
+        if rc != 0:
+            raise RuntimeError(f"hipEventElapsedTime failed ({rc})")
+        return ms.value
+
+    def __del__(self):
+        if getattr(self, "ev", None) and TimingEvent._hip is not None:
+            TimingEvent._hip.hipEventDestroy(self.ev)
+
+
+def timing_event():
+    """A GPU timing event on torch's current stream (TimingEvent, or
+    torch.cuda.Event with --torch-events)."""
+    import torch
+    return torch.cuda.Event(enable_timing=True) if USE_TORCH_EVENTS else TimingEvent()
+
+
+def event_kind() -> str:
+    return ("torch.cuda.Event (default HIP event)" if USE_TORCH_EVENTS
+            else "HIP event with hipEventDisableSystemFence")
 
 
 def settle_clocks(fn, ms: float = SETTLE_MS) -> int:
@@ -140,16 +206,17 @@ def copy_bandwidth(nbytes: int = 256 << 20) -> dict:
 
 
 def time_events(fn, reps: int) -> float:
-    """Average GPU duration (ms) of fn() over reps, HIP events on the current stream."""
+    """Average GPU duration (ms) of fn() over reps, HIP events on the current
+    stream: one marker between consecutive calls ends one interval and starts
+    the next."""
     import torch
-    start = [torch.cuda.Event(enable_timing=True) for _ in range(reps)]
-    stop = [torch.cuda.Event(enable_timing=True) for _ in range(reps)]
+    ev = [timing_event() for _ in range(reps + 1)]
+    ev[0].record()
     for i in range(reps):
-        start[i].record()
         fn()
-        stop[i].record()
+        ev[i + 1].record()
     torch.cuda.synchronize()
-    return sum(s.elapsed_time(e) for s, e in zip(start, stop)) / reps
+    return sum(ev[i].elapsed_time(ev[i + 1]) for i in range(reps)) / reps
 
 
 def cpu_baseline_scan(bt, t_len, d, n, reps: int = 3, warmup: int = 2, grad: bool = True,
@@ -684,7 +751,7 @@ def infer_measure() -> dict:
 
     decode()
     torch.cuda.synchronize()
-    start, stop = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    start, stop = timing_event(), timing_event()
     start.record()
     decode()
     stop.record()
@@ -743,10 +810,18 @@ def bench_scan(args) -> dict:
     # forward launch and its backward launch, on the stream the kernels run
     # on (torch's current stream, which the autograd backward also uses): the
     # per-launch averages come from the timed steps themselves. Each event is
-    # a marker packet that costs the GPU about 2.5 us; on every step the four
-    # of them would add 5% to the step time.
-    events = [[torch.cuda.Event(enable_timing=True) for _ in range(4)]
-              for _ in range((args.steps + EVENT_EVERY - 1) // EVENT_EVERY)]
+    # a marker packet that costs the GPU time (in a kernel trace about 5 us
+    # each for torch's default events, 4 us without the system fence,
+    # TimingEvent); on every step they would add that to the step time.
+    # Three events per instrumented step: before the forward, between the
+    # forward and the backward (one marker serves both intervals), after the
+    # backward. The instrumented steps are the last of every EVENT_EVERY: the
+    # timed region starts from a synchronized, idle GPU, and its first step's
+    # forward would include the host's launch latency.
+    marked = [i for i in range(args.steps) if i % EVENT_EVERY == EVENT_EVERY - 1] or \
+        [args.steps - 1]
+    events = [[timing_event() for _ in range(3)] for _ in marked]
+    event_of = dict(zip(marked, events))
 
     def step(ev=None):
         for t in leaves:
@@ -756,10 +831,9 @@ def bench_scan(args) -> dict:
         y = selective_scan_hip(*leaves, chunk=chunk)
         if ev is not None:
             ev[1].record()
-            ev[2].record()
         y.backward(dy)
         if ev is not None:
-            ev[3].record()
+            ev[2].record()
 
     settled = settle_clocks(step)
     for _ in range(args.warmup):
@@ -767,12 +841,12 @@ def bench_scan(args) -> dict:
     torch.cuda.synchronize()
     t0 = time.perf_counter()
     for i in range(args.steps):
-        step(events[i // EVENT_EVERY] if i % EVENT_EVERY == 0 else None)
+        step(event_of.get(i))
     torch.cuda.synchronize()
     elapsed = time.perf_counter() - t0
     ms = elapsed * 1e3 / args.steps
     fwd_ms = sum(e[0].elapsed_time(e[1]) for e in events) / len(events)
-    bwd_ms = sum(e[2].elapsed_time(e[3]) for e in events) / len(events)
+    bwd_ms = sum(e[1].elapsed_time(e[2]) for e in events) / len(events)
     nbytes = scan_bytes(bt, t_len, d, n)
     bwd_gbs = nbytes["bwd"] / (bwd_ms * 1e-3) / 1e9
     fwd_gbs = nbytes["fwd"] / (fwd_ms * 1e-3) / 1e9
@@ -805,7 +879,7 @@ def bench_scan(args) -> dict:
                                         if counters else None),
                      "kernel": "scan backward launch (bwd_kernel + bwd_reduce_kernel)",
                      "avg_ms": bwd_ms, "algorithmic_bytes": nbytes["bwd"],
-                     "timed_launches": len(events)},
+                     "timed_launches": len(events), "events": event_kind()},
         "valu": valu_block(counters),
         "scan_fwd": {"avg_ms": fwd_ms, "achieved_GBs": fwd_gbs,
                      "algorithmic_bytes": nbytes["fwd"]},
@@ -880,6 +954,9 @@ def main() -> int:
     ap.add_argument("--d-state", dest="d_state", type=int, default=16)
     ap.add_argument("--chunk", type=int, default=16)
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--torch-events", action="store_true",
+                    help="time with torch.cuda.Event (default HIP events, with the system-scope "
+                         "fence) instead of HIP events created with hipEventDisableSystemFence")
     ap.add_argument("--no-extra", action="store_true",
                     help="only the headline workload (no chunk-64, atomic, long-sequence and "
                          "inference figures)")
@@ -894,6 +971,8 @@ def main() -> int:
     ap.add_argument("--trace-summary", default=None, metavar="DIR",
                     help="summarise a kernel-trace run of --workload train under DIR")
     args = ap.parse_args()
+    global USE_TORCH_EVENTS
+    USE_TORCH_EVENTS = args.torch_events
 
     from mamba_metal_scan_amd import _native
     _native.set_reduction({"auto": _native.REDUCTION_AUTO, "fixed": _native.REDUCTION_FIXED,
