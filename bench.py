@@ -428,11 +428,31 @@ def pmc_summary(args) -> None:
     # Kernel-trace durations: the last `steps` dispatches of each kernel are
     # those of bench.py's timed steps.
     durs: dict = {}
+    spans = None
     trace = os.path.join(args.pmc_summary, "kt", "run_kernel_trace.csv")
     if os.path.exists(trace):
-        for r in csv.DictReader(open(trace)):
+        rows = sorted(csv.DictReader(open(trace)), key=lambda r: int(r["Start_Timestamp"]))
+        for r in rows:
             durs.setdefault(_short_kernel(r["Kernel_Name"]), []).append(
                 (int(r["End_Timestamp"]) - int(r["Start_Timestamp"])) / 1e3)
+        # The timed steps' launches as the bench's events bracket them: the
+        # backward launch from bwd_kernel's start to bwd_reduce_kernel's end,
+        # and the idle gaps before each forward and each backward (markers).
+        scan = [(_short_kernel(r["Kernel_Name"]), int(r["Start_Timestamp"]),
+                 int(r["End_Timestamp"])) for r in rows
+                if _short_kernel(r["Kernel_Name"]) in ("fwd_kernel", "bwd_kernel",
+                                                       "bwd_reduce_kernel")]
+        steps = [scan[i:i + 3] for i in range(len(scan) - 3 * args.steps, len(scan), 3)]
+        if steps and all([k[0] for k in st] == ["fwd_kernel", "bwd_kernel", "bwd_reduce_kernel"]
+                         for st in steps):
+            n = len(steps)
+            spans = {"steps": n,
+                     "fwd_us": sum(st[0][2] - st[0][1] for st in steps) / n / 1e3,
+                     "bwd_launch_us": sum(st[2][2] - st[1][1] for st in steps) / n / 1e3,
+                     "gap_before_bwd_us": sum(st[1][1] - st[0][2] for st in steps) / n / 1e3,
+                     "gap_before_fwd_us": sum(b[0][1] - a[2][2] for a, b in zip(steps, steps[1:]))
+                     / max(n - 1, 1) / 1e3,
+                     "steps_with_gaps": sum(1 for st in steps if st[1][1] - st[0][2] > 1000)}
     kernels = {}
     for kern in ("fwd_kernel", "bwd_kernel", "bwd_reduce_kernel"):
         if (kern, "FETCH_SIZE") not in mean:
@@ -467,6 +487,7 @@ def pmc_summary(args) -> None:
         "fwd_launch": {"hbm_bytes": kernels["fwd_kernel"]["hbm_bytes"],
                        "algorithmic_bytes": nbytes["fwd"]},
         "kernels": kernels,
+        "trace_launch": spans,
         "calibration": {"copy_bytes": COPY_BYTES, "fetch_factor": fetch_factor,
                         "write_factor": write_factor},
         "commands": {
@@ -503,6 +524,17 @@ def pmc_summary(args) -> None:
                   "`bwd_reduce_kernel`. The calls include bench.py's untimed clock-settle "
                   "steps, which begin at the idle clock; the last column averages the "
                   "timed steps' launches only.", ""]
+        if spans:
+            lines += [f"Over the {spans['steps']} timed steps the backward launch spans "
+                      f"{spans['bwd_launch_us']:.1f} us from `bwd_kernel`'s start to "
+                      f"`bwd_reduce_kernel`'s end, the forward {spans['fwd_us']:.1f} us; the "
+                      f"GPU idles {spans['gap_before_bwd_us']:.1f} us before a backward and "
+                      f"{spans['gap_before_fwd_us']:.1f} us before a forward on average "
+                      f"(a gap over 1 us before the backward at {spans['steps_with_gaps']} of "
+                      f"{spans['steps']} steps: bench.py times one step in four with events, "
+                      "and each marker holds the queue for a few us). bench.py's event-timed "
+                      "launches include one such marker each, and so read a few us above "
+                      "these spans.", ""]
     lines += ["## HBM traffic per launch", "",
               f"Calibration: a {COPY_BYTES} B device copy reads FETCH_SIZE x{fetch_factor:.3f} and "
               f"WRITE_SIZE x{write_factor:.3f} of its true bytes; the figures below are scaled by "
