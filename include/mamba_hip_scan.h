@@ -71,11 +71,14 @@ int mhs_set_variant(int states_per_lane);
  * a workspace) and the backward split the sequence into (1..8; 0 restores the
  * automatic choice: one segment while the grid has at least two blocks of 32
  * channels per compute unit, otherwise enough segments of at least 128 steps
- * for about three). Segments run in parallel after a short pass that carries
- * the state (forward) or the adjoint (backward) across segment boundaries;
- * results equal the unsegmented scan up to rounding. The workspace sizes
- * depend on it. No counterpart in the reference (its kernels walk each
- * channel's whole sequence in one thread, scan.py:78-127, :132-261). */
+ * for about two blocks per compute unit in the forward and three in the
+ * backward, at most 8). Segments run in parallel after a short pass that
+ * carries the state (forward) or the adjoint (backward) across segment
+ * boundaries, over carry units of each segment sized for about four blocks
+ * per compute unit; results equal the unsegmented scan up to rounding. The
+ * workspace sizes depend on it. No counterpart in the reference (its kernels
+ * walk each channel's whole sequence in one thread, scan.py:78-127,
+ * :132-261). */
 int mhs_set_time_segments(int segments);
 
 /* The compute-unit count the automatic time-segment choice plans for: the
@@ -187,9 +190,10 @@ size_t mhs_scan_bwd_workspace_bytes(int64_t batch, int64_t seqlen, int64_t d_inn
  *              reference drops it, scan.py:390-393)
  *   dx, ddt, daneg, dB, dC : fully written (no pre-zeroing needed). dB, dC and
  *              daneg are sums over channels / (batch, time), reduced as
- *              mhs_set_reduction selects (fixed order, the default: bit-for-bit
- *              reproducible; atomics: reproducible to rounding). dx and ddt are
- *              reproducible bit for bit either way.
+ *              mhs_set_reduction selects (fixed order: bit-for-bit
+ *              reproducible; atomics: reproducible to rounding; the default
+ *              chooses per shape). dx and ddt are reproducible bit for bit
+ *              either way.
  *   workspace: >= mhs_scan_bwd_workspace_bytes(...) bytes of device memory,
  *              256-byte aligned; its contents on entry do not matter.
  */
@@ -233,14 +237,15 @@ int mhs_scan_gated_fwd_f32(const float* x, const float* dt_raw, const float* A,
  *     ddt_raw = ddt * (dt_max - dt_min) * s * (1 - s),   s = sigmoid(dt_raw)
  *     dA      = dAneg * sigmoid(A)
  * and dx, dB, dC as mhs_scan_bwd_f32. Workspace: mhs_scan_bwd_workspace_bytes
- * of the same shape. Bit-for-bit reproducible.
+ * of the same shape. Reproducible as mhs_scan_bwd_f32 (bit for bit under the
+ * fixed-order reduction).
  * ld_dt, ld_bc: input row strides as in mhs_scan_gated_fwd_f32; ld_ddt,
  * ld_dbc: row strides of the outputs ddt_raw and dB, dC (0: contiguous), so
  * that they can be written into the column slices of one gradient tensor of
  * the projection. dx is contiguous.
  * dt_bias: as in the forward. ddt_bias: NULL, or d_inner fp32 that receive
- * the gradient of the bias, sum over batch and time of ddt_raw (a fixed-order
- * reduction: also bit-for-bit reproducible).
+ * the gradient of the bias, sum over batch and time of ddt_raw (reduced as
+ * dAneg is).
  */
 int mhs_scan_gated_bwd_f32(const float* x, const float* dt_raw, const float* A,
                            const float* B, const float* C, float dt_min, float dt_max,
