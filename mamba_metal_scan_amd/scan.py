@@ -31,8 +31,10 @@ Differences from the reference, by design:
   backward kernel's register window on gfx950; any ``chunk >= 1`` gives the
   same results.
 * d_state is any value in 1..64 (the reference needs a multiple of 4).
-* dB, dC and dAneg are reduced in a fixed order: the backward is bit-for-bit
-  reproducible.
+* dB, dC and dAneg are reduced in a fixed order (bit-for-bit reproducible)
+  where the grid fills the GPU, and with fp32 atomics (reproducible to
+  rounding) where the backward runs in time segments; ``_native.set_reduction``
+  overrides the choice and torch's deterministic mode forces the fixed order.
 """
 from __future__ import annotations
 
