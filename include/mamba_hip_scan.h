@@ -61,8 +61,9 @@ int64_t mhs_num_chunks(int64_t seqlen, int64_t chunk);
 int64_t mhs_preferred_chunk(int64_t d_state);
 
 /* Tuning knob, process-wide: force the number of d_state entries each GPU
- * lane carries per channel (2 or 4; 0 restores the automatic choice: 2 up to
- * d_state 32, 4 above). With 2, d_state above 32 becomes unsupported. No
+ * lane carries per channel (1, 2 or 4; 0 restores the automatic choice: 2 up
+ * to d_state 32, 4 above). With 2, d_state above 32 becomes unsupported; with
+ * 1, d_state above 16 (d_state is padded to 8 or 16). No
  * counterpart in the reference (its Metal kernels keep all d_state entries of
  * a channel in one thread, scan.py:67-69). */
 int mhs_set_variant(int states_per_lane);

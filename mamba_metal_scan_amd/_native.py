@@ -175,7 +175,7 @@ def preferred_chunk(d_state: int) -> int:
 
 
 def set_variant(states_per_lane: int) -> None:
-    """Force 2 or 4 states per lane (0 = automatic), process-wide."""
+    """Force 1, 2 or 4 states per lane (0 = automatic), process-wide."""
     _check(library().mhs_set_variant(int(states_per_lane)), "mhs_set_variant")
 
 

@@ -145,10 +145,12 @@ bwd_kernel(BwdArgs a) {
   constexpr int PER = (kCH * kQuads + NT - 1) / NT;
   constexpr int PERS = (kSteps * NP + NT - 1) / NT;
   constexpr int FT = (kSteps / 2 * kCH + NT - 1) / NT;      // dx/ddt tasks per thread
-  constexpr int FK = kSteps * NP / NT;                      // dB (or dC) copies per thread
+  constexpr int FK = (kSteps * NP + NT - 1) / NT;           // dB (or dC) copies per thread
+  // One state per lane gives a tile of kSteps * NP = NT / 2 sums: half the
+  // threads copy one each. Two or four: every thread copies FK.
+  constexpr bool kFKExact = FK * NT == kSteps * NP;
   constexpr int M = 4 * NPL;            // dB/dC products per lane per two steps
-  static_assert(NPL == 2 || NPL == 4, "two or four states per lane");
-  static_assert(FK * NT == kSteps * NP, "dB/dC copy-out must tile the block");
+  static_assert(NPL == 1 || NPL == 2 || NPL == 4, "one, two or four states per lane");
   static_assert(!ATOM || !CARRY, "atomics: gradient pass only");
 
   extern __shared__ float lds[];
@@ -355,9 +357,11 @@ bwd_kernel(BwdArgs a) {
     const int ldr = ATOM ? a.ld_dbc : N;
 #pragma unroll
     for (int f = 0; f < FK; ++f) {
-      const int r = tid + f * NT;                 // (k, n) of the tile, n fastest
+      const int r0 = tid + f * NT;                // (k, n) of the tile, n fastest
+      const bool okr = kFKExact || r0 < kSteps * NP;
+      const int r = okr ? r0 : 0;
       const int k = r / NP, n = r % NP;
-      const unsigned o = n < N ? 4u * (unsigned)(k * ldr + n) : kOOB;
+      const unsigned o = okr && n < N ? 4u * (unsigned)(k * ldr + n) : kOOB;
       if constexpr (ATOM) {
         gbs.atomic_add(tDBC[r], o);
         gcs.atomic_add(tDBC[kSteps * NP + r], o);

@@ -236,7 +236,7 @@ void fill_elem(Kernels& k) {
 
 template <int NPL, int G>
 void fill(Plan& p) {
-  constexpr int MINW = NPL == 2 ? 3 : 2;
+  constexpr int MINW = NPL == 1 ? 4 : NPL == 2 ? 3 : 2;
   fill_elem<NPL, G, MINW, 4>(p.k[kF32]);
   fill_elem<NPL, G, MINW, 2>(p.k[kBF16]);
   p.fwd_lds = mhs::fwd_lds_floats(G, NPL) * 4;
@@ -259,10 +259,22 @@ bool fill_g(int G, Plan& p) {
   return true;
 }
 
+// One state per lane: plans for d_state 5..8 (G 4) and 9..16 (G 8) only.
+bool fill_g1(int G, Plan& p) {
+  switch (G) {
+    case 4: fill<1, 4>(p); break;
+    case 8: fill<1, 8>(p); break;
+    default: return false;
+  }
+  return true;
+}
+
 bool plan_for(int N, int npl, Plan& p) {
-  const int G = (N + 2 * npl - 1) / (2 * npl);
+  // One state per lane: the instantiated plans pad d_state to 8 or 16.
+  const int G = npl == 1 ? (N <= 8 ? 4 : N <= 16 ? 8 : 0) : (N + 2 * npl - 1) / (2 * npl);
   if (G < 1 || G > kMaxG) return false;
-  const bool ok = npl == 2 ? fill_g<2>(G, p) : npl == 4 ? fill_g<4>(G, p) : false;
+  const bool ok = npl == 2 ? fill_g<2>(G, p) : npl == 4 ? fill_g<4>(G, p)
+                  : npl == 1 ? fill_g1(G, p) : false;
   if (!ok) return false;
   p.npl = npl;
   p.G = G;
@@ -715,8 +727,8 @@ int64_t mhs_num_chunks(int64_t seqlen, int64_t chunk) {
 }
 
 int mhs_set_variant(int npl) {
-  if (npl != 0 && npl != 2 && npl != 4)
-    return fail(MHS_EINVAL, "states per lane must be 0 (auto), 2 or 4; got %d", npl);
+  if (npl != 0 && npl != 1 && npl != 2 && npl != 4)
+    return fail(MHS_EINVAL, "states per lane must be 0 (auto), 1, 2 or 4; got %d", npl);
   g_npl_override.store(npl, std::memory_order_relaxed);
   return MHS_OK;
 }

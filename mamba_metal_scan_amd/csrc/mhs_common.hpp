@@ -134,7 +134,20 @@ __device__ __forceinline__ void rs_bits32_16(const float (&a)[8], float (&c)[2])
         "v"(a[7]));
 }
 
-// Sums M values (M in {8, 16}) over the 32 lanes of each half-wave, as a
+// The stage over lane bit 3 alone, for a pair: (x, y) becomes x + x' in the
+// banks whose bit 3 is 0 and y + y' in the others (as in rs_bits32_8).
+__device__ __forceinline__ float rs_bit3_4(const float (&a)[2]) {
+  float b;
+  asm("s_nop 1\n\t"
+      "v_add_f32_dpp %0, %1, %1 row_ror:8 row_mask:0xf bank_mask:0x3\n\t"
+      "v_add_f32_dpp %0, %2, %2 row_ror:8 row_mask:0xf bank_mask:0xc\n\t"
+      "s_nop 1"
+      : "=&v"(b)
+      : "v"(a[0]), "v"(a[1]));
+  return b;
+}
+
+// Sums M values (M in {4, 8, 16}) over the 32 lanes of each half-wave, as a
 // reduce-scatter: v_permlane16_swap across lane bit 4, then DPP row_ror:8
 // (bit 3), row_half_mirror (bit 2) and quad_perm xor 2 (bit 1), each halving
 // the values a lane holds, then plain DPP adds over the lane bits left. Lane l
@@ -142,7 +155,7 @@ __device__ __forceinline__ void rs_bits32_16(const float (&a)[8], float (&c)[2])
 // the result is bit-for-bit reproducible.
 template <int M>
 __device__ __forceinline__ float half_wave_reduce_scatter(const float (&v)[M], int lane) {
-  static_assert(M == 8 || M == 16, "8 or 16 values per lane");
+  static_assert(M == 4 || M == 8 || M == 16, "4, 8 or 16 values per lane");
   float a[M / 2];
 #pragma unroll
   for (int i = 0; i < M / 2; ++i) {
@@ -150,25 +163,31 @@ __device__ __forceinline__ float half_wave_reduce_scatter(const float (&v)[M], i
                                                     __float_as_uint(v[2 * i + 1]), false, false);
     a[i] = __uint_as_float(sw[0]) + __uint_as_float(sw[1]);
   }
-  float c[M / 8];
-  if constexpr (M == 8) {
-    c[0] = rs_bits32_8(a);
+  if constexpr (M == 4) {
+    // Bits 2, 1, 0 are all left: a plain sum over each group of 8 lanes.
+    return group_sum<8>(rs_bit3_4(a));
   } else {
-    rs_bits32_16(a, c);
+    float c[M / 8];
+    if constexpr (M == 8) {
+      c[0] = rs_bits32_8(a);
+    } else {
+      rs_bits32_16(a, c);
+    }
+    float r;
+    if constexpr (M == 8) {
+      r = dpp_add<kDppXor2>(c[0]);
+    } else {
+      float d[1];
+      rs_stage_dpp<kDppXor2>(c, d, (lane >> 1) & 1);
+      r = d[0];
+    }
+    return dpp_add<kDppXor1>(r);
   }
-  float r;
-  if constexpr (M == 8) {
-    r = dpp_add<kDppXor2>(c[0]);
-  } else {
-    float d[1];
-    rs_stage_dpp<kDppXor2>(c, d, (lane >> 1) & 1);
-    r = d[0];
-  }
-  return dpp_add<kDppXor1>(r);
 }
 // Index of the value whose total half_wave_reduce_scatter<M> leaves in lane l.
 template <int M>
 __device__ __forceinline__ int rs_index(int lane) {
+  if constexpr (M == 4) return 2 * ((lane >> 3) & 1) + ((lane >> 4) & 1);
   const int i = 4 * ((lane >> 2) & 1) + 2 * ((lane >> 3) & 1) + ((lane >> 4) & 1);
   return M == 8 ? i : i + 8 * ((lane >> 1) & 1);
 }

@@ -3,8 +3,9 @@
 // them, so that the four groups compile in parallel.
 //
 // Plans: NPL states per lane in {2, 4}, G waves in 1..8, MINW the
-// waves-per-SIMD target (3 for NPL 2, 2 for NPL 4). ES: element bytes of the
-// activations (4: fp32, 2: bf16).
+// waves-per-SIMD target (3 for NPL 2, 2 for NPL 4); and one state per lane
+// for d_state 8 and 16 (G 4 and 8, 512-thread blocks at 16), MINW 4. ES:
+// element bytes of the activations (4: fp32, 2: bf16).
 #pragma once
 
 #include "mhs_bwd.hpp"
@@ -16,7 +17,8 @@
   X(PREFIX, 2, 7, 3, ES) X(PREFIX, 2, 8, 3, ES)                                        \
   X(PREFIX, 4, 1, 2, ES) X(PREFIX, 4, 2, 2, ES) X(PREFIX, 4, 3, 2, ES)                 \
   X(PREFIX, 4, 4, 2, ES) X(PREFIX, 4, 5, 2, ES) X(PREFIX, 4, 6, 2, ES)                 \
-  X(PREFIX, 4, 7, 2, ES) X(PREFIX, 4, 8, 2, ES)
+  X(PREFIX, 4, 7, 2, ES) X(PREFIX, 4, 8, 2, ES)                                        \
+  X(PREFIX, 1, 4, 4, ES) X(PREFIX, 1, 8, 4, ES)
 
 // Forward: checkpoint stride aligned / any, ungated / gated; the carry pass
 // of the time segments and the checkpoint-only pass (ungated / gated).

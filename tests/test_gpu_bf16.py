@@ -61,6 +61,16 @@ def test_bf16_scan_matches_the_oracle(bt, t_len, d, n, chunk):
         assert_close(name, g, r, TOL_F32 if name == "dAneg" else TOL_BF16)
 
 
+@pytest.mark.parametrize("bt,t_len,d,n,chunk", [(2, 64, 96, 16, 16), (2, 77, 64, 8, 64)])
+def test_bf16_scan_with_one_state_per_lane(bt, t_len, d, n, chunk):
+    """The bf16 scan's checks with one state per lane forced."""
+    _native.set_variant(1)
+    try:
+        test_bf16_scan_matches_the_oracle(bt, t_len, d, n, chunk)
+    finally:
+        _native.set_variant(0)
+
+
 @pytest.mark.parametrize("bt,t_len,d,n,segs,bias", [(2, 130, 70, 16, 0, False),
                                                     (16, 512, 1432, 16, 0, False),
                                                     (1, 300, 64, 16, 3, False),

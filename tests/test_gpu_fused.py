@@ -108,6 +108,19 @@ def test_gated_scan_with_dt_bias_matches_the_oracle(bt, t_len, d, n, chunk):
     assert_same("dbias", runs[0][1][5], runs[1][1][5], atomic)
 
 
+@pytest.mark.parametrize("bt,t_len,d,n,chunk", [(1, 600, 64, 16, 16), (3, 130, 70, 5, 7),
+                                                  (2, 77, 64, 16, 64)])
+def test_gated_scan_with_one_state_per_lane(bt, t_len, d, n, chunk):
+    """The same checks with one state per lane forced (8-wave blocks at
+    d_state 16, 4-wave blocks at 5): the gate, the bias partials and, in the
+    first case, the time segments' carry passes."""
+    _native.set_variant(1)
+    try:
+        test_gated_scan_with_dt_bias_matches_the_oracle(bt, t_len, d, n, chunk)
+    finally:
+        _native.set_variant(0)
+
+
 def test_gated_scan_rejects_a_bad_dt_bias():
     arrs = [torch.from_numpy(a).to(DEV) for a in _gated_inputs(1, 8, 32, 16, seed=1)]
     with pytest.raises(ValueError, match="dt_bias"):

@@ -249,10 +249,12 @@ def test_atomic_and_fixed_order_reductions_agree_at_the_training_shape():
     assert max(spread.values()) <= RED_TOL
 
 
-@pytest.mark.parametrize("npl,n", [(2, 16), (4, 16), (2, 7), (4, 7), (4, 24), (2, 32)])
+@pytest.mark.parametrize("npl,n", [(2, 16), (4, 16), (2, 7), (4, 7), (4, 24), (2, 32),
+                                   (1, 16), (1, 13), (1, 8), (1, 3)])
 def test_every_state_split_agrees(npl, n):
-    """Forcing 2 or 4 states per lane (other block shapes, other padding of
-    d_state) gives the same results."""
+    """Forcing 1, 2 or 4 states per lane (other block shapes, other padding
+    of d_state; one state per lane runs 8-wave blocks at d_state 9..16 and
+    4-wave blocks up to 8) gives the same results."""
     bt, t_len, d = 2, 100, 130
     print(f"[case] npl {npl} d_state {n}", flush=True)
     arrs = oracle.make_inputs(bt, t_len, d, n, seed=31, style="bench")
@@ -352,6 +354,42 @@ def test_time_segments_match_the_oracle(bt, t_len, d, n, chunk, segs, mode):
             torch.cuda.synchronize()
     finally:
         _native.set_time_segments(0)
+    assert_close("y", y, y_ref)
+    assert_close("h_last", h_last, h_ref)
+    assert_close("ckpt", ckpt, oracle.scan_fwd(*arrs, chunk=chunk)[1])
+    for name, g, r in zip(("dx", "ddt", "dAneg", "dB", "dC"), grads, g_ref):
+        assert_close(name, g, r)
+
+
+# One state per lane (d_state <= 16) under forced time segments: the carry
+# passes, the segmented gradient pass and both reductions with 8-wave blocks
+# (d_state 9..16) and 4-wave blocks (d_state <= 8).
+NPL1_SEGMENT_CASES = [(2, 100, 64, 16, 16, 2), (1, 300, 96, 8, 16, 3), (2, 257, 40, 13, 7, 5),
+                      (1, 1000, 64, 16, 48, 4), (3, 200, 130, 5, 64, 1)]
+
+
+@pytest.mark.parametrize("mode", ["auto", "fixed"])
+@pytest.mark.parametrize("bt,t_len,d,n,chunk,segs", NPL1_SEGMENT_CASES)
+def test_one_state_per_lane_matches_the_oracle(bt, t_len, d, n, chunk, segs, mode):
+    print(f"[case] one state per lane, {segs} segments: {bt}x{t_len}x{d}x{n} chunk {chunk} "
+          f"{mode}", flush=True)
+    arrs = oracle.make_inputs(bt, t_len, d, n, seed=177 + d, style="bench")
+    rng = np.random.default_rng(79)
+    dy = rng.standard_normal((bt, t_len, d), dtype=np.float32)
+    dh = rng.standard_normal((bt, d, n), dtype=np.float32)
+    y_ref, _, h_ref = oracle.scan_fwd(*arrs)
+    g_ref = oracle.scan_bwd(*arrs, dy, dh_last=dh)
+    _native.set_variant(1)
+    _native.set_time_segments(segs)
+    try:
+        with reduction(_native.REDUCTION_FIXED if mode == "fixed" else _native.REDUCTION_ATOMIC):
+            y, h_last, grads = _run_hip(_to_dev(arrs), torch.from_numpy(dy).to(DEV), chunk=chunk,
+                                        dh_last=torch.from_numpy(dh).to(DEV))
+            _, ckpt, _ = torch.ops.mamba_hip.scan_fwd(*_to_dev(arrs), chunk, True)
+            torch.cuda.synchronize()
+    finally:
+        _native.set_time_segments(0)
+        _native.set_variant(0)
     assert_close("y", y, y_ref)
     assert_close("h_last", h_last, h_ref)
     assert_close("ckpt", ckpt, oracle.scan_fwd(*arrs, chunk=chunk)[1])

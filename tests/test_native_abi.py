@@ -118,12 +118,16 @@ def test_set_variant_rejects_unknown_splits():
     lib = _native.library()
     with pytest.raises(_native.HipScanError, match="states per lane"):
         _native.set_variant(3)
-    assert lib.mhs_set_variant(1) == MHS_EINVAL
+    assert lib.mhs_set_variant(8) == MHS_EINVAL
     assert lib.mhs_set_variant(0) == MHS_OK
-    # With two states per lane, d_state above 32 has no plan.
+    # With two states per lane, d_state above 32 has no plan; with one, d_state
+    # above 16.
     try:
         _native.set_variant(2)
         assert lib.mhs_preferred_chunk(40) == 0
+        _native.set_variant(1)
+        assert lib.mhs_preferred_chunk(16) == 16
+        assert lib.mhs_preferred_chunk(17) == 0
     finally:
         _native.set_variant(0)
     assert lib.mhs_preferred_chunk(40) == 16
