@@ -115,7 +115,7 @@ struct BwdArgs {
 // One staging buffer (the kernel keeps two) and the single-buffered rest.
 __host__ __device__ constexpr int bwd_buf_floats(int G, int NPL) {
   return 4 * kCH * kSteps               // dt, dy, x, dt*x (channel-major)
-         + 2 * kSteps * 2 * G * NPL;    // B, C tiles
+         + 2 * bc_tile_floats(2 * G, NPL);   // B, C tiles
 }
 __host__ __device__ constexpr int bwd_lds_floats(int G, int NPL) {
   return 2 * bwd_buf_floats(G, NPL)
@@ -177,7 +177,7 @@ bwd_kernel(BwdArgs a) {
   float* tDBC = tS + G * 64 * kSteps;                 // [2][16][NP]
   // Staging buffer j: dt, dy, x (channel-major), B, C (per lane group).
   constexpr int oDY = kCH * kSteps, oX = 2 * kCH * kSteps, oDTX = 3 * kCH * kSteps,
-                oB = 4 * kCH * kSteps, oC = oB + kSteps * NP;
+                oB = 4 * kCH * kSteps, oC = oB + bc_tile_floats(2 * G, NPL);
   // The reduce-scatter leaves lane `lane` with the total of product rs_index:
   // products are numbered kind * 2NPL + slot * NPL + j (kind 0: dB, 1: dC;
   // slot: step k + slot; j: state n0 + j of this half-wave's group).
@@ -395,8 +395,8 @@ bwd_kernel(BwdArgs a) {
     prio.step(i);
     const int ci = c_hi - 1 - i;
     const float* s0 = lds + (i & 1) * BUF;
-    const float* gB = s0 + oB + q * kSteps * NPL;
-    const float* gC = s0 + oC + q * kSteps * NPL;
+    const float* gB = s0 + oB + q * bc_group_floats(NPL);
+    const float* gC = s0 + oC + q * bc_group_floats(NPL);
 
     if constexpr (CARRY) {
       // The adjoint alone: G_t = dy_t C_t + dA_{t+1} G_{t+1}, dA formed on

@@ -577,11 +577,28 @@ struct QuadLoader {
   }
 };
 
+// B / C tiles in LDS: per state group q (NPL states), the 16 steps x NPL
+// states of the group, [16][NPL], followed by kBCPad floats of padding. The
+// padding puts the two half-waves' groups (read at the same instant, each
+// half-wave broadcasting one address) 16 bytes apart modulo the bank width
+// instead of on the same banks, and keeps consecutive staging slots on
+// consecutive banks across a group boundary.
+constexpr int kBCPad = 4;
+__host__ __device__ constexpr int bc_group_floats(int NPL) { return kSteps * NPL + kBCPad; }
+// A B or C tile of NQ state groups.
+__host__ __device__ constexpr int bc_tile_floats(int NQ, int NPL) {
+  return NQ * bc_group_floats(NPL);
+}
+
 // Staging of 16 rows of a (batch, T, N) tensor (B or C) into an LDS tile of
-// NP >= N (padded) states laid out per state group, [NP/NPL][16][NPL]: group
-// q reads NPL states of 4 steps as NPL float4s at q*16*NPL + 4*m*NPL.
-// Thread tid moves tile elements tid, tid+nthreads, ... (PERS of them);
-// padded states and steps past T are zero.
+// NP >= N (padded) states laid out per state group (see bc_group_floats):
+// group q reads NPL states of 4 steps as NPL float4s at
+// q*bc_group_floats(NPL) + 4*m*NPL. Thread tid moves tile elements tid,
+// tid+nthreads, ... (PERS of them), state fastest, so that a wave's loads
+// read whole rows; with the groups' padding the states of one step then fall
+// on distinct banks (SQ_LDS_BANK_CONFLICT reads 0 for the forward at
+// 16x512x1536x16; unpadded, the 16 states of a step shared two banks).
+// Padded states and steps past T are zero.
 template <int PERS, int NPL, int ES = 4>
 struct RowLoader {
   unsigned src[PERS];  // byte offset in the sub-chunk's global [16][ld] block, or kOOB
@@ -594,7 +611,7 @@ struct RowLoader {
       const int k = e / NP, n = e % NP;
       const bool in_tile = e < kSteps * NP;
       src[i] = (in_tile && n < N) ? (unsigned)ES * (unsigned)(k * ld + n) : kOOB;
-      dst[i] = in_tile ? (n / NPL) * (kSteps * NPL) + k * NPL + (n % NPL) : -1;
+      dst[i] = in_tile ? (n / NPL) * bc_group_floats(NPL) + k * NPL + (n % NPL) : -1;
     }
   }
   __device__ __forceinline__ void load(float (&v)[PERS], const GBuf& g) const {

@@ -80,7 +80,7 @@ constexpr int kCH = 32;   // channels per block
 // One pipeline buffer (the kernel keeps two).
 __host__ __device__ constexpr int fwd_buf_floats(int G, int NPL) {
   return 2 * kCH * kSteps               // dt, dt*x tiles (channel-major)
-         + 2 * kSteps * 2 * G * NPL     // B, C tiles
+         + 2 * bc_tile_floats(2 * G, NPL)   // B, C tiles
          + G * kCH * kSteps;            // per-wave y partials (both half-waves added)
 }
 __host__ __device__ constexpr int fwd_lds_floats(int G, int NPL) {
@@ -109,6 +109,7 @@ fwd_kernel(FwdArgs a) {
   constexpr int NT = 64 * G;                    // threads
   constexpr int NP = 2 * G * NPL;               // padded states
   constexpr int BUF = fwd_buf_floats(G, NPL);
+  constexpr int TILE = bc_tile_floats(2 * G, NPL);   // one B or C tile
   constexpr int PER = (kCH * kQuads + NT - 1) / NT;
   constexpr int PERS = (kSteps * NP + NT - 1) / NT;
   extern __shared__ float lds[];
@@ -175,7 +176,7 @@ fwd_kernel(FwdArgs a) {
     ql.store_cm(buf, pd);
     ql.store_cm_product(buf + kCH * kSteps, pd, px);
     rl.store(buf + 2 * kCH * kSteps, pb);
-    if constexpr (!NOY) rl.store(buf + 2 * kCH * kSteps + kSteps * NP, pc);
+    if constexpr (!NOY) rl.store(buf + 2 * kCH * kSteps + TILE, pc);
   };
   // y of sub-chunk i: every wave leaves, per channel and step, the sum over
   // its two half-waves (added in registers), in a step-pair-major tile
@@ -189,7 +190,7 @@ fwd_kernel(FwdArgs a) {
   constexpr int YT = (YTASKS + NT - 1) / NT;             // y tasks per thread
   float2 ypart[YT][G];
   auto y_read = [&](int i) {
-    const float* yp = lds + (i & 1) * BUF + 2 * kCH * kSteps + 2 * kSteps * NP;
+    const float* yp = lds + (i & 1) * BUF + 2 * kCH * kSteps + 2 * TILE;
 #pragma unroll
     for (int f = 0; f < YT; ++f) {
       const int t0 = tid + f * NT;
@@ -263,9 +264,9 @@ fwd_kernel(FwdArgs a) {
     const float* buf = lds + (i & 1) * BUF;
     const float* cDT = buf;
     const float* cBX = buf + kCH * kSteps;
-    const float* gB = buf + 2 * kCH * kSteps + q * kSteps * NPL;
-    const float* gC = buf + 2 * kCH * kSteps + kSteps * NP + q * kSteps * NPL;
-    float* myY = lds + (i & 1) * BUF + 2 * kCH * kSteps + 2 * kSteps * NP + wave * kCH * kSteps;
+    const float* gB = buf + 2 * kCH * kSteps + q * bc_group_floats(NPL);
+    const float* gC = buf + 2 * kCH * kSteps + TILE + q * bc_group_floats(NPL);
+    float* myY = lds + (i & 1) * BUF + 2 * kCH * kSteps + 2 * TILE + wave * kCH * kSteps;
 
     // A quad's LDS operands, read one quad ahead of their use.
     float4 qdt, qbx, qB[NPL], qC[NPL];
