@@ -476,12 +476,14 @@ template <int CH, int PER, int ES = 4>
 struct QuadLoader {
   static constexpr int TASKS = CH * kQuads;
   int tid, nthreads;
+  int w0;               // the wave's first thread index (wave-uniform)
   unsigned rs;          // row (time step) stride in bytes
   unsigned toff[PER];   // byte offset of step 4m of channel c from the sub-chunk base, or kOOB
   // D: channels; ld: elements between consecutive time steps (>= D; D for a
   // contiguous (batch, T, D) tensor, more for a column slice of a wider one).
   __device__ __forceinline__ QuadLoader(int tid_, int nthreads_, int D, int d0, int ld)
-      : tid(tid_), nthreads(nthreads_), rs((unsigned)ES * (unsigned)ld) {
+      : tid(tid_), nthreads(nthreads_), w0(__builtin_amdgcn_readfirstlane(tid_) & ~63),
+        rs((unsigned)ES * (unsigned)ld) {
 #pragma unroll
     for (int i = 0; i < PER; ++i) {
       const int e = tid + i * nthreads;
@@ -491,7 +493,18 @@ struct QuadLoader {
                     : kOOB;
     }
   }
-  __device__ __forceinline__ bool valid(int i) const { return tid + i * nthreads < TASKS; }
+  // Whether task i of this thread exists. With whole waves of tasks (TASKS a
+  // multiple of 64, as nthreads is) it is the same for every lane of a wave,
+  // and the test reads the wave's first thread index from an SGPR: a scalar
+  // branch around the LDS store instead of an exec-mask save and restore.
+  __device__ __forceinline__ bool valid(int i) const {
+    if ((i + 1) * nthreads <= TASKS) return true;
+    if constexpr (TASKS % 64 == 0) {
+      return w0 + i * nthreads < TASKS;
+    } else {
+      return tid + i * nthreads < TASKS;
+    }
+  }
   __device__ __forceinline__ int chan(int i) const { return (tid + i * nthreads) % CH; }
   __device__ __forceinline__ int quad(int i) const { return (tid + i * nthreads) / CH; }
   // g covers (b, t0.., d0..) up to the end of the batch row (steps past T
@@ -603,8 +616,12 @@ template <int PERS, int NPL, int ES = 4>
 struct RowLoader {
   unsigned src[PERS];  // byte offset in the sub-chunk's global [16][ld] block, or kOOB
   int dst[PERS];       // slot in the tile, or -1
+  int tid, nthreads, ntile;
+  int w0;              // the wave's first thread index (wave-uniform)
   // ld: elements between consecutive time steps (>= N).
-  __device__ __forceinline__ RowLoader(int tid, int nthreads, int N, int NP, int ld) {
+  __device__ __forceinline__ RowLoader(int tid_, int nthreads_, int N, int NP, int ld)
+      : tid(tid_), nthreads(nthreads_), ntile(kSteps * NP),
+        w0(__builtin_amdgcn_readfirstlane(tid_) & ~63) {
 #pragma unroll
     for (int i = 0; i < PERS; ++i) {
       const int e = tid + i * nthreads;       // tile element (k, n), n fastest
@@ -621,9 +638,17 @@ struct RowLoader {
   __device__ __forceinline__ void store(float* tile, const float (&v)[PERS]) const {
 #pragma unroll
     for (int i = 0; i < PERS; ++i) {
-      if (dst[i] >= 0) tile[dst[i]] = v[i];
+      if (valid(i)) tile[dst[i]] = v[i];
       asm volatile("" ::"v"(v[i]));   // as consume(): the wait happens here on every path
     }
+  }
+  // Whether element i of this thread lies in the tile (dst[i] >= 0): true
+  // at compile time when the threads cover the tile exactly, else a scalar
+  // test of the wave's first thread index when the tile is whole waves.
+  __device__ __forceinline__ bool valid(int i) const {
+    if ((i + 1) * nthreads <= ntile) return true;
+    if (ntile % 64 == 0) return w0 + i * nthreads < ntile;
+    return dst[i] >= 0;
   }
 };
 

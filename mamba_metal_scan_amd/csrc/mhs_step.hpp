@@ -3,7 +3,10 @@
 //   h[b,d,:] <- h[b,d,:] * exp(-dt[b,d] * Aneg[d,:]) + dt[b,d] * x[b,d] * B[b,:]
 //   y[b,d]    = sum_n C[b,n] * h[b,d,n]
 // Memory-bound (h is read and written once): the lanes of a wave read and
-// write contiguous h, VPL float4s per lane.
+// write contiguous h, VPL float4s per lane. h is read and written with the
+// default cache policy: a decode loop touches the same state every step, and
+// with non-temporal hints a step took 4.90 instead of 4.69 us (32 x 4096 x 16,
+// 256 steps replayed from a HIP graph, MI355X).
 #pragma once
 
 #include "mhs_common.hpp"
@@ -12,8 +15,7 @@ namespace mhs {
 
 // N == 4 * VPL * LPC: LPC lanes share a channel, lane q holding the VPL
 // float4s n in [4*VPL*q, 4*VPL*(q+1)). One thread per (b, d, q); y is summed
-// over the LPC lanes with DPP (fixed order). h is read and written once, with
-// non-temporal hints (it is not reused within the step).
+// over the LPC lanes with DPP (fixed order).
 template <int VPL, int LPC>
 __global__ void __launch_bounds__(256)
 step_kernel_vec(float* __restrict__ h, const float* __restrict__ x,
@@ -39,7 +41,7 @@ step_kernel_vec(float* __restrict__ h, const float* __restrict__ x,
     const float4* cp = reinterpret_cast<const float4*>(Cm + (size_t)b * N) + q * VPL;
     v4f hv[VPL];
 #pragma unroll
-    for (int v = 0; v < VPL; ++v) hv[v] = __builtin_nontemporal_load(hp + v);
+    for (int v = 0; v < VPL; ++v) hv[v] = hp[v];
 #pragma unroll
     for (int v = 0; v < VPL; ++v) {
       const float4 av = ap[v], bv = bp[v], cv = cp[v];
@@ -48,7 +50,7 @@ step_kernel_vec(float* __restrict__ h, const float* __restrict__ x,
       o.y = __builtin_fmaf(exp2_hw(a2 * av.y), hv[v].y, bv.y * bx);
       o.z = __builtin_fmaf(exp2_hw(a2 * av.z), hv[v].z, bv.z * bx);
       o.w = __builtin_fmaf(exp2_hw(a2 * av.w), hv[v].w, bv.w * bx);
-      __builtin_nontemporal_store(o, hp + v);
+      hp[v] = o;
       part = __builtin_fmaf(cv.x, o.x, part);
       part = __builtin_fmaf(cv.y, o.y, part);
       part = __builtin_fmaf(cv.z, o.z, part);
