@@ -307,6 +307,8 @@ def _short_kernel(name: str) -> str:
     return name[:40]
 
 
+PROFILE_RUN_NOTE = ("All commands run from /tmp with `TMPDIR=/tmp`, `bench.py` standing for the "
+                    "path of the repository's bench.py; OUT is the output folder.")
 ISSUE_COUNTERS = ("GRBM_GUI_ACTIVE SQ_WAVES SQ_ACTIVE_INST_VALU SQ_ACTIVE_INST_VALU2 SQ_INSTS_VALU "
                   "SQ_INSTS_VALU_TRANS_F32 SQ_WAVE_CYCLES SQ_LDS_BANK_CONFLICT")
 N_XCD, N_CU = 8, 256   # MI355X: GRBM_GUI_ACTIVE is summed over its 8 XCDs
@@ -410,6 +412,21 @@ def _read_pmc(root: str) -> dict:
     return {k: sum(v) / len(v) for k, v in vals.items()}
 
 
+def traced_step_us(out_dir: str):
+    """us per autograd step that bench.py printed under the kernel tracer
+    (OUT/kt.log, the traced command's output), or None."""
+    log = os.path.join(out_dir, "kt.log")
+    if not os.path.exists(log):
+        return None
+    for line in open(log):
+        if line.startswith("{"):
+            try:
+                return 1e3 * float(json.loads(line)["ms_per_step"])
+            except (ValueError, KeyError):
+                return None
+    return None
+
+
 def pmc_summary(args) -> None:
     """Per-launch HBM traffic from two rocprofv3 --pmc passes (FETCH_SIZE, then
     WRITE_SIZE, KiB per dispatch), each scaled by what the counter reads for
@@ -493,7 +510,7 @@ def pmc_summary(args) -> None:
         "commands": {
             "kernel_trace": "rocprofv3 --kernel-trace --stats -d OUT/kt -o run --output-format csv "
                             f"-- python3 bench.py --steps {args.steps} --warmup {args.warmup} "
-                            f"--no-cpu-baseline --no-train --no-extra {extra}".strip(),
+                            f"--no-cpu-baseline --no-train --no-extra {extra}".strip() + " > OUT/kt.log",
             "fetch": f"rocprofv3 --pmc FETCH_SIZE -d OUT/fetch -o run --output-format csv -- "
                      f"python3 bench.py --launches 5 {extra}".strip(),
             "write": f"rocprofv3 --pmc WRITE_SIZE -d OUT/write -o run --output-format csv -- "
@@ -506,7 +523,7 @@ def pmc_summary(args) -> None:
     path.write_text(json.dumps(out, indent=1) + "\n")
     lines = [f"# Scan kernels at {tag}, chunk {args.chunk} (fp32, {out['reduction']}-order "
              "reduction): kernel time, HBM traffic, VALU issue", "",
-             "All commands run from /tmp with `TMPDIR=/tmp`; OUT is the output folder.", "",
+             PROFILE_RUN_NOTE, "",
              "    " + out["commands"]["kernel_trace"], "    " + out["commands"]["fetch"],
              "    " + out["commands"]["write"], "    " + out["commands"]["valu"],
              "    " + out["commands"]["summary"], ""]
@@ -525,16 +542,24 @@ def pmc_summary(args) -> None:
                   "steps, which begin at the idle clock; the last column averages the "
                   "timed steps' launches only.", ""]
         if spans:
+            kernel_us = spans["fwd_us"] + spans["bwd_launch_us"]
+            host_us = traced_step_us(args.pmc_summary)
+            if host_us is not None and host_us > kernel_us + 10:
+                why = (f"the traced run's host loop took {host_us:.1f} us per autograd step "
+                       f"against {kernel_us:.1f} us of kernel time, so the GPU waited for the "
+                       "host's launches (the tracer's interception slows the host; untraced, "
+                       "bench.py's step takes about the kernel time)")
+            else:
+                why = ("bench.py times one step in four with events, and each marker holds "
+                       "the queue for a few us; bench.py's event-timed launches include one "
+                       "such marker each, and so read a few us above these spans")
             lines += [f"Over the {spans['steps']} timed steps the backward launch spans "
                       f"{spans['bwd_launch_us']:.1f} us from `bwd_kernel`'s start to "
                       f"`bwd_reduce_kernel`'s end, the forward {spans['fwd_us']:.1f} us; the "
                       f"GPU idles {spans['gap_before_bwd_us']:.1f} us before a backward and "
                       f"{spans['gap_before_fwd_us']:.1f} us before a forward on average "
                       f"(a gap over 1 us before the backward at {spans['steps_with_gaps']} of "
-                      f"{spans['steps']} steps: bench.py times one step in four with events, "
-                      "and each marker holds the queue for a few us). bench.py's event-timed "
-                      "launches include one such marker each, and so read a few us above "
-                      "these spans.", ""]
+                      f"{spans['steps']} steps): {why}.", ""]
     lines += ["## HBM traffic per launch", "",
               f"Calibration: a {COPY_BYTES} B device copy reads FETCH_SIZE x{fetch_factor:.3f} and "
               f"WRITE_SIZE x{write_factor:.3f} of its true bytes; the figures below are scaled by "
@@ -584,7 +609,7 @@ def trace_summary(args) -> None:
         groups[label] = groups.get(label, 0.0) + per(r)
     total = sum(groups.values())
     lines = ["# 80M TinyMamba train step (batch 16 x seq 512, fp32): kernel time per step", "",
-             "All commands run from /tmp with `TMPDIR=/tmp`; OUT is the output folder.", "",
+             PROFILE_RUN_NOTE, "",
              "    rocprofv3 --kernel-trace --stats -d OUT/kt -o run --output-format csv -- \\",
              f"        python3 bench.py --workload train --steps {args.steps} --warmup {args.warmup}",
              f"    python3 bench.py --trace-summary OUT --steps {args.steps} --warmup {args.warmup}",
@@ -616,7 +641,7 @@ def workload_trace_summary(args, rows) -> None:
         run = "python3 bench.py --workload infer"
         md = ROOT / "profiles" / "infer_32x2048x4096x16.md"
     lines = [f"# {title}: kernel time", "",
-             "All commands run from /tmp with `TMPDIR=/tmp`; OUT is the output folder.", "",
+             PROFILE_RUN_NOTE, "",
              "    rocprofv3 --kernel-trace --stats -d OUT/kt -o run --output-format csv -- \\",
              f"        {run}",
              f"    python3 bench.py --trace-summary OUT --workload {args.workload}"
