@@ -375,6 +375,34 @@ int mhs_out_gate_bwd_f32(const float* y, const float* d_skip, const float* z,
                          void* workspace, size_t workspace_bytes,
                          int64_t batch, int64_t seqlen, int64_t d_inner, void* stream);
 
+/*
+ * Cross-entropy of the model head, forward: for each row r of logits
+ * (rows, vocab) fp32 (row-major, contiguous) and int64 targets (rows),
+ *     lse[r] = log sum_j exp(logits[r, j]);
+ *     loss_rows[r] = lse[r] - logits[r, targets[r]], or 0 where
+ *     targets[r] == ignore_index (NaN for any other target outside [0, vocab)).
+ * The mean loss is sum(loss_rows) / (rows whose target is not ignore_index).
+ * Replaces F.cross_entropy's log_softmax + nll_loss over the tied head's
+ * logits (mamba_metal/model.py:296-297), which write and keep the (rows, vocab)
+ * log-probabilities; this reads the logits once and keeps lse (4 bytes per
+ * row). Each row's sum runs in a fixed order (bit-for-bit reproducible).
+ */
+int mhs_xent_fwd_f32(const float* logits, const int64_t* targets, float* lse,
+                     float* loss_rows, int64_t rows, int64_t vocab, int64_t ignore_index,
+                     void* stream);
+
+/*
+ * Its backward: dlogits[r, j] = scale[0] * (exp(logits[r, j] - lse[r]) - [j == targets[r]])
+ * for rows whose target is not ignore_index, 0 for the others. scale is one
+ * device float: the loss's upstream gradient over the count of rows not
+ * ignored (the mean's factor). dlogits (rows, vocab) is fully written and may
+ * not alias logits. Replaces the log_softmax / nll_loss backward
+ * (the autograd of mamba_metal/model.py:296-297).
+ */
+int mhs_xent_bwd_f32(const float* logits, const int64_t* targets, const float* lse,
+                     const float* scale, float* dlogits, int64_t rows, int64_t vocab,
+                     int64_t ignore_index, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -34,7 +34,7 @@ EXPORTED_SYMBOLS = (
     "mhs_scan_bwd_bf16", "mhs_scan_gated_fwd_bf16", "mhs_scan_gated_bwd_bf16",
     "mhs_set_cu_count", "mhs_cu_count", "mhs_scan_fwd_noalloc_f32", "mhs_set_reduction",
     "mhs_deterministic",
-    "mhs_scan_bwd_reduction",
+    "mhs_scan_bwd_reduction", "mhs_xent_fwd_f32", "mhs_xent_bwd_f32",
 )
 
 # Size of the static device scratch of mhs_scan_fwd_noalloc_f32 (the header's
@@ -129,6 +129,10 @@ def library() -> ctypes.CDLL:
             lib.mhs_scan_gated_fwd_bf16.argtypes = lib.mhs_scan_gated_fwd_f32.argtypes
             lib.mhs_scan_gated_bwd_bf16.restype = ctypes.c_int
             lib.mhs_scan_gated_bwd_bf16.argtypes = lib.mhs_scan_gated_bwd_f32.argtypes
+            lib.mhs_xent_fwd_f32.restype = ctypes.c_int
+            lib.mhs_xent_fwd_f32.argtypes = [_P] * 4 + [_I64] * 3 + [_P]
+            lib.mhs_xent_bwd_f32.restype = ctypes.c_int
+            lib.mhs_xent_bwd_f32.argtypes = [_P] * 5 + [_I64] * 3 + [_P]
             _lib = lib
     return _lib
 
@@ -848,3 +852,66 @@ out_gate_bwd_into = _register(
 @out_gate_bwd_into.register_fake
 def _out_gate_bwd_into_fake(y, d_skip, z, dout, dz):
     return y.new_empty(y.shape), torch.empty_like(d_skip)
+
+
+# ----------------------------------------------------------- cross-entropy
+
+def _check_xent(what: str, logits, targets, lse=None, scale=None) -> None:
+    """logits (R, V) fp32 contiguous, targets (R) int64 contiguous, lse (R)
+    and scale (1) fp32, all on one ROCm device."""
+    _on_one_device(what, logits, targets, lse, scale)
+    _need(logits.dim() == 2 and targets.shape == (logits.shape[0],), what,
+          f"logits must be (R, V) and targets (R,); got {tuple(logits.shape)}, "
+          f"{tuple(targets.shape)}")
+    _need(logits.shape[1] >= 1, what, "the vocabulary must not be empty")
+    _need(targets.dtype == torch.int64, what, f"targets must be int64; got {targets.dtype}")
+    _fp32(what, logits=logits, lse=lse, scale=scale)
+    _shaped(what, "lse", lse, (logits.shape[0],))
+    _shaped(what, "scale", scale, (1,))
+    _dense(what, logits=logits, targets=targets, lse=lse)
+
+
+def _xent_fwd_impl(logits: torch.Tensor, targets: torch.Tensor, ignore_index: int
+                   ) -> tuple[torch.Tensor, torch.Tensor]:
+    """(lse (R), loss_rows (R)) for logits (R, V) and targets (R)."""
+    rows, vocab = logits.shape
+    lse = logits.new_empty((rows,))
+    loss_rows = logits.new_empty((rows,))
+    with _on(logits.device):
+        rc = library().mhs_xent_fwd_f32(_ptr(logits), _ptr(targets), _ptr(lse), _ptr(loss_rows),
+                                        rows, vocab, ignore_index, _stream(logits.device))
+    _check(rc, "mhs_xent_fwd_f32")
+    return lse, loss_rows
+
+
+xent_fwd = _register("xent_fwd", _xent_fwd_impl, (),
+                     lambda logits, targets, ignore_index: _check_xent("xent_fwd", logits, targets))
+
+
+@xent_fwd.register_fake
+def _xent_fwd_fake(logits, targets, ignore_index):
+    return logits.new_empty((logits.shape[0],)), logits.new_empty((logits.shape[0],))
+
+
+def _xent_bwd_impl(logits: torch.Tensor, targets: torch.Tensor, lse: torch.Tensor,
+                   scale: torch.Tensor, ignore_index: int) -> torch.Tensor:
+    """dlogits (R, V), scale (1) = the loss's upstream gradient / rows not ignored."""
+    rows, vocab = logits.shape
+    dlogits = torch.empty_like(logits)
+    with _on(logits.device):
+        rc = library().mhs_xent_bwd_f32(_ptr(logits), _ptr(targets), _ptr(lse), _ptr(scale),
+                                        _ptr(dlogits), rows, vocab, ignore_index,
+                                        _stream(logits.device))
+    _check(rc, "mhs_xent_bwd_f32")
+    return dlogits
+
+
+xent_bwd = _register(
+    "xent_bwd", _xent_bwd_impl, (),
+    lambda logits, targets, lse, scale, ignore_index:
+    _check_xent("xent_bwd", logits, targets, lse, scale))
+
+
+@xent_bwd.register_fake
+def _xent_bwd_fake(logits, targets, lse, scale, ignore_index):
+    return torch.empty_like(logits)

@@ -21,6 +21,7 @@
 #include "mhs_gate.hpp"
 #include "mhs_instances.hpp"
 #include "mhs_step.hpp"
+#include "mhs_xent.hpp"
 
 // The scan kernels are instantiated in the mhs_kern_*.hip units.
 namespace mhs {
@@ -34,7 +35,7 @@ MHS_FOR_PLANS(MHS_BWD_ATOM_INST, extern, 2)
 
 namespace {
 
-constexpr int kVersion = (0 << 16) | (3 << 8) | 0;   // 0.3: atomic reduction, no-alloc forward
+constexpr int kVersion = (0 << 16) | (4 << 8) | 0;   // 0.4: fused cross-entropy
 
 thread_local char g_err[512] = "";
 
@@ -1137,6 +1138,67 @@ int mhs_out_gate_bwd_f32(const float* y, const float* d_skip, const float* z, in
   hipLaunchKernelGGL(mhs::conv_reduce_kernel, dim3((unsigned)((D + 3) / 4)), dim3(256), 0, s, wsp,
                      nullptr, dd_skip, (int)(grid.y * grid.z), 0, D);
   return check_launch("output gate reduction kernel");
+}
+
+}  // extern "C"
+
+// ------------------------------------------------------------- cross-entropy
+
+namespace {
+
+int check_xent(const float* logits, const int64_t* targets, int64_t rows, int64_t vocab) {
+  if (rows < 0 || vocab < 1)
+    return fail(MHS_EINVAL, "rows must be >= 0 and vocab >= 1; got %lld, %lld", (long long)rows,
+                (long long)vocab);
+  if (rows > 0x7FFFFFFF) return fail(MHS_EINVAL, "rows %lld exceeds 2^31 - 1", (long long)rows);
+  if (rows > 0 && (!logits || !targets)) return fail(MHS_EINVAL, "null pointer argument");
+  return MHS_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+int mhs_xent_fwd_f32(const float* logits, const int64_t* targets, float* lse, float* loss_rows,
+                     int64_t rows, int64_t vocab, int64_t ignore_index, void* stream) {
+  g_err[0] = '\0';
+  int rc = check_xent(logits, targets, rows, vocab);
+  if (rc) return rc;
+  if (rows == 0) return MHS_OK;
+  if (!lse || !loss_rows) return fail(MHS_EINVAL, "null pointer argument");
+  const auto* t = reinterpret_cast<const long long*>(targets);
+  const bool vec = vocab % 4 == 0 && aligned16(logits);
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  if (vec)
+    hipLaunchKernelGGL(mhs::xent_fwd_kernel<4>, dim3((unsigned)rows), dim3(mhs::kXentThreads), 0,
+                       s, logits, t, lse, loss_rows, (long long)vocab, (long long)ignore_index);
+  else
+    hipLaunchKernelGGL(mhs::xent_fwd_kernel<1>, dim3((unsigned)rows), dim3(mhs::kXentThreads), 0,
+                       s, logits, t, lse, loss_rows, (long long)vocab, (long long)ignore_index);
+  return check_launch("cross-entropy forward kernel");
+}
+
+int mhs_xent_bwd_f32(const float* logits, const int64_t* targets, const float* lse,
+                     const float* scale, float* dlogits, int64_t rows, int64_t vocab,
+                     int64_t ignore_index, void* stream) {
+  g_err[0] = '\0';
+  int rc = check_xent(logits, targets, rows, vocab);
+  if (rc) return rc;
+  if (rows == 0) return MHS_OK;
+  if (!lse || !scale || !dlogits) return fail(MHS_EINVAL, "null pointer argument");
+  if (dlogits == logits) return fail(MHS_EINVAL, "dlogits may not alias logits");
+  const auto* t = reinterpret_cast<const long long*>(targets);
+  const bool vec = vocab % 4 == 0 && aligned16(logits) && aligned16(dlogits);
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  if (vec)
+    hipLaunchKernelGGL(mhs::xent_bwd_kernel<4>, dim3((unsigned)rows), dim3(mhs::kXentThreads), 0,
+                       s, logits, t, lse, scale, dlogits, (long long)vocab,
+                       (long long)ignore_index);
+  else
+    hipLaunchKernelGGL(mhs::xent_bwd_kernel<1>, dim3((unsigned)rows), dim3(mhs::kXentThreads), 0,
+                       s, logits, t, lse, scale, dlogits, (long long)vocab,
+                       (long long)ignore_index);
+  return check_launch("cross-entropy backward kernel");
 }
 
 }  // extern "C"

@@ -40,6 +40,7 @@ import torch.nn.functional as F
 from .conv import conv1d_silu
 from .fused import mamba_inner, out_gate, selective_scan_gated
 from .scan import SSM_CHUNK, _hip_device, selective_scan, selective_state_step
+from .xent import cross_entropy
 
 
 @dataclass
@@ -332,8 +333,14 @@ class TinyMamba(nn.Module):
         logits = self.head(self.ln_f(x))
         loss = None
         if targets is not None:
-            loss = F.cross_entropy(logits.reshape(-1, logits.size(-1)), targets.reshape(-1),
-                                   ignore_index=-100)
+            flat, tflat = logits.reshape(-1, logits.size(-1)), targets.reshape(-1)
+            if (self.cfg.scan_impl != "torch" and _hip_device(flat)
+                    and flat.dtype == torch.float32):
+                # The fused HIP cross-entropy: the same mean loss and gradient
+                # without the (rows, vocab) log-probabilities in memory.
+                loss = cross_entropy(flat, tflat, ignore_index=-100)
+            else:
+                loss = F.cross_entropy(flat, tflat, ignore_index=-100)
         return logits, loss
 
     def count_params(self) -> int:

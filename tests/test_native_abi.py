@@ -326,3 +326,18 @@ def test_segment_split_follows_the_compute_unit_count():
     finally:
         _native.set_cu_count(0)
     assert lib.mhs_cu_count() == 256
+
+
+def test_xent_argument_errors():
+    lib = _native.library()
+    assert lib.mhs_xent_fwd_f32(A16, A16, A16, A16, 0, 16, -100, None) == MHS_OK   # no rows
+    rc = lib.mhs_xent_fwd_f32(A16, A16, A16, A16, 4, 0, -100, None)
+    assert rc == MHS_EINVAL and "vocab" in _err(lib)
+    rc = lib.mhs_xent_fwd_f32(A16, None, A16, A16, 4, 16, -100, None)
+    assert rc == MHS_EINVAL and "null" in _err(lib)
+    rc = lib.mhs_xent_fwd_f32(A16, A16, A16, A16, 1 << 31, 16, -100, None)
+    assert rc == MHS_EINVAL and "rows" in _err(lib)
+    rc = lib.mhs_xent_bwd_f32(A16, A16, A16, None, A16, 4, 16, -100, None)
+    assert rc == MHS_EINVAL and "null" in _err(lib)
+    rc = lib.mhs_xent_bwd_f32(A16, A16, A16, A16, A16, 4, 16, -100, None)
+    assert rc == MHS_EINVAL and "alias" in _err(lib)
