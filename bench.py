@@ -582,7 +582,7 @@ TRAIN_GROUPS = (  # (label, substrings of the kernel name), first match wins
     ("HIP scan (fwd, bwd, reduce)", ("mhs::fwd_kernel", "mhs::bwd_kernel", "mhs::bwd_reduce")),
     ("HIP conv1d + SiLU", ("mhs::conv",)),
     ("HIP output gate", ("mhs::out_gate",)),
-    ("softmax / cross-entropy", ("SoftMax", "nll_loss")),
+    ("cross-entropy (HIP, or the framework's softmax)", ("mhs::xent", "SoftMax", "nll_loss")),
     ("AdamW (fused)", ("FusedOpti",)),
     ("RMSNorm", ("layer_norm", "rms_norm", "RmsNorm")),
 )
