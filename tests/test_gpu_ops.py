@@ -90,6 +90,17 @@ def test_opcheck_conv_and_gate_ops():
     torch.library.opcheck(OPS.out_gate_bwd_into, (y, d_skip, z, dout, dxz[..., d:]))
 
 
+def test_opcheck_cross_entropy_ops():
+    print("[case] opcheck cross-entropy ops", flush=True)
+    g = _gen(4)
+    logits = torch.randn(6, 1000, generator=g).to(DEV)
+    targets = torch.tensor([3, -100, 999, 0, 512, 7]).to(DEV)
+    torch.library.opcheck(OPS.xent_fwd, (logits, targets, -100))
+    lse, _ = OPS.xent_fwd(logits, targets, -100)
+    scale = torch.full((1,), 0.2, device=DEV)
+    torch.library.opcheck(OPS.xent_bwd, (logits, targets, lse, scale, -100))
+
+
 def test_compiled_scan_matches_eager():
     """torch.compile (aot_eager) of a function around the scan: the traced
     graph calls the registered ops; values and all gradients match eager."""
