@@ -97,6 +97,10 @@ struct BwdArgs {
   float* carryL;
   float* carrySdt;
   int cunits = 1, nunits = 0;
+  // In-kernel sweep kernels only (SWEEP > 0): ckpt holds the caller's
+  // checkpoints at stride km x 16 steps (ck_nchunk of them per batch row),
+  // K is 16 and nchunk counts 16-step chunks.
+  int km = 1, ck_nchunk = 0;
   // Row strides (elements between consecutive time steps) of dt, of B and C,
   // and of ddt: D, N and D for contiguous tensors, more for column slices of
   // a wider projection output (and its gradient). x, dy, dx are contiguous.
@@ -112,6 +116,11 @@ struct BwdArgs {
   int ld_dbc = 0;
 };
 
+// Largest number of 16-step chunks per caller checkpoint that the backward
+// sweeps inside the kernel (checkpoint strides 32, 48 and 64 steps); larger
+// strides recompute stride-16 checkpoints in a separate pass.
+constexpr int kSweepMax = 4;
+
 // One staging buffer (the kernel keeps two) and the single-buffered rest.
 __host__ __device__ constexpr int bwd_buf_floats(int G, int NPL) {
   return 4 * kCH * kSteps               // dt, dy, x, dt*x (channel-major)
@@ -121,6 +130,11 @@ __host__ __device__ constexpr int bwd_lds_floats(int G, int NPL) {
   return 2 * bwd_buf_floats(G, NPL)
          + G * 64 * kSteps                       // (s1, s2) per wave
          + 2 * kSteps * 2 * G * NPL;             // dB, dC block sums of a chunk
+}
+// The swept kernels (SWEEP > 0) keep each lane's swept states in LDS after
+// that: kSweepMax slots of NPL floats per thread, [slot][thread][NPL].
+__host__ __device__ constexpr int bwd_sweep_lds_floats(int G, int NPL) {
+  return bwd_lds_floats(G, NPL) + kSweepMax * 64 * G * NPL;
 }
 
 // GATED: see BwdArgs. The staging threads gate each dt once per block as they
@@ -136,7 +150,8 @@ __host__ __device__ constexpr int bwd_lds_floats(int G, int NPL) {
 // partials, no reduction kernel; the order of the additions, and so the
 // rounding, varies from run to run). For bf16 activations dB and dC go to
 // fp32 buffers that a later pass rounds to bf16.
-template <int NPL, int G, int MINW, bool GATED, bool CARRY, int ES = 4, bool ATOM = false>
+template <int NPL, int G, int MINW, bool GATED, bool CARRY, int ES = 4, bool ATOM = false,
+          int SWEEP = 0>
 __global__ void __launch_bounds__(64 * G, MINW)
 bwd_kernel(BwdArgs a) {
   constexpr int NT = 64 * G;
@@ -238,21 +253,28 @@ bwd_kernel(BwdArgs a) {
   float dbias_acc = 0.f;   // GATED: this thread's sum of the raw dt gradient (channel tid % 32)
 
   // Chunk ci (any integer): its length (0 outside this block's segment, so
-  // that every load and store of a chunk outside it is empty).
+  // that every load and store of a chunk outside it is empty). The swept
+  // kernel also reads dt, x and B from the chunks of the segment's first
+  // caller chunk that lie before the segment (from c_in): their states are
+  // swept, not walked.
   const int last_len = T - (nch - 1) * K;
+  const int c_in = SWEEP > 0 ? c_lo / a.km * a.km : c_lo;
   auto chunk_len = [&](int ci) {
     return (ci < c_lo || ci >= c_hi) ? 0 : ci == nch - 1 ? last_len : K;
   };
+  auto in_len = [&](int ci) {
+    return (ci < c_in || ci >= c_hi) ? 0 : ci == nch - 1 ? last_len : K;
+  };
   // Resources over chunk ci of the operands (channels d0 .. D-1 of the
   // (batch, T, D) ones, all N states of B, C and of the dB / dC rows; see
-  // SubStream): empty outside [c_lo, c_hi).
-  auto stream = [&](const void* base, int ld, int c0, int width) {
-    return SubStream<ES>(base, row0, ld, c0, width, K, c_lo, c_hi, nch - 1, last_len);
+  // SubStream): empty outside [c_lo, c_hi) ([c_in, c_hi) for dt, x, B).
+  auto stream = [&](const void* base, int ld, int c0, int width, int lo) {
+    return SubStream<ES>(base, row0, ld, c0, width, K, lo, c_hi, nch - 1, last_len);
   };
-  const SubStream<ES> sx = stream(a.x, D, d0, D), sdt = stream(a.dt, ld_dt, d0, D),
-                      sdy = stream(a.dy, D, d0, D), sB = stream(a.B, ld_bc, 0, N),
-                      sC = stream(a.C, ld_bc, 0, N), sdx = stream(a.dx, D, d0, D),
-                      sddt = stream(a.ddt, ld_ddt, d0, D);
+  const SubStream<ES> sx = stream(a.x, D, d0, D, c_in), sdt = stream(a.dt, ld_dt, d0, D, c_in),
+                      sdy = stream(a.dy, D, d0, D, c_lo), sB = stream(a.B, ld_bc, 0, N, c_in),
+                      sC = stream(a.C, ld_bc, 0, N, c_lo), sdx = stream(a.dx, D, d0, D, c_lo),
+                      sddt = stream(a.ddt, ld_ddt, d0, D, c_lo);
   // global -> staging registers: chunk ci (the prologue), or the chunk of
   // the loop's load cursors (two below the chunk walked).
   auto load_sub = [&](int ci) {
@@ -290,7 +312,7 @@ bwd_kernel(BwdArgs a) {
   int ck_i = c_hi - 3;
   auto store_sub = [&](int j, int ci) {   // staging registers (chunk ci) -> buffer j
     float* s0 = lds + j * BUF;
-    if constexpr (GATED) qdt.gate(pd, chunk_len(ci), a.dt_lo, a.dt_span, gbias);
+    if constexpr (GATED) qdt.gate(pd, in_len(ci), a.dt_lo, a.dt_span, gbias);
     ql.store_cm(s0, pd);
     ql.store_cm(s0 + oDY, py);
     if constexpr (!CARRY) ql.store_cm(s0 + oX, px);
@@ -375,146 +397,343 @@ bwd_kernel(BwdArgs a) {
   StreamCursor<ES> fdx(sdx, c_hi), fddt(sddt, c_hi);
   StreamCursor<4> fbs(sBsum, c_hi), fcs(sCsum, c_hi);
 
-  // Prologue: the segment's last chunk staged in LDS buffer 0, the one
-  // before it in the staging registers.
   float hc[NPL];                          // h at the start of the current chunk
-  load_sub(c_hi - 1);
-  if constexpr (!CARRY) load_h0(c_hi - 1);
-  store_sub(0, c_hi - 1);
-  if constexpr (!CARRY) {
+  int last_par;                           // LDS buffer of the segment's last chunk
+  if constexpr (SWEEP > 0) {
+    // Checkpoint stride a.km x 16 steps (2 <= a.km <= SWEEP), the caller's
+    // own checkpoints: the walk goes over 16-step chunks as usual, and the
+    // states at the 16-step boundaries inside a caller chunk are rebuilt in
+    // this kernel, by "sweep" items of the same pipeline. For each caller
+    // chunk cc (last to first), holding n walk chunks: sweep its chunks 0 ..
+    // n-2 forward from the caller's checkpoint (each rebuilds its dA and h
+    // as the walk's recompute phase does, and keeps only the end state, in
+    // H[l + 1]), then walk chunks n-1 .. 0 backwards from H[l] (in a time
+    // segment that starts inside a caller chunk, only its own chunks of
+    // that caller chunk are walked: the segments are the stride-16 ones, so
+    // the results equal those at stride 16 bit for bit). The sweeps
+    // stage dt, x and B only (their dy and C loads are empty). An item
+    // that follows a walk has the walk's two barriers (the first after that
+    // walk's finishing step), one that follows a sweep only the last.
+    static_assert(!CARRY, "the in-kernel sweep: gradient pass only");
+    const int KM = a.km;
+    const int cc_lo = c_lo / KM, cc_top = (c_hi - 1) / KM;
+    const int n_top = c_hi - cc_top * KM;
+    const int lo_first = c_lo - cc_lo * KM;   // the segment may start inside a caller chunk
+    // Per caller chunk cc: n walk chunks (n_top for the segment's last
+    // caller chunk), of which those from lo (lo_first in its first, else 0)
+    // belong to this segment: n - 1 sweeps, then n - lo walks.
+    const int nitem = 2 * (c_hi - cc_lo * KM) - (cc_top - cc_lo + 1) - lo_first;
+    // Position in the item sequence: caller chunk cc, item l of its
+    // 2n - 1 - lo. Advanced by one per item (no divisions in the loop).
+    struct Pos {
+      int cc, l, n, lo;
+    };
+    auto advance = [&](Pos p) {
+      if (++p.l == 2 * p.n - 1 - p.lo) {
+        --p.cc;
+        p.l = 0;
+        p.n = KM;
+        p.lo = p.cc == cc_lo ? lo_first : 0;
+      }
+      return p;
+    };
+    struct Item {
+      int ci;      // walk chunk (16 steps); -1: none (empty resources)
+      int loc;     // its index inside the caller chunk
+      bool sweep;  // sweep (forward, end state only) or walk (gradients)
+      bool first;  // the caller chunk's first item
+    };
+    auto item_at = [&](const Pos& p) {
+      Item it{-1, 0, false, false};
+      if (p.cc < cc_lo) return it;   // past the segment's first chunk
+      it.sweep = p.l < p.n - 1;
+      it.loc = it.sweep ? p.l : 2 * (p.n - 1) - p.l;
+      it.ci = p.cc * KM + it.loc;
+      it.first = p.l == 0;
+      return it;
+    };
+    // The caller's checkpoint before caller chunk cc (0 for the first).
+    const float* ckc = a.ckpt + ((size_t)b * a.ck_nchunk - 1) * slice;
+    auto load_h0c = [&](int cc) {
+      load_states<NPL>(ph, GBuf(ckc + (ptrdiff_t)cc * (ptrdiff_t)slice, cc > 0 ? slice_bytes : 0u),
+                       st_lane, nvalid);
+    };
+    auto load_item = [&](const Item& it) {
+      const int cy = it.sweep ? -1 : it.ci;
+      ql.load(px, sx.at(it.ci));
+      qdt.load(pd, sdt.at(it.ci));
+      ql.load(py, sdy.at(cy));
+      rl.load(pb, sB.at(it.ci));
+      rl.load(pc, sC.at(cy));
+    };
+    // H[l], the state at the start of walk chunk l of the caller chunk, in
+    // this thread's LDS slot l (lanes contiguous: conflict-free 32 / 64 /
+    // 128-bit accesses); registers are what the walk is short of.
+    static_assert(SWEEP <= kSweepMax, "LDS slots for the swept states");
+    float* const tH = lds + bwd_lds_floats(G, NPL) + tid * NPL;
+    auto h_slot = [&](int l) { return tH + l * NT * NPL; };
+    Pos pos{cc_top, 0, n_top, cc_top == cc_lo ? lo_first : 0};
+    const Item it0 = item_at(pos);
+    load_h0c(cc_top);
+    load_item(it0);
+    store_sub(0, it0.ci);
+    load_item(item_at(advance(pos)));
+    __syncthreads();
+
+    Item itp{-1, 0, false, false};   // the previous item
+    ProgressPriority prio(nitem);
+    for (int k = 0; k < nitem; ++k) {
+      prio.step(k);
+      const Item it = item_at(pos);
+      const Pos pos1 = advance(pos);
+      const Item it1 = item_at(pos1), it2 = item_at(advance(pos1));
+      const float* s0 = lds + (k & 1) * BUF;
+      const float* gB = s0 + oB + q * bc_group_floats(NPL);
+      const float* gC = s0 + oC + q * bc_group_floats(NPL);
+      if (it.first) {
+        float h0[NPL];
 #pragma unroll
-    for (int j = 0; j < NPL; ++j) hc[j] = opaque_copy(ph[j]);
-  }
-  load_sub(c_hi - 2);
-  if constexpr (!CARRY) load_h0(c_hi - 2);
-  __syncthreads();
+        for (int j = 0; j < NPL; ++j) h0[j] = opaque_copy(ph[j]);
+        store_vec<NPL>(h_slot(0), h0);
+        load_h0c(it.ci / KM - 1);   // the next caller chunk's
+      }
+      load_vec<NPL>(hc, h_slot(it.loc));
+      // The previous item's gradients (if it was a walk) are finished here,
+      // in this item's first phase; only then does the item need a barrier
+      // between its phases (finalize reads the previous buffer and the
+      // (s1, s2) and dB / dC tiles that this item's second phase rewrites).
+      const bool fin = !itp.sweep && itp.ci >= 0;
 
-  const int nit = c_hi - c_lo;
-  ProgressPriority prio(nit);
-  for (int i = 0; i < nit; ++i) {
-    prio.step(i);
-    const int ci = c_hi - 1 - i;
-    const float* s0 = lds + (i & 1) * BUF;
-    const float* gB = s0 + oB + q * bc_group_floats(NPL);
-    const float* gC = s0 + oC + q * bc_group_floats(NPL);
+      // ---- recompute (walk) or sweep: dA and h of the chunk
+      float da[kSteps][NPL], hs[kSteps][NPL];
+#pragma unroll
+      for (int m = 0; m < kQuads; ++m) {
+        float dts[4], dtxs[4], Bq[4][NPL];
+        f4_to(dts, lds4(s0 + cm_quad(c, m)));
+        f4_to(dtxs, lds4(s0 + oDTX + cm_quad(c, m)));
+        load_quad_rows<NPL>(Bq, gB, m);
+#pragma unroll
+        for (int s = 0; s < 4; ++s) {
+#pragma unroll
+          for (int j = 0; j < NPL; ++j) {
+            da[4 * m + s][j] = exp2_hw(dts[s] * a2[j]);
+            hs[4 * m + s][j] = Bq[s][j] * dtxs[s];
+          }
+        }
+        if (m == 0 && fin)
+          finalize((k + 1) & 1, chunk_len(itp.ci), sdx.at(itp.ci), sddt.at(itp.ci),
+                   sBsum.at(itp.ci), sCsum.at(itp.ci));
+      }
+#pragma unroll
+      for (int kk = 0; kk < kSteps; ++kk)
+#pragma unroll
+        for (int j = 0; j < NPL; ++j)
+          hs[kk][j] = __builtin_fmaf(da[kk][j], kk == 0 ? hc[j] : hs[kk - 1][j], hs[kk][j]);
+      if (it.sweep) {
+        store_vec<NPL>(h_slot(it.loc + 1), hs[kSteps - 1]);
+        if (fin) __syncthreads();   // finalize(previous) is done with its buffer
+        store_sub((k + 1) & 1, it1.ci);
+        load_item(it2);
+        __syncthreads();   // the next item staged
+        itp = it;
+        pos = pos1;
+        continue;
+      }
+      if (fin) __syncthreads();   // finalize(previous) is done with tS, tDBC and its buffer
 
-    if constexpr (CARRY) {
-      // The adjoint alone: G_t = dy_t C_t + dA_{t+1} G_{t+1}, dA formed on
-      // the way (no state needed).
+      // ---- reverse phase (the walk's)
 #pragma unroll
       for (int m = kQuads - 1; m >= 0; --m) {
-        float dts[4], dys[4], Cq[4][NPL];
+        float dts[4], dys[4], dtxs[4], Bq[4][NPL], Cq[4][NPL], s1q[4], s2q[4];
         f4_to(dts, lds4(s0 + cm_quad(c, m)));
         f4_to(dys, lds4(s0 + oDY + cm_quad(c, m)));
+        f4_to(dtxs, lds4(s0 + oDTX + cm_quad(c, m)));
+        load_quad_rows<NPL>(Bq, gB, m);
         load_quad_rows<NPL>(Cq, gC, m);
+        float pv[M];
 #pragma unroll
         for (int s = 3; s >= 0; --s) {
-          sdt_acc += dts[s];
+          const int kk = 4 * m + s;
+          const int slot = kk & 1;
+          float s1 = 0.f, s2 = 0.f, gk[NPL];
 #pragma unroll
-          for (int j = 0; j < NPL; ++j)
-            u[j] = exp2_hw(dts[s] * a2[j]) * __builtin_fmaf(dys[s], Cq[s][j], u[j]);
+          for (int j = 0; j < NPL; ++j) {
+            gk[j] = __builtin_fmaf(dys[s], Cq[s][j], u[j]);
+            u[j] = da[kk][j] * gk[j];
+            const float qv = u[j] * (kk == 0 ? hc[j] : hs[kk - 1][j]);
+            s1 = __builtin_fmaf(gk[j], Bq[s][j], s1);
+            s2 = __builtin_fmaf(an[j], qv, s2);
+            acc[j] = __builtin_fmaf(dts[s], qv, acc[j]);
+          }
+          s1q[s] = s1;
+          s2q[s] = s2;
+#pragma unroll
+          for (int j = 0; j < NPL; ++j) {
+            pv[slot * NPL + j] = gk[j] * dtxs[s];
+            pv[2 * NPL + slot * NPL + j] = hs[kk][j] * dys[s];
+          }
+          if (slot == 0) *(dbc_out + kk * NP) = half_wave_reduce_scatter<M>(pv, lane);
         }
-        if (m == 2) store_sub((i + 1) & 1, ci - 1);
-        if (m == 1) load_next();
+        float o[4];
+#pragma unroll
+        for (int s = 0; s < 4; ++s) {
+          const auto sw = __builtin_amdgcn_permlane32_swap(__float_as_uint(s1q[s]),
+                                                          __float_as_uint(s2q[s]), false, false);
+          o[s] = __uint_as_float(sw[0]) + __uint_as_float(sw[1]);
+        }
+        float* const ts = tS + wave * 64 * kSteps;
+        *reinterpret_cast<float2*>(ts + (2 * m * 64 + lane) * 2) = make_float2(o[0], o[1]);
+        *reinterpret_cast<float2*>(ts + ((2 * m + 1) * 64 + lane) * 2) = make_float2(o[2], o[3]);
+        if (m == 2) store_sub((k + 1) & 1, it1.ci);
+        if (m == 1) load_item(it2);
       }
+      __syncthreads();   // tS / tDBC complete; the next item staged
+      itp = it;
+      pos = pos1;
+    }
+    last_par = (nitem - 1) & 1;
+  } else {
+    // Prologue: the segment's last chunk staged in LDS buffer 0, the one
+    // before it in the staging registers.
+    load_sub(c_hi - 1);
+    if constexpr (!CARRY) load_h0(c_hi - 1);
+    store_sub(0, c_hi - 1);
+    if constexpr (!CARRY) {
+#pragma unroll
+      for (int j = 0; j < NPL; ++j) hc[j] = opaque_copy(ph[j]);
+    }
+    load_sub(c_hi - 2);
+    if constexpr (!CARRY) load_h0(c_hi - 2);
+    __syncthreads();
+
+    const int nit = c_hi - c_lo;
+    ProgressPriority prio(nit);
+    for (int i = 0; i < nit; ++i) {
+      prio.step(i);
+      const int ci = c_hi - 1 - i;
+      const float* s0 = lds + (i & 1) * BUF;
+      const float* gB = s0 + oB + q * bc_group_floats(NPL);
+      const float* gC = s0 + oC + q * bc_group_floats(NPL);
+
+      if constexpr (CARRY) {
+        // The adjoint alone: G_t = dy_t C_t + dA_{t+1} G_{t+1}, dA formed on
+        // the way (no state needed).
+#pragma unroll
+        for (int m = kQuads - 1; m >= 0; --m) {
+          float dts[4], dys[4], Cq[4][NPL];
+          f4_to(dts, lds4(s0 + cm_quad(c, m)));
+          f4_to(dys, lds4(s0 + oDY + cm_quad(c, m)));
+          load_quad_rows<NPL>(Cq, gC, m);
+#pragma unroll
+          for (int s = 3; s >= 0; --s) {
+            sdt_acc += dts[s];
+#pragma unroll
+            for (int j = 0; j < NPL; ++j)
+              u[j] = exp2_hw(dts[s] * a2[j]) * __builtin_fmaf(dys[s], Cq[s][j], u[j]);
+          }
+          if (m == 2) store_sub((i + 1) & 1, ci - 1);
+          if (m == 1) load_next();
+        }
+        load_down();
+        __syncthreads();   // chunk ci-1 staged
+        continue;
+      }
+
+      // ---- recompute phase, with the pipeline work of the neighbouring chunks
+      float da[kSteps][NPL], hs[kSteps][NPL];
+#pragma unroll
+      for (int m = 0; m < kQuads; ++m) {
+        float dts[4], dtxs[4], Bq[4][NPL];
+        f4_to(dts, lds4(s0 + cm_quad(c, m)));
+        f4_to(dtxs, lds4(s0 + oDTX + cm_quad(c, m)));
+        load_quad_rows<NPL>(Bq, gB, m);
+#pragma unroll
+        for (int s = 0; s < 4; ++s) {
+#pragma unroll
+          for (int j = 0; j < NPL; ++j) {
+            da[4 * m + s][j] = exp2_hw(dts[s] * a2[j]);
+            hs[4 * m + s][j] = Bq[s][j] * dtxs[s];       // b_k, turned into h_k below
+          }
+        }
+        if (m == 0)   // no-op stores past the sequence end
+          finalize((i + 1) & 1, chunk_len(ci + 1), fdx.get(sdx), fddt.get(sddt), fbs.get(sBsum),
+                   fcs.get(sCsum));
+      }
+#pragma unroll
+      for (int k = 0; k < kSteps; ++k)
+#pragma unroll
+        for (int j = 0; j < NPL; ++j)
+          hs[k][j] = __builtin_fmaf(da[k][j], k == 0 ? hc[j] : hs[k - 1][j], hs[k][j]);
+      __syncthreads();   // finalize(ci+1) is done with tS, tDBC and its buffer
+
+      // ---- reverse phase
+#pragma unroll
+      for (int m = kQuads - 1; m >= 0; --m) {
+        float dts[4], dys[4], dtxs[4], Bq[4][NPL], Cq[4][NPL], s1q[4], s2q[4];
+        f4_to(dts, lds4(s0 + cm_quad(c, m)));
+        f4_to(dys, lds4(s0 + oDY + cm_quad(c, m)));
+        f4_to(dtxs, lds4(s0 + oDTX + cm_quad(c, m)));
+        load_quad_rows<NPL>(Bq, gB, m);
+        load_quad_rows<NPL>(Cq, gC, m);
+        float pv[M];   // dB/dC products of the step pair (k, k+1), k even, numbered as for rs_index
+#pragma unroll
+        for (int s = 3; s >= 0; --s) {
+          const int k = 4 * m + s;
+          const int slot = k & 1;
+          float s1 = 0.f, s2 = 0.f, gk[NPL];
+#pragma unroll
+          for (int j = 0; j < NPL; ++j) {
+            gk[j] = __builtin_fmaf(dys[s], Cq[s][j], u[j]);            // G_k
+            u[j] = da[k][j] * gk[j];                                   // dA_k G_k
+            const float qv = u[j] * (k == 0 ? hc[j] : hs[k - 1][j]);   // G_k * hm_k
+            s1 = __builtin_fmaf(gk[j], Bq[s][j], s1);
+            s2 = __builtin_fmaf(an[j], qv, s2);
+            acc[j] = __builtin_fmaf(dts[s], qv, acc[j]);
+          }
+          s1q[s] = s1;
+          s2q[s] = s2;
+#pragma unroll
+          for (int j = 0; j < NPL; ++j) {
+            pv[slot * NPL + j] = gk[j] * dtxs[s];             // dB: G * dt * x
+            pv[2 * NPL + slot * NPL + j] = hs[k][j] * dys[s];   // dC: h * dy
+          }
+          if (slot == 0) *(dbc_out + k * NP) = half_wave_reduce_scatter<M>(pv, lane);
+        }
+        // Add the two half-waves: lanes 0-31 end with s1, lanes 32-63 with s2.
+        float o[4];
+#pragma unroll
+        for (int s = 0; s < 4; ++s) {
+          const auto sw = __builtin_amdgcn_permlane32_swap(__float_as_uint(s1q[s]),
+                                                          __float_as_uint(s2q[s]), false, false);
+          o[s] = __uint_as_float(sw[0]) + __uint_as_float(sw[1]);
+        }
+        // tS: per wave a step-pair-major tile [8 pairs][64 rows][2] (rows 0-31:
+        // s1 of the channels, 32-63: s2), so that finalize's 64-bit reads of
+        // one pair over 32 rows are contiguous (no bank conflicts).
+        float* const ts = tS + wave * 64 * kSteps;
+        *reinterpret_cast<float2*>(ts + (2 * m * 64 + lane) * 2) = make_float2(o[0], o[1]);
+        *reinterpret_cast<float2*>(ts + ((2 * m + 1) * 64 + lane) * 2) = make_float2(o[2], o[3]);
+        if (m == 2) store_sub((i + 1) & 1, ci - 1);  // unused when ci == 0
+        if (m == 1) load_next();             // chunk ci - 2: loads nothing when ci < 2
+      }
+      // h at the start of chunk ci-1, copied here and now (an opaque copy the
+      // compiler cannot sink): ph's registers are then free for the next
+      // checkpoint load. A copy left at the loop back-edge would move that load's
+      // result, i.e. wait for it, and vmcnt being in order, for every load and
+      // store still in flight: a full memory drain per chunk.
+#pragma unroll
+      for (int j = 0; j < NPL; ++j) hc[j] = opaque_copy(ph[j]);
+      load_states<NPL>(ph, GBuf(ck_next, ck_i > 0 ? slice_bytes : 0u), st_lane, nvalid);   // h0(ci-2)
+      ck_next -= slice;
+      --ck_i;
       load_down();
-      __syncthreads();   // chunk ci-1 staged
-      continue;
+      fdx.down(sdx);
+      fddt.down(sddt);
+      fbs.down(sBsum);
+      fcs.down(sCsum);
+      __syncthreads();   // tS / tDBC complete; chunk ci-1 staged
     }
-
-    // ---- recompute phase, with the pipeline work of the neighbouring chunks
-    float da[kSteps][NPL], hs[kSteps][NPL];
-#pragma unroll
-    for (int m = 0; m < kQuads; ++m) {
-      float dts[4], dtxs[4], Bq[4][NPL];
-      f4_to(dts, lds4(s0 + cm_quad(c, m)));
-      f4_to(dtxs, lds4(s0 + oDTX + cm_quad(c, m)));
-      load_quad_rows<NPL>(Bq, gB, m);
-#pragma unroll
-      for (int s = 0; s < 4; ++s) {
-#pragma unroll
-        for (int j = 0; j < NPL; ++j) {
-          da[4 * m + s][j] = exp2_hw(dts[s] * a2[j]);
-          hs[4 * m + s][j] = Bq[s][j] * dtxs[s];       // b_k, turned into h_k below
-        }
-      }
-      if (m == 0)   // no-op stores past the sequence end
-        finalize((i + 1) & 1, chunk_len(ci + 1), fdx.get(sdx), fddt.get(sddt), fbs.get(sBsum),
-                 fcs.get(sCsum));
-    }
-#pragma unroll
-    for (int k = 0; k < kSteps; ++k)
-#pragma unroll
-      for (int j = 0; j < NPL; ++j)
-        hs[k][j] = __builtin_fmaf(da[k][j], k == 0 ? hc[j] : hs[k - 1][j], hs[k][j]);
-    __syncthreads();   // finalize(ci+1) is done with tS, tDBC and its buffer
-
-    // ---- reverse phase
-#pragma unroll
-    for (int m = kQuads - 1; m >= 0; --m) {
-      float dts[4], dys[4], dtxs[4], Bq[4][NPL], Cq[4][NPL], s1q[4], s2q[4];
-      f4_to(dts, lds4(s0 + cm_quad(c, m)));
-      f4_to(dys, lds4(s0 + oDY + cm_quad(c, m)));
-      f4_to(dtxs, lds4(s0 + oDTX + cm_quad(c, m)));
-      load_quad_rows<NPL>(Bq, gB, m);
-      load_quad_rows<NPL>(Cq, gC, m);
-      float pv[M];   // dB/dC products of the step pair (k, k+1), k even, numbered as for rs_index
-#pragma unroll
-      for (int s = 3; s >= 0; --s) {
-        const int k = 4 * m + s;
-        const int slot = k & 1;
-        float s1 = 0.f, s2 = 0.f, gk[NPL];
-#pragma unroll
-        for (int j = 0; j < NPL; ++j) {
-          gk[j] = __builtin_fmaf(dys[s], Cq[s][j], u[j]);            // G_k
-          u[j] = da[k][j] * gk[j];                                   // dA_k G_k
-          const float qv = u[j] * (k == 0 ? hc[j] : hs[k - 1][j]);   // G_k * hm_k
-          s1 = __builtin_fmaf(gk[j], Bq[s][j], s1);
-          s2 = __builtin_fmaf(an[j], qv, s2);
-          acc[j] = __builtin_fmaf(dts[s], qv, acc[j]);
-        }
-        s1q[s] = s1;
-        s2q[s] = s2;
-#pragma unroll
-        for (int j = 0; j < NPL; ++j) {
-          pv[slot * NPL + j] = gk[j] * dtxs[s];             // dB: G * dt * x
-          pv[2 * NPL + slot * NPL + j] = hs[k][j] * dys[s];   // dC: h * dy
-        }
-        if (slot == 0) *(dbc_out + k * NP) = half_wave_reduce_scatter<M>(pv, lane);
-      }
-      // Add the two half-waves: lanes 0-31 end with s1, lanes 32-63 with s2.
-      float o[4];
-#pragma unroll
-      for (int s = 0; s < 4; ++s) {
-        const auto sw = __builtin_amdgcn_permlane32_swap(__float_as_uint(s1q[s]),
-                                                        __float_as_uint(s2q[s]), false, false);
-        o[s] = __uint_as_float(sw[0]) + __uint_as_float(sw[1]);
-      }
-      // tS: per wave a step-pair-major tile [8 pairs][64 rows][2] (rows 0-31:
-      // s1 of the channels, 32-63: s2), so that finalize's 64-bit reads of
-      // one pair over 32 rows are contiguous (no bank conflicts).
-      float* const ts = tS + wave * 64 * kSteps;
-      *reinterpret_cast<float2*>(ts + (2 * m * 64 + lane) * 2) = make_float2(o[0], o[1]);
-      *reinterpret_cast<float2*>(ts + ((2 * m + 1) * 64 + lane) * 2) = make_float2(o[2], o[3]);
-      if (m == 2) store_sub((i + 1) & 1, ci - 1);  // unused when ci == 0
-      if (m == 1) load_next();             // chunk ci - 2: loads nothing when ci < 2
-    }
-    // h at the start of chunk ci-1, copied here and now (an opaque copy the
-    // compiler cannot sink): ph's registers are then free for the next
-    // checkpoint load. A copy left at the loop back-edge would move that load's
-    // result, i.e. wait for it, and vmcnt being in order, for every load and
-    // store still in flight: a full memory drain per chunk.
-#pragma unroll
-    for (int j = 0; j < NPL; ++j) hc[j] = opaque_copy(ph[j]);
-    load_states<NPL>(ph, GBuf(ck_next, ck_i > 0 ? slice_bytes : 0u), st_lane, nvalid);   // h0(ci-2)
-    ck_next -= slice;
-    --ck_i;
-    load_down();
-    fdx.down(sdx);
-    fddt.down(sddt);
-    fbs.down(sBsum);
-    fcs.down(sCsum);
-    __syncthreads();   // tS / tDBC complete; chunk ci-1 staged
+    last_par = (nit - 1) & 1;
   }
   const size_t slot = (size_t)seg * a.batch + b;
   if constexpr (CARRY) {
@@ -523,7 +742,7 @@ bwd_kernel(BwdArgs a) {
     if (q == 0 && act) a.carrySdt[slot * D + d] = sdt_acc;
     return;
   }
-  finalize((nit - 1) & 1, chunk_len(c_lo), sdx.at(c_lo), sddt.at(c_lo), sBsum.at(c_lo),
+  finalize(last_par, chunk_len(c_lo), sdx.at(c_lo), sddt.at(c_lo), sBsum.at(c_lo),
            sCsum.at(c_lo));
 
   float out[NPL];

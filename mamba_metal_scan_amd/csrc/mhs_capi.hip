@@ -194,6 +194,9 @@ struct Kernels {
   BwdFn carry_g = nullptr;  // gated
   BwdFn bwd_atom = nullptr;   // fp32 atomics for the reduced gradients
   BwdFn bwd_atom_g = nullptr; // gated
+  // The same four gradient passes with the in-kernel sweep (checkpoint
+  // strides of 2..kSweepMax 16-step chunks).
+  BwdFn bwd_sw = nullptr, bwd_sw_g = nullptr, bwd_atom_sw = nullptr, bwd_atom_sw_g = nullptr;
   void (*reduce)(const float*, const float*, const float*, const float*, void*, void*, float*,
                  int, int, long long, long long, int, long long, const float*, float*,
                  int) = nullptr;
@@ -210,6 +213,7 @@ struct Plan {
   int fwd_lds = 0;  // bytes
   int bwd_ki = 0;   // largest chunk the backward walks directly
   int bwd_lds = 0;  // bytes
+  int bwd_sw_lds = 0;  // bytes, the swept kernels
 };
 
 // Kernel instantiations: NPL in {2, 4}, G in 1..8 (d_state up to 64).
@@ -232,6 +236,10 @@ void fill_elem(Kernels& k) {
   k.carry_g = &mhs::bwd_kernel<NPL, G, MINW, true, true, ES>;
   k.bwd_atom = &mhs::bwd_kernel<NPL, G, MINW, false, false, ES, true>;
   k.bwd_atom_g = &mhs::bwd_kernel<NPL, G, MINW, true, false, ES, true>;
+  k.bwd_sw = &mhs::bwd_kernel<NPL, G, MINW, false, false, ES, false, mhs::kSweepMax>;
+  k.bwd_sw_g = &mhs::bwd_kernel<NPL, G, MINW, true, false, ES, false, mhs::kSweepMax>;
+  k.bwd_atom_sw = &mhs::bwd_kernel<NPL, G, MINW, false, false, ES, true, mhs::kSweepMax>;
+  k.bwd_atom_sw_g = &mhs::bwd_kernel<NPL, G, MINW, true, false, ES, true, mhs::kSweepMax>;
   k.reduce = &mhs::bwd_reduce_kernel<ES>;
 }
 
@@ -242,6 +250,7 @@ void fill(Plan& p) {
   fill_elem<NPL, G, MINW, 2>(p.k[kBF16]);
   p.fwd_lds = mhs::fwd_lds_floats(G, NPL) * 4;
   p.bwd_lds = mhs::bwd_lds_floats(G, NPL) * 4;
+  p.bwd_sw_lds = mhs::bwd_sweep_lds_floats(G, NPL) * 4;
 }
 
 template <int NPL>
@@ -280,7 +289,7 @@ bool plan_for(int N, int npl, Plan& p) {
   p.npl = npl;
   p.G = G;
   p.bwd_ki = kKI;
-  return p.fwd_lds <= kMaxLdsBytes && p.bwd_lds <= kMaxLdsBytes;
+  return p.fwd_lds <= kMaxLdsBytes && p.bwd_lds <= kMaxLdsBytes && p.bwd_sw_lds <= kMaxLdsBytes;
 }
 
 // Resolve the kernel variant for d_state N. Returns false if unsupported.
@@ -344,11 +353,23 @@ struct WsLayout {
   bool atomic = false;
 };
 
+// 16-step chunks per checkpoint when the backward sweeps them inside the
+// kernel (an effective stride K = min(chunk, T) of 2..kSweepMax register
+// windows, a multiple of the window), else 0.
+int sweep_km(int64_t chunk, int64_t T, int bwd_ki) {
+  const int64_t K = std::min<int64_t>(chunk, T);
+  if (K <= bwd_ki || K % bwd_ki != 0 || K / bwd_ki > mhs::kSweepMax) return 0;
+  return (int)(K / bwd_ki);
+}
+
 WsLayout ws_layout(int64_t batch, int64_t T, int64_t D, int64_t N, int64_t chunk, int bwd_ki) {
   WsLayout w;
   const size_t nblk = (size_t)((D + mhs::kCH - 1) / mhs::kCH);
   const size_t S = (size_t)batch * T * N;
   const int kb = (int)std::min<int64_t>(chunk, T) > bwd_ki ? bwd_ki : (int)std::min<int64_t>(chunk, T);
+  const int km = sweep_km(chunk, T, bwd_ki);
+  // Segments of the walk's chunks, the same as at stride bwd_ki (a segment
+  // of the swept kernel may start inside a caller chunk).
   w.sg = segments_for(batch, D, (int)((T + kb - 1) / kb), kBwdBlocksPerCU);
   w.nseg = w.sg.nseg;
   w.atomic = atomic_reduction(w.nseg > 1);
@@ -370,8 +391,9 @@ WsLayout ws_layout(int64_t batch, int64_t T, int64_t D, int64_t N, int64_t chunk
     w.carryS = off;
     off += round_up((size_t)w.sg.nunits * batch * D * 4, 256);
   }
-  w.fine = off;
-  if (chunk > bwd_ki) off += round_up((size_t)batch * ((T + bwd_ki - 1) / bwd_ki) * D * N * 4, 256);
+  w.fine = off;   // fine checkpoints: strides above the window that are not swept
+  if (std::min<int64_t>(chunk, T) > bwd_ki && km == 0)
+    off += round_up((size_t)batch * ((T + bwd_ki - 1) / bwd_ki) * D * N * 4, 256);
   w.total = off;
   return w;
 }
@@ -604,10 +626,15 @@ int scan_bwd(const void* x, const void* dt, const float* aneg, const void* B, co
   const int K = (int)std::min<int64_t>(chunk, seqlen);
 
   // Checkpoints at the backward's stride: the forward's own if chunk fits the
-  // register window, else recomputed into the workspace at stride bwd_ki.
+  // register window; for 2..kSweepMax windows the kernel sweeps the states
+  // between the caller's checkpoints itself; else recomputed into the
+  // workspace at stride bwd_ki.
   const float* ck = ckpt;
   int Kb = K;
-  if (K > p.bwd_ki) {
+  const int km = sweep_km(chunk, seqlen, p.bwd_ki);
+  if (km > 0) {
+    Kb = p.bwd_ki;
+  } else if (K > p.bwd_ki) {
     mhs::FwdArgs f;
     f.x = x; f.dt = dt; f.aneg = aneg; f.B = B; f.C = C;
     f.y = nullptr;
@@ -643,6 +670,8 @@ int scan_bwd(const void* x, const void* dt, const float* aneg, const void* B, co
   a.wsA = reinterpret_cast<float*>(ws + w.partA);
   a.batch = (int)batch; a.T = T; a.D = D; a.N = N; a.K = Kb;
   a.nchunk = (int)mhs_num_chunks(T, Kb);
+  a.km = km > 0 ? km : 1;
+  a.ck_nchunk = km > 0 ? (int)mhs_num_chunks(T, K) : 0;
   a.dt_lo = g.lo;
   a.dt_span = g.span;
   a.dt_inv_span = g.on ? 1.f / g.span : 0.f;
@@ -690,10 +719,14 @@ int scan_bwd(const void* x, const void* dt, const float* aneg, const void* B, co
     if (rc) return rc;
   }
   const Kernels& kk = p.k[e];
-  const BwdFn fn = w.atomic ? (g.on ? kk.bwd_atom_g : kk.bwd_atom) : (g.on ? kk.bwd_g : kk.bwd);
-  rc = ensure_lds(reinterpret_cast<const void*>(fn), p.bwd_lds);
+  const BwdFn fn = km > 0 ? (w.atomic ? (g.on ? kk.bwd_atom_sw_g : kk.bwd_atom_sw)
+                                      : (g.on ? kk.bwd_sw_g : kk.bwd_sw))
+                         : (w.atomic ? (g.on ? kk.bwd_atom_g : kk.bwd_atom)
+                                     : (g.on ? kk.bwd_g : kk.bwd));
+  const int lds_bytes = km > 0 ? p.bwd_sw_lds : p.bwd_lds;
+  rc = ensure_lds(reinterpret_cast<const void*>(fn), lds_bytes);
   if (rc) return rc;
-  hipLaunchKernelGGL(fn, dim3(nblk, (unsigned)(batch * w.nseg)), dim3(64 * p.G), p.bwd_lds, s, a);
+  hipLaunchKernelGGL(fn, dim3(nblk, (unsigned)(batch * w.nseg)), dim3(64 * p.G), lds_bytes, s, a);
   rc = check_launch("backward scan kernel");
   if (rc) return rc;
 

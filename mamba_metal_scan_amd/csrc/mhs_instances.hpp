@@ -32,15 +32,25 @@
   PREFIX template __global__ void fwd_kernel<NPL, G, MINW, true, false, kPassCkpt, ES>(FwdArgs);  \
   PREFIX template __global__ void fwd_kernel<NPL, G, MINW, true, true, kPassCkpt, ES>(FwdArgs);
 
-// Backward: ungated / gated, gradient pass / adjoint-carry pass.
+// Backward: ungated / gated, gradient pass / adjoint-carry pass; the
+// gradient pass with the in-kernel sweep of the checkpoint strides 32..64
+// (kSweepMax 16-step chunks per caller checkpoint), ungated / gated.
 #define MHS_BWD_INST(PREFIX, NPL, G, MINW, ES)                                    \
   PREFIX template __global__ void bwd_kernel<NPL, G, MINW, false, false, ES>(BwdArgs); \
   PREFIX template __global__ void bwd_kernel<NPL, G, MINW, true, false, ES>(BwdArgs);  \
   PREFIX template __global__ void bwd_kernel<NPL, G, MINW, false, true, ES>(BwdArgs);  \
-  PREFIX template __global__ void bwd_kernel<NPL, G, MINW, true, true, ES>(BwdArgs);
+  PREFIX template __global__ void bwd_kernel<NPL, G, MINW, true, true, ES>(BwdArgs);   \
+  PREFIX template __global__ void bwd_kernel<NPL, G, MINW, false, false, ES, false, kSweepMax>( \
+      BwdArgs);                                                                              \
+  PREFIX template __global__ void bwd_kernel<NPL, G, MINW, true, false, ES, false, kSweepMax>( \
+      BwdArgs);
 
 // Backward with fp32 atomics for dB, dC, dAneg and the dt bias: ungated /
 // gated.
 #define MHS_BWD_ATOM_INST(PREFIX, NPL, G, MINW, ES)                                    \
   PREFIX template __global__ void bwd_kernel<NPL, G, MINW, false, false, ES, true>(BwdArgs); \
-  PREFIX template __global__ void bwd_kernel<NPL, G, MINW, true, false, ES, true>(BwdArgs);
+  PREFIX template __global__ void bwd_kernel<NPL, G, MINW, true, false, ES, true>(BwdArgs);  \
+  PREFIX template __global__ void bwd_kernel<NPL, G, MINW, false, false, ES, true, kSweepMax>( \
+      BwdArgs);                                                                             \
+  PREFIX template __global__ void bwd_kernel<NPL, G, MINW, true, false, ES, true, kSweepMax>( \
+      BwdArgs);

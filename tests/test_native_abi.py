@@ -62,7 +62,8 @@ def test_workspace_size_formula():
     """Fixed-order reduction: dB/dC block partials (48 blocks of 32 channels)
     + dAneg batch partials + the gated dt-bias batch partials. Atomic
     reduction: only the fp32 dB/dC sums a bf16 backward rounds from. Either
-    way + fine checkpoints when the stride exceeds the 16-step window."""
+    way + fine checkpoints when the stride exceeds the 16-step window and is
+    not swept in the kernel (strides 32, 48 and 64 are)."""
     lib = _native.library()
     nblk, s, a = 48, 16 * 512 * 16, 16 * 1536 * 16
     try:
@@ -70,12 +71,15 @@ def test_workspace_size_formula():
         assert lib.mhs_deterministic() == 1
         base = 2 * nblk * s * 4 + a * 4 + 16 * 1536 * 4
         assert lib.mhs_scan_bwd_workspace_bytes(16, 512, 1536, 16, 16) == base
-        assert lib.mhs_scan_bwd_workspace_bytes(16, 512, 1536, 16, 64) == base + 32 * a * 4
+        assert lib.mhs_scan_bwd_workspace_bytes(16, 512, 1536, 16, 64) == base
+        assert lib.mhs_scan_bwd_workspace_bytes(16, 512, 1536, 16, 128) == base + 32 * a * 4
+        assert lib.mhs_scan_bwd_workspace_bytes(16, 512, 1536, 16, 40) == base + 32 * a * 4
         assert lib.mhs_scan_bwd_workspace_bytes(16, 512, 1536, 0, 16) == 0
         _native.set_reduction(_native.REDUCTION_ATOMIC)
         assert lib.mhs_deterministic() == 0
         assert lib.mhs_scan_bwd_workspace_bytes(16, 512, 1536, 16, 16) == 2 * s * 4
-        assert lib.mhs_scan_bwd_workspace_bytes(16, 512, 1536, 16, 64) == 2 * s * 4 + 32 * a * 4
+        assert lib.mhs_scan_bwd_workspace_bytes(16, 512, 1536, 16, 64) == 2 * s * 4
+        assert lib.mhs_scan_bwd_workspace_bytes(16, 512, 1536, 16, 128) == 2 * s * 4 + 32 * a * 4
     finally:
         _native.set_reduction(_native.REDUCTION_AUTO)
     # automatic: per shape, so not bit for bit at every shape
