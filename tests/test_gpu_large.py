@@ -94,6 +94,11 @@ def test_db_is_linear_in_dy(problem):
 
 
 def test_checkpoint_stride_is_not_a_result(problem):
+    """Bit for bit across strides, although the forward runs in two time
+    segments here: over its 2048-step carry units the state carried in from
+    before a unit decays below fp32 rounding, so the second segment's
+    combined start state equals the sequential one exactly (with short units
+    they agree to rounding only)."""
     with reduction(_native.REDUCTION_FIXED):
         base = _fwd_bwd(problem, 16)
         for chunk in (32, 64, 128):

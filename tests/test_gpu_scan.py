@@ -325,12 +325,54 @@ def test_empty_sequence():
 # blocks per CU): segment counts above the chunk count, uneven last segments,
 # chunk strides off the 16-step window, the fine-checkpoint recompute path and
 # the state gradient entering the last segment.
-# With chunk > 16 the backward first recomputes stride-16 checkpoints, in
-# segments that start on the caller's checkpoints (lcm(16, chunk) steps).
+# Strides 32, 48 and 64 are swept inside the backward kernel, from the
+# caller's checkpoints, also in segments that start inside a caller chunk;
+# other strides above 16 first recompute stride-16 checkpoints, in segments
+# that start on the caller's checkpoints (lcm(16, chunk) steps).
 SEGMENT_CASES = [(2, 100, 64, 16, 16, 2), (1, 300, 96, 16, 16, 3), (2, 257, 40, 8, 7, 5),
                  (1, 64, 64, 16, 16, 8), (3, 200, 130, 5, 64, 3), (1, 20, 32, 16, 16, 4),
                  (2, 513, 64, 32, 16, 8), (1, 1000, 64, 16, 48, 4), (2, 777, 96, 16, 20, 6),
                  (1, 2048, 64, 16, 64, 0)]
+
+
+def _run_hip_split(inp, dy, chunk, fwd_segs, bwd_segs):
+    """_run_hip with the forced time-segment count set separately for the
+    forward and the backward launch (the count is process-wide)."""
+    leaves = [t.clone().requires_grad_(True) for t in inp]
+    try:
+        _native.set_time_segments(fwd_segs)
+        y, h_last = selective_scan_hip(*leaves, return_state=True, chunk=chunk)
+        _native.set_time_segments(bwd_segs)
+        grads = torch.autograd.grad([y], leaves, grad_outputs=[dy])
+        torch.cuda.synchronize()
+    finally:
+        _native.set_time_segments(0)
+    return y.detach(), h_last.detach(), grads
+
+
+@pytest.mark.parametrize("segs", [1, 3, 5])
+def test_swept_strides_equal_stride_16_bit_for_bit(segs):
+    """The swept backward (strides 32, 48, 64) keeps the stride-16 time
+    segments; with 3 or 5 of them over 1000 steps (63 chunks of 16) some
+    segments start inside a caller chunk, and the last caller chunk is
+    partial. With the forward unsegmented (every checkpoint a sequential
+    state) every gradient equals stride 16's bit for bit (fixed order).
+    A segmented forward starts each segment from its combined carry, and
+    stride 16 then checkpoints states that derive from it where a sweep
+    rebuilds them from the caller's checkpoint before the segment: equal to
+    fp32 rounding, not bit for bit (the oracle tests cover that case)."""
+    bt, t_len, d, n = 2, 1000, 96, 16
+    arrs = oracle.make_inputs(bt, t_len, d, n, seed=4242, style="bench")
+    dy = torch.from_numpy(np.random.default_rng(43).standard_normal((bt, t_len, d),
+                                                                     dtype=np.float32)).to(DEV)
+    with reduction(_native.REDUCTION_FIXED):
+        base = _run_hip_split(_to_dev(arrs), dy, 16, 1, segs)
+        for chunk in (32, 48, 64):
+            print(f"[case] swept stride {chunk} vs 16, {segs} backward segments", flush=True)
+            other = _run_hip_split(_to_dev(arrs), dy, chunk, 1, segs)
+            assert torch.equal(base[0], other[0]) and torch.equal(base[1], other[1])
+            for name, a, b in zip(("dx", "ddt", "dAneg", "dB", "dC"), base[2], other[2]):
+                assert torch.equal(a, b), f"chunk {chunk}, {segs} segments: {name}"
 
 
 @pytest.mark.parametrize("mode", ["auto", "fixed"])
