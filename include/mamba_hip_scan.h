@@ -406,6 +406,34 @@ int mhs_xent_bwd_f32(const float* logits, const int64_t* targets, const float* l
                      const float* scale, float* dlogits, int64_t rows, int64_t vocab,
                      int64_t ignore_index, void* stream);
 
+/*
+ * RMSNorm of the residual stream, fp32: for each of `rows` rows of `cols`
+ * features, y = x * r * weight with r = 1 / sqrt(mean(x^2) + eps); rstd[row]
+ * receives r. Replaces the reference's RMSNorm.forward
+ * (mamba_metal/model.py:85-95), applied before every block's in_proj
+ * (model.py:225) and before the head (model.py:293). cols is a multiple of 4
+ * in [4, 2048]; every pointer 16-byte aligned; y may not alias x; eps finite
+ * and >= 0. Each row's sum of squares runs in a fixed order.
+ */
+int mhs_rmsnorm_fwd_f32(const float* x, const float* weight, float* y, float* rstd,
+                        int64_t rows, int64_t cols, float eps, void* stream);
+
+/* Workspace bytes of mhs_rmsnorm_bwd_f32 for rows x cols. */
+size_t mhs_rmsnorm_bwd_workspace_bytes(int64_t rows, int64_t cols);
+
+/*
+ * Its backward, the autograd of model.py:85-95: with g = dy * weight,
+ * dx = r * g - x * r^3 * sum(g * x) / cols, plus dres (the residual stream's
+ * other gradient, may be null) added in the same pass; dweight (cols) = the
+ * sum over rows of dy * x * r, fully written (zeros for rows = 0). dx may
+ * alias dres, not x or dy. The workspace (mhs_rmsnorm_bwd_workspace_bytes,
+ * 256-byte aligned) holds per-block partials of dweight, summed in a fixed
+ * order: bit-for-bit reproducible.
+ */
+int mhs_rmsnorm_bwd_f32(const float* dy, const float* x, const float* weight, const float* rstd,
+                        const float* dres, float* dx, float* dweight, void* workspace,
+                        size_t workspace_bytes, int64_t rows, int64_t cols, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -35,6 +35,7 @@ EXPORTED_SYMBOLS = (
     "mhs_set_cu_count", "mhs_cu_count", "mhs_scan_fwd_noalloc_f32", "mhs_set_reduction",
     "mhs_deterministic",
     "mhs_scan_bwd_reduction", "mhs_xent_fwd_f32", "mhs_xent_bwd_f32",
+    "mhs_rmsnorm_fwd_f32", "mhs_rmsnorm_bwd_workspace_bytes", "mhs_rmsnorm_bwd_f32",
 )
 
 # Size of the static device scratch of mhs_scan_fwd_noalloc_f32 (the header's
@@ -133,6 +134,12 @@ def library() -> ctypes.CDLL:
             lib.mhs_xent_fwd_f32.argtypes = [_P] * 4 + [_I64] * 3 + [_P]
             lib.mhs_xent_bwd_f32.restype = ctypes.c_int
             lib.mhs_xent_bwd_f32.argtypes = [_P] * 5 + [_I64] * 3 + [_P]
+            lib.mhs_rmsnorm_fwd_f32.restype = ctypes.c_int
+            lib.mhs_rmsnorm_fwd_f32.argtypes = [_P] * 4 + [_I64] * 2 + [ctypes.c_float, _P]
+            lib.mhs_rmsnorm_bwd_workspace_bytes.restype = ctypes.c_size_t
+            lib.mhs_rmsnorm_bwd_workspace_bytes.argtypes = [_I64] * 2
+            lib.mhs_rmsnorm_bwd_f32.restype = ctypes.c_int
+            lib.mhs_rmsnorm_bwd_f32.argtypes = [_P] * 8 + [ctypes.c_size_t] + [_I64] * 2 + [_P]
             _lib = lib
     return _lib
 
@@ -915,3 +922,86 @@ xent_bwd = _register(
 @xent_bwd.register_fake
 def _xent_bwd_fake(logits, targets, lse, scale, ignore_index):
     return torch.empty_like(logits)
+
+
+# ------------------------------------------------------------------ RMSNorm
+
+NORM_MAX_COLS = 2048   # the kernels' limit: rows of at most 2048 features
+
+
+def rmsnorm_supported(x: torch.Tensor) -> bool:
+    """Whether the HIP RMSNorm takes rows of x's last dimension: fp32 on a ROCm
+    device, a multiple of 4 features up to NORM_MAX_COLS, at least one row."""
+    c = x.shape[-1] if x.dim() >= 1 else 0
+    return (x.dtype == torch.float32 and x.device.type == "cuda" and c % 4 == 0
+            and 4 <= c <= NORM_MAX_COLS and x.numel() > 0)
+
+
+def _check_norm(what: str, x, weight, rstd=None, dy=None, dres=None) -> None:
+    """x (R, C) fp32 contiguous with C a multiple of 4 in [4, 2048]; weight
+    (C) fp32; rstd (R) fp32; dy, dres (R, C) fp32; all on one ROCm device and
+    16-byte aligned."""
+    _on_one_device(what, x, weight, rstd, dy, dres)
+    _need(x.dim() == 2, what, f"x must be (rows, cols); got {tuple(x.shape)}")
+    rows, cols = x.shape
+    _need(cols % 4 == 0 and 4 <= cols <= NORM_MAX_COLS, what,
+          f"cols must be a multiple of 4 in [4, {NORM_MAX_COLS}]; got {cols}")
+    _fp32(what, x=x, weight=weight, rstd=rstd, dy=dy, dres=dres)
+    _shaped(what, "weight", weight, (cols,))
+    _shaped(what, "rstd", rstd, (rows,))
+    _shaped(what, "dy", dy, (rows, cols))
+    _shaped(what, "dres", dres, (rows, cols))
+    _dense(what, x=x, weight=weight, rstd=rstd, dy=dy, dres=dres)
+    for name, t in (("x", x), ("weight", weight), ("rstd", rstd), ("dy", dy), ("dres", dres)):
+        _need(t is None or t.data_ptr() % 16 == 0, what, f"{name} must be 16-byte aligned")
+
+
+def _rmsnorm_fwd_impl(x: torch.Tensor, weight: torch.Tensor, eps: float
+                      ) -> tuple[torch.Tensor, torch.Tensor]:
+    """(y (R, C), rstd (R)) for x (R, C): y = x * rstd * weight."""
+    rows, cols = x.shape
+    y = torch.empty_like(x)
+    rstd = x.new_empty((rows,))
+    with _on(x.device):
+        rc = library().mhs_rmsnorm_fwd_f32(_ptr(x), _ptr(weight), _ptr(y), _ptr(rstd), rows, cols,
+                                           eps, _stream(x.device))
+    _check(rc, "mhs_rmsnorm_fwd_f32")
+    return y, rstd
+
+
+rmsnorm_fwd = _register("rmsnorm_fwd", _rmsnorm_fwd_impl, (),
+                        lambda x, weight, eps: _check_norm("rmsnorm_fwd", x, weight))
+
+
+@rmsnorm_fwd.register_fake
+def _rmsnorm_fwd_fake(x, weight, eps):
+    return torch.empty_like(x), x.new_empty((x.shape[0],))
+
+
+def _rmsnorm_bwd_impl(dy: torch.Tensor, x: torch.Tensor, weight: torch.Tensor,
+                      rstd: torch.Tensor, dres: Optional[torch.Tensor]
+                      ) -> tuple[torch.Tensor, torch.Tensor]:
+    """(dx (R, C), dweight (C)); dres, the residual stream's other gradient,
+    is added into dx when given."""
+    rows, cols = x.shape
+    dx = torch.empty_like(x)
+    dweight = torch.empty_like(weight)
+    lib = library()
+    nbytes = int(lib.mhs_rmsnorm_bwd_workspace_bytes(rows, cols))
+    ws = torch.empty((max(nbytes, 1),), dtype=torch.uint8, device=x.device)
+    with _on(x.device):
+        rc = lib.mhs_rmsnorm_bwd_f32(_ptr(dy), _ptr(x), _ptr(weight), _ptr(rstd), _ptr(dres),
+                                     _ptr(dx), _ptr(dweight), _ptr(ws), nbytes, rows, cols,
+                                     _stream(x.device))
+    _check(rc, "mhs_rmsnorm_bwd_f32")
+    return dx, dweight
+
+
+rmsnorm_bwd = _register(
+    "rmsnorm_bwd", _rmsnorm_bwd_impl, (),
+    lambda dy, x, weight, rstd, dres: _check_norm("rmsnorm_bwd", x, weight, rstd, dy, dres))
+
+
+@rmsnorm_bwd.register_fake
+def _rmsnorm_bwd_fake(dy, x, weight, rstd, dres):
+    return torch.empty_like(x), torch.empty_like(weight)

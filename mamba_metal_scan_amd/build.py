@@ -28,7 +28,7 @@ SOURCES = ["mhs_capi.hip", "mhs_kern_fwd_f32.hip", "mhs_kern_fwd_bf16.hip",
            "mhs_kern_bwd_f32.hip", "mhs_kern_bwd_bf16.hip", "mhs_kern_bwd_atom.hip",
            "mhs_kern_bwd_atom_bf16.hip"]
 HEADERS = ["mhs_common.hpp", "mhs_fwd.hpp", "mhs_bwd.hpp", "mhs_step.hpp", "mhs_conv.hpp",
-           "mhs_gate.hpp", "mhs_instances.hpp", "mhs_xent.hpp"]
+           "mhs_gate.hpp", "mhs_instances.hpp", "mhs_xent.hpp", "mhs_norm.hpp"]
 
 
 def hipcc() -> str:

@@ -11,6 +11,7 @@
 #include <cstdarg>
 #include <cstdio>
 #include <cstring>
+#include <initializer_list>
 #include <mutex>
 #include <numeric>
 
@@ -22,6 +23,7 @@
 #include "mhs_instances.hpp"
 #include "mhs_step.hpp"
 #include "mhs_xent.hpp"
+#include "mhs_norm.hpp"
 
 // The scan kernels are instantiated in the mhs_kern_*.hip units.
 namespace mhs {
@@ -35,7 +37,7 @@ MHS_FOR_PLANS(MHS_BWD_ATOM_INST, extern, 2)
 
 namespace {
 
-constexpr int kVersion = (0 << 16) | (4 << 8) | 0;   // 0.4: fused cross-entropy
+constexpr int kVersion = (0 << 16) | (5 << 8) | 0;   // 0.5: RMSNorm
 
 thread_local char g_err[512] = "";
 
@@ -1232,6 +1234,117 @@ int mhs_xent_bwd_f32(const float* logits, const int64_t* targets, const float* l
                        s, logits, t, lse, scale, dlogits, (long long)vocab,
                        (long long)ignore_index);
   return check_launch("cross-entropy backward kernel");
+}
+
+}  // extern "C"
+
+// ------------------------------------------------------------------- RMSNorm
+
+namespace {
+
+// Rows of cols features: cols a multiple of 4 in [4, 256 * kNormMaxNV],
+// rows < 2^31, 16-byte aligned pointers.
+int check_norm(int64_t rows, int64_t cols, std::initializer_list<const void*> ptrs) {
+  if (rows < 0 || cols < 4 || cols % 4 != 0 || cols > 256 * mhs::kNormMaxNV)
+    return fail(MHS_EINVAL, "rows must be >= 0 and cols a multiple of 4 in [4, %d]; got %lld, %lld",
+                256 * mhs::kNormMaxNV, (long long)rows, (long long)cols);
+  if (rows > 0x7FFFFFFF) return fail(MHS_EINVAL, "rows %lld exceeds 2^31 - 1", (long long)rows);
+  for (const void* q : ptrs) {
+    if (!q) return fail(MHS_EINVAL, "null pointer argument");
+    if (!aligned16(q)) return fail(MHS_EINVAL, "device pointers must be 16-byte aligned");
+  }
+  return MHS_OK;
+}
+
+int64_t norm_bwd_blocks(int64_t rows) {
+  return std::min<int64_t>((rows + 3) / 4, mhs::kNormBwdBlocks);
+}
+
+template <int NV>
+void launch_norm(bool bwd, const float* a, const float* b, const float* w, const float* rstd,
+                 const float* dres, float* out, float* aux, int rows, int cols, float eps,
+                 unsigned blocks, hipStream_t s) {
+  if (bwd)
+    hipLaunchKernelGGL(mhs::rmsnorm_bwd_kernel<NV>, dim3(blocks), dim3(mhs::kNormThreads), 0, s,
+                       a, b, w, rstd, dres, out, aux, rows, cols);
+  else
+    hipLaunchKernelGGL(mhs::rmsnorm_fwd_kernel<NV>, dim3(blocks), dim3(mhs::kNormThreads), 0, s,
+                       a, w, out, aux, rows, cols, eps);
+}
+
+// The kernel instance for cols features (NV float4 per lane).
+void dispatch_norm(bool bwd, const float* a, const float* b, const float* w, const float* rstd,
+                   const float* dres, float* out, float* aux, int rows, int cols, float eps,
+                   unsigned blocks, hipStream_t s) {
+  static_assert(mhs::kNormMaxNV == 8, "one case per NV");
+  switch ((cols + 255) / 256) {
+    case 1: launch_norm<1>(bwd, a, b, w, rstd, dres, out, aux, rows, cols, eps, blocks, s); break;
+    case 2: launch_norm<2>(bwd, a, b, w, rstd, dres, out, aux, rows, cols, eps, blocks, s); break;
+    case 3: launch_norm<3>(bwd, a, b, w, rstd, dres, out, aux, rows, cols, eps, blocks, s); break;
+    case 4: launch_norm<4>(bwd, a, b, w, rstd, dres, out, aux, rows, cols, eps, blocks, s); break;
+    case 5: launch_norm<5>(bwd, a, b, w, rstd, dres, out, aux, rows, cols, eps, blocks, s); break;
+    case 6: launch_norm<6>(bwd, a, b, w, rstd, dres, out, aux, rows, cols, eps, blocks, s); break;
+    case 7: launch_norm<7>(bwd, a, b, w, rstd, dres, out, aux, rows, cols, eps, blocks, s); break;
+    default: launch_norm<8>(bwd, a, b, w, rstd, dres, out, aux, rows, cols, eps, blocks, s); break;
+  }
+}
+
+}  // namespace
+
+extern "C" {
+
+int mhs_rmsnorm_fwd_f32(const float* x, const float* weight, float* y, float* rstd, int64_t rows,
+                        int64_t cols, float eps, void* stream) {
+  g_err[0] = '\0';
+  if (!(eps >= 0.f) || eps == INFINITY)
+    return fail(MHS_EINVAL, "eps must be finite and >= 0; got %g", (double)eps);
+  if (rows == 0) return check_norm(rows, cols, {});
+  const int rc = check_norm(rows, cols, {x, weight, y, rstd});
+  if (rc) return rc;
+  if (y == x) return fail(MHS_EINVAL, "y may not alias x");
+  const unsigned blocks = (unsigned)std::min<int64_t>((rows + 3) / 4, 8 * 1024);
+  dispatch_norm(false, x, nullptr, weight, nullptr, nullptr, y, rstd, (int)rows, (int)cols, eps,
+                blocks, static_cast<hipStream_t>(stream));
+  return check_launch("RMSNorm forward kernel");
+}
+
+size_t mhs_rmsnorm_bwd_workspace_bytes(int64_t rows, int64_t cols) {
+  if (rows < 0 || cols < 0) return 0;
+  return round_up((size_t)norm_bwd_blocks(rows) * (size_t)cols * 4, 256);
+}
+
+int mhs_rmsnorm_bwd_f32(const float* dy, const float* x, const float* weight, const float* rstd,
+                        const float* dres, float* dx, float* dweight, void* workspace,
+                        size_t workspace_bytes, int64_t rows, int64_t cols, void* stream) {
+  g_err[0] = '\0';
+  int rc = check_norm(rows, cols, {weight, dweight});
+  if (rc) return rc;
+  if (rows > 0) {
+    rc = check_norm(rows, cols, {dy, x, rstd, dx});
+    if (rc) return rc;
+    if (dres && !aligned16(dres))
+      return fail(MHS_EINVAL, "device pointers must be 16-byte aligned");
+    if (dx == x || dx == dy) return fail(MHS_EINVAL, "dx may alias only dres");
+  }
+  const size_t need = mhs_rmsnorm_bwd_workspace_bytes(rows, cols);
+  if (need > 0 && (!workspace || workspace_bytes < need))
+    return fail(MHS_EINVAL, "workspace too small: %zu < %zu bytes", workspace_bytes, need);
+  if (workspace && (reinterpret_cast<uintptr_t>(workspace) & 255u))
+    return fail(MHS_EINVAL, "workspace must be 256-byte aligned");
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  float* part = static_cast<float*>(workspace);
+  const int64_t P = norm_bwd_blocks(rows);
+  if (P > 0) {
+    dispatch_norm(true, dy, x, weight, rstd, dres, dx, part, (int)rows, (int)cols, 0.f,
+                  (unsigned)P, s);
+    rc = check_launch("RMSNorm backward kernel");
+    if (rc) return rc;
+  }
+  // dweight: the partial rows summed in a fixed order (zeros for rows == 0)
+  const unsigned rblocks = (unsigned)((cols / 4 + mhs::kNormReduceCols - 1) / mhs::kNormReduceCols);
+  hipLaunchKernelGGL(mhs::rmsnorm_dw_reduce_kernel, dim3(rblocks), dim3(256), 0, s, part, dweight,
+                     (int)P, (int)cols);
+  return check_launch("RMSNorm weight-gradient reduction kernel");
 }
 
 }  // extern "C"

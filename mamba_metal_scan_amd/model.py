@@ -37,8 +37,10 @@ import torch
 import torch.nn as nn
 import torch.nn.functional as F
 
+from ._native import rmsnorm_supported
 from .conv import conv1d_silu
 from .fused import mamba_inner, out_gate, selective_scan_gated
+from .norm import rms_norm, rms_norm_residual
 from .scan import SSM_CHUNK, _hip_device, selective_scan, selective_state_step
 from .xent import cross_entropy
 
@@ -94,16 +96,23 @@ def d_inner_for_budget(target: int, d_model: int, d_state: int, d_conv: int) -> 
 
 class RMSNorm(nn.Module):
     """weight * x * rsqrt(mean(x^2) + eps) over the last dim, in fp32
-    (mamba_metal/model.py:85-95). Computed by the framework's fused rms_norm
-    (one kernel per direction on the device instead of five elementwise and
-    reduction passes); same parameter name and function as the reference's."""
+    (mamba_metal/model.py:85-95); same parameter name and function as the
+    reference's. With `hip` set (the model's scan_impl is not 'torch') fp32
+    rows on a ROCm device go through the HIP RMSNorm kernels (norm.py), else
+    through the framework's fused rms_norm."""
 
     def __init__(self, d: int, eps: float = 1e-6):
         super().__init__()
         self.weight = nn.Parameter(torch.ones(d))
         self.eps = eps
+        self.hip = False
+
+    def uses_hip(self, x) -> bool:
+        return self.hip and rmsnorm_supported(x)
 
     def forward(self, x):
+        if self.uses_hip(x):
+            return rms_norm(x, self.weight, self.eps)
         xf = x.float()
         return F.rms_norm(xf, (xf.shape[-1],), self.weight, self.eps).to(x.dtype)
 
@@ -177,6 +186,7 @@ class MambaBlock(nn.Module):
         self.ckpt_chunk = cfg.ckpt_chunk
         self.dt_min, self.dt_max = cfg.dt_min, cfg.dt_max
         self.norm = RMSNorm(d_model, cfg.norm_eps)
+        self.norm.hip = cfg.scan_impl != "torch"
         self.in_proj = nn.Linear(d_model, 2 * d_inner, bias=False)
         # Left-padded by d_conv-1 and cut to T outputs: causal.
         self.conv = nn.Conv1d(d_inner, d_inner, kernel_size=d_conv, padding=d_conv - 1,
@@ -268,8 +278,13 @@ class MambaBlock(nn.Module):
                 and self.conv.kernel_size[0] <= 8)
 
     def forward(self, x, cache=None):
-        residual = x
-        xz = self.in_proj(self.norm(x))
+        if self.norm.uses_hip(x):
+            # x itself, and its norm; the backward adds x's two gradients in
+            # the norm's kernel.
+            residual, h = rms_norm_residual(x, self.norm.weight, self.norm.eps)
+        else:
+            residual, h = x, self.norm(x)
+        xz = self.in_proj(h)
         if cache is None and self._inner(xz):
             out = mamba_inner(xz, self.conv.weight, self.conv.bias, self.dt_proj.weight,
                               self.dt_proj.bias, self.B_proj.weight, self.C_proj.weight, self.A,
@@ -310,6 +325,7 @@ class TinyMamba(nn.Module):
         self.tok = nn.Embedding(cfg.vocab_size, cfg.d_model)
         self.blocks = nn.ModuleList(MambaBlock(cfg, d_inner) for _ in range(cfg.n_layers))
         self.ln_f = RMSNorm(cfg.d_model, cfg.norm_eps)
+        self.ln_f.hip = cfg.scan_impl != "torch"
         self.head = nn.Linear(cfg.d_model, cfg.vocab_size, bias=False)
         self.head.weight = self.tok.weight          # tied
         self.apply(self._init)

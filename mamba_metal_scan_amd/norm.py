@@ -1,0 +1,63 @@
+"""RMSNorm of the residual stream on the HIP kernels.
+
+The reference's RMSNorm (mamba_metal/model.py:85-95) computes
+``weight * x * rsqrt(mean(x^2) + eps)`` in fp32 before every block's in_proj
+(model.py:225) and before the head (model.py:293). ``rms_norm`` runs it as one
+HIP kernel forward and one backward pass (plus a small fixed-order sum of the
+weight gradient's per-block partials). ``rms_norm_residual`` also returns the
+block's residual stream: its backward then receives both gradients of x, the
+normalised path's and the residual's, and adds them in the same pass, where
+the framework would add them with a kernel of its own.
+"""
+from __future__ import annotations
+
+import torch
+
+from . import _native
+from ._native import HipScanError, dispatch, rmsnorm_supported
+
+
+class RMSNormHIP(torch.autograd.Function):
+    """y = weight * x * rsqrt(mean(x^2) + eps) over the last dimension; with
+    `residual`, (x, y), the first an alias of x whose gradient is added into
+    x's in the backward kernel."""
+
+    @staticmethod
+    def forward(ctx, x, weight, eps, residual):
+        if not rmsnorm_supported(x):
+            raise HipScanError(
+                f"rms_norm: x must be float32 on a ROCm device with a last dimension that "
+                f"is a multiple of 4 in [4, {_native.NORM_MAX_COLS}]; got {x.dtype}, "
+                f"{x.device}, {tuple(x.shape)}")
+        shape = x.shape
+        x2 = x.reshape(-1, shape[-1]).contiguous()
+        w = weight.contiguous()
+        y, rstd = dispatch("rmsnorm_fwd")(x2, w, float(eps))
+        ctx.save_for_backward(x2, w, rstd)
+        ctx.shape = shape
+        ctx.residual = residual
+        y = y.view(shape)
+        return (x, y) if residual else y
+
+    @staticmethod
+    def backward(ctx, *grads):
+        x2, w, rstd = ctx.saved_tensors
+        cols = x2.shape[1]
+        g_res, g_y = grads if ctx.residual else (None, grads[0])
+        dy = g_y.reshape(-1, cols).contiguous()
+        dres = g_res.reshape(-1, cols).contiguous() if g_res is not None else None
+        dx, dw = dispatch("rmsnorm_bwd")(dy, x2, w, rstd, dres)
+        return dx.view(ctx.shape), dw, None, None
+
+
+def rms_norm(x: torch.Tensor, weight: torch.Tensor, eps: float) -> torch.Tensor:
+    """The reference's RMSNorm on the HIP kernels (fp32, ROCm, last dimension
+    a multiple of 4 up to 2048)."""
+    return RMSNormHIP.apply(x, weight, eps, False)
+
+
+def rms_norm_residual(x: torch.Tensor, weight: torch.Tensor, eps: float
+                      ) -> tuple[torch.Tensor, torch.Tensor]:
+    """(residual, rms_norm(x)): the residual is x itself (an alias); the
+    gradients reaching both are added in the norm's backward kernel."""
+    return RMSNormHIP.apply(x, weight, eps, True)

@@ -101,6 +101,19 @@ def test_opcheck_cross_entropy_ops():
     torch.library.opcheck(OPS.xent_bwd, (logits, targets, lse, scale, -100))
 
 
+def test_opcheck_rmsnorm_ops():
+    print("[case] opcheck RMSNorm ops", flush=True)
+    g = _gen(5)
+    x = torch.randn(37, 132, generator=g).to(DEV)
+    w = torch.randn(132, generator=g).to(DEV)
+    torch.library.opcheck(OPS.rmsnorm_fwd, (x, w, 1e-6))
+    _, rstd = OPS.rmsnorm_fwd(x, w, 1e-6)
+    dy = torch.randn(37, 132, generator=g).to(DEV)
+    dres = torch.randn(37, 132, generator=g).to(DEV)
+    torch.library.opcheck(OPS.rmsnorm_bwd, (dy, x, w, rstd, dres))
+    torch.library.opcheck(OPS.rmsnorm_bwd, (dy, x, w, rstd, None))
+
+
 def test_compiled_scan_matches_eager():
     """torch.compile (aot_eager) of a function around the scan: the traced
     graph calls the registered ops; values and all gradients match eager."""

@@ -345,3 +345,33 @@ def test_xent_argument_errors():
     assert rc == MHS_EINVAL and "null" in _err(lib)
     rc = lib.mhs_xent_bwd_f32(A16, A16, A16, A16, A16, 4, 16, -100, None)
     assert rc == MHS_EINVAL and "alias" in _err(lib)
+
+
+def test_rmsnorm_argument_errors():
+    """Host-side checks of the RMSNorm entry points (no launch reaches a
+    device: every call here fails or has no rows)."""
+    lib = _native.library()
+    a, b = A16.value, A16.value + 1024     # distinct, 16-byte aligned stand-ins
+    assert lib.mhs_rmsnorm_fwd_f32(None, None, None, None, 0, 640, 1e-6, None) == MHS_OK
+    rc = lib.mhs_rmsnorm_fwd_f32(a, a, b, a, 4, 6, 1e-6, None)
+    assert rc == MHS_EINVAL and "multiple of 4" in _err(lib)
+    rc = lib.mhs_rmsnorm_fwd_f32(a, a, b, a, 4, 4096, 1e-6, None)
+    assert rc == MHS_EINVAL and "2048" in _err(lib)
+    rc = lib.mhs_rmsnorm_fwd_f32(a, None, b, a, 4, 640, 1e-6, None)
+    assert rc == MHS_EINVAL and "null" in _err(lib)
+    rc = lib.mhs_rmsnorm_fwd_f32(a + 4, a, b, a, 4, 640, 1e-6, None)
+    assert rc == MHS_EINVAL and "aligned" in _err(lib)
+    rc = lib.mhs_rmsnorm_fwd_f32(a, a, b, a, 4, 640, float("nan"), None)
+    assert rc == MHS_EINVAL and "eps" in _err(lib)
+    rc = lib.mhs_rmsnorm_fwd_f32(a, a, a, b, 4, 640, 1e-6, None)
+    assert rc == MHS_EINVAL and "alias" in _err(lib)
+    ws = lib.mhs_rmsnorm_bwd_workspace_bytes(8192, 640)
+    assert ws == 512 * 640 * 4 and lib.mhs_rmsnorm_bwd_workspace_bytes(5, 8) == 256
+    rc = lib.mhs_rmsnorm_bwd_f32(a, a, a, a, None, b, a, b, 16, 8192, 640, None)
+    assert rc == MHS_EINVAL and "workspace" in _err(lib)
+    rc = lib.mhs_rmsnorm_bwd_f32(a, a, a, a, None, a, a, b, ws, 8192, 640, None)
+    assert rc == MHS_EINVAL and "alias" in _err(lib)
+    rc = lib.mhs_rmsnorm_bwd_f32(a, a, a, a, a + 8, b, a, b, ws, 8192, 640, None)
+    assert rc == MHS_EINVAL and "aligned" in _err(lib)
+    rc = lib.mhs_rmsnorm_bwd_f32(a, a, a, None, None, b, a, b, ws, 8192, 640, None)
+    assert rc == MHS_EINVAL and "null" in _err(lib)
