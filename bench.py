@@ -584,7 +584,8 @@ TRAIN_GROUPS = (  # (label, substrings of the kernel name), first match wins
     ("HIP output gate", ("mhs::out_gate",)),
     ("cross-entropy (HIP, or the framework's softmax)", ("mhs::xent", "SoftMax", "nll_loss")),
     ("AdamW (fused)", ("FusedOpti",)),
-    ("RMSNorm", ("layer_norm", "rms_norm", "RmsNorm")),
+    ("RMSNorm (HIP, or the framework's rms_norm)", ("mhs::rmsnorm", "layer_norm", "rms_norm",
+                                                    "RmsNorm")),
 )
 
 
