@@ -159,8 +159,8 @@ rmsnorm_bwd_kernel(const float* __restrict__ dy, const float* __restrict__ x,
 
 // dw (C) = the sum of the P partial rows of dwp (P, C), in a fixed order:
 // a block owns kNormReduceCols float4 columns; its G = 256 / kNormReduceCols
-// thread groups each add every G-th partial row (g, g + G, ...), then group 0
-// adds the groups' sums in order.
+// thread groups each add every G-th partial row (g, g + G, ...), then the
+// groups' sums are added pairwise in LDS (a fixed tree of log2 G steps).
 __global__ void __launch_bounds__(256)
 rmsnorm_dw_reduce_kernel(const float* __restrict__ dwp, float* __restrict__ dw, int P, int C) {
   constexpr int G = 256 / kNormReduceCols;
@@ -187,13 +187,17 @@ rmsnorm_dw_reduce_kernel(const float* __restrict__ dwp, float* __restrict__ dw, 
   }
   red[g][cq] = s;
   __syncthreads();
-  if (g != 0 || i >= C4) return;
+  // The groups' sums added pairwise, a fixed tree: g += g + h for h = G/2 .. 1.
 #pragma unroll
-  for (int q = 1; q < G; ++q) {
-    const float4 t = red[q][cq];
-    s.x += t.x; s.y += t.y; s.z += t.z; s.w += t.w;
+  for (int h = G / 2; h >= 1; h >>= 1) {
+    if (g < h) {
+      const float4 t = red[g + h][cq];
+      float4& u = red[g][cq];
+      u.x += t.x; u.y += t.y; u.z += t.z; u.w += t.w;
+    }
+    __syncthreads();
   }
-  reinterpret_cast<float4*>(dw)[i] = s;
+  if (g == 0 && i < C4) reinterpret_cast<float4*>(dw)[i] = red[0][cq];
 }
 
 }  // namespace mhs
