@@ -418,6 +418,19 @@ int mhs_xent_bwd_f32(const float* logits, const int64_t* targets, const float* l
 int mhs_rmsnorm_fwd_f32(const float* x, const float* weight, float* y, float* rstd,
                         int64_t rows, int64_t cols, float eps, void* stream);
 
+/*
+ * The residual stream's update and the next norm in one pass: x_out = x +
+ * delta, then y and rstd of x_out as mhs_rmsnorm_fwd_f32. Replaces the
+ * block's residual add (mamba_metal/model.py:256) followed by the next
+ * block's RMSNorm (model.py:225) or the final one (model.py:293). x_out may
+ * not alias x, delta or y; y may not alias x or delta. The backward is
+ * mhs_rmsnorm_bwd_f32 on x_out, with x_out's own gradient as dres; x and
+ * delta both receive the resulting dx.
+ */
+int mhs_add_rmsnorm_fwd_f32(const float* x, const float* delta, const float* weight,
+                            float* x_out, float* y, float* rstd, int64_t rows, int64_t cols,
+                            float eps, void* stream);
+
 /* Workspace bytes of mhs_rmsnorm_bwd_f32 for rows x cols. */
 size_t mhs_rmsnorm_bwd_workspace_bytes(int64_t rows, int64_t cols);
 

@@ -7,7 +7,7 @@ from .conv import ConvSiluHIP, conv1d_silu
 from .fused import (MambaInnerHIP, OutGateHIP, SelectiveScanGatedHIP, mamba_inner, out_gate,
                     selective_scan_gated)
 from .model import MambaConfig, TinyMamba
-from .norm import RMSNormHIP, rms_norm, rms_norm_residual
+from .norm import AddRMSNormHIP, RMSNormHIP, add_rms_norm, rms_norm, rms_norm_residual
 from .xent import CrossEntropyHIP, cross_entropy
 from .scan import (SSM_CHUNK, SelectiveScanHIP, selective_scan, selective_scan_hip,
                    selective_scan_metal, selective_scan_ref, selective_state_step)
@@ -16,4 +16,5 @@ __all__ = ["MambaConfig", "TinyMamba", "SSM_CHUNK", "SelectiveScanHIP", "selecti
            "selective_scan_hip", "selective_scan_metal", "selective_scan_ref",
            "selective_state_step", "conv1d_silu", "ConvSiluHIP", "selective_scan_gated",
            "SelectiveScanGatedHIP", "out_gate", "OutGateHIP", "mamba_inner", "MambaInnerHIP",
-           "cross_entropy", "CrossEntropyHIP", "rms_norm", "rms_norm_residual", "RMSNormHIP"]
+           "cross_entropy", "CrossEntropyHIP", "rms_norm", "rms_norm_residual", "RMSNormHIP",
+           "add_rms_norm", "AddRMSNormHIP"]

@@ -36,6 +36,7 @@ EXPORTED_SYMBOLS = (
     "mhs_deterministic",
     "mhs_scan_bwd_reduction", "mhs_xent_fwd_f32", "mhs_xent_bwd_f32",
     "mhs_rmsnorm_fwd_f32", "mhs_rmsnorm_bwd_workspace_bytes", "mhs_rmsnorm_bwd_f32",
+    "mhs_add_rmsnorm_fwd_f32",
 )
 
 # Size of the static device scratch of mhs_scan_fwd_noalloc_f32 (the header's
@@ -136,6 +137,8 @@ def library() -> ctypes.CDLL:
             lib.mhs_xent_bwd_f32.argtypes = [_P] * 5 + [_I64] * 3 + [_P]
             lib.mhs_rmsnorm_fwd_f32.restype = ctypes.c_int
             lib.mhs_rmsnorm_fwd_f32.argtypes = [_P] * 4 + [_I64] * 2 + [ctypes.c_float, _P]
+            lib.mhs_add_rmsnorm_fwd_f32.restype = ctypes.c_int
+            lib.mhs_add_rmsnorm_fwd_f32.argtypes = [_P] * 6 + [_I64] * 2 + [ctypes.c_float, _P]
             lib.mhs_rmsnorm_bwd_workspace_bytes.restype = ctypes.c_size_t
             lib.mhs_rmsnorm_bwd_workspace_bytes.argtypes = [_I64] * 2
             lib.mhs_rmsnorm_bwd_f32.restype = ctypes.c_int
@@ -937,22 +940,24 @@ def rmsnorm_supported(x: torch.Tensor) -> bool:
             and 4 <= c <= NORM_MAX_COLS and x.numel() > 0)
 
 
-def _check_norm(what: str, x, weight, rstd=None, dy=None, dres=None) -> None:
+def _check_norm(what: str, x, weight, rstd=None, dy=None, dres=None, delta=None) -> None:
     """x (R, C) fp32 contiguous with C a multiple of 4 in [4, 2048]; weight
-    (C) fp32; rstd (R) fp32; dy, dres (R, C) fp32; all on one ROCm device and
-    16-byte aligned."""
-    _on_one_device(what, x, weight, rstd, dy, dres)
+    (C) fp32; rstd (R) fp32; dy, dres, delta (R, C) fp32; all on one ROCm
+    device and 16-byte aligned."""
+    _on_one_device(what, x, weight, rstd, dy, dres, delta)
     _need(x.dim() == 2, what, f"x must be (rows, cols); got {tuple(x.shape)}")
     rows, cols = x.shape
     _need(cols % 4 == 0 and 4 <= cols <= NORM_MAX_COLS, what,
           f"cols must be a multiple of 4 in [4, {NORM_MAX_COLS}]; got {cols}")
-    _fp32(what, x=x, weight=weight, rstd=rstd, dy=dy, dres=dres)
+    _fp32(what, x=x, weight=weight, rstd=rstd, dy=dy, dres=dres, delta=delta)
     _shaped(what, "weight", weight, (cols,))
     _shaped(what, "rstd", rstd, (rows,))
     _shaped(what, "dy", dy, (rows, cols))
     _shaped(what, "dres", dres, (rows, cols))
-    _dense(what, x=x, weight=weight, rstd=rstd, dy=dy, dres=dres)
-    for name, t in (("x", x), ("weight", weight), ("rstd", rstd), ("dy", dy), ("dres", dres)):
+    _shaped(what, "delta", delta, (rows, cols))
+    _dense(what, x=x, weight=weight, rstd=rstd, dy=dy, dres=dres, delta=delta)
+    for name, t in (("x", x), ("weight", weight), ("rstd", rstd), ("dy", dy), ("dres", dres),
+                    ("delta", delta)):
         _need(t is None or t.data_ptr() % 16 == 0, what, f"{name} must be 16-byte aligned")
 
 
@@ -976,6 +981,31 @@ rmsnorm_fwd = _register("rmsnorm_fwd", _rmsnorm_fwd_impl, (),
 @rmsnorm_fwd.register_fake
 def _rmsnorm_fwd_fake(x, weight, eps):
     return torch.empty_like(x), x.new_empty((x.shape[0],))
+
+
+def _add_rmsnorm_fwd_impl(x: torch.Tensor, delta: torch.Tensor, weight: torch.Tensor, eps: float
+                          ) -> tuple[torch.Tensor, torch.Tensor, torch.Tensor]:
+    """(x_out = x + delta, y = rms_norm(x_out), rstd) for x, delta (R, C)."""
+    rows, cols = x.shape
+    x_out = torch.empty_like(x)
+    y = torch.empty_like(x)
+    rstd = x.new_empty((rows,))
+    with _on(x.device):
+        rc = library().mhs_add_rmsnorm_fwd_f32(_ptr(x), _ptr(delta), _ptr(weight), _ptr(x_out),
+                                               _ptr(y), _ptr(rstd), rows, cols, eps,
+                                               _stream(x.device))
+    _check(rc, "mhs_add_rmsnorm_fwd_f32")
+    return x_out, y, rstd
+
+
+add_rmsnorm_fwd = _register(
+    "add_rmsnorm_fwd", _add_rmsnorm_fwd_impl, (),
+    lambda x, delta, weight, eps: _check_norm("add_rmsnorm_fwd", x, weight, delta=delta))
+
+
+@add_rmsnorm_fwd.register_fake
+def _add_rmsnorm_fwd_fake(x, delta, weight, eps):
+    return torch.empty_like(x), torch.empty_like(x), x.new_empty((x.shape[0],))
 
 
 def _rmsnorm_bwd_impl(dy: torch.Tensor, x: torch.Tensor, weight: torch.Tensor,

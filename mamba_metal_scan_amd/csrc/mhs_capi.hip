@@ -1260,33 +1260,66 @@ int64_t norm_bwd_blocks(int64_t rows) {
   return std::min<int64_t>((rows + 3) / 4, mhs::kNormBwdBlocks);
 }
 
+// The norm kernels' operands: forward (x, delta or null, w -> y, x_out,
+// rstd), backward (dy = a, x = b, w, rstd, dres -> dx = out, partials = aux).
+struct NormArgs {
+  const float *a, *b, *w, *rstd, *dres;
+  float *out, *out2, *aux;
+  int rows, cols;
+  float eps;
+};
+
+enum NormKind { kNormFwd, kNormAddFwd, kNormBwd };
+
 template <int NV>
-void launch_norm(bool bwd, const float* a, const float* b, const float* w, const float* rstd,
-                 const float* dres, float* out, float* aux, int rows, int cols, float eps,
-                 unsigned blocks, hipStream_t s) {
-  if (bwd)
-    hipLaunchKernelGGL(mhs::rmsnorm_bwd_kernel<NV>, dim3(blocks), dim3(mhs::kNormThreads), 0, s,
-                       a, b, w, rstd, dres, out, aux, rows, cols);
+void launch_norm(NormKind k, const NormArgs& n, unsigned blocks, hipStream_t s) {
+  const dim3 g(blocks), t(mhs::kNormThreads);
+  if (k == kNormBwd)
+    hipLaunchKernelGGL(mhs::rmsnorm_bwd_kernel<NV>, g, t, 0, s, n.a, n.b, n.w, n.rstd, n.dres,
+                       n.out, n.aux, n.rows, n.cols);
+  else if (k == kNormAddFwd)
+    hipLaunchKernelGGL((mhs::rmsnorm_fwd_kernel<NV, true>), g, t, 0, s, n.a, n.b, n.w, n.out,
+                       n.out2, n.aux, n.rows, n.cols, n.eps);
   else
-    hipLaunchKernelGGL(mhs::rmsnorm_fwd_kernel<NV>, dim3(blocks), dim3(mhs::kNormThreads), 0, s,
-                       a, w, out, aux, rows, cols, eps);
+    hipLaunchKernelGGL((mhs::rmsnorm_fwd_kernel<NV, false>), g, t, 0, s, n.a, nullptr, n.w,
+                       n.out, nullptr, n.aux, n.rows, n.cols, n.eps);
 }
 
 // The kernel instance for cols features (NV float4 per lane).
-void dispatch_norm(bool bwd, const float* a, const float* b, const float* w, const float* rstd,
-                   const float* dres, float* out, float* aux, int rows, int cols, float eps,
-                   unsigned blocks, hipStream_t s) {
+void dispatch_norm(NormKind k, const NormArgs& n, unsigned blocks, hipStream_t s) {
   static_assert(mhs::kNormMaxNV == 8, "one case per NV");
-  switch ((cols + 255) / 256) {
-    case 1: launch_norm<1>(bwd, a, b, w, rstd, dres, out, aux, rows, cols, eps, blocks, s); break;
-    case 2: launch_norm<2>(bwd, a, b, w, rstd, dres, out, aux, rows, cols, eps, blocks, s); break;
-    case 3: launch_norm<3>(bwd, a, b, w, rstd, dres, out, aux, rows, cols, eps, blocks, s); break;
-    case 4: launch_norm<4>(bwd, a, b, w, rstd, dres, out, aux, rows, cols, eps, blocks, s); break;
-    case 5: launch_norm<5>(bwd, a, b, w, rstd, dres, out, aux, rows, cols, eps, blocks, s); break;
-    case 6: launch_norm<6>(bwd, a, b, w, rstd, dres, out, aux, rows, cols, eps, blocks, s); break;
-    case 7: launch_norm<7>(bwd, a, b, w, rstd, dres, out, aux, rows, cols, eps, blocks, s); break;
-    default: launch_norm<8>(bwd, a, b, w, rstd, dres, out, aux, rows, cols, eps, blocks, s); break;
+  switch ((n.cols + 255) / 256) {
+    case 1: launch_norm<1>(k, n, blocks, s); break;
+    case 2: launch_norm<2>(k, n, blocks, s); break;
+    case 3: launch_norm<3>(k, n, blocks, s); break;
+    case 4: launch_norm<4>(k, n, blocks, s); break;
+    case 5: launch_norm<5>(k, n, blocks, s); break;
+    case 6: launch_norm<6>(k, n, blocks, s); break;
+    case 7: launch_norm<7>(k, n, blocks, s); break;
+    default: launch_norm<8>(k, n, blocks, s); break;
   }
+}
+
+int norm_fwd(const float* x, const float* delta, const float* weight, float* x_out, float* y,
+             float* rstd, int64_t rows, int64_t cols, float eps, void* stream) {
+  g_err[0] = '\0';
+  if (!(eps >= 0.f) || eps == INFINITY)
+    return fail(MHS_EINVAL, "eps must be finite and >= 0; got %g", (double)eps);
+  if (rows == 0) return check_norm(rows, cols, {});
+  int rc = check_norm(rows, cols, {x, weight, y, rstd});
+  if (rc) return rc;
+  if (delta) {
+    rc = check_norm(rows, cols, {delta, x_out});
+    if (rc) return rc;
+    if (x_out == x || x_out == delta || x_out == y)
+      return fail(MHS_EINVAL, "x_out may not alias x, delta or y");
+    if (y == delta) return fail(MHS_EINVAL, "y may not alias delta");
+  }
+  if (y == x) return fail(MHS_EINVAL, "y may not alias x");
+  const unsigned blocks = (unsigned)std::min<int64_t>((rows + 3) / 4, 8 * 1024);
+  NormArgs n{x, delta, weight, nullptr, nullptr, y, x_out, rstd, (int)rows, (int)cols, eps};
+  dispatch_norm(delta ? kNormAddFwd : kNormFwd, n, blocks, static_cast<hipStream_t>(stream));
+  return check_launch("RMSNorm forward kernel");
 }
 
 }  // namespace
@@ -1295,17 +1328,17 @@ extern "C" {
 
 int mhs_rmsnorm_fwd_f32(const float* x, const float* weight, float* y, float* rstd, int64_t rows,
                         int64_t cols, float eps, void* stream) {
-  g_err[0] = '\0';
-  if (!(eps >= 0.f) || eps == INFINITY)
-    return fail(MHS_EINVAL, "eps must be finite and >= 0; got %g", (double)eps);
-  if (rows == 0) return check_norm(rows, cols, {});
-  const int rc = check_norm(rows, cols, {x, weight, y, rstd});
-  if (rc) return rc;
-  if (y == x) return fail(MHS_EINVAL, "y may not alias x");
-  const unsigned blocks = (unsigned)std::min<int64_t>((rows + 3) / 4, 8 * 1024);
-  dispatch_norm(false, x, nullptr, weight, nullptr, nullptr, y, rstd, (int)rows, (int)cols, eps,
-                blocks, static_cast<hipStream_t>(stream));
-  return check_launch("RMSNorm forward kernel");
+  return norm_fwd(x, nullptr, weight, nullptr, y, rstd, rows, cols, eps, stream);
+}
+
+int mhs_add_rmsnorm_fwd_f32(const float* x, const float* delta, const float* weight,
+                            float* x_out, float* y, float* rstd, int64_t rows, int64_t cols,
+                            float eps, void* stream) {
+  if (rows > 0 && !delta) {
+    g_err[0] = '\0';
+    return fail(MHS_EINVAL, "null pointer argument");
+  }
+  return norm_fwd(x, delta, weight, x_out, y, rstd, rows, cols, eps, stream);
 }
 
 size_t mhs_rmsnorm_bwd_workspace_bytes(int64_t rows, int64_t cols) {
@@ -1335,8 +1368,8 @@ int mhs_rmsnorm_bwd_f32(const float* dy, const float* x, const float* weight, co
   float* part = static_cast<float*>(workspace);
   const int64_t P = norm_bwd_blocks(rows);
   if (P > 0) {
-    dispatch_norm(true, dy, x, weight, rstd, dres, dx, part, (int)rows, (int)cols, 0.f,
-                  (unsigned)P, s);
+    NormArgs n{dy, x, weight, rstd, dres, dx, nullptr, part, (int)rows, (int)cols, 0.f};
+    dispatch_norm(kNormBwd, n, (unsigned)P, s);
     rc = check_launch("RMSNorm backward kernel");
     if (rc) return rc;
   }

@@ -36,11 +36,14 @@ __device__ __forceinline__ float wave_sum64(float v) {
 
 __device__ __forceinline__ float4 f4_zero() { return make_float4(0.f, 0.f, 0.f, 0.f); }
 
-// y (rows, C) = x * r * w; rstd (rows) = r.
-template <int NV>
+// y (rows, C) = x * r * w; rstd (rows) = r. ADD: the row is x + delta (the
+// residual stream's update by the previous block), written to x_out, and
+// normalised.
+template <int NV, bool ADD = false>
 __global__ void __launch_bounds__(kNormThreads)
-rmsnorm_fwd_kernel(const float* __restrict__ x, const float* __restrict__ w,
-                   float* __restrict__ y, float* __restrict__ rstd, int rows, int C, float eps) {
+rmsnorm_fwd_kernel(const float* __restrict__ x, const float* __restrict__ delta,
+                   const float* __restrict__ w, float* __restrict__ y, float* __restrict__ x_out,
+                   float* __restrict__ rstd, int rows, int C, float eps) {
   const int lane = threadIdx.x & 63;
   const int nw = gridDim.x * (kNormThreads / 64);
   const int C4 = C >> 2;
@@ -52,20 +55,28 @@ rmsnorm_fwd_kernel(const float* __restrict__ x, const float* __restrict__ w,
   }
   const float inv_c = 1.f / (float)C;
   for (int r = blockIdx.x * (kNormThreads / 64) + (threadIdx.x >> 6); r < rows; r += nw) {
-    const float4* xr = reinterpret_cast<const float4*>(x + (size_t)r * C);
+    const size_t o = (size_t)r * C;
+    const float4* xr = reinterpret_cast<const float4*>(x + o);
     float4 xv[NV];
     float ss = 0.f;
 #pragma unroll
     for (int v = 0; v < NV; ++v) {
       const int i = lane + 64 * v;
       xv[v] = i < C4 ? xr[i] : f4_zero();
+      if constexpr (ADD) {
+        if (i < C4) {
+          const float4 dv = reinterpret_cast<const float4*>(delta + o)[i];
+          xv[v] = make_float4(xv[v].x + dv.x, xv[v].y + dv.y, xv[v].z + dv.z, xv[v].w + dv.w);
+          reinterpret_cast<float4*>(x_out + o)[i] = xv[v];
+        }
+      }
       ss = __builtin_fmaf(xv[v].x, xv[v].x, ss);
       ss = __builtin_fmaf(xv[v].y, xv[v].y, ss);
       ss = __builtin_fmaf(xv[v].z, xv[v].z, ss);
       ss = __builtin_fmaf(xv[v].w, xv[v].w, ss);
     }
     const float rs = 1.f / __fsqrt_rn(__builtin_fmaf(wave_sum64(ss), inv_c, eps));
-    float4* yr = reinterpret_cast<float4*>(y + (size_t)r * C);
+    float4* yr = reinterpret_cast<float4*>(y + o);
 #pragma unroll
     for (int v = 0; v < NV; ++v) {
       const int i = lane + 64 * v;

@@ -40,7 +40,7 @@ import torch.nn.functional as F
 from ._native import rmsnorm_supported
 from .conv import conv1d_silu
 from .fused import mamba_inner, out_gate, selective_scan_gated
-from .norm import rms_norm, rms_norm_residual
+from .norm import add_rms_norm, rms_norm, rms_norm_residual
 from .scan import SSM_CHUNK, _hip_device, selective_scan, selective_state_step
 from .xent import cross_entropy
 
@@ -284,12 +284,17 @@ class MambaBlock(nn.Module):
             residual, h = rms_norm_residual(x, self.norm.weight, self.norm.eps)
         else:
             residual, h = x, self.norm(x)
+        return residual + self.mix(h, cache)
+
+    def mix(self, h, cache=None):
+        """The block after its norm, without the residual add: in_proj, conv,
+        scan, gate, out_proj of the normalised h (model.py:226-256)."""
         xz = self.in_proj(h)
         if cache is None and self._inner(xz):
             out = mamba_inner(xz, self.conv.weight, self.conv.bias, self.dt_proj.weight,
                               self.dt_proj.bias, self.B_proj.weight, self.C_proj.weight, self.A,
                               self.D_skip, self.dt_min, self.dt_max, chunk=self.ckpt_chunk)
-            return residual + self.out_proj(out)
+            return self.out_proj(out)
         x, z = xz.chunk(2, dim=-1)
         k = self.conv.kernel_size[0]
         if cache is not None and cache.get("h") is not None and x.shape[1] == 1:
@@ -306,9 +311,9 @@ class MambaBlock(nn.Module):
             if cache is not None:
                 cache["h"] = h_last
         if self._fused(y):
-            return residual + self.out_proj(out_gate(y, self.D_skip, z))
+            return self.out_proj(out_gate(y, self.D_skip, z))
         y = y + self.D_skip
-        return residual + self.out_proj(y * F.silu(z))
+        return self.out_proj(y * F.silu(z))
 
 
 class TinyMamba(nn.Module):
@@ -344,9 +349,23 @@ class TinyMamba(nn.Module):
             cache["blocks"] = [{} for _ in self.blocks]
         x = self.tok(idx)
         caches = cache["blocks"] if cache is not None else [None] * len(self.blocks)
-        for block, bc in zip(self.blocks, caches):
-            x = block(x, bc)
-        logits = self.head(self.ln_f(x))
+        if self.ln_f.uses_hip(x) and all(b.norm.uses_hip(x) for b in self.blocks):
+            # The HIP norms: each block's residual add goes into the next norm's
+            # kernel (x + delta and its norm in one pass).
+            delta = None
+            for block, bc in zip(self.blocks, caches):
+                if delta is None:
+                    x, h = rms_norm_residual(x, block.norm.weight, block.norm.eps)
+                else:
+                    x, h = add_rms_norm(x, delta, block.norm.weight, block.norm.eps)
+                delta = block.mix(h, bc)
+            h = (add_rms_norm(x, delta, self.ln_f.weight, self.ln_f.eps)[1] if delta is not None
+                 else self.ln_f(x))
+        else:
+            for block, bc in zip(self.blocks, caches):
+                x = block(x, bc)
+            h = self.ln_f(x)
+        logits = self.head(h)
         loss = None
         if targets is not None:
             flat, tflat = logits.reshape(-1, logits.size(-1)), targets.reshape(-1)

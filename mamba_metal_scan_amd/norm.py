@@ -7,7 +7,9 @@ HIP kernel forward and one backward pass (plus a small fixed-order sum of the
 weight gradient's per-block partials). ``rms_norm_residual`` also returns the
 block's residual stream: its backward then receives both gradients of x, the
 normalised path's and the residual's, and adds them in the same pass, where
-the framework would add them with a kernel of its own.
+the framework would add them with a kernel of its own. ``add_rms_norm``
+also folds in the residual add before the norm (the block's
+``residual + out_proj(...)``, model.py:256).
 """
 from __future__ import annotations
 
@@ -36,6 +38,7 @@ class RMSNormHIP(torch.autograd.Function):
         ctx.save_for_backward(x2, w, rstd)
         ctx.shape = shape
         ctx.residual = residual
+        ctx.set_materialize_grads(False)   # an unused residual adds nothing
         y = y.view(shape)
         return (x, y) if residual else y
 
@@ -44,10 +47,46 @@ class RMSNormHIP(torch.autograd.Function):
         x2, w, rstd = ctx.saved_tensors
         cols = x2.shape[1]
         g_res, g_y = grads if ctx.residual else (None, grads[0])
-        dy = g_y.reshape(-1, cols).contiguous()
+        dy = g_y.reshape(-1, cols).contiguous() if g_y is not None else torch.zeros_like(x2)
         dres = g_res.reshape(-1, cols).contiguous() if g_res is not None else None
         dx, dw = dispatch("rmsnorm_bwd")(dy, x2, w, rstd, dres)
         return dx.view(ctx.shape), dw, None, None
+
+
+class AddRMSNormHIP(torch.autograd.Function):
+    """(x + delta, rms_norm(x + delta)) in one pass: the residual stream's
+    update by a block and the next norm. Both inputs receive the gradient of
+    the sum, formed in the norm's backward kernel from the gradients of both
+    outputs."""
+
+    @staticmethod
+    def forward(ctx, x, delta, weight, eps):
+        if not rmsnorm_supported(x) or delta.shape != x.shape or delta.dtype != x.dtype:
+            raise HipScanError(
+                f"add_rms_norm: x and delta must be float32 on a ROCm device, of one shape "
+                f"whose last dimension is a multiple of 4 in [4, {_native.NORM_MAX_COLS}]; got "
+                f"{x.dtype}, {delta.dtype}, {x.device}, {tuple(x.shape)}, {tuple(delta.shape)}")
+        shape = x.shape
+        cols = shape[-1]
+        w = weight.contiguous()
+        x_out, y, rstd = dispatch("add_rmsnorm_fwd")(x.reshape(-1, cols).contiguous(),
+                                                     delta.reshape(-1, cols).contiguous(), w,
+                                                     float(eps))
+        ctx.save_for_backward(x_out, w, rstd)
+        ctx.shape = shape
+        ctx.set_materialize_grads(False)   # an unused x_out adds nothing
+        return x_out.view(shape), y.view(shape)
+
+    @staticmethod
+    def backward(ctx, g_x, g_y):
+        x_out, w, rstd = ctx.saved_tensors
+        cols = x_out.shape[1]
+        dy = (g_y.reshape(-1, cols).contiguous() if g_y is not None
+              else torch.zeros_like(x_out))
+        dres = g_x.reshape(-1, cols).contiguous() if g_x is not None else None
+        dx, dw = dispatch("rmsnorm_bwd")(dy, x_out, w, rstd, dres)
+        dx = dx.view(ctx.shape)
+        return dx, dx, dw, None
 
 
 def rms_norm(x: torch.Tensor, weight: torch.Tensor, eps: float) -> torch.Tensor:
@@ -61,3 +100,11 @@ def rms_norm_residual(x: torch.Tensor, weight: torch.Tensor, eps: float
     """(residual, rms_norm(x)): the residual is x itself (an alias); the
     gradients reaching both are added in the norm's backward kernel."""
     return RMSNormHIP.apply(x, weight, eps, True)
+
+
+def add_rms_norm(x: torch.Tensor, delta: torch.Tensor, weight: torch.Tensor, eps: float
+                 ) -> tuple[torch.Tensor, torch.Tensor]:
+    """(x + delta, rms_norm(x + delta)) in one HIP pass; the gradients reaching
+    both outputs are added in the norm's backward kernel, and x and delta
+    both receive the sum's gradient."""
+    return AddRMSNormHIP.apply(x, delta, weight, eps)

@@ -13,7 +13,7 @@ import torch
 import torch.nn.functional as F
 
 from helpers import assert_close
-from mamba_metal_scan_amd import rms_norm, rms_norm_residual
+from mamba_metal_scan_amd import add_rms_norm, rms_norm, rms_norm_residual
 from mamba_metal_scan_amd._native import HipScanError
 from mamba_metal_scan_amd.model import MambaConfig, TinyMamba
 
@@ -69,6 +69,40 @@ def test_matches_float64_reference(rows, cols, residual):
     assert_close("dweight", dw, dw_ref, TOL)
 
 
+@pytest.mark.parametrize("rows,cols", [(8192, 640), (37, 132), (1, 2048)])
+@pytest.mark.parametrize("use_sum", [True, False])
+def test_add_then_norm_matches_float64_reference(rows, cols, use_sum):
+    """add_rms_norm(x, delta) = (x + delta, its norm); both inputs get the
+    sum's gradient: dy through the norm plus the sum's own gradient (absent
+    when the sum is not used, as for the final norm)."""
+    print(f"[case] add+rmsnorm {rows}x{cols} sum used {use_sum}", flush=True)
+    x, w, dy, ds = _inputs(rows, cols, seed=7 * rows + cols)
+    delta = torch.randn(rows, cols, generator=torch.Generator().manual_seed(cols))
+    xd = x.double().requires_grad_(True)
+    dd = delta.double().requires_grad_(True)
+    wd = w.double().requires_grad_(True)
+    sd = xd + dd
+    yd = wd * (sd * torch.rsqrt(sd.pow(2).mean(-1, keepdim=True) + EPS))
+    outs, gouts = [yd], [dy.double()]
+    if use_sum:
+        outs.append(sd)
+        gouts.append(ds.double())
+    torch.autograd.backward(outs, gouts)
+    xl, dl, wl = (t.to(DEV).requires_grad_(True) for t in (x, delta, w))
+    s, y = add_rms_norm(xl, dl, wl, EPS)
+    outs, gouts = [y], [dy.to(DEV)]
+    if use_sum:
+        outs.append(s)
+        gouts.append(ds.to(DEV))
+    gx, gd, gw = torch.autograd.grad(outs, [xl, dl, wl], gouts)
+    torch.cuda.synchronize()
+    assert_close("sum", s, sd.detach(), TOL)
+    assert_close("y", y, yd.detach(), TOL)
+    assert_close("dx", gx, xd.grad, TOL)
+    assert_close("ddelta", gd, dd.grad, TOL)
+    assert_close("dweight", gw, wd.grad, TOL)
+
+
 def test_matches_the_framework_rms_norm():
     """The framework's fused rms_norm in fp32 on the GPU, on (B, T, C) input."""
     print("[case] rmsnorm vs framework", flush=True)
@@ -121,6 +155,10 @@ def test_op_argument_errors():
         torch.ops.mamba_hip.rmsnorm_bwd(x, x, w, rstd, torch.zeros(4, 320, device=DEV))
     with pytest.raises(HipScanError, match="rms_norm"):
         rms_norm(torch.zeros(4, 6, device=DEV), torch.ones(6, device=DEV), EPS)
+    with pytest.raises(HipScanError, match="delta"):
+        torch.ops.mamba_hip.add_rmsnorm_fwd(x, torch.zeros(4, 320, device=DEV), w, EPS)
+    with pytest.raises(HipScanError, match="add_rms_norm"):
+        add_rms_norm(x, torch.zeros(4, 640, device=DEV, dtype=torch.float64), w, EPS)
 
 
 def test_model_norms_match_the_framework_path():

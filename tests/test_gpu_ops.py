@@ -112,6 +112,7 @@ def test_opcheck_rmsnorm_ops():
     dres = torch.randn(37, 132, generator=g).to(DEV)
     torch.library.opcheck(OPS.rmsnorm_bwd, (dy, x, w, rstd, dres))
     torch.library.opcheck(OPS.rmsnorm_bwd, (dy, x, w, rstd, None))
+    torch.library.opcheck(OPS.add_rmsnorm_fwd, (x, dres, w, 1e-6))
 
 
 def test_compiled_scan_matches_eager():

@@ -365,6 +365,15 @@ def test_rmsnorm_argument_errors():
     assert rc == MHS_EINVAL and "eps" in _err(lib)
     rc = lib.mhs_rmsnorm_fwd_f32(a, a, a, b, 4, 640, 1e-6, None)
     assert rc == MHS_EINVAL and "alias" in _err(lib)
+    c, d = b + 1024, b + 2048
+    rc = lib.mhs_add_rmsnorm_fwd_f32(a, None, a, b, c, d, 4, 640, 1e-6, None)
+    assert rc == MHS_EINVAL and "null" in _err(lib)
+    rc = lib.mhs_add_rmsnorm_fwd_f32(a, b, a, a, c, d, 4, 640, 1e-6, None)
+    assert rc == MHS_EINVAL and "x_out may not alias" in _err(lib)
+    rc = lib.mhs_add_rmsnorm_fwd_f32(a, b, a, c, b, d, 4, 640, 1e-6, None)
+    assert rc == MHS_EINVAL and "y may not alias delta" in _err(lib)
+    assert lib.mhs_add_rmsnorm_fwd_f32(None, None, None, None, None, None, 0, 640, 1e-6,
+                                       None) == MHS_OK
     ws = lib.mhs_rmsnorm_bwd_workspace_bytes(8192, 640)
     assert ws == 512 * 640 * 4 and lib.mhs_rmsnorm_bwd_workspace_bytes(5, 8) == 256
     rc = lib.mhs_rmsnorm_bwd_f32(a, a, a, a, None, b, a, b, 16, 8192, 640, None)
