@@ -358,7 +358,8 @@ class TinyMamba(nn.Module):
                     x, h = rms_norm_residual(x, block.norm.weight, block.norm.eps)
                 else:
                     x, h = add_rms_norm(x, delta, block.norm.weight, block.norm.eps)
-                delta = block.mix(h, bc)
+                # (under autocast out_proj yields bf16: widened exactly, as x + delta would)
+                delta = block.mix(h, bc).to(x.dtype)
             h = (add_rms_norm(x, delta, self.ln_f.weight, self.ln_f.eps)[1] if delta is not None
                  else self.ln_f(x))
         else:

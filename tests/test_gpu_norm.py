@@ -183,3 +183,23 @@ def test_model_norms_match_the_framework_path():
     assert_close("loss", l1, l2, 1e-5)
     for name in g1:
         assert_close(name, g1[name], g2[name], 1e-4)
+
+
+def test_model_under_autocast_matches_the_per_block_path():
+    """Under bf16 autocast the blocks' outputs are bf16: the folded residual
+    add widens them as the per-block path's x + delta does (same loss)."""
+    print("[case] rmsnorm in TinyMamba under autocast", flush=True)
+    torch.manual_seed(1)
+    cfg = MambaConfig(vocab_size=512, d_model=256, n_layers=2, d_state=16, scan_impl="hip")
+    model = TinyMamba(cfg).to(DEV)
+    idx = torch.randint(0, 512, (2, 64), device=DEV)
+    losses = []
+    for fused in (True, False):
+        if not fused:
+            model.ln_f.uses_hip = lambda x: False   # the per-block branch (framework final norm)
+        with torch.autocast("cuda", dtype=torch.bfloat16):
+            _, loss = model(idx, idx)
+        loss.backward()
+        losses.append(float(loss.detach()))
+    del model.ln_f.uses_hip
+    assert abs(losses[0] - losses[1]) <= 1e-3 * abs(losses[1])
