@@ -233,11 +233,14 @@ def bwd_reduction(batch: int, seqlen: int, d_inner: int, d_state: int, chunk: in
 def _bwd_reduction():
     """Around one backward call (workspace query and launch): the fixed-order
     reduction while torch's deterministic algorithms are enabled, else the
-    process-wide mode."""
-    if not torch.are_deterministic_algorithms_enabled():
-        yield
-        return
+    process-wide mode. Every backward holds the lock from its workspace query
+    to its launch, so that a deterministic call in another thread cannot
+    switch the library's mode in between (the workspace would then be sized
+    for the other reduction)."""
     with _reduction_lock:
+        if not torch.are_deterministic_algorithms_enabled():
+            yield
+            return
         lib = library()
         lib.mhs_set_reduction(REDUCTION_FIXED)
         try:
@@ -936,8 +939,8 @@ def rmsnorm_supported(x: torch.Tensor) -> bool:
     """Whether the HIP RMSNorm takes rows of x's last dimension: fp32 on a ROCm
     device, a multiple of 4 features up to NORM_MAX_COLS, at least one row."""
     c = x.shape[-1] if x.dim() >= 1 else 0
-    return (x.dtype == torch.float32 and x.device.type == "cuda" and c % 4 == 0
-            and 4 <= c <= NORM_MAX_COLS and x.numel() > 0)
+    return (x.dtype == torch.float32 and x.is_cuda and torch.version.hip is not None
+            and c % 4 == 0 and 4 <= c <= NORM_MAX_COLS and x.numel() > 0)
 
 
 def _check_norm(what: str, x, weight, rstd=None, dy=None, dres=None, delta=None) -> None:

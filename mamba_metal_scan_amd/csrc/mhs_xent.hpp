@@ -23,16 +23,23 @@ namespace mhs {
 constexpr int kXentThreads = 256;
 constexpr float kLn2 = 0.6931471805599453f;
 
-// (m, s) represents s * 2^m; combine two such partial sums.
+// (m, s) represents s * 2^m; combine two such partial sums. The side that
+// holds the maximum is scaled by exactly 1 (m - mm is not formed for it):
+// with both maxima -inf (a row, or a thread's share of it, masked with -inf
+// logits) 2^(-inf - -inf) would be NaN, where the sum is 0 * 2^-inf. An
+// empty side (s = 0) adds 0. A NaN partial sum (from a NaN logit) is not 0
+// and propagates.
 __device__ __forceinline__ void lse2_combine(float& m, float& s, float m2, float s2) {
   const float mm = fmaxf(m, m2);
-  // 2^(-inf - -inf) would be NaN: an empty side (s = 0, m = -inf) adds 0.
-  // A NaN partial sum (from a NaN logit) is not 0 and propagates.
-  const float a = s != 0.f ? s * exp2_hw(m - mm) : 0.f;
-  const float b = s2 != 0.f ? s2 * exp2_hw(m2 - mm) : 0.f;
+  const float a = s != 0.f ? (m == mm ? s : s * exp2_hw(m - mm)) : 0.f;
+  const float b = s2 != 0.f ? (m2 == mm ? s2 : s2 * exp2_hw(m2 - mm)) : 0.f;
   m = mm;
   s = a + b;
 }
+
+// The shift of a group's terms 2^(y - mc): its maximum mc, or 0 when every
+// term is -inf (the group's sum is then 2^-inf = 0, not 2^(-inf - -inf)).
+__device__ __forceinline__ float lse2_shift(float mc) { return mc == -INFINITY ? 0.f : mc; }
 
 // The block's (m, s) combined over its threads in a fixed order: within each
 // wave by xor shuffles, then the waves' results in order through LDS. Every
@@ -85,17 +92,19 @@ xent_fwd_kernel(const float* __restrict__ logits, const long long* __restrict__ 
       float mc = y[0];
 #pragma unroll
       for (int k = 1; k < 4 * U; ++k) mc = fmaxf(mc, y[k]);
+      const float sh = lse2_shift(mc);
       float sc = 0.f;
 #pragma unroll
-      for (int k = 0; k < 4 * U; ++k) sc += exp2_hw(y[k] - mc);
+      for (int k = 0; k < 4 * U; ++k) sc += exp2_hw(y[k] - sh);
       lse2_combine(m, s, mc, sc);
     }
     for (; i < n4; i += kXentThreads) {
       const float4 v = x4[i];
       const float y0 = v.x * kLog2e, y1 = v.y * kLog2e, y2 = v.z * kLog2e, y3 = v.w * kLog2e;
       const float mc = fmaxf(fmaxf(y0, y1), fmaxf(y2, y3));
+      const float sh = lse2_shift(mc);
       lse2_combine(m, s, mc,
-                   exp2_hw(y0 - mc) + exp2_hw(y1 - mc) + exp2_hw(y2 - mc) + exp2_hw(y3 - mc));
+                   exp2_hw(y0 - sh) + exp2_hw(y1 - sh) + exp2_hw(y2 - sh) + exp2_hw(y3 - sh));
     }
   } else {
     for (long long j = threadIdx.x; j < vocab; j += kXentThreads) {

@@ -316,6 +316,17 @@ class MambaBlock(nn.Module):
         return self.out_proj(y * F.silu(z))
 
 
+def _plain_block(b: nn.Module) -> bool:
+    """Whether calling b.mix() in place of b(x) skips nothing: b is a
+    MambaBlock itself (not a wrapper or a subclass) and neither it nor the
+    module-global registries hold forward or backward hooks."""
+    g = nn.modules.module
+    return (type(b) is MambaBlock and not b._forward_hooks and not b._forward_pre_hooks
+            and not b._backward_hooks and not b._backward_pre_hooks
+            and not g._global_forward_hooks and not g._global_forward_pre_hooks
+            and not g._global_backward_hooks and not g._global_backward_pre_hooks)
+
+
 class TinyMamba(nn.Module):
     """A Mamba language model sized to a transformer's parameter budget."""
 
@@ -349,9 +360,13 @@ class TinyMamba(nn.Module):
             cache["blocks"] = [{} for _ in self.blocks]
         x = self.tok(idx)
         caches = cache["blocks"] if cache is not None else [None] * len(self.blocks)
-        if self.ln_f.uses_hip(x) and all(b.norm.uses_hip(x) for b in self.blocks):
+        if self.ln_f.uses_hip(x) and all(_plain_block(b) and b.norm.uses_hip(x)
+                                         for b in self.blocks):
             # The HIP norms: each block's residual add goes into the next norm's
-            # kernel (x + delta and its norm in one pass).
+            # kernel (x + delta and its norm in one pass). This calls each
+            # block's mix() rather than the block itself, so it is taken only
+            # for unwrapped MambaBlocks without hooks (any other block is
+            # called as block(x, cache) in the loop below).
             delta = None
             for block, bc in zip(self.blocks, caches):
                 if delta is None:

@@ -34,6 +34,9 @@ class RMSNormHIP(torch.autograd.Function):
         shape = x.shape
         x2 = x.reshape(-1, shape[-1]).contiguous()
         w = weight.contiguous()
+        # dispatch() skips the op's own checks: weight's device, dtype, shape
+        # and alignment are checked here, before any launch.
+        _native._check_norm("rms_norm", x2, w)
         y, rstd = dispatch("rmsnorm_fwd")(x2, w, float(eps))
         ctx.save_for_backward(x2, w, rstd)
         ctx.shape = shape
@@ -69,9 +72,10 @@ class AddRMSNormHIP(torch.autograd.Function):
         shape = x.shape
         cols = shape[-1]
         w = weight.contiguous()
-        x_out, y, rstd = dispatch("add_rmsnorm_fwd")(x.reshape(-1, cols).contiguous(),
-                                                     delta.reshape(-1, cols).contiguous(), w,
-                                                     float(eps))
+        x2 = x.reshape(-1, cols).contiguous()
+        d2 = delta.reshape(-1, cols).contiguous()
+        _native._check_norm("add_rms_norm", x2, w, delta=d2)   # as in RMSNormHIP.forward
+        x_out, y, rstd = dispatch("add_rmsnorm_fwd")(x2, d2, w, float(eps))
         ctx.save_for_backward(x_out, w, rstd)
         ctx.shape = shape
         ctx.set_materialize_grads(False)   # an unused x_out adds nothing

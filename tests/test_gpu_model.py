@@ -61,6 +61,23 @@ def test_end_to_end_torch_vs_hip():
         assert_close(name, p1.grad, p2.grad, tol=2e-4)
 
 
+def test_block_hooks_run_and_keep_the_loss():
+    """A forward hook on a block makes TinyMamba call block(x) for every block
+    (the folded-norm path calls block.mix() and would skip the hook): the hook
+    runs once per block and the loss equals the folded path's."""
+    torch.manual_seed(SEED)
+    model = TinyMamba(_cfg(scan_impl="hip")).to(DEV)
+    x = torch.randint(0, VOCAB, (4, 48), generator=torch.Generator().manual_seed(SEED)).to(DEV)
+    with torch.no_grad():
+        _, l_folded = model(x, x)
+        seen = []
+        h = model.blocks[1].register_forward_hook(lambda m, i, o: seen.append(o.shape))
+        _, l_hooked = model(x, x)
+        h.remove()
+    assert seen == [torch.Size((4, 48, 64))]
+    assert torch.allclose(l_folded, l_hooked, atol=1e-5, rtol=1e-5)
+
+
 def test_recurrent_cache_on_device_matches_full_recomputation():
     torch.manual_seed(SEED)
     model = TinyMamba(_cfg(scan_impl="hip")).to(DEV).eval()

@@ -161,6 +161,25 @@ def test_op_argument_errors():
         add_rms_norm(x, torch.zeros(4, 640, device=DEV, dtype=torch.float64), w, EPS)
 
 
+@pytest.mark.parametrize("fn", ["rms_norm", "rms_norm_residual", "add_rms_norm"])
+def test_public_functions_check_the_weight(fn):
+    """The autograd Functions (which call the ops' plain implementations) check
+    the weight's length, dtype and device before any launch: a short, bf16 or
+    host weight would be read past its end or through a host pointer."""
+    x = torch.zeros(4, 640, device=DEV)
+    call = {"rms_norm": lambda w: rms_norm(x, w, EPS),
+            "rms_norm_residual": lambda w: rms_norm_residual(x, w, EPS),
+            "add_rms_norm": lambda w: add_rms_norm(x, torch.zeros_like(x), w, EPS)}[fn]
+    for bad, msg in ((torch.ones(320, device=DEV), "weight"),
+                     (torch.ones(640, device=DEV, dtype=torch.bfloat16), "float32"),
+                     (torch.ones(640), "device")):
+        with pytest.raises(HipScanError, match=msg):
+            call(bad)
+    torch.cuda.synchronize()
+    call(torch.ones(640, device=DEV))   # and a good weight still runs
+    torch.cuda.synchronize()
+
+
 def test_model_norms_match_the_framework_path():
     """TinyMamba's loss and every parameter gradient with the HIP norms
     against the same model with the framework's rms_norm (one block of the

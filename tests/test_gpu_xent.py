@@ -111,6 +111,36 @@ def test_misaligned_rows_take_the_scalar_path():
     assert _rel(l_hip, l_ref) <= 1e-5 and _rel(g_hip, g_ref) <= 1e-5
 
 
+@pytest.mark.parametrize("rows,vocab,lo,hi,storage_offset",
+                         [(8, 32768, 32000, 32768, 0),   # 16-value groups all -inf (vec4)
+                          (6, 5000, 4000, 5000, 0),      # float4 tail groups all -inf
+                          (5, 301, 40, 301, 0),          # scalar threads of -inf only
+                          (5, 2048, 0, 1500, 1),         # leading mask, scalar (misaligned)
+                          (4, 4096, 0, 3000, 0)])        # leading mask, vec4
+def test_minus_inf_masked_columns(rows, vocab, lo, hi, storage_offset):
+    """Vocabulary padding masked with -inf: the loss and gradient stay finite
+    and match the framework's (the masked columns get gradient 0). Targets lie
+    outside the mask."""
+    print(f"[case] xent -inf columns {rows}x{vocab} [{lo}, {hi}) off {storage_offset}",
+          flush=True)
+    logits, _ = _case(rows, vocab, seed=vocab + lo)
+    logits[:, lo:hi] = float("-inf")
+    free = torch.cat([torch.arange(0, lo), torch.arange(hi, vocab)])
+    g = torch.Generator().manual_seed(7)
+    targets = free[torch.randint(0, free.numel(), (rows,), generator=g)]
+    l_ref, g_ref = _reference(logits, targets, 1.0)
+    assert torch.isfinite(l_ref) and torch.isfinite(g_ref).all()
+    storage = None
+    if storage_offset:
+        buf = torch.empty(rows * vocab + storage_offset, device=DEV)
+        storage = buf[storage_offset:].view(rows, vocab)
+        storage.copy_(logits.to(DEV))
+    l_hip, g_hip = _hip(logits, targets, 1.0, storage=storage)
+    assert torch.isfinite(l_hip) and torch.isfinite(g_hip).all()
+    assert _rel(l_hip, l_ref) <= 1e-5 and _rel(g_hip, g_ref) <= 1e-5
+    assert (g_hip[:, lo:hi] == 0).all()
+
+
 def test_bitwise_reproducible():
     print("[case] xent determinism", flush=True)
     logits, targets = _case(256, 32768, seed=6)

@@ -142,3 +142,27 @@ def test_recurrent_cache_matches_full_recomputation():
             full_logits, _ = model(torch.cat([ctx, rest[:, :t + 1]], dim=1))
             delta = (step_logits[:, -1] - full_logits[:, -1]).abs().max().item()
             assert delta < 1e-5, f"step {t}: cache diverges by {delta:.2e}"
+
+
+def test_folded_norm_path_only_for_plain_blocks():
+    """The HIP forward that folds each residual add into the next norm calls
+    block.mix() instead of block(x): it is taken only for MambaBlocks that
+    are neither wrapped, subclassed nor hooked, so that hooks still run."""
+    from mamba_metal_scan_amd.model import MambaBlock, _plain_block
+    model = TinyMamba(small_cfg())
+    assert all(_plain_block(b) for b in model.blocks)
+    h = model.blocks[0].register_forward_hook(lambda *a: None)
+    assert not _plain_block(model.blocks[0]) and _plain_block(model.blocks[1])
+    h.remove()
+    assert _plain_block(model.blocks[0])
+
+    class Sub(MambaBlock):
+        pass
+
+    assert not _plain_block(Sub(small_cfg(), model.blocks[0].d_inner))
+    assert not _plain_block(torch.nn.Sequential(model.blocks[0]))
+    g = torch.nn.modules.module.register_module_forward_hook(lambda *a: None)
+    try:
+        assert not _plain_block(model.blocks[1])
+    finally:
+        g.remove()
