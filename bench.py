@@ -17,7 +17,11 @@ Reported:
   clock_settle   untimed steps run before the warmup until the GPU clock
                  is steady (about 40 ms of load from idle)
   cpu_baseline   selective_scan(impl="torch") fwd+bwd on the host CPU, same
-                 inputs, all threads of the process's CPU share
+                 inputs, all threads of the process's CPU share; the
+                 long-sequence and prefill keys carry their own, each on the
+                 whole workload, one rep in a child process under a
+                 wall-clock limit (timeouts and out-of-memory are recorded),
+                 with a bounded sample of the same sizes beside it
 
   train_80m      the 80M TinyMamba train step (fwd + bwd + AdamW) with the HIP
                  scan at batch 16 x seq 512: tokens/s and peak HBM
@@ -275,6 +279,77 @@ def cpu_baseline_scan(bt, t_len, d, n, reps: int = 3, warmup: int = 2, grad: boo
             "warmup_minor_faults": [f for _, f in warm],
             "sample": f"selective_scan(impl='torch') {kind} on {bt}x{t_len}x{d}x{n} ({what}), "
                       f"{warmup} warm-up + median of {reps} reps, torch CPU threads={threads}"}
+
+
+# Wall-clock limits of the CPU baselines that run in a child process. The
+# limits stay under three minutes, so that a run is never silent for longer.
+CPU_CHILD_LIMIT_S = {"longt": 150, "infer": 120}
+
+
+# The bounded samples run first in the same child: (batch, steps, d_inner,
+# d_state) sequences of the workload's other sizes, short enough for seconds.
+CPU_CHILD_SAMPLE = {"longt": (4, 1024, 2048, 16), "infer": (32, 256, 4096, 16)}
+
+
+def cpu_baseline_child(workload: str) -> dict:
+    """The CPU baseline of a whole workload, one rep, in a fresh child
+    process under a wall-clock limit: "longt" (4 x 16384 x 2048 x 16
+    fwd+bwd; the torch path keeps a tape of about 26 GB) or "infer" (the
+    32 x 2048 x 4096 x 16 prefill under no_grad). The child first times a
+    bounded sample of the same shape ("sample"), then the whole workload. A
+    child that runs out of time or host memory is recorded as such (value
+    None, "result" the reason, the sample kept), not retried."""
+    import subprocess
+    limit = CPU_CHILD_LIMIT_S[workload]
+    bt, t_len, d, n = {"longt": LONGT, "infer": INFER}[workload]
+    kind = "fwd+bwd" if workload == "longt" else "fwd (no_grad)"
+    what = (f"selective_scan(impl='torch') {kind} on {bt}x{t_len}x{d}x{n} (the full workload), "
+            f"one rep in a child process, wall-clock limit {limit} s")
+    cmd = [sys.executable, str(ROOT / "bench.py"), "--cpu-baseline-only", workload]
+    print(f"cpu baseline {workload}: started, limit {limit} s", file=sys.stderr, flush=True)
+    t0 = time.perf_counter()
+    failed = None
+    try:
+        res = subprocess.run(cmd, stdout=subprocess.PIPE, text=True, timeout=limit)
+        stdout, rc = res.stdout, res.returncode
+    except subprocess.TimeoutExpired as exc:
+        stdout = exc.stdout.decode() if isinstance(exc.stdout, bytes) else (exc.stdout or "")
+        rc, failed = None, f"timeout after {limit} s"
+    wall = time.perf_counter() - t0
+    lines = [json.loads(ln) for ln in stdout.splitlines() if ln.startswith("{")]
+    if rc:
+        sig = -rc if rc < 0 else None
+        failed = (f"killed by signal {sig}" + (" (out of host memory)" if sig == 9 else "")
+                  if sig else f"exit status {rc}")
+    print(f"cpu baseline {workload}: ended after {wall:.1f} s"
+          + (f" ({failed})" if failed else ""), file=sys.stderr, flush=True)
+    sample = lines[0] if lines else None
+    if failed or len(lines) < 2:
+        return {"value": None, "unit": "tokens/s", "cores": cpu_threads(), "kind": "port",
+                "result": failed or "no result", "sample": what, "bounded_sample": sample}
+    out = lines[1]
+    out["sample"] = what + (f"; {out['result']}" if out.get("result") else "")
+    out["child_wall_s"] = round(wall, 1)
+    out["bounded_sample"] = sample
+    return out
+
+
+def cpu_baseline_only(workload: str) -> int:
+    """The child of cpu_baseline_child (touches no GPU): one JSON line for
+    the bounded sample, then one for the whole workload."""
+    grad = workload == "longt"
+    full = LONGT if grad else INFER
+    sb, st, sd, sn = CPU_CHILD_SAMPLE[workload]
+    r = cpu_baseline_scan(sb, st, sd, sn, reps=1, warmup=0, grad=grad,
+                          what=f"a {st}-step sequence of the workload's other sizes")
+    print(json.dumps(r), flush=True)
+    print(f"cpu baseline {workload}: sample done ({r.get('ms_per_step', 0) / 1e3:.1f} s), "
+          f"whole workload next", file=sys.stderr, flush=True)
+    r = cpu_baseline_scan(*full, reps=1, warmup=0, grad=grad)
+    if r.get("value") is None:
+        r["result"] = r["sample"].rsplit(": ", 1)[-1]
+    print(json.dumps(r), flush=True)
+    return 0
 
 
 def run_launches(args) -> None:
@@ -589,6 +664,121 @@ TRAIN_GROUPS = (  # (label, substrings of the kernel name), first match wins
 )
 
 
+def kernel_label(name: str) -> str:
+    """A scan kernel's role from its template arguments (the demangled name):
+    fwd_kernel<NPL, G, MINW, KALIGNED, GATED, PASS, ES> and
+    bwd_kernel<NPL, G, MINW, GATED, CARRY, ES, ATOM, SWEEP>."""
+    import re
+    m = re.search(r"(fwd_kernel|bwd_kernel)<([^>]*)>", name)
+    if m:
+        a = [v.strip() for v in m.group(2).split(",")]
+        if m.group(1) == "fwd_kernel":
+            return {"0": "forward", "1": "forward carry pass", "2": "forward checkpoint pass"}[a[5]]
+        if a[4] == "true":
+            return "backward carry pass"
+        red = "atomics" if len(a) > 6 and a[6] == "true" else "fixed order"
+        sweep = " swept" if len(a) > 7 and a[7] != "0" else ""
+        return f"backward{sweep} ({red})"
+    for key, short in (("bwd_reduce", "backward reduction"), ("zero_grads", "zero fill"),
+                       ("copyBuffer", "copy")):
+        if key in name:
+            return short
+    return name[:40]
+
+
+def kernel_counters(args) -> None:
+    """Per-kernel counters of one scan workload (args' shape and --chunk),
+    every kernel labelled by its role: kernel-trace durations (OUT/kt, a
+    `--launches` run), HBM traffic from FETCH_SIZE and WRITE_SIZE passes
+    (copy-calibrated) and the VALU issue counters. Writes
+    profiles/scan_<shape>_chunk<K>_kernels.md and prints it."""
+    import csv
+    import glob
+    root = args.kernel_counters
+    vals: dict = {}
+    for f in glob.glob(os.path.join(root, "**", "*counter_collection.csv"), recursive=True):
+        for r in csv.DictReader(open(f)):
+            vals.setdefault((kernel_label(r["Kernel_Name"]), r["Counter_Name"]),
+                            []).append(float(r["Counter_Value"]))
+    mean = {k: sum(v) / len(v) for k, v in vals.items()}
+    # A counter summed over a launch's dispatches of one kernel role (the
+    # forward's carry pass and main pass are separate roles; a role
+    # dispatched once per launch is the common case).
+    per_launch = {k: sum(v) / args.launches for k, v in vals.items()}
+    fetch_factor = COPY_BYTES / (mean[("copy", "FETCH_SIZE")] * 1024)
+    write_factor = COPY_BYTES / (mean[("copy", "WRITE_SIZE")] * 1024)
+    durs: dict = {}
+    trace = os.path.join(root, "kt", "run_kernel_trace.csv")
+    for r in csv.DictReader(open(trace)):
+        durs.setdefault(kernel_label(r["Kernel_Name"]), []).append(
+            (int(r["End_Timestamp"]) - int(r["Start_Timestamp"])) / 1e3)
+    shape = (args.batch, args.seqlen, args.d_inner, args.d_state)
+    tag = shape_tag(*shape)
+    nbytes = scan_bytes(*shape)
+    extra = (f"--batch {args.batch} --seqlen {args.seqlen} --d-inner {args.d_inner} "
+             f"--d-state {args.d_state} --chunk {args.chunk}")
+    cmds = [f"rocprofv3 --kernel-trace --stats -d OUT/kt -o run --output-format csv -- "
+            f"python3 bench.py --launches {args.launches} {extra}",
+            f"rocprofv3 --pmc FETCH_SIZE -d OUT/fetch -o run --output-format csv -- "
+            f"python3 bench.py --launches {args.launches} {extra}",
+            f"rocprofv3 --pmc WRITE_SIZE -d OUT/write -o run --output-format csv -- "
+            f"python3 bench.py --launches {args.launches} {extra}",
+            f"rocprofv3 --pmc {ISSUE_COUNTERS} -d OUT/valu -o run --output-format csv -- "
+            f"python3 bench.py --launches {args.launches} {extra}",
+            f"python3 bench.py --kernel-counters OUT --launches {args.launches} {extra}"]
+    lines = [f"# Scan kernels at {tag}, chunk {args.chunk} (fp32, "
+             f"{reduction_name(*shape, args.chunk)} reduction): per-kernel time, HBM traffic, "
+             "VALU issue", "", PROFILE_RUN_NOTE, ""] + ["    " + c for c in cmds] + [
+        "", f"{args.launches} launches of the forward and the backward. Durations: kernel-trace "
+        "average over all dispatches (the first launch included). HBM traffic per launch: the "
+        f"counters summed over a launch's dispatches of the kernel, scaled by what a "
+        f"{COPY_BYTES} B device copy reads (FETCH_SIZE x{fetch_factor:.3f}, WRITE_SIZE "
+        f"x{write_factor:.3f}). Issue counters as in `scan_16x512x1536x16.md`: cycles = "
+        f"GRBM_GUI_ACTIVE / {N_XCD} per dispatch, VALU busy = SQ_ACTIVE_INST_VALU / ({N_CU} "
+        "CUs x cycles), waves / CU = 4 x SQ_WAVE_CYCLES / (CUs x cycles), VALU / wave = "
+        "SQ_INSTS_VALU / SQ_WAVES.", "",
+        "| kernel | dispatches per launch | avg us | read MB | write MB | HBM MB | achieved GB/s "
+        "| cycles | VALU busy | waves / CU | VALU / wave | LDS conflict |",
+        "|---|---|---|---|---|---|---|---|---|---|---|---|"]
+    order = ["forward carry pass", "forward", "forward checkpoint pass", "zero fill",
+             "backward carry pass"]
+    labels = sorted({k for k, _ in vals} - {"copy"},
+                    key=lambda k: (order.index(k) if k in order else len(order), k))
+    tot = {"fwd": 0.0, "bwd": 0.0, "fwd_us": 0.0, "bwd_us": 0.0}
+    for lab in labels:
+        g = lambda c: mean.get((lab, c), 0.0)
+        d = durs.get(lab, [])
+        disp = len(d) / args.launches if d else 0
+        avg = sum(d) / len(d) if d else 0.0
+        rd = per_launch.get((lab, "FETCH_SIZE"), 0.0) * 1024 * fetch_factor
+        wr = per_launch.get((lab, "WRITE_SIZE"), 0.0) * 1024 * write_factor
+        side = "fwd" if lab.startswith("forward") else "bwd"
+        tot[side] += rd + wr
+        tot[side + "_us"] += avg * disp
+        row = f"| {lab} | {disp:g} | {avg:.1f} | {rd / 1e6:.1f} | {wr / 1e6:.1f} | " \
+              f"{(rd + wr) / 1e6:.1f} | {(rd + wr) / (avg * disp * 1e-6) / 1e9 if avg else 0:.0f} | "
+        if (lab, "SQ_INSTS_VALU") in mean:
+            cyc = g("GRBM_GUI_ACTIVE") / N_XCD
+            row += (f"{cyc:.0f} | {g('SQ_ACTIVE_INST_VALU') / (N_CU * cyc):.2f} | "
+                    f"{4 * g('SQ_WAVE_CYCLES') / (N_CU * cyc):.1f} | "
+                    f"{g('SQ_INSTS_VALU') / max(g('SQ_WAVES'), 1.0):.0f} | "
+                    f"{g('SQ_LDS_BANK_CONFLICT') / (N_CU * cyc):.3f} |")
+        else:
+            row += " |  |  |  |  |"
+        lines.append(row)
+    lines += ["", "| launch | kernel time us | HBM MB | algorithmic MB | HBM / algorithmic "
+              "| algorithmic GB/s over kernel time |", "|---|---|---|---|---|---|"]
+    for side, name in (("fwd", "forward"), ("bwd", "backward")):
+        alg = nbytes[side]
+        us = tot[side + "_us"]
+        lines.append(f"| {name} | {us:.1f} | {tot[side] / 1e6:.1f} | {alg / 1e6:.1f} | "
+                     f"{tot[side] / alg:.2f} | {alg / (us * 1e-6) / 1e9 if us else 0:.0f} |")
+    md = ROOT / "profiles" / f"scan_{tag}_chunk{args.chunk}_kernels.md"
+    md.write_text("\n".join(lines) + "\n")
+    print("\n".join(lines))
+    print(f"\nwrote {md.relative_to(ROOT)}")
+
+
 def trace_summary(args) -> None:
     """Per-step kernel time of the train step from a rocprofv3 --kernel-trace
     --stats run under args.trace_summary (kt/run_kernel_stats.csv), grouped
@@ -764,10 +954,10 @@ def bench_longt(args) -> dict:
     rows = longt_measure([int(v) for v in args.strides.split(",")])
     best = min(rows, key=lambda r: r["fwd_bwd_ms"])
     nbytes = scan_bytes(bt, t_len, d, n)
-    # The CPU path on the first 1024 of the 16384 steps (the full sequence
-    # would take minutes): the same per-token work.
-    cpu = cpu_baseline_scan(bt, 1024, d, n, reps=1, warmup=0,
-                            what=f"the first 1024 of the workload's {t_len} steps")
+    # The CPU path on the whole workload, one rep under a wall-clock limit
+    # (value None with the reason when it runs out of time or memory), and on
+    # a bounded sample beside it: a 1024-step sequence of the same sizes.
+    cpu = cpu_baseline_child("longt")
     return {"metric": "long-sequence scan fwd+bwd GB/s (4x16384x2048x16 fp32)",
             "value": best["fwd_bwd_GBs"], "unit": "GB/s", "n_gpus": 1,
             "ms_per_step": best["fwd_bwd_ms"], "higher_is_better": True, "dtype": "f32",
@@ -847,7 +1037,7 @@ def bench_infer(args) -> dict:
     """Prefill 32 x 2048 x 4096 x 16 (forward + final state), then 256 decode steps."""
     bt, t_len, d, n = INFER
     m = infer_measure()
-    cpu = cpu_baseline_scan(bt, t_len, d, n, reps=1, warmup=0, grad=False)
+    cpu = cpu_baseline_child("infer")
     return {"metric": "prefill GB/s and decode us/step (32x2048x4096x16 fp32)",
             "value": m["prefill_GBs"], "unit": "GB/s", "n_gpus": 1,
             "ms_per_step": m["prefill_ms"], "higher_is_better": True, "dtype": "f32",
@@ -964,13 +1154,17 @@ def bench_scan(args) -> dict:
     torch.cuda.empty_cache()
     if not args.no_extra:
         out["longt_4x16384x2048x16"] = {
-            "strides": longt_measure([16, 64]),
+            "strides": longt_measure([16, 32, 64, 128]),
             "algorithmic_bytes": scan_bytes(*LONGT)["fwd_bwd"]}
         out["infer_32x2048x4096x16"] = infer_measure()
     if not args.no_train:
         out["train_80m"] = bench_train()
     if not args.no_cpu_baseline:
         out["cpu_baseline"] = cpu_baseline_scan(bt, t_len, d, n)
+        if not args.no_extra:
+            # The other configurations' CPU paths, each on its whole workload.
+            out["longt_4x16384x2048x16"]["cpu_baseline"] = cpu_baseline_child("longt")
+            out["infer_32x2048x4096x16"]["cpu_baseline_prefill"] = cpu_baseline_child("infer")
     return out
 
 
@@ -1026,9 +1220,18 @@ def main() -> int:
                     help="summarise rocprofv3 FETCH_SIZE / WRITE_SIZE passes under DIR")
     ap.add_argument("--strides", default="16,32,64,128",
                     help="checkpoint strides of --workload longt (comma-separated)")
+    ap.add_argument("--kernel-counters", default=None, metavar="DIR",
+                    help="summarise per-kernel rocprofv3 passes of --launches runs under DIR "
+                         "(any shape; every scan kernel labelled by its role)")
     ap.add_argument("--trace-summary", default=None, metavar="DIR",
                     help="summarise a kernel-trace run of --workload train under DIR")
+    ap.add_argument("--cpu-baseline-only", default=None, choices=["longt", "infer"],
+                    help="internal: the CPU baseline of a workload alone, one JSON line "
+                         "(the child process of the default line's long-sequence and "
+                         "prefill baselines; touches no GPU)")
     args = ap.parse_args()
+    if args.cpu_baseline_only:
+        return cpu_baseline_only(args.cpu_baseline_only)
     global USE_TORCH_EVENTS
     USE_TORCH_EVENTS = args.torch_events
 
@@ -1040,6 +1243,9 @@ def main() -> int:
         return 0
     if args.trace_summary:
         trace_summary(args)
+        return 0
+    if args.kernel_counters:
+        kernel_counters(args)
         return 0
 
     if args.gpus != 1:

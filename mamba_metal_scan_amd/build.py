@@ -89,5 +89,136 @@ def emit_assembly(out_dir: Path) -> Path:
     return asm
 
 
+# ----------------------------------------------------- register / LDS audit
+#
+# The compiler's resource remarks (-Rpass-analysis=kernel-resource-usage) for
+# every kernel of the library, and the dynamic LDS each scan kernel is
+# launched with. The LDS sizes mirror the constexpr helpers of the kernel
+# headers (fwd_lds_floats in mhs_fwd.hpp, bwd_lds_floats and
+# bwd_sweep_lds_floats in mhs_bwd.hpp) with the header constants below, which
+# tests/test_build.py reads back from the headers.
+K_CH, K_STEPS, K_BC_PAD, K_SWEEP_MAX = 32, 16, 4, 4
+LDS_PER_CU = 160 * 1024          # gfx950
+VGPRS_PER_SIMD_LANE = 512        # wave64 VGPR file per SIMD lane (gfx950, no AGPR split used)
+
+
+def _bc_tile_floats(nq: int, npl: int) -> int:
+    return nq * (K_STEPS * npl + K_BC_PAD)
+
+
+def scan_lds_bytes(kind: str, g: int, npl: int) -> int:
+    """Dynamic LDS per block of the scan kernels of plan (NPL, G): "fwd",
+    "bwd" or "bwd_sweep" (the swept backward, checkpoint strides 32-64)."""
+    if kind == "fwd":
+        buf = 2 * K_CH * K_STEPS + 2 * _bc_tile_floats(2 * g, npl) + g * K_CH * K_STEPS
+        return 4 * 2 * buf
+    buf = 4 * K_CH * K_STEPS + 2 * _bc_tile_floats(2 * g, npl)
+    floats = 2 * buf + g * 64 * K_STEPS + 2 * K_STEPS * 2 * g * npl
+    if kind == "bwd_sweep":
+        floats += K_SWEEP_MAX * 64 * g * npl
+    return 4 * floats
+
+
+def resource_usage(verbose: bool = False) -> dict:
+    """{demangled kernel name: {remark: value}} from a device-only compile of
+    every source with the compiler's kernel-resource-usage remarks."""
+    import re
+    with tempfile.TemporaryDirectory(prefix="mhs_ru_") as objdir:
+        cmds = [[hipcc(), *compile_flags(), "--cuda-device-only", "-c", "-o",
+                 str(Path(objdir) / (Path(src).stem + ".o")), str(CSRC / src),
+                 "-Rpass-analysis=kernel-resource-usage"] for src in SOURCES]
+        with ThreadPoolExecutor(max_workers=min(len(cmds), os.cpu_count() or 1)) as pool:
+            res = list(pool.map(lambda c: subprocess.run(c, capture_output=True, text=True),
+                                cmds))
+    rows: dict = {}
+    cur = None
+    for r in res:
+        if r.returncode != 0:
+            raise RuntimeError(f"hipcc failed ({r.returncode}):\n{r.stderr}")
+        for ln in r.stderr.splitlines():
+            m = re.search(r"remark: Function Name: (\S+)", ln)
+            if m:
+                cur = rows.setdefault(m.group(1), {})
+                continue
+            m = re.search(r"remark:\s+([^:]+): (\S+) \[-Rpass-analysis", ln)
+            if m and cur is not None:
+                cur[m.group(1).strip()] = m.group(2)
+    names = list(rows)
+    dem = subprocess.run(["c++filt"], input="\n".join(names), capture_output=True, text=True,
+                         check=True).stdout.splitlines()
+    return {d.replace("mhs::", ""): rows[n] for n, d in zip(names, dem)}
+
+
+# The kernels of the benchmarked workloads (d_state 16: NPL 2, G 4; the
+# one-state-per-lane plan NPL 1, G 8 beside them), with what each one is.
+AUDIT = [
+    ("fwd_kernel<2, 4, 3, true, false, 0, 4>", "forward, checkpoint stride a multiple of 16",
+     "fwd", 4, 2),
+    ("fwd_kernel<2, 4, 3, true, false, 1, 4>", "forward carry pass (time segments)", "fwd", 4, 2),
+    ("fwd_kernel<2, 4, 3, true, true, 0, 4>", "gated forward (TinyMamba block)", "fwd", 4, 2),
+    ("bwd_kernel<2, 4, 3, false, false, 4, false, 0>", "backward, fixed-order partials",
+     "bwd", 4, 2),
+    ("bwd_kernel<2, 4, 3, false, false, 4, true, 0>", "backward, fp32 atomics", "bwd", 4, 2),
+    ("bwd_kernel<2, 4, 3, false, false, 4, false, 4>", "backward, swept strides 32-64",
+     "bwd_sweep", 4, 2),
+    ("bwd_kernel<2, 4, 3, false, false, 4, true, 4>", "backward, swept strides, atomics",
+     "bwd_sweep", 4, 2),
+    ("bwd_kernel<2, 4, 3, false, true, 4, false, 0>", "backward carry pass (time segments)",
+     "bwd", 4, 2),
+    ("bwd_kernel<2, 4, 3, true, false, 4, false, 0>", "gated backward (TinyMamba block)",
+     "bwd", 4, 2),
+    ("fwd_kernel<1, 8, 4, true, false, 0, 4>", "forward, one state per lane", "fwd", 8, 1),
+    ("bwd_kernel<1, 8, 4, false, false, 4, false, 0>", "backward, one state per lane",
+     "bwd", 8, 1),
+    ("bwd_reduce_kernel<4>", "dB / dC / dAneg partial sums", None, 4, 0),
+    ("zero_grads_kernel<0>", "zero fill before the atomics", None, 4, 0),
+    ("step_kernel_vec<1, 4>", "decode step, d_state 16", None, 4, 0),
+]
+
+
+def resource_table(usage: dict) -> list:
+    """Markdown rows of the audited kernels: registers, scratch, spills,
+    dynamic LDS, and the waves per SIMD each of them allows."""
+    out = ["| kernel | what | VGPRs | AGPRs | SGPRs | scratch B/lane | VGPR / SGPR spills "
+           "| waves/SIMD (registers) | LDS B/block | waves/SIMD (LDS) |",
+           "|---|---|---|---|---|---|---|---|---|---|"]
+    for prefix, what, kind, waves_per_block, npl in AUDIT:
+        hits = [k for k in usage if k.startswith("void " + prefix + "(")]
+        if not hits:
+            raise KeyError(f"no kernel {prefix} in the library's resource remarks")
+        r = usage[hits[0]]
+        lds = scan_lds_bytes(kind, waves_per_block, npl) if kind else 0
+        lds_waves = (f"{(LDS_PER_CU // lds) * waves_per_block // 4}" if lds else "-")
+        out.append(f"| `{prefix}` | {what} | {r['VGPRs']} | {r['AGPRs']} | {r['TotalSGPRs']} | "
+                   f"{r['ScratchSize [bytes/lane]']} | {r['VGPRs Spill']} / {r['SGPRs Spill']} | "
+                   f"{r['Occupancy [waves/SIMD]']} | {lds or '-'} | {lds_waves} |")
+    return out
+
+
+def write_resource_profile(path: Path) -> Path:
+    """profiles/kernel_resources_gfx950.md: the register and LDS audit."""
+    usage = resource_usage()
+    lines = ["# Scan kernels on gfx950: registers, scratch, LDS and the occupancy they allow",
+             "", "Made by", "",
+             "    python3 -m mamba_metal_scan_amd.build --resource-usage "
+             "profiles/kernel_resources_gfx950.md", "",
+             "from the compiler's `-Rpass-analysis=kernel-resource-usage` remarks of a "
+             "device-only build of the library's sources (the flags of `build.py`). "
+             "`waves/SIMD (registers)` is the compiler's occupancy from VGPRs, SGPRs and the "
+             "launch bounds; `LDS B/block` is the dynamic LDS the host launches each scan "
+             f"kernel with, and `waves/SIMD (LDS)` what {LDS_PER_CU // 1024} KiB of LDS per CU "
+             "allows for that block size (blocks per CU x waves per block / 4 SIMDs). A kernel "
+             "runs at the smaller of the two, or fewer when its grid is smaller than the GPU: "
+             "at 16x512x1536x16 the forward and backward grids are 768 blocks of 4 waves, 3 per "
+             "SIMD (the resident waves the issue counters measure are in "
+             "`scan_16x512x1536x16.md`).", ""]
+    lines += resource_table(usage)
+    path.write_text("\n".join(lines) + "\n")
+    return path
+
+
 if __name__ == "__main__":
-    print(build_library(verbose=True))
+    if len(sys.argv) == 3 and sys.argv[1] == "--resource-usage":
+        print(write_resource_profile(Path(sys.argv[2])))
+    else:
+        print(build_library(verbose=True))

@@ -41,3 +41,13 @@ def test_algorithmic_bytes():
     assert b["fwd"] == 4 * (3 * 12_582_912 + 2 * 131_072 + 24_576)
     assert abs(b["fwd_bwd"] / 8e12 * 1e6 - 50.76) < 0.01
     assert round(bench.scan_bytes(16, 512, 1432, 16)["fwd_bwd"] / 1e6, 1) == 378.8
+
+
+def test_cpu_baseline_child_records_a_timeout(monkeypatch):
+    """The long-sequence and prefill CPU baselines run in a child process
+    under a wall-clock limit; one that runs out of time is recorded with the
+    reason and no value (here: a 3 s limit on the prefill)."""
+    monkeypatch.setitem(bench.CPU_CHILD_LIMIT_S, "infer", 3)
+    r = bench.cpu_baseline_child("infer")
+    assert r["value"] is None and r["result"] == "timeout after 3 s"
+    assert "32x2048x4096x16 (the full workload)" in r["sample"] and r["kind"] == "port"
