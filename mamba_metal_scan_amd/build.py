@@ -97,7 +97,7 @@ def emit_assembly(out_dir: Path) -> Path:
 # headers (fwd_lds_floats in mhs_fwd.hpp, bwd_lds_floats and
 # bwd_sweep_lds_floats in mhs_bwd.hpp) with the header constants below, which
 # tests/test_build.py reads back from the headers.
-K_CH, K_STEPS, K_BC_PAD, K_SWEEP_MAX = 32, 16, 4, 4
+K_CH, K_STEPS, K_BC_PAD, K_SWEEP_MAX, K_RP_SWAP_PAD = 32, 16, 4, 4, 8
 LDS_PER_CU = 160 * 1024          # gfx950
 VGPRS_PER_SIMD_LANE = 512        # wave64 VGPR file per SIMD lane (gfx950, no AGPR split used)
 
@@ -108,12 +108,19 @@ def _bc_tile_floats(nq: int, npl: int) -> int:
 
 def scan_lds_bytes(kind: str, g: int, npl: int) -> int:
     """Dynamic LDS per block of the scan kernels of plan (NPL, G): "fwd",
-    "bwd" or "bwd_sweep" (the swept backward, checkpoint strides 32-64)."""
+    "bwd" (the gradient kernels), "bwd_carry" (the adjoint-carry pass) or
+    "bwd_sweep" (the swept backward, checkpoint strides 32-64)."""
     if kind == "fwd":
         buf = 2 * K_CH * K_STEPS + 2 * _bc_tile_floats(2 * g, npl) + g * K_CH * K_STEPS
         return 4 * 2 * buf
+    rl = kind != "bwd_carry" and npl == 2   # swapped state pairs (bwd_relabel)
+    rp = kind == "bwd" and npl == 2         # row-partial channel sums (bwd_row_partial)
+    np_ = 2 * g * npl
     buf = 4 * K_CH * K_STEPS + 2 * _bc_tile_floats(2 * g, npl)
-    floats = 2 * buf + g * 64 * K_STEPS + 2 * K_STEPS * 2 * g * npl
+    if rl:
+        buf += 2 * _bc_tile_floats(2 * g, npl) + K_RP_SWAP_PAD
+    sums = 4 * (K_STEPS * (16 if np_ <= 16 else 48) + 4) if rp else 2 * K_STEPS * np_
+    floats = 2 * buf + g * 64 * K_STEPS + sums
     if kind == "bwd_sweep":
         floats += K_SWEEP_MAX * 64 * g * npl
     return 4 * floats
@@ -164,7 +171,7 @@ AUDIT = [
     ("bwd_kernel<2, 4, 3, false, false, 4, true, 4>", "backward, swept strides, atomics",
      "bwd_sweep", 4, 2),
     ("bwd_kernel<2, 4, 3, false, true, 4, false, 0>", "backward carry pass (time segments)",
-     "bwd", 4, 2),
+     "bwd_carry", 4, 2),
     ("bwd_kernel<2, 4, 3, true, false, 4, false, 0>", "gated backward (TinyMamba block)",
      "bwd", 4, 2),
     ("fwd_kernel<1, 8, 4, true, false, 0, 4>", "forward, one state per lane", "fwd", 8, 1),

@@ -121,20 +121,47 @@ struct BwdArgs {
 // strides recompute stride-16 checkpoints in a separate pass.
 constexpr int kSweepMax = 4;
 
-// One staging buffer (the kernel keeps two) and the single-buffered rest.
-__host__ __device__ constexpr int bwd_buf_floats(int G, int NPL) {
-  return 4 * kCH * kSteps               // dt, dy, x, dt*x (channel-major)
-         + 2 * bc_tile_floats(2 * G, NPL);   // B, C tiles
+// Channel sums of the two-state plans' gradient kernels (RL): the lanes of
+// odd channel hold their two states in swapped order, and the dB / dC
+// products are summed over each 16-lane row in registers (row_partial_rs8).
+// Such kernels stage B and C a second time with each state pair swapped (the
+// copies sit kRPSwapPad floats after the C tile, so that the four addresses
+// a read broadcasts, two groups in two orders, fall on distinct banks). The
+// two rows of a half-wave are then added in the finishing step (RP: the
+// kernels without the in-kernel sweep, which keep two row partials per block
+// sum: tile [row][kind][16 steps][rp_step_floats], kind kRPKind apart, the
+// rows 2 kRPKind apart, so that the 32 lanes of a half-wave that write one
+// step pair's partials hit 32 distinct banks), or in registers by one more
+// v_permlane16_swap stage (the swept kernels, whose LDS, with the sweep's
+// state slots, has no room for the partials). Both add the two rows in the
+// same order, so every checkpoint stride gives the same sums.
+constexpr int kRPSwapPad = 8;
+__host__ __device__ constexpr int rp_step_floats(int NP) { return NP <= 16 ? 16 : 48; }
+__host__ __device__ constexpr int rp_kind_floats(int NP) {
+  return kSteps * rp_step_floats(NP) + 4;
 }
-__host__ __device__ constexpr int bwd_lds_floats(int G, int NPL) {
-  return 2 * bwd_buf_floats(G, NPL)
+__host__ __device__ constexpr bool bwd_relabel(int NPL, bool CARRY) { return NPL == 2 && !CARRY; }
+__host__ __device__ constexpr bool bwd_row_partial(int NPL, bool CARRY, int SWEEP) {
+  return bwd_relabel(NPL, CARRY) && SWEEP == 0;
+}
+
+// One staging buffer (the kernel keeps two) and the single-buffered rest.
+__host__ __device__ constexpr int bwd_buf_floats(int G, int NPL, bool rl = false) {
+  return 4 * kCH * kSteps               // dt, dy, x, dt*x (channel-major)
+         + 2 * bc_tile_floats(2 * G, NPL)   // B, C tiles
+         + (rl ? 2 * bc_tile_floats(2 * G, NPL) + kRPSwapPad : 0);   // swapped copies
+}
+__host__ __device__ constexpr int bwd_lds_floats(int G, int NPL, bool rl = false,
+                                                 bool rp = false) {
+  return 2 * bwd_buf_floats(G, NPL, rl)
          + G * 64 * kSteps                       // (s1, s2) per wave
-         + 2 * kSteps * 2 * G * NPL;             // dB, dC block sums of a chunk
+         + (rp ? 4 * rp_kind_floats(2 * G * NPL)  // dB, dC row partials of a chunk
+               : 2 * kSteps * 2 * G * NPL);      // dB, dC block sums of a chunk
 }
 // The swept kernels (SWEEP > 0) keep each lane's swept states in LDS after
 // that: kSweepMax slots of NPL floats per thread, [slot][thread][NPL].
 __host__ __device__ constexpr int bwd_sweep_lds_floats(int G, int NPL) {
-  return bwd_lds_floats(G, NPL) + kSweepMax * 64 * G * NPL;
+  return bwd_lds_floats(G, NPL, bwd_relabel(NPL, false), false) + kSweepMax * 64 * G * NPL;
 }
 
 // GATED: see BwdArgs. The staging threads gate each dt once per block as they
@@ -156,7 +183,9 @@ __global__ void __launch_bounds__(64 * G, MINW)
 bwd_kernel(BwdArgs a) {
   constexpr int NT = 64 * G;
   constexpr int NP = 2 * G * NPL;
-  constexpr int BUF = bwd_buf_floats(G, NPL);
+  constexpr bool RL = bwd_relabel(NPL, CARRY);
+  constexpr bool RP = bwd_row_partial(NPL, CARRY, SWEEP);
+  constexpr int BUF = bwd_buf_floats(G, NPL, RL);
   constexpr int PER = (kCH * kQuads + NT - 1) / NT;
   constexpr int PERS = (kSteps * NP + NT - 1) / NT;
   constexpr int FT = (kSteps / 2 * kCH + NT - 1) / NT;      // dx/ddt tasks per thread
@@ -177,6 +206,9 @@ bwd_kernel(BwdArgs a) {
   const int c = lane & 31;
   const int q = wave * 2 + hh;
   const int n0 = q * NPL;
+  // RL: lanes of odd channel hold their two states in swapped order
+  // (register j holds state n0 + (j ^ sw)); memory layouts are unchanged.
+  const int sw = RL ? (lane & 1) : 0;
   const int b = blockIdx.y % a.batch;
   const int seg = blockIdx.y / a.batch + (CARRY ? a.cunits : 0);   // CARRY: the unit
   const int d0 = blockIdx.x * kCH;
@@ -189,16 +221,42 @@ bwd_kernel(BwdArgs a) {
   const int c_hi = min(c_lo + a.cps, nch);
 
   float* tS = lds + 2 * BUF;                          // [G][64][16]
-  float* tDBC = tS + G * 64 * kSteps;                 // [2][16][NP]
-  // Staging buffer j: dt, dy, x (channel-major), B, C (per lane group).
+  float* tDBC = tS + G * 64 * kSteps;                 // [2][16][NP], RP: [2][2][16][RPS]
+  // Staging buffer j: dt, dy, x (channel-major), B, C (per lane group), and
+  // with RL the swapped copies of B and C.
   constexpr int oDY = kCH * kSteps, oX = 2 * kCH * kSteps, oDTX = 3 * kCH * kSteps,
-                oB = 4 * kCH * kSteps, oC = oB + bc_tile_floats(2 * G, NPL);
+                oB = 4 * kCH * kSteps, oC = oB + bc_tile_floats(2 * G, NPL),
+                oBs = oC + bc_tile_floats(2 * G, NPL) + kRPSwapPad,
+                oCs = oBs + bc_tile_floats(2 * G, NPL);
+  constexpr int RPS = rp_step_floats(NP), RPK = rp_kind_floats(NP);
   // The reduce-scatter leaves lane `lane` with the total of product rs_index:
   // products are numbered kind * 2NPL + slot * NPL + j (kind 0: dB, 1: dC;
-  // slot: step k + slot; j: state n0 + j of this half-wave's group).
+  // slot: step k + slot; j: state n0 + j of this half-wave's group). With RL
+  // it leaves the sum over the lane's 16-lane row (RP), or over its
+  // half-wave, of product (kind (lane >> 3) & 1, slot (lane >> 2) & 1, state
+  // n0 + (lane & 1)).
   const int rs = rs_index<M>(lane);
-  const int rs_kind = rs / (2 * NPL), rs_slot = (rs / NPL) & 1;
-  float* const dbc_out = tDBC + rs_kind * kSteps * NP + rs_slot * NP + n0 + (rs % NPL);
+  const int rs_kind = RL ? (lane >> 3) & 1 : rs / (2 * NPL);
+  const int rs_slot = RL ? (lane >> 2) & 1 : (rs / NPL) & 1;
+  const int rs_n = RL ? (lane & 1) : rs % NPL;
+  float* const dbc_out =
+      RP ? tDBC + ((lane >> 4) & 1) * 2 * RPK + rs_kind * RPK + rs_slot * RPS + n0 + rs_n
+         : tDBC + rs_kind * kSteps * NP + rs_slot * NP + n0 + rs_n;
+  constexpr int kDbcStep = RP ? RPS : NP;   // dbc_out's stride per step
+  // The dB / dC products of a step pair summed as dbc_out holds them.
+  auto channel_sums = [&](const float (&pv)[M]) {
+    if constexpr (RP) {
+      return row_partial_rs8(pv);
+    } else if constexpr (RL) {
+      // the two rows of the half-wave added in registers (row 0's first)
+      const float r = row_partial_rs8(pv);
+      const auto sw16 = __builtin_amdgcn_permlane16_swap(__float_as_uint(r), __float_as_uint(r),
+                                                         false, false);
+      return __uint_as_float(sw16[0]) + __uint_as_float(sw16[1]);
+    } else {
+      return half_wave_reduce_scatter<M>(pv, lane);
+    }
+  };
 
   const size_t slice = (size_t)D * N;
   const unsigned slice_bytes = 4u * (unsigned)slice;
@@ -209,8 +267,9 @@ bwd_kernel(BwdArgs a) {
   float an[NPL], a2[NPL], u[NPL], acc[NPL];
 #pragma unroll
   for (int j = 0; j < NPL; ++j) {
-    an[j] = (act && j < nvalid) ? a.aneg[(size_t)d * N + n0 + j] : 0.f;
-    if constexpr (GATED) an[j] = (act && j < nvalid) ? softplus_f(an[j]) : 0.f;
+    const int nj = j ^ sw;
+    an[j] = (act && nj < nvalid) ? a.aneg[(size_t)d * N + n0 + nj] : 0.f;
+    if constexpr (GATED) an[j] = (act && nj < nvalid) ? softplus_f(an[j]) : 0.f;
     a2[j] = -an[j] * kLog2e;
     acc[j] = 0.f;
     u[j] = 0.f;
@@ -219,11 +278,12 @@ bwd_kernel(BwdArgs a) {
     // The adjoint entering this segment: dh_last for the last one, folded
     // with the carries of the later segments for the others.
     const float* dhl = a.dh_last != nullptr ? a.dh_last + (size_t)b * slice : a.aneg;
-    load_states<NPL>(u, GBuf(dhl, a.dh_last != nullptr ? slice_bytes : 0u), st_lane, nvalid);
+    load_states<NPL>(u, GBuf(dhl, a.dh_last != nullptr ? slice_bytes : 0u), st_lane, nvalid,
+                     sw);
     for (int s2 = a.nunits - 1; s2 >= (seg + 1) * a.cunits; --s2) {
       float lv[NPL];
       const size_t slot = (size_t)s2 * a.batch + b;
-      load_states<NPL>(lv, GBuf(a.carryL + slot * slice, slice_bytes), st_lane, nvalid);
+      load_states<NPL>(lv, GBuf(a.carryL + slot * slice, slice_bytes), st_lane, nvalid, sw);
       const float sdt = act ? a.carrySdt[slot * D + d] : 0.f;
 #pragma unroll
       for (int j = 0; j < NPL; ++j) u[j] = __builtin_fmaf(exp2_hw(sdt * a2[j]), u[j], lv[j]);
@@ -306,7 +366,7 @@ bwd_kernel(BwdArgs a) {
   const float* ck_row = a.ckpt + ((size_t)b * nch - 1) * slice;
   auto load_h0 = [&](int ci) {
     load_states<NPL>(ph, GBuf(ck_row + (ptrdiff_t)ci * (ptrdiff_t)slice, ci > 0 ? slice_bytes : 0u),
-                     st_lane, nvalid);
+                     st_lane, nvalid, sw);
   };
   const float* ck_next = ck_row + (ptrdiff_t)(c_hi - 3) * (ptrdiff_t)slice;
   int ck_i = c_hi - 3;
@@ -319,6 +379,10 @@ bwd_kernel(BwdArgs a) {
     if constexpr (!CARRY) ql.store_cm_product(s0 + oDTX, pd, px);   // dt * x, once per block
     if constexpr (!CARRY) rl.store(s0 + oB, pb);
     rl.store(s0 + oC, pc);
+    if constexpr (RL) {
+      rl.store_swapped(s0 + oBs, pb);
+      rl.store_swapped(s0 + oCs, pc);
+    }
   };
   // The fp32 rows of the dB / dC block sums of chunk ci: this block's
   // partials (rows of N), or with ATOM the gradients themselves (rows ld_dbc
@@ -384,12 +448,22 @@ bwd_kernel(BwdArgs a) {
       const int r = okr ? r0 : 0;
       const int k = r / NP, n = r % NP;
       const unsigned o = okr && n < N ? 4u * (unsigned)(k * ldr + n) : kOOB;
-      if constexpr (ATOM) {
-        gbs.atomic_add(tDBC[r], o);
-        gcs.atomic_add(tDBC[kSteps * NP + r], o);
+      float vb, vc;
+      if constexpr (RP) {
+        // the two rows' partials of the half-wave, added in a fixed order
+        const int rr = k * RPS + n;
+        vb = tDBC[rr] + tDBC[2 * RPK + rr];
+        vc = tDBC[RPK + rr] + tDBC[3 * RPK + rr];
       } else {
-        gbs.st<kStream>(tDBC[r], o);
-        gcs.st<kStream>(tDBC[kSteps * NP + r], o);
+        vb = tDBC[r];
+        vc = tDBC[kSteps * NP + r];
+      }
+      if constexpr (ATOM) {
+        gbs.atomic_add(vb, o);
+        gcs.atomic_add(vc, o);
+      } else {
+        gbs.st<kStream>(vb, o);
+        gcs.st<kStream>(vc, o);
       }
     }
   };
@@ -456,7 +530,7 @@ bwd_kernel(BwdArgs a) {
     const float* ckc = a.ckpt + ((size_t)b * a.ck_nchunk - 1) * slice;
     auto load_h0c = [&](int cc) {
       load_states<NPL>(ph, GBuf(ckc + (ptrdiff_t)cc * (ptrdiff_t)slice, cc > 0 ? slice_bytes : 0u),
-                       st_lane, nvalid);
+                       st_lane, nvalid, sw);
     };
     auto load_item = [&](const Item& it) {
       const int cy = it.sweep ? -1 : it.ci;
@@ -470,7 +544,7 @@ bwd_kernel(BwdArgs a) {
     // this thread's LDS slot l (lanes contiguous: conflict-free 32 / 64 /
     // 128-bit accesses); registers are what the walk is short of.
     static_assert(SWEEP <= kSweepMax, "LDS slots for the swept states");
-    float* const tH = lds + bwd_lds_floats(G, NPL) + tid * NPL;
+    float* const tH = lds + bwd_lds_floats(G, NPL, RL, RP) + tid * NPL;
     auto h_slot = [&](int l) { return tH + l * NT * NPL; };
     Pos pos{cc_top, 0, n_top, cc_top == cc_lo ? lo_first : 0};
     const Item it0 = item_at(pos);
@@ -488,8 +562,8 @@ bwd_kernel(BwdArgs a) {
       const Pos pos1 = advance(pos);
       const Item it1 = item_at(pos1), it2 = item_at(advance(pos1));
       const float* s0 = lds + (k & 1) * BUF;
-      const float* gB = s0 + oB + q * bc_group_floats(NPL);
-      const float* gC = s0 + oC + q * bc_group_floats(NPL);
+      const float* gB = s0 + (sw ? oBs : oB) + q * bc_group_floats(NPL);
+      const float* gC = s0 + (sw ? oCs : oC) + q * bc_group_floats(NPL);
       if (it.first) {
         float h0[NPL];
 #pragma unroll
@@ -572,7 +646,7 @@ bwd_kernel(BwdArgs a) {
             pv[slot * NPL + j] = gk[j] * dtxs[s];
             pv[2 * NPL + slot * NPL + j] = hs[kk][j] * dys[s];
           }
-          if (slot == 0) *(dbc_out + kk * NP) = half_wave_reduce_scatter<M>(pv, lane);
+          if (slot == 0) *(dbc_out + kk * kDbcStep) = channel_sums(pv);
         }
         float o[4];
 #pragma unroll
@@ -612,8 +686,9 @@ bwd_kernel(BwdArgs a) {
       prio.step(i);
       const int ci = c_hi - 1 - i;
       const float* s0 = lds + (i & 1) * BUF;
-      const float* gB = s0 + oB + q * bc_group_floats(NPL);
-      const float* gC = s0 + oC + q * bc_group_floats(NPL);
+      // RP: the lanes holding their states swapped read the swapped copies.
+      const float* gB = s0 + (sw ? oBs : oB) + q * bc_group_floats(NPL);
+      const float* gC = s0 + (sw ? oCs : oC) + q * bc_group_floats(NPL);
 
       if constexpr (CARRY) {
         // The adjoint alone: G_t = dy_t C_t + dA_{t+1} G_{t+1}, dA formed on
@@ -697,7 +772,7 @@ bwd_kernel(BwdArgs a) {
             pv[slot * NPL + j] = gk[j] * dtxs[s];             // dB: G * dt * x
             pv[2 * NPL + slot * NPL + j] = hs[k][j] * dys[s];   // dC: h * dy
           }
-          if (slot == 0) *(dbc_out + k * NP) = half_wave_reduce_scatter<M>(pv, lane);
+          if (slot == 0) *(dbc_out + k * kDbcStep) = channel_sums(pv);
         }
         // Add the two half-waves: lanes 0-31 end with s1, lanes 32-63 with s2.
         float o[4];
@@ -723,7 +798,8 @@ bwd_kernel(BwdArgs a) {
       // store still in flight: a full memory drain per chunk.
 #pragma unroll
       for (int j = 0; j < NPL; ++j) hc[j] = opaque_copy(ph[j]);
-      load_states<NPL>(ph, GBuf(ck_next, ck_i > 0 ? slice_bytes : 0u), st_lane, nvalid);   // h0(ci-2)
+      load_states<NPL>(ph, GBuf(ck_next, ck_i > 0 ? slice_bytes : 0u), st_lane, nvalid,
+                       sw);   // h0(ci-2)
       ck_next -= slice;
       --ck_i;
       load_down();
@@ -738,7 +814,7 @@ bwd_kernel(BwdArgs a) {
   const size_t slot = (size_t)seg * a.batch + b;
   if constexpr (CARRY) {
     // L_s = dA_a * G_a, a the segment's first step: u after the walk.
-    store_states<NPL>(GBuf(a.carryL + slot * slice, slice_bytes), st_lane, nvalid, u);
+    store_states<NPL>(GBuf(a.carryL + slot * slice, slice_bytes), st_lane, nvalid, u, sw);
     if (q == 0 && act) a.carrySdt[slot * D + d] = sdt_acc;
     return;
   }
@@ -753,13 +829,14 @@ bwd_kernel(BwdArgs a) {
     const GBuf gda(a.daneg, slice_bytes);
 #pragma unroll
     for (int j = 0; j < NPL; ++j) {
+      const int nj = j ^ sw;
       float v = out[j];
       if constexpr (GATED)
-        v *= (act && j < nvalid) ? sigmoid_f(a.aneg[(size_t)d * N + n0 + j]) : 0.f;
-      gda.atomic_add(v, (st_lane != kOOB && j < nvalid) ? st_lane + 4u * j : kOOB);
+        v *= (act && nj < nvalid) ? sigmoid_f(a.aneg[(size_t)d * N + n0 + nj]) : 0.f;
+      gda.atomic_add(v, (st_lane != kOOB && nj < nvalid) ? st_lane + 4u * nj : kOOB);
     }
   } else {
-    store_states<NPL>(GBuf(a.wsA + slot * slice, slice_bytes), st_lane, nvalid, out);
+    store_states<NPL>(GBuf(a.wsA + slot * slice, slice_bytes), st_lane, nvalid, out, sw);
   }
   if constexpr (GATED) {
     if (ATOM ? a.dbias != nullptr : a.wsDB != nullptr) {

@@ -214,7 +214,8 @@ struct Plan {
   Kernels k[2];     // by Elem
   int fwd_lds = 0;  // bytes
   int bwd_ki = 0;   // largest chunk the backward walks directly
-  int bwd_lds = 0;  // bytes
+  int bwd_lds = 0;  // bytes, the gradient kernels
+  int bwd_carry_lds = 0;  // bytes, the adjoint-carry kernels
   int bwd_sw_lds = 0;  // bytes, the swept kernels
 };
 
@@ -251,7 +252,10 @@ void fill(Plan& p) {
   fill_elem<NPL, G, MINW, 4>(p.k[kF32]);
   fill_elem<NPL, G, MINW, 2>(p.k[kBF16]);
   p.fwd_lds = mhs::fwd_lds_floats(G, NPL) * 4;
-  p.bwd_lds = mhs::bwd_lds_floats(G, NPL) * 4;
+  p.bwd_lds = mhs::bwd_lds_floats(G, NPL, mhs::bwd_relabel(NPL, false),
+                                   mhs::bwd_row_partial(NPL, false, 0)) * 4;
+  p.bwd_carry_lds = mhs::bwd_lds_floats(G, NPL, mhs::bwd_relabel(NPL, true),
+                                         mhs::bwd_row_partial(NPL, true, 0)) * 4;
   p.bwd_sw_lds = mhs::bwd_sweep_lds_floats(G, NPL) * 4;
 }
 
@@ -711,12 +715,12 @@ int scan_bwd(const void* x, const void* dt, const float* aneg, const void* B, co
     // Adjoint carries of the units of segments 1..nseg-1 (segment 0 passes
     // nothing on): one block per unit.
     const BwdFn cfn = g.on ? p.k[e].carry_g : p.k[e].carry;
-    rc = ensure_lds(reinterpret_cast<const void*>(cfn), p.bwd_lds);
+    rc = ensure_lds(reinterpret_cast<const void*>(cfn), p.bwd_carry_lds);
     if (rc) return rc;
     mhs::BwdArgs c = a;
     c.cps = w.sg.ups;
     hipLaunchKernelGGL(cfn, dim3(nblk, (unsigned)(batch * (w.sg.nunits - w.sg.cunits))),
-                       dim3(64 * p.G), p.bwd_lds, s, c);
+                       dim3(64 * p.G), p.bwd_carry_lds, s, c);
     rc = check_launch("backward carry kernel");
     if (rc) return rc;
   }

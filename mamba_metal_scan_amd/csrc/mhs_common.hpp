@@ -134,6 +134,49 @@ __device__ __forceinline__ void rs_bits32_16(const float (&a)[8], float (&c)[2])
         "v"(a[7]));
 }
 
+// The stages over lane bits 3 and 2 of the row-partial reduce-scatter of 8
+// values per lane (see row_partial_rs8): a = (x0, x1, y0, y1). Bit 3 by
+// bank-masked row_ror:8 adds (pairs (x0, y0) and (x1, y1): x in the banks
+// whose bit 3 is 0, y in the others), then bit 2 by bank-masked row shifts
+// (partner lane i ^ 4: row_shl:4, lane i reads lane i + 4, in banks 0 and
+// 2; row_shr:4, lane i reads lane i - 4, in banks 1 and 3): the first
+// result in the banks whose bit 2 is 0, the second in the others. Wait
+// states as in rs_bits32_8.
+__device__ __forceinline__ float rs_bits32_shift(const float (&a)[4]) {
+  float b0, b1, c;
+  asm("s_nop 1\n\t"
+      "v_add_f32_dpp %1, %3, %3 row_ror:8 row_mask:0xf bank_mask:0x3\n\t"
+      "v_add_f32_dpp %1, %5, %5 row_ror:8 row_mask:0xf bank_mask:0xc\n\t"
+      "v_add_f32_dpp %2, %4, %4 row_ror:8 row_mask:0xf bank_mask:0x3\n\t"
+      "v_add_f32_dpp %2, %6, %6 row_ror:8 row_mask:0xf bank_mask:0xc\n\t"
+      "s_nop 0\n\t"
+      "v_add_f32_dpp %0, %1, %1 row_shl:4 row_mask:0xf bank_mask:0x5\n\t"
+      "v_add_f32_dpp %0, %2, %2 row_shr:4 row_mask:0xf bank_mask:0xa\n\t"
+      "s_nop 1"
+      : "=&v"(c), "=&v"(b0), "=&v"(b1)
+      : "v"(a[0]), "v"(a[1]), "v"(a[2]), "v"(a[3]));
+  return c;
+}
+
+// Partial sums over each 16-lane row of 8 values per lane, with the lanes of
+// odd index holding their two states in swapped order (the lane's register
+// j holds state j ^ (lane & 1)). v[kind * 4 + slot * 2 + j]: kind 0 / 1,
+// slot 0 / 1 (two steps), j the register of the state. Stage over lane bit
+// 0 (quad_perm [1, 0, 3, 2]): v[.. + 0] + the partner's v[.. + 1] is the
+// pair sum of one state, state n0 + (lane & 1), in every lane, so one DPP add
+// per pair; then bit 3 (kind) and bit 2 (slot) as bank-masked stages, and
+// bit 1 (quad_perm [2, 3, 0, 1]) as a plain add: 11 instructions. Lane l
+// returns the sum over the 16 lanes of its row of the value (kind (l >> 3)
+// & 1, slot (l >> 2) & 1, state n0 + (l & 1)); the two rows of a half-wave
+// (lane bit 4) are added later, in a fixed order.
+__device__ __forceinline__ float row_partial_rs8(const float (&v)[8]) {
+  float a[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) a[i] = v[2 * i] + dpp_get<kDppXor1>(v[2 * i + 1]);
+  // a = (kind 0 slot 0, kind 0 slot 1, kind 1 slot 0, kind 1 slot 1)
+  return dpp_add<kDppXor2>(rs_bits32_shift(a));
+}
+
 // The stage over lane bit 3 alone, for a pair: (x, y) becomes x + x' in the
 // banks whose bit 3 is 0 and y + y' in the others (as in rs_bits32_8).
 __device__ __forceinline__ float rs_bit3_4(const float (&a)[2]) {
@@ -440,20 +483,26 @@ struct StreamCursor {
 };
 
 // NPL consecutive states of one lane at byte offset `off` (kOOB: none);
-// states at or beyond `nvalid` are padding and are not stored.
+// states at or beyond `nvalid` are padding and are not stored. Register j
+// holds state j ^ sw of the lane's group (sw: 0, or 1 for a lane that keeps
+// its two states in swapped order; see the backward's channel sums).
 template <int NPL, int POL = 0>
 __device__ __forceinline__ void store_states(const GBuf& g, unsigned off, int nvalid,
-                                             const float (&v)[NPL]) {
+                                             const float (&v)[NPL], int sw = 0) {
 #pragma unroll
-  for (int j = 0; j < NPL; ++j)
-    g.st<POL>(v[j], (off != kOOB && j < nvalid) ? off + 4u * j : kOOB);
+  for (int j = 0; j < NPL; ++j) {
+    const int n = j ^ sw;
+    g.st<POL>(v[j], (off != kOOB && n < nvalid) ? off + 4u * n : kOOB);
+  }
 }
 template <int NPL, int POL = 0>
 __device__ __forceinline__ void load_states(float (&v)[NPL], const GBuf& g, unsigned off,
-                                            int nvalid) {
+                                            int nvalid, int sw = 0) {
 #pragma unroll
-  for (int j = 0; j < NPL; ++j)
-    v[j] = g.ld<POL>((off != kOOB && j < nvalid) ? off + 4u * j : kOOB);
+  for (int j = 0; j < NPL; ++j) {
+    const int n = j ^ sw;
+    v[j] = g.ld<POL>((off != kOOB && n < nvalid) ? off + 4u * n : kOOB);
+  }
 }
 
 __device__ __forceinline__ void sts4(float* p, float4 v) { *reinterpret_cast<float4*>(p) = v; }
@@ -629,6 +678,16 @@ struct RowLoader {
       const bool in_tile = e < kSteps * NP;
       src[i] = (in_tile && n < N) ? (unsigned)ES * (unsigned)(k * ld + n) : kOOB;
       dst[i] = in_tile ? (n / NPL) * bc_group_floats(NPL) + k * NPL + (n % NPL) : -1;
+    }
+  }
+  // The same tile with each group's NPL = 2 states of a step in swapped
+  // order (the copy that lanes holding their states swapped read).
+  __device__ __forceinline__ void store_swapped(float* tile, const float (&v)[PERS]) const {
+    static_assert(NPL == 2, "state pairs");
+#pragma unroll
+    for (int i = 0; i < PERS; ++i) {
+      if (valid(i)) tile[dst[i] ^ 1] = v[i];
+      asm volatile("" ::"v"(v[i]));
     }
   }
   __device__ __forceinline__ void load(float (&v)[PERS], const GBuf& g) const {

@@ -34,9 +34,12 @@ class RMSNormHIP(torch.autograd.Function):
         shape = x.shape
         x2 = x.reshape(-1, shape[-1]).contiguous()
         w = weight.contiguous()
-        # dispatch() skips the op's own checks: weight's device, dtype, shape
-        # and alignment are checked here, before any launch.
-        _native._check_norm("rms_norm", x2, w)
+        # In eager mode dispatch() calls the op's plain implementation, which
+        # skips the op's own checks: weight's device, dtype, shape and
+        # alignment are checked here, before any launch (under torch.compile
+        # the registered op checks them itself).
+        if not torch.compiler.is_compiling():
+            _native._check_norm("rms_norm", x2, w)
         y, rstd = dispatch("rmsnorm_fwd")(x2, w, float(eps))
         ctx.save_for_backward(x2, w, rstd)
         ctx.shape = shape
@@ -74,7 +77,8 @@ class AddRMSNormHIP(torch.autograd.Function):
         w = weight.contiguous()
         x2 = x.reshape(-1, cols).contiguous()
         d2 = delta.reshape(-1, cols).contiguous()
-        _native._check_norm("add_rms_norm", x2, w, delta=d2)   # as in RMSNormHIP.forward
+        if not torch.compiler.is_compiling():   # as in RMSNormHIP.forward
+            _native._check_norm("add_rms_norm", x2, w, delta=d2)
         x_out, y, rstd = dispatch("add_rmsnorm_fwd")(x2, d2, w, float(eps))
         ctx.save_for_backward(x_out, w, rstd)
         ctx.shape = shape
