@@ -111,7 +111,9 @@ def scan_lds_bytes(kind: str, g: int, npl: int) -> int:
     "bwd" (the gradient kernels), "bwd_carry" (the adjoint-carry pass) or
     "bwd_sweep" (the swept backward, checkpoint strides 32-64)."""
     if kind == "fwd":
-        buf = 2 * K_CH * K_STEPS + 2 * _bc_tile_floats(2 * g, npl) + g * K_CH * K_STEPS
+        # two states per lane: the broadcast tile (fwd_bc_floats, kBCGroup2 = 80)
+        bc = 2 * g * 80 if npl == 2 else 2 * _bc_tile_floats(2 * g, npl)
+        buf = 2 * K_CH * K_STEPS + bc + g * K_CH * K_STEPS
         return 4 * 2 * buf
     rl = kind != "bwd_carry" and npl == 2   # swapped state pairs (bwd_relabel)
     rp = kind == "bwd" and npl == 2         # row-partial channel sums (bwd_row_partial)

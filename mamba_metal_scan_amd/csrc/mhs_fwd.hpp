@@ -77,11 +77,101 @@ struct FwdArgs {
 
 constexpr int kCH = 32;   // channels per block
 
+// Two states per lane (NPL 2): B and C reach the lanes by DPP row broadcasts.
+// Per state group q and quad m the tile holds the 16 values [kind][step][j]
+// (kind 0: B, 1: C; 4 steps; the group's 2 states), one per lane of a 16-lane
+// row: each lane reads one float per quad, and the multiply (B) and the fma
+// (C) that use a value broadcast it from its lane with row_newbcast. Groups
+// are kBCGroup2 floats apart (16 banks): the two half-waves' groups fall on
+// disjoint banks, and the two rows of a half-wave read the same 16 floats.
+constexpr int kBCGroup2 = kQuads * 16 + 16;
+__host__ __device__ constexpr int fwd_bc_floats(int G, int NPL) {
+  return NPL == 2 ? 2 * G * kBCGroup2 : 2 * bc_tile_floats(2 * G, NPL);
+}
+
 // One pipeline buffer (the kernel keeps two).
 __host__ __device__ constexpr int fwd_buf_floats(int G, int NPL) {
   return 2 * kCH * kSteps               // dt, dt*x tiles (channel-major)
-         + 2 * bc_tile_floats(2 * G, NPL)   // B, C tiles
+         + fwd_bc_floats(G, NPL)        // B, C tiles
          + G * kCH * kSteps;            // per-wave y partials (both half-waves added)
+}
+
+// Staging of 16 rows of B and C (fp32 or bf16, rows ld apart) into the
+// broadcast tile of the two-state plans (see kBCGroup2): thread tid moves
+// tile elements tid, tid + nthreads, ... (PERS of them), state fastest, of
+// both B and C. Padded states and steps past T are zero.
+template <int PERS, int ES = 4>
+struct BCRowLoader {
+  unsigned src[PERS];  // byte offset in the sub-chunk's global [16][ld] block, or kOOB
+  int dst[PERS];       // B's slot in the tile (C's is 8 further), or -1
+  int tid, nthreads, ntile;
+  int w0;
+  __device__ __forceinline__ BCRowLoader(int tid_, int nthreads_, int N, int NP, int ld)
+      : tid(tid_), nthreads(nthreads_), ntile(kSteps * NP),
+        w0(__builtin_amdgcn_readfirstlane(tid_) & ~63) {
+#pragma unroll
+    for (int i = 0; i < PERS; ++i) {
+      const int e = tid + i * nthreads;       // tile element (k, n), n fastest
+      const int k = e / NP, n = e % NP;
+      const bool in_tile = e < kSteps * NP;
+      src[i] = (in_tile && n < N) ? (unsigned)ES * (unsigned)(k * ld + n) : kOOB;
+      dst[i] = in_tile ? (n / 2) * kBCGroup2 + (k / 4) * 16 + (k % 4) * 2 + (n % 2) : -1;
+    }
+  }
+  __device__ __forceinline__ void load(float (&v)[PERS], const GBuf& g) const {
+#pragma unroll
+    for (int i = 0; i < PERS; ++i) v[i] = ld_elem<ES>(g, src[i]);
+  }
+  __device__ __forceinline__ bool valid(int i) const {
+    if ((i + 1) * nthreads <= ntile) return true;
+    if (ntile % 64 == 0) return w0 + i * nthreads < ntile;
+    return dst[i] >= 0;
+  }
+  // kind 0 (B) or 1 (C)
+  __device__ __forceinline__ void store(float* tile, const float (&v)[PERS], int kind) const {
+#pragma unroll
+    for (int i = 0; i < PERS; ++i) {
+      if (valid(i)) tile[dst[i] + 8 * kind] = v[i];
+      asm volatile("" ::"v"(v[i]));
+    }
+  }
+};
+
+// u[s][j] = B * bx[s] for the quad's 4 steps and 2 states, B broadcast from
+// lane 2s + j of the row's value r (read from the broadcast tile). The
+// leading s_nop gives the 2 wait states a DPP read of r needs should r have
+// been written by a VALU instruction just before.
+__device__ __forceinline__ void bcast_mul_b(float (&u)[4][2], float r, const float (&bx)[4]) {
+  asm("s_nop 1\n\t"
+      "v_mul_f32_dpp %0, %8, %9 row_newbcast:0 row_mask:0xf bank_mask:0xf\n\t"
+      "v_mul_f32_dpp %1, %8, %9 row_newbcast:1 row_mask:0xf bank_mask:0xf\n\t"
+      "v_mul_f32_dpp %2, %8, %10 row_newbcast:2 row_mask:0xf bank_mask:0xf\n\t"
+      "v_mul_f32_dpp %3, %8, %10 row_newbcast:3 row_mask:0xf bank_mask:0xf\n\t"
+      "v_mul_f32_dpp %4, %8, %11 row_newbcast:4 row_mask:0xf bank_mask:0xf\n\t"
+      "v_mul_f32_dpp %5, %8, %11 row_newbcast:5 row_mask:0xf bank_mask:0xf\n\t"
+      "v_mul_f32_dpp %6, %8, %12 row_newbcast:6 row_mask:0xf bank_mask:0xf\n\t"
+      "v_mul_f32_dpp %7, %8, %12 row_newbcast:7 row_mask:0xf bank_mask:0xf"
+      : "=&v"(u[0][0]), "=&v"(u[0][1]), "=&v"(u[1][0]), "=&v"(u[1][1]), "=&v"(u[2][0]),
+        "=&v"(u[2][1]), "=&v"(u[3][0]), "=&v"(u[3][1])
+      : "v"(r), "v"(bx[0]), "v"(bx[1]), "v"(bx[2]), "v"(bx[3]));
+}
+// y[s] = C_0 h[s][0] + C_1 h[s][1] (as fma(C_1, h_1, C_0 h_0)), C_j broadcast
+// from lane 8 + 2s + j of r. The trailing s_nop covers DPP or permlane reads
+// of y by the compiled code that follows.
+__device__ __forceinline__ void bcast_dot_c(float (&y)[4], float r, const float (&h)[4][2]) {
+  asm("s_nop 1\n\t"
+      "v_mul_f32_dpp %0, %4, %5 row_newbcast:8 row_mask:0xf bank_mask:0xf\n\t"
+      "v_mul_f32_dpp %1, %4, %7 row_newbcast:10 row_mask:0xf bank_mask:0xf\n\t"
+      "v_mul_f32_dpp %2, %4, %9 row_newbcast:12 row_mask:0xf bank_mask:0xf\n\t"
+      "v_mul_f32_dpp %3, %4, %11 row_newbcast:14 row_mask:0xf bank_mask:0xf\n\t"
+      "v_fmac_f32_dpp %0, %4, %6 row_newbcast:9 row_mask:0xf bank_mask:0xf\n\t"
+      "v_fmac_f32_dpp %1, %4, %8 row_newbcast:11 row_mask:0xf bank_mask:0xf\n\t"
+      "v_fmac_f32_dpp %2, %4, %10 row_newbcast:13 row_mask:0xf bank_mask:0xf\n\t"
+      "v_fmac_f32_dpp %3, %4, %12 row_newbcast:15 row_mask:0xf bank_mask:0xf\n\t"
+      "s_nop 1"
+      : "=&v"(y[0]), "=&v"(y[1]), "=&v"(y[2]), "=&v"(y[3])
+      : "v"(r), "v"(h[0][0]), "v"(h[0][1]), "v"(h[1][0]), "v"(h[1][1]), "v"(h[2][0]),
+        "v"(h[2][1]), "v"(h[3][0]), "v"(h[3][1]));
 }
 __host__ __device__ constexpr int fwd_lds_floats(int G, int NPL) {
   return 2 * fwd_buf_floats(G, NPL);
@@ -109,7 +199,9 @@ fwd_kernel(FwdArgs a) {
   constexpr int NT = 64 * G;                    // threads
   constexpr int NP = 2 * G * NPL;               // padded states
   constexpr int BUF = fwd_buf_floats(G, NPL);
-  constexpr int TILE = bc_tile_floats(2 * G, NPL);   // one B or C tile
+  constexpr int TILE = bc_tile_floats(2 * G, NPL);   // one B or C tile (NPL 1, 4)
+  constexpr int BCF = fwd_bc_floats(G, NPL);         // the B and C tiles
+  constexpr bool BCAST = NPL == 2;                   // B, C by DPP row broadcasts
   constexpr int PER = (kCH * kQuads + NT - 1) / NT;
   constexpr int PERS = (kSteps * NP + NT - 1) / NT;
   extern __shared__ float lds[];
@@ -147,6 +239,7 @@ fwd_kernel(FwdArgs a) {
   const QuadLoader<kCH, PER, ES> ql(tid, NT, D, d0, D);
   const QuadLoader<kCH, PER, ES> qdt(tid, NT, D, d0, ld_dt);
   const RowLoader<PERS, NPL, ES> rl(tid, NT, N, NP, ld_bc);
+  const BCRowLoader<PERS, ES> rlb(tid, NT, N, NP, ld_bc);
   float4 px[PER], pd[PER];
   float pb[PERS], pc[PERS];
   float gbias[PER];   // GATED: the dt bias of each staging task's channel
@@ -175,8 +268,13 @@ fwd_kernel(FwdArgs a) {
     if constexpr (GATED) qdt.gate(pd, sub_len(i), a.dt_lo, a.dt_span, gbias);
     ql.store_cm(buf, pd);
     ql.store_cm_product(buf + kCH * kSteps, pd, px);
-    rl.store(buf + 2 * kCH * kSteps, pb);
-    if constexpr (!NOY) rl.store(buf + 2 * kCH * kSteps + TILE, pc);
+    if constexpr (BCAST) {
+      rlb.store(buf + 2 * kCH * kSteps, pb, 0);
+      if constexpr (!NOY) rlb.store(buf + 2 * kCH * kSteps, pc, 1);
+    } else {
+      rl.store(buf + 2 * kCH * kSteps, pb);
+      if constexpr (!NOY) rl.store(buf + 2 * kCH * kSteps + TILE, pc);
+    }
   };
   // y of sub-chunk i: every wave leaves, per channel and step, the sum over
   // its two half-waves (added in registers), in a step-pair-major tile
@@ -190,7 +288,7 @@ fwd_kernel(FwdArgs a) {
   constexpr int YT = (YTASKS + NT - 1) / NT;             // y tasks per thread
   float2 ypart[YT][G];
   auto y_read = [&](int i) {
-    const float* yp = lds + (i & 1) * BUF + 2 * kCH * kSteps + 2 * TILE;
+    const float* yp = lds + (i & 1) * BUF + 2 * kCH * kSteps + BCF;
 #pragma unroll
     for (int f = 0; f < YT; ++f) {
       const int t0 = tid + f * NT;
@@ -266,17 +364,24 @@ fwd_kernel(FwdArgs a) {
     const float* cBX = buf + kCH * kSteps;
     const float* gB = buf + 2 * kCH * kSteps + q * bc_group_floats(NPL);
     const float* gC = buf + 2 * kCH * kSteps + TILE + q * bc_group_floats(NPL);
-    float* myY = lds + (i & 1) * BUF + 2 * kCH * kSteps + 2 * TILE + wave * kCH * kSteps;
+    // BCAST: this lane's value of its group's broadcast tile
+    const float* gBC = buf + 2 * kCH * kSteps + q * kBCGroup2 + (lane & 15);
+    float* myY = lds + (i & 1) * BUF + 2 * kCH * kSteps + BCF + wave * kCH * kSteps;
 
     // A quad's LDS operands, read one quad ahead of their use.
     float4 qdt, qbx, qB[NPL], qC[NPL];
+    float qr;   // BCAST: B and C of the quad, one value per lane
     auto read_quad = [&](int m) {
       qdt = lds4(cDT + cm_quad(c, m));
       qbx = lds4(cBX + cm_quad(c, m));
+      if constexpr (BCAST) {
+        qr = gBC[16 * m];
+      } else {
 #pragma unroll
-      for (int j = 0; j < NPL; ++j) {
-        qB[j] = lds4(gB + 4 * m * NPL + 4 * j);
-        if constexpr (!NOY) qC[j] = lds4(gC + 4 * m * NPL + 4 * j);
+        for (int j = 0; j < NPL; ++j) {
+          qB[j] = lds4(gB + 4 * m * NPL + 4 * j);
+          if constexpr (!NOY) qC[j] = lds4(gC + 4 * m * NPL + 4 * j);
+        }
       }
     };
     read_quad(0);
@@ -288,12 +393,17 @@ fwd_kernel(FwdArgs a) {
       float dts[4], bxs[4], Bq[4][NPL], Cq[4][NPL];
       f4_to(dts, qdt);
       f4_to(bxs, qbx);
+      float r = 0.f;
+      if constexpr (BCAST) {
+        r = qr;
+      } else {
 #pragma unroll
-      for (int e = 0; e < 4 * NPL; ++e) {
-        const float4 tb = qB[e / 4], tc = NOY ? tb : qC[e / 4];
-        const float vb[4] = {tb.x, tb.y, tb.z, tb.w}, vc[4] = {tc.x, tc.y, tc.z, tc.w};
-        Bq[e / NPL][e % NPL] = vb[e % 4];
-        Cq[e / NPL][e % NPL] = vc[e % 4];
+        for (int e = 0; e < 4 * NPL; ++e) {
+          const float4 tb = qB[e / 4], tc = NOY ? tb : qC[e / 4];
+          const float vb[4] = {tb.x, tb.y, tb.z, tb.w}, vc[4] = {tc.x, tc.y, tc.z, tc.w};
+          Bq[e / NPL][e % NPL] = vb[e % 4];
+          Cq[e / NPL][e % NPL] = vc[e % 4];
+        }
       }
       if (m + 1 < kQuads) read_quad(m + 1);
       float da[4][NPL], u[4][NPL];
@@ -303,9 +413,10 @@ fwd_kernel(FwdArgs a) {
 #pragma unroll
         for (int j = 0; j < NPL; ++j) {
           da[s][j] = exp2_hw(dts[s] * a2[j]);
-          u[s][j] = Bq[s][j] * bxs[s];
+          if constexpr (!BCAST) u[s][j] = Bq[s][j] * bxs[s];
         }
       }
+      if constexpr (BCAST) bcast_mul_b(u, r, bxs);
       float yq[4], hq[4][NPL];
 #pragma unroll
       for (int s = 0; s < 4; ++s) {
@@ -313,11 +424,12 @@ fwd_kernel(FwdArgs a) {
 #pragma unroll
         for (int j = 0; j < NPL; ++j) {
           h[j] = __builtin_fmaf(da[s][j], h[j], u[s][j]);
-          if constexpr (!NOY) acc = __builtin_fmaf(Cq[s][j], h[j], acc);
+          if constexpr (!NOY && !BCAST) acc = __builtin_fmaf(Cq[s][j], h[j], acc);
           hq[s][j] = h[j];
         }
         yq[s] = acc;
       }
+      if constexpr (!NOY && BCAST) bcast_dot_c(yq, r, hq);
       if constexpr (!NOY) {
         // Add the two half-waves (same channels, different states): lanes
         // 0-31 end with steps 0, 1 of the quad, lanes 32-63 with steps 2, 3.

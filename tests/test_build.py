@@ -26,14 +26,17 @@ def test_audit_constants_match_the_headers():
     assert build.K_BC_PAD == _constant("mhs_common.hpp", "kBCPad")
     assert build.K_SWEEP_MAX == _constant("mhs_bwd.hpp", "kSweepMax")
     assert build.K_RP_SWAP_PAD == _constant("mhs_bwd.hpp", "kRPSwapPad")
+    m = re.search(r"constexpr int kBCGroup2 = kQuads \* 16 \+ 16;", (CSRC / "mhs_fwd.hpp").read_text())
+    assert m and _constant("mhs_common.hpp", "kQuads") * 16 + 16 == 80
 
 
 def test_lds_sizes_of_the_training_plan():
-    """d_state 16 (NPL 2, G 4): forward 29,184 B; backward 46,208 B with the
+    """d_state 16 (NPL 2, G 4): forward 29,696 B (B and C in the broadcast
+    tile); backward 46,208 B with the
     row-partial sums and the swapped B / C copies (3 blocks per CU fit the
     160 KiB of gfx950); carry pass 39,424 B; swept backward 52,288 B (the
     swapped copies and the sweep's state slots, no row partials)."""
-    assert build.scan_lds_bytes("fwd", 4, 2) == 29184
+    assert build.scan_lds_bytes("fwd", 4, 2) == 4 * 2 * (1024 + 8 * 80 + 4 * 512) == 29696
     assert build.scan_lds_bytes("bwd_carry", 4, 2) == 39424
     assert build.scan_lds_bytes("bwd_sweep", 4, 2) == 47616 + 4 * 2 * (2 * 288 + 8) == 52288
     rp = build.scan_lds_bytes("bwd", 4, 2)
