@@ -716,16 +716,19 @@ def kernel_counters(args) -> None:
     tag = shape_tag(*shape)
     nbytes = scan_bytes(*shape)
     extra = (f"--batch {args.batch} --seqlen {args.seqlen} --d-inner {args.d_inner} "
-             f"--d-state {args.d_state} --chunk {args.chunk}")
+             f"--d-state {args.d_state} --chunk {args.chunk}"
+             + (f" --reduction {args.reduction}" if args.reduction != "auto" else ""))
+    # One --pmc pass per sub-folder, with the counters its CSV holds.
     cmds = [f"rocprofv3 --kernel-trace --stats -d OUT/kt -o run --output-format csv -- "
-            f"python3 bench.py --launches {args.launches} {extra}",
-            f"rocprofv3 --pmc FETCH_SIZE -d OUT/fetch -o run --output-format csv -- "
-            f"python3 bench.py --launches {args.launches} {extra}",
-            f"rocprofv3 --pmc WRITE_SIZE -d OUT/write -o run --output-format csv -- "
-            f"python3 bench.py --launches {args.launches} {extra}",
-            f"rocprofv3 --pmc {ISSUE_COUNTERS} -d OUT/valu -o run --output-format csv -- "
-            f"python3 bench.py --launches {args.launches} {extra}",
-            f"python3 bench.py --kernel-counters OUT --launches {args.launches} {extra}"]
+            f"python3 bench.py --launches {args.launches} {extra}"]
+    for sub in sorted(os.listdir(root)):
+        f = glob.glob(os.path.join(root, sub, "*counter_collection.csv"))
+        if not f:
+            continue
+        names = list(dict.fromkeys(r["Counter_Name"] for r in csv.DictReader(open(f[0]))))
+        cmds.append(f"rocprofv3 --pmc {' '.join(names)} -d OUT/{sub} -o run --output-format csv "
+                    f"-- python3 bench.py --launches {args.launches} {extra}")
+    cmds.append(f"python3 bench.py --kernel-counters OUT --launches {args.launches} {extra}")
     lines = [f"# Scan kernels at {tag}, chunk {args.chunk} (fp32, "
              f"{reduction_name(*shape, args.chunk)} reduction): per-kernel time, HBM traffic, "
              "VALU issue", "", PROFILE_RUN_NOTE, ""] + ["    " + c for c in cmds] + [
@@ -773,7 +776,19 @@ def kernel_counters(args) -> None:
         us = tot[side + "_us"]
         lines.append(f"| {name} | {us:.1f} | {tot[side] / 1e6:.1f} | {alg / 1e6:.1f} | "
                      f"{tot[side] / alg:.2f} | {alg / (us * 1e-6) / 1e9 if us else 0:.0f} |")
-    md = ROOT / "profiles" / f"scan_{tag}_chunk{args.chunk}_kernels.md"
+    known = {"FETCH_SIZE", "WRITE_SIZE"} | set(ISSUE_COUNTERS.split())
+    other = sorted({c for _, c in vals} - known)
+    if other:
+        lines += ["", "Other counters, summed over a launch's dispatches of the kernel (the "
+                  "`_sum` counters are summed over the hardware instances):", "",
+                  "| kernel | " + " | ".join(other) + " |",
+                  "|---|" + "---|" * len(other)]
+        for lab in labels:
+            lines.append(f"| {lab} | " + " | ".join(
+                f"{per_launch[(lab, c)]:.4g}" if (lab, c) in per_launch else ""
+                for c in other) + " |")
+    red = "" if args.reduction == "auto" else f"_{args.reduction}"
+    md = ROOT / "profiles" / f"scan_{tag}_chunk{args.chunk}{red}_kernels.md"
     md.write_text("\n".join(lines) + "\n")
     print("\n".join(lines))
     print(f"\nwrote {md.relative_to(ROOT)}")
