@@ -840,11 +840,11 @@ def workload_trace_summary(args, rows) -> None:
     durations."""
     if args.workload == "longt":
         title = f"Long-sequence scan 4x16384x2048x16 fwd+bwd, stride {args.strides}"
-        run = f"python3 bench.py --workload longt --strides {args.strides}"
+        run = f"python3 bench.py --workload longt --strides {args.strides} --no-cpu-baseline"
         md = ROOT / "profiles" / f"longt_4x16384x2048x16_stride{args.strides.replace(',', '_')}.md"
     else:
         title = "Prefill 32x2048x4096x16 (forward + final state) and 256 decode steps"
-        run = "python3 bench.py --workload infer"
+        run = "python3 bench.py --workload infer --no-cpu-baseline"
         md = ROOT / "profiles" / "infer_32x2048x4096x16.md"
     lines = [f"# {title}: kernel time", "",
              PROFILE_RUN_NOTE, "",
@@ -972,7 +972,7 @@ def bench_longt(args) -> dict:
     # The CPU path on the whole workload, one rep under a wall-clock limit
     # (value None with the reason when it runs out of time or memory), and on
     # a bounded sample beside it: a 1024-step sequence of the same sizes.
-    cpu = cpu_baseline_child("longt")
+    cpu = cpu_baseline_child("longt") if not args.no_cpu_baseline else None
     return {"metric": "long-sequence scan fwd+bwd GB/s (4x16384x2048x16 fp32)",
             "value": best["fwd_bwd_GBs"], "unit": "GB/s", "n_gpus": 1,
             "ms_per_step": best["fwd_bwd_ms"], "higher_is_better": True, "dtype": "f32",
@@ -1052,7 +1052,7 @@ def bench_infer(args) -> dict:
     """Prefill 32 x 2048 x 4096 x 16 (forward + final state), then 256 decode steps."""
     bt, t_len, d, n = INFER
     m = infer_measure()
-    cpu = cpu_baseline_child("infer")
+    cpu = cpu_baseline_child("infer") if not args.no_cpu_baseline else None
     return {"metric": "prefill GB/s and decode us/step (32x2048x4096x16 fp32)",
             "value": m["prefill_GBs"], "unit": "GB/s", "n_gpus": 1,
             "ms_per_step": m["prefill_ms"], "higher_is_better": True, "dtype": "f32",
