@@ -51,3 +51,21 @@ def test_cpu_baseline_child_records_a_timeout(monkeypatch):
     r = bench.cpu_baseline_child("infer")
     assert r["value"] is None and r["result"] == "timeout after 3 s"
     assert "32x2048x4096x16 (the full workload)" in r["sample"] and r["kind"] == "port"
+
+
+def test_kernel_labels_name_each_pass():
+    """The per-kernel counter summary labels every scan kernel by the role its
+    template arguments give it."""
+    f = "void mhs::fwd_kernel<2, 4, 3, true, false, {}, 4>(mhs::FwdArgs)"
+    b = "void mhs::bwd_kernel<2, 4, 3, false, {}, 4, {}, {}>(mhs::BwdArgs)"
+    assert bench.kernel_label(f.format(0)) == "forward"
+    assert bench.kernel_label(f.format(1)) == "forward carry pass"
+    assert bench.kernel_label(f.format(2)) == "forward checkpoint pass"
+    assert bench.kernel_label(b.format("true", "false", 0)) == "backward carry pass"
+    assert bench.kernel_label(b.format("false", "false", 0)) == "backward (fixed order)"
+    assert bench.kernel_label(b.format("false", "true", 0)) == "backward (atomics)"
+    assert bench.kernel_label(b.format("false", "true", 4)) == "backward swept (atomics)"
+    assert bench.kernel_label("void mhs::bwd_reduce_kernel<4>(float const*)") == \
+        "backward reduction"
+    assert bench.kernel_label("void mhs::zero_grads_kernel<0>(float*)") == "zero fill"
+    assert bench.kernel_label("__amd_rocclr_copyBuffer") == "copy"
