@@ -316,7 +316,12 @@ def cpu_baseline_child(workload: str) -> dict:
         stdout = exc.stdout.decode() if isinstance(exc.stdout, bytes) else (exc.stdout or "")
         rc, failed = None, f"timeout after {limit} s"
     wall = time.perf_counter() - t0
-    lines = [json.loads(ln) for ln in stdout.splitlines() if ln.startswith("{")]
+    lines = []
+    for ln in stdout.splitlines():   # a line cut short by the kill is dropped
+        try:
+            lines.append(json.loads(ln))
+        except ValueError:
+            pass
     if rc:
         sig = -rc if rc < 0 else None
         failed = (f"killed by signal {sig}" + (" (out of host memory)" if sig == 9 else "")
