@@ -129,9 +129,9 @@ constexpr int kSweepMax = 4;
 // a read broadcasts, two groups in two orders, fall on distinct banks). The
 // two rows of a half-wave are then added in the finishing step (RP: the
 // kernels without the in-kernel sweep, which keep two row partials per block
-// sum: tile [row][kind][16 steps][rp_step_floats], kind kRPKind apart, the
-// rows 2 kRPKind apart, so that the 32 lanes of a half-wave that write one
-// step pair's partials hit 32 distinct banks), or in registers by one more
+// sum: tile [row][kind][16 steps][rp_step_floats], the kinds rp_kind_floats
+// apart and the rows twice that, so that the 32 lanes of a half-wave that
+// write one step pair's partials hit 32 distinct banks), or in registers by one more
 // v_permlane16_swap stage (the swept kernels, whose LDS, with the sweep's
 // state slots, has no room for the partials). Both add the two rows in the
 // same order, so every checkpoint stride gives the same sums.
@@ -686,7 +686,7 @@ bwd_kernel(BwdArgs a) {
       prio.step(i);
       const int ci = c_hi - 1 - i;
       const float* s0 = lds + (i & 1) * BUF;
-      // RP: the lanes holding their states swapped read the swapped copies.
+      // RL: the lanes holding their states swapped read the swapped copies.
       const float* gB = s0 + (sw ? oBs : oB) + q * bc_group_floats(NPL);
       const float* gC = s0 + (sw ? oCs : oC) + q * bc_group_floats(NPL);
 
