@@ -60,20 +60,88 @@ def _run(cmd: list[str], verbose: bool) -> None:
         print("\n".join(msgs), file=sys.stderr)
 
 
+def _vgprs(operand: str) -> set[int]:
+    import re
+    m = re.fullmatch(r"v\[(\d+):(\d+)\]", operand.strip())
+    if m:
+        return set(range(int(m.group(1)), int(m.group(2)) + 1))
+    m = re.fullmatch(r"v(\d+)", operand.strip())
+    return {int(m.group(1))} if m else set()
+
+
+def dpp_hazards(asm: str) -> list[str]:
+    """DPP reads of a VGPR that a VALU instruction wrote less than 2 wait
+    states before, in the inline-asm blocks of gfx950 assembly (between the
+    compiler's ;;#ASMSTART and ;;#ASMEND): the hardware then reads the old
+    value. The compiler pads its own DPP instructions; the kernels'
+    inline-asm ones (v_fmac_f32_dpp of the quad broadcasts, the bank-masked
+    adds) rely on their DPP source coming from an LDS load or on their own
+    s_nop, which this checks on the code that ships. Such a DPP instruction
+    within 2 wait states after a label is reported too (the predecessors
+    are not followed)."""
+    import re
+    found: list[str] = []
+    func, hist = "?", []          # (opcode, VGPRs written, wait states)
+    in_asm = False
+    for ln, raw in enumerate(asm.splitlines(), 1):
+        if ";;#ASMSTART" in raw or ";;#ASMEND" in raw:
+            in_asm = ";;#ASMSTART" in raw
+            continue
+        s = raw.split(";")[0].strip()
+        if re.match(r"^[_A-Za-z.][\w.$]*:$", s):
+            if s.startswith(".LBB"):
+                hist.append(("label", set(), 0))
+            else:
+                func, hist = s[:-1], []
+            continue
+        if not s or s.startswith("."):
+            continue
+        op = s.split()[0]
+        ops = [o.strip() for o in s[len(op):].split(",")]
+        if in_asm and op.startswith("v_") and ("_dpp" in op or "quad_perm" in s or "row_" in s):
+            src0 = _vgprs(ops[1].split()[0]) if len(ops) > 1 and ops[1] else set()
+            ws = 0
+            for hop, hdst, hw in reversed(hist):
+                if ws >= 2:
+                    break
+                if hop == "label":
+                    found.append(f"line {ln} ({func}): DPP after a label: {s}")
+                    break
+                if hop.startswith("v_") and hdst & src0:
+                    found.append(f"line {ln} ({func}): DPP source written {ws} wait "
+                                 f"states before: {s}")
+                    break
+                ws += hw
+        dst = _vgprs(ops[0].split()[0]) if op.startswith("v_") and ops and ops[0] else set()
+        m = re.match(r"s_nop\s+(\d+)", s)
+        hist = (hist + [(op, dst, int(m.group(1)) + 1 if m else 1)])[-8:]
+    return found
+
+
 def build_library(verbose: bool = False, out: Path | None = None) -> Path:
     """Compile csrc/*.hip into the in-tree shared library; returns its path.
 
-    Each source compiles to an object in a temporary folder, in parallel;
-    hipcc then links them into the library."""
+    Each source compiles to an object in a temporary folder, in parallel,
+    keeping its device assembly (-save-temps: the object is assembled from
+    it), which is checked for DPP wait-state hazards (dpp_hazards); hipcc
+    then links the objects into the library."""
     out = Path(out) if out is not None else LIB_PATH
     tmp = out.with_suffix(".so.tmp")
     with tempfile.TemporaryDirectory(prefix="mhs_build_") as objdir:
         objs = [str(Path(objdir) / (Path(src).stem + ".o")) for src in SOURCES]
-        cmds = [[hipcc(), *compile_flags(), "-c", "-o", obj, str(CSRC / src)]
+        cmds = [[hipcc(), *compile_flags(), "-save-temps=obj", "-c", "-o", obj, str(CSRC / src)]
                 for src, obj in zip(SOURCES, objs)]
         with ThreadPoolExecutor(max_workers=min(len(cmds), os.cpu_count() or 1)) as pool:
             for f in [pool.submit(_run, c, verbose) for c in cmds]:
                 f.result()
+        for src in SOURCES:
+            asm = Path(objdir) / f"{Path(src).stem}-hip-amdgcn-amd-amdhsa-{ARCH}.s"
+            if not asm.exists():
+                raise RuntimeError(f"device assembly of {src} not found ({asm.name})")
+            bad = dpp_hazards(asm.read_text())
+            if bad:
+                raise RuntimeError(f"{src}: {len(bad)} DPP wait-state hazard(s):\n"
+                                   + "\n".join(bad[:10]))
         _run([hipcc(), *compile_flags(), "-shared", "-o", str(tmp), *objs], verbose)
     os.replace(tmp, out)
     return out
@@ -97,7 +165,8 @@ def emit_assembly(out_dir: Path) -> Path:
 # headers (fwd_lds_floats in mhs_fwd.hpp, bwd_lds_floats and
 # bwd_sweep_lds_floats in mhs_bwd.hpp) with the header constants below, which
 # tests/test_build.py reads back from the headers.
-K_CH, K_STEPS, K_BC_PAD, K_SWEEP_MAX, K_RP_SWAP_PAD = 32, 16, 4, 4, 8
+K_CH, K_STEPS, K_BC_PAD, K_SWEEP_MAX = 32, 16, 4, 4
+K_BC_GROUP2 = 4 * 16 + 16        # kBCGroup2: a state group of a broadcast tile
 LDS_PER_CU = 160 * 1024          # gfx950
 VGPRS_PER_SIMD_LANE = 512        # wave64 VGPR file per SIMD lane (gfx950, no AGPR split used)
 
@@ -111,16 +180,16 @@ def scan_lds_bytes(kind: str, g: int, npl: int) -> int:
     "bwd" (the gradient kernels), "bwd_carry" (the adjoint-carry pass) or
     "bwd_sweep" (the swept backward, checkpoint strides 32-64)."""
     if kind == "fwd":
-        # two states per lane: the broadcast tile (fwd_bc_floats, kBCGroup2 = 80)
-        bc = 2 * g * 80 if npl == 2 else 2 * _bc_tile_floats(2 * g, npl)
+        # two states per lane: the broadcast tile (fwd_bc_floats)
+        bc = 2 * g * K_BC_GROUP2 if npl == 2 else 2 * _bc_tile_floats(2 * g, npl)
         buf = 2 * K_CH * K_STEPS + bc + g * K_CH * K_STEPS
         return 4 * 2 * buf
     rl = kind != "bwd_carry" and npl == 2   # swapped state pairs (bwd_relabel)
     rp = kind == "bwd" and npl == 2         # row-partial channel sums (bwd_row_partial)
     np_ = 2 * g * npl
-    buf = 4 * K_CH * K_STEPS + 2 * _bc_tile_floats(2 * g, npl)
-    if rl:
-        buf += 2 * _bc_tile_floats(2 * g, npl) + K_RP_SWAP_PAD
+    # B and C: the quad broadcast tile (rl) or the per-group tiles
+    bc = 2 * g * K_BC_GROUP2 if rl else 2 * _bc_tile_floats(2 * g, npl)
+    buf = 4 * K_CH * K_STEPS + bc
     sums = 4 * (K_STEPS * (16 if np_ <= 16 else 48) + 4) if rp else 2 * K_STEPS * np_
     floats = 2 * buf + g * 64 * K_STEPS + sums
     if kind == "bwd_sweep":

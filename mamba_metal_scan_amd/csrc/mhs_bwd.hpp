@@ -123,11 +123,12 @@ constexpr int kSweepMax = 4;
 
 // Channel sums of the two-state plans' gradient kernels (RL): the lanes of
 // odd channel hold their two states in swapped order, and the dB / dC
-// products are summed over each 16-lane row in registers (row_partial_rs8).
-// Such kernels stage B and C a second time with each state pair swapped (the
-// copies sit kRPSwapPad floats after the C tile, so that the four addresses
-// a read broadcasts, two groups in two orders, fall on distinct banks). The
-// two rows of a half-wave are then added in the finishing step (RP: the
+// products are summed over each 16-lane row in registers (pair_sum_xor1, then
+// row_partial_pairs: each lane reads its partner channel's dt * x and dy too).
+// Such kernels stage B and C in a quad broadcast tile (BCLayout::kQuad, one
+// 128-bit read per lane and quad) and take each value from the right lane of
+// the quad with quad_perm DPP (qp_get, qp_fmac), which serves both state
+// orders. The two rows of a half-wave are then added in the finishing step (RP: the
 // kernels without the in-kernel sweep, which keep two row partials per block
 // sum: tile [row][kind][16 steps][rp_step_floats], the kinds rp_kind_floats
 // apart and the rows twice that, so that the 32 lanes of a half-wave that
@@ -135,7 +136,6 @@ constexpr int kSweepMax = 4;
 // v_permlane16_swap stage (the swept kernels, whose LDS, with the sweep's
 // state slots, has no room for the partials). Both add the two rows in the
 // same order, so every checkpoint stride gives the same sums.
-constexpr int kRPSwapPad = 8;
 __host__ __device__ constexpr int rp_step_floats(int NP) { return NP <= 16 ? 16 : 48; }
 __host__ __device__ constexpr int rp_kind_floats(int NP) {
   return kSteps * rp_step_floats(NP) + 4;
@@ -148,8 +148,8 @@ __host__ __device__ constexpr bool bwd_row_partial(int NPL, bool CARRY, int SWEE
 // One staging buffer (the kernel keeps two) and the single-buffered rest.
 __host__ __device__ constexpr int bwd_buf_floats(int G, int NPL, bool rl = false) {
   return 4 * kCH * kSteps               // dt, dy, x, dt*x (channel-major)
-         + 2 * bc_tile_floats(2 * G, NPL)   // B, C tiles
-         + (rl ? 2 * bc_tile_floats(2 * G, NPL) + kRPSwapPad : 0);   // swapped copies
+         + (rl ? 2 * G * kBCGroup2      // B, C quad broadcast tile
+               : 2 * bc_tile_floats(2 * G, NPL));   // B, C tiles
 }
 __host__ __device__ constexpr int bwd_lds_floats(int G, int NPL, bool rl = false,
                                                  bool rp = false) {
@@ -222,12 +222,10 @@ bwd_kernel(BwdArgs a) {
 
   float* tS = lds + 2 * BUF;                          // [G][64][16]
   float* tDBC = tS + G * 64 * kSteps;                 // [2][16][NP], RP: [2][2][16][RPS]
-  // Staging buffer j: dt, dy, x (channel-major), B, C (per lane group), and
-  // with RL the swapped copies of B and C.
+  // Staging buffer j: dt, dy, x (channel-major), B, C (per lane group; with
+  // RL one quad broadcast tile of both, at oB).
   constexpr int oDY = kCH * kSteps, oX = 2 * kCH * kSteps, oDTX = 3 * kCH * kSteps,
-                oB = 4 * kCH * kSteps, oC = oB + bc_tile_floats(2 * G, NPL),
-                oBs = oC + bc_tile_floats(2 * G, NPL) + kRPSwapPad,
-                oCs = oBs + bc_tile_floats(2 * G, NPL);
+                oB = 4 * kCH * kSteps, oC = oB + bc_tile_floats(2 * G, NPL);
   constexpr int RPS = rp_step_floats(NP), RPK = rp_kind_floats(NP);
   // The reduce-scatter leaves lane `lane` with the total of product rs_index:
   // products are numbered kind * 2NPL + slot * NPL + j (kind 0: dB, 1: dC;
@@ -243,13 +241,15 @@ bwd_kernel(BwdArgs a) {
       RP ? tDBC + ((lane >> 4) & 1) * 2 * RPK + rs_kind * RPK + rs_slot * RPS + n0 + rs_n
          : tDBC + rs_kind * kSteps * NP + rs_slot * NP + n0 + rs_n;
   constexpr int kDbcStep = RP ? RPS : NP;   // dbc_out's stride per step
-  // The dB / dC products of a step pair summed as dbc_out holds them.
-  auto channel_sums = [&](const float (&pv)[M]) {
+  // The dB / dC products of a step pair summed as dbc_out holds them: from
+  // the products pv (numbered as for rs_index) or, with RL, from their
+  // bit-0 pair sums pa (kind * 2 + slot, pair_sum_xor1).
+  auto channel_sums = [&](const float (&pv)[M], const float (&pa)[4]) {
     if constexpr (RP) {
-      return row_partial_rs8(pv);
+      return row_partial_pairs(pa);
     } else if constexpr (RL) {
       // the two rows of the half-wave added in registers (row 0's first)
-      const float r = row_partial_rs8(pv);
+      const float r = row_partial_pairs(pa);
       const auto sw16 = __builtin_amdgcn_permlane16_swap(__float_as_uint(r), __float_as_uint(r),
                                                          false, false);
       return __uint_as_float(sw16[0]) + __uint_as_float(sw16[1]);
@@ -257,6 +257,9 @@ bwd_kernel(BwdArgs a) {
       return half_wave_reduce_scatter<M>(pv, lane);
     }
   };
+  // RL: the partner channel's row of the channel-major tiles (its dt * x and
+  // dy for pair_sum_xor1).
+  const int cp = c ^ 1;
 
   const size_t slice = (size_t)D * N;
   const unsigned slice_bytes = 4u * (unsigned)slice;
@@ -306,6 +309,7 @@ bwd_kernel(BwdArgs a) {
   const QuadLoader<kCH, PER, ES> ql(tid, NT, D, d0, D);
   const QuadLoader<kCH, PER, ES> qdt(tid, NT, D, d0, ld_dt);
   const RowLoader<PERS, NPL, ES> rl(tid, NT, N, NP, ld_bc);
+  const BCRowLoader<PERS, ES, BCLayout::kQuad> rlq(tid, NT, N, NP, ld_bc);   // RL: stores
   float4 px[PER], pd[PER], py[PER];
   float pb[PERS], pc[PERS], ph[NPL];
   float gbias[PER];   // GATED: the dt bias of each staging task's channel
@@ -377,11 +381,12 @@ bwd_kernel(BwdArgs a) {
     ql.store_cm(s0 + oDY, py);
     if constexpr (!CARRY) ql.store_cm(s0 + oX, px);
     if constexpr (!CARRY) ql.store_cm_product(s0 + oDTX, pd, px);   // dt * x, once per block
-    if constexpr (!CARRY) rl.store(s0 + oB, pb);
-    rl.store(s0 + oC, pc);
     if constexpr (RL) {
-      rl.store_swapped(s0 + oBs, pb);
-      rl.store_swapped(s0 + oCs, pc);
+      rlq.store(s0 + oB, pb, 0);
+      rlq.store(s0 + oB, pc, 1);
+    } else {
+      if constexpr (!CARRY) rl.store(s0 + oB, pb);
+      rl.store(s0 + oC, pc);
     }
   };
   // The fp32 rows of the dB / dC block sums of chunk ci: this block's
@@ -562,8 +567,9 @@ bwd_kernel(BwdArgs a) {
       const Pos pos1 = advance(pos);
       const Item it1 = item_at(pos1), it2 = item_at(advance(pos1));
       const float* s0 = lds + (k & 1) * BUF;
-      const float* gB = s0 + (sw ? oBs : oB) + q * bc_group_floats(NPL);
-      const float* gC = s0 + (sw ? oCs : oC) + q * bc_group_floats(NPL);
+      const float* gB = s0 + oB + q * bc_group_floats(NPL);
+      const float* gC = s0 + oC + q * bc_group_floats(NPL);
+      const float* gQ = s0 + oB + q * kBCGroup2 + (lane & 3) * 4;   // RL
       if (it.first) {
         float h0[NPL];
 #pragma unroll
@@ -583,15 +589,21 @@ bwd_kernel(BwdArgs a) {
 #pragma unroll
       for (int m = 0; m < kQuads; ++m) {
         float dts[4], dtxs[4], Bq[4][NPL];
+        float2 qb;   // RL: B of the quad broadcast tile
         f4_to(dts, lds4(s0 + cm_quad(c, m)));
         f4_to(dtxs, lds4(s0 + oDTX + cm_quad(c, m)));
-        load_quad_rows<NPL>(Bq, gB, m);
+        if constexpr (RL) {
+          qb = lds2(gQ + 16 * m);
+        } else {
+          load_quad_rows<NPL>(Bq, gB, m);
+        }
 #pragma unroll
         for (int s = 0; s < 4; ++s) {
 #pragma unroll
           for (int j = 0; j < NPL; ++j) {
             da[4 * m + s][j] = exp2_hw(dts[s] * a2[j]);
-            hs[4 * m + s][j] = Bq[s][j] * dtxs[s];
+            const float bv = RL ? qp_get((s >> 1) ? qb.y : qb.x, qp_sel(s, j)) : Bq[s][j];
+            hs[4 * m + s][j] = bv * dtxs[s];
           }
         }
         if (m == 0 && fin)
@@ -619,12 +631,22 @@ bwd_kernel(BwdArgs a) {
 #pragma unroll
       for (int m = kQuads - 1; m >= 0; --m) {
         float dts[4], dys[4], dtxs[4], Bq[4][NPL], Cq[4][NPL], s1q[4], s2q[4];
+        float dysp[4], dtxsp[4];   // RL: the partner channel's
         f4_to(dts, lds4(s0 + cm_quad(c, m)));
         f4_to(dys, lds4(s0 + oDY + cm_quad(c, m)));
         f4_to(dtxs, lds4(s0 + oDTX + cm_quad(c, m)));
-        load_quad_rows<NPL>(Bq, gB, m);
-        load_quad_rows<NPL>(Cq, gC, m);
-        float pv[M];
+        if constexpr (RL) {
+          f4_to(dysp, lds4(s0 + oDY + cm_quad(cp, m)));
+          f4_to(dtxsp, lds4(s0 + oDTX + cm_quad(cp, m)));
+        }
+        float4 qbc;   // RL: B and C of the quad broadcast tile
+        if constexpr (RL) {
+          qbc = lds4(gQ + 16 * m);
+        } else {
+          load_quad_rows<NPL>(Bq, gB, m);
+          load_quad_rows<NPL>(Cq, gC, m);
+        }
+        float pv[M], pa[4];
 #pragma unroll
         for (int s = 3; s >= 0; --s) {
           const int kk = 4 * m + s;
@@ -632,21 +654,37 @@ bwd_kernel(BwdArgs a) {
           float s1 = 0.f, s2 = 0.f, gk[NPL];
 #pragma unroll
           for (int j = 0; j < NPL; ++j) {
-            gk[j] = __builtin_fmaf(dys[s], Cq[s][j], u[j]);
+            if constexpr (RL) {
+              gk[j] = u[j];
+              qp_fmac(gk[j], (s >> 1) ? qbc.w : qbc.z, dys[s], qp_sel(s, j));
+            } else {
+              gk[j] = __builtin_fmaf(dys[s], Cq[s][j], u[j]);
+            }
             u[j] = da[kk][j] * gk[j];
             const float qv = u[j] * (kk == 0 ? hc[j] : hs[kk - 1][j]);
-            s1 = __builtin_fmaf(gk[j], Bq[s][j], s1);
+            if constexpr (RL) {
+              const float br = (s >> 1) ? qbc.y : qbc.x;
+              if (j == 0) s1 = qp_get(br, qp_sel(s, 0)) * gk[0];
+              else qp_fmac(s1, br, gk[j], qp_sel(s, j));
+            } else {
+              s1 = __builtin_fmaf(gk[j], Bq[s][j], s1);
+            }
             s2 = __builtin_fmaf(an[j], qv, s2);
             acc[j] = __builtin_fmaf(dts[s], qv, acc[j]);
           }
           s1q[s] = s1;
           s2q[s] = s2;
+          if constexpr (RL) {
+            pa[slot] = pair_sum_xor1(gk[0], gk[1], dtxs[s], dtxsp[s]);
+            pa[2 + slot] = pair_sum_xor1(hs[kk][0], hs[kk][1], dys[s], dysp[s]);
+          } else {
 #pragma unroll
-          for (int j = 0; j < NPL; ++j) {
-            pv[slot * NPL + j] = gk[j] * dtxs[s];
-            pv[2 * NPL + slot * NPL + j] = hs[kk][j] * dys[s];
+            for (int j = 0; j < NPL; ++j) {
+              pv[slot * NPL + j] = gk[j] * dtxs[s];
+              pv[2 * NPL + slot * NPL + j] = hs[kk][j] * dys[s];
+            }
           }
-          if (slot == 0) *(dbc_out + kk * kDbcStep) = channel_sums(pv);
+          if (slot == 0) *(dbc_out + kk * kDbcStep) = channel_sums(pv, pa);
         }
         float o[4];
 #pragma unroll
@@ -686,9 +724,10 @@ bwd_kernel(BwdArgs a) {
       prio.step(i);
       const int ci = c_hi - 1 - i;
       const float* s0 = lds + (i & 1) * BUF;
-      // RL: the lanes holding their states swapped read the swapped copies.
-      const float* gB = s0 + (sw ? oBs : oB) + q * bc_group_floats(NPL);
-      const float* gC = s0 + (sw ? oCs : oC) + q * bc_group_floats(NPL);
+      const float* gB = s0 + oB + q * bc_group_floats(NPL);
+      const float* gC = s0 + oC + q * bc_group_floats(NPL);
+      // RL: this lane's 4 floats of each quad of the quad broadcast tile
+      const float* gQ = s0 + oB + q * kBCGroup2 + (lane & 3) * 4;
 
       if constexpr (CARRY) {
         // The adjoint alone: G_t = dy_t C_t + dA_{t+1} G_{t+1}, dA formed on
@@ -719,15 +758,21 @@ bwd_kernel(BwdArgs a) {
 #pragma unroll
       for (int m = 0; m < kQuads; ++m) {
         float dts[4], dtxs[4], Bq[4][NPL];
+        float2 qb;   // RL: B of the quad broadcast tile
         f4_to(dts, lds4(s0 + cm_quad(c, m)));
         f4_to(dtxs, lds4(s0 + oDTX + cm_quad(c, m)));
-        load_quad_rows<NPL>(Bq, gB, m);
+        if constexpr (RL) {
+          qb = lds2(gQ + 16 * m);
+        } else {
+          load_quad_rows<NPL>(Bq, gB, m);
+        }
 #pragma unroll
         for (int s = 0; s < 4; ++s) {
 #pragma unroll
           for (int j = 0; j < NPL; ++j) {
             da[4 * m + s][j] = exp2_hw(dts[s] * a2[j]);
-            hs[4 * m + s][j] = Bq[s][j] * dtxs[s];       // b_k, turned into h_k below
+            const float bv = RL ? qp_get((s >> 1) ? qb.y : qb.x, qp_sel(s, j)) : Bq[s][j];
+            hs[4 * m + s][j] = bv * dtxs[s];       // b_k, turned into h_k below
           }
         }
         if (m == 0)   // no-op stores past the sequence end
@@ -745,12 +790,24 @@ bwd_kernel(BwdArgs a) {
 #pragma unroll
       for (int m = kQuads - 1; m >= 0; --m) {
         float dts[4], dys[4], dtxs[4], Bq[4][NPL], Cq[4][NPL], s1q[4], s2q[4];
+        float dysp[4], dtxsp[4];   // RL: the partner channel's
         f4_to(dts, lds4(s0 + cm_quad(c, m)));
         f4_to(dys, lds4(s0 + oDY + cm_quad(c, m)));
         f4_to(dtxs, lds4(s0 + oDTX + cm_quad(c, m)));
-        load_quad_rows<NPL>(Bq, gB, m);
-        load_quad_rows<NPL>(Cq, gC, m);
-        float pv[M];   // dB/dC products of the step pair (k, k+1), k even, numbered as for rs_index
+        if constexpr (RL) {
+          f4_to(dysp, lds4(s0 + oDY + cm_quad(cp, m)));
+          f4_to(dtxsp, lds4(s0 + oDTX + cm_quad(cp, m)));
+        }
+        float4 qbc;   // RL: B and C of the quad broadcast tile
+        if constexpr (RL) {
+          qbc = lds4(gQ + 16 * m);
+        } else {
+          load_quad_rows<NPL>(Bq, gB, m);
+          load_quad_rows<NPL>(Cq, gC, m);
+        }
+        // dB/dC products of the step pair (k, k+1), k even, numbered as for
+        // rs_index, or with RL their bit-0 pair sums
+        float pv[M], pa[4];
 #pragma unroll
         for (int s = 3; s >= 0; --s) {
           const int k = 4 * m + s;
@@ -758,21 +815,39 @@ bwd_kernel(BwdArgs a) {
           float s1 = 0.f, s2 = 0.f, gk[NPL];
 #pragma unroll
           for (int j = 0; j < NPL; ++j) {
-            gk[j] = __builtin_fmaf(dys[s], Cq[s][j], u[j]);            // G_k
+            if constexpr (RL) {
+              gk[j] = u[j];                                            // G_k
+              qp_fmac(gk[j], (s >> 1) ? qbc.w : qbc.z, dys[s], qp_sel(s, j));
+            } else {
+              gk[j] = __builtin_fmaf(dys[s], Cq[s][j], u[j]);          // G_k
+            }
             u[j] = da[k][j] * gk[j];                                   // dA_k G_k
             const float qv = u[j] * (k == 0 ? hc[j] : hs[k - 1][j]);   // G_k * hm_k
-            s1 = __builtin_fmaf(gk[j], Bq[s][j], s1);
+            if constexpr (RL) {
+              // G_k . B_k: the first product a DPP multiply, as the fma
+              // into 0 of the other plans rounds it
+              const float br = (s >> 1) ? qbc.y : qbc.x;
+              if (j == 0) s1 = qp_get(br, qp_sel(s, 0)) * gk[0];
+              else qp_fmac(s1, br, gk[j], qp_sel(s, j));
+            } else {
+              s1 = __builtin_fmaf(gk[j], Bq[s][j], s1);
+            }
             s2 = __builtin_fmaf(an[j], qv, s2);
             acc[j] = __builtin_fmaf(dts[s], qv, acc[j]);
           }
           s1q[s] = s1;
           s2q[s] = s2;
+          if constexpr (RL) {
+            pa[slot] = pair_sum_xor1(gk[0], gk[1], dtxs[s], dtxsp[s]);            // dB
+            pa[2 + slot] = pair_sum_xor1(hs[k][0], hs[k][1], dys[s], dysp[s]);    // dC
+          } else {
 #pragma unroll
-          for (int j = 0; j < NPL; ++j) {
-            pv[slot * NPL + j] = gk[j] * dtxs[s];             // dB: G * dt * x
-            pv[2 * NPL + slot * NPL + j] = hs[k][j] * dys[s];   // dC: h * dy
+            for (int j = 0; j < NPL; ++j) {
+              pv[slot * NPL + j] = gk[j] * dtxs[s];             // dB: G * dt * x
+              pv[2 * NPL + slot * NPL + j] = hs[k][j] * dys[s];   // dC: h * dy
+            }
           }
-          if (slot == 0) *(dbc_out + k * kDbcStep) = channel_sums(pv);
+          if (slot == 0) *(dbc_out + k * kDbcStep) = channel_sums(pv, pa);
         }
         // Add the two half-waves: lanes 0-31 end with s1, lanes 32-63 with s2.
         float o[4];

@@ -135,7 +135,7 @@ __device__ __forceinline__ void rs_bits32_16(const float (&a)[8], float (&c)[2])
 }
 
 // The stages over lane bits 3 and 2 of the row-partial reduce-scatter of 8
-// values per lane (see row_partial_rs8): a = (x0, x1, y0, y1). Bit 3 by
+// values per lane (see row_partial_pairs): a = (x0, x1, y0, y1). Bit 3 by
 // bank-masked row_ror:8 adds (pairs (x0, y0) and (x1, y1): x in the banks
 // whose bit 3 is 0, y in the others), then bit 2 by bank-masked row shifts
 // (partner lane i ^ 4: row_shl:4, lane i reads lane i + 4, in banks 0 and
@@ -158,22 +158,29 @@ __device__ __forceinline__ float rs_bits32_shift(const float (&a)[4]) {
   return c;
 }
 
-// Partial sums over each 16-lane row of 8 values per lane, with the lanes of
-// odd index holding their two states in swapped order (the lane's register
-// j holds state j ^ (lane & 1)). v[kind * 4 + slot * 2 + j]: kind 0 / 1,
-// slot 0 / 1 (two steps), j the register of the state. Stage over lane bit
-// 0 (quad_perm [1, 0, 3, 2]): v[.. + 0] + the partner's v[.. + 1] is the
-// pair sum of one state, state n0 + (lane & 1), in every lane, so one DPP add
-// per pair; then bit 3 (kind) and bit 2 (slot) as bank-masked stages, and
-// bit 1 (quad_perm [2, 3, 0, 1]) as a plain add: 11 instructions. Lane l
-// returns the sum over the 16 lanes of its row of the value (kind (l >> 3)
-// & 1, slot (l >> 2) & 1, state n0 + (l & 1)); the two rows of a half-wave
-// (lane bit 4) are added later, in a fixed order.
-__device__ __forceinline__ float row_partial_rs8(const float (&v)[8]) {
-  float a[4];
-#pragma unroll
-  for (int i = 0; i < 4; ++i) a[i] = v[2 * i] + dpp_get<kDppXor1>(v[2 * i + 1]);
-  // a = (kind 0 slot 0, kind 0 slot 1, kind 1 slot 0, kind 1 slot 1)
+// Partial sums over each 16-lane row of 8 products per lane, with the lanes
+// of odd index holding their two states in swapped order (the lane's
+// register j holds state j ^ (lane & 1)). Products x_j * q: kind 0 / 1 (x
+// the adjoint G or the state h, q the channel's dt * x or dy), slot 0 / 1
+// (two steps), j the register of the state. Stage over lane bit 0
+// (quad_perm [1, 0, 3, 2]): the lane's product of register 0 plus the
+// partner's product of register 1 is the pair sum of one state, state n0 +
+// (lane & 1), in every lane. pair_sum_xor1 forms it from the factors, with
+// the partner's operand q' held by this lane: the partner's product in one
+// v_mul_f32_dpp (the compiler folds the DPP read into a plain multiply),
+// rounded as the partner would round it, then fma(x0, q, x1' * q'), two
+// VALU per pair, where products formed first and a DPP read of the
+// partner's take three.
+__device__ __forceinline__ float pair_sum_xor1(float x0, float x1, float q, float qp) {
+  return __builtin_fmaf(x0, q, dpp_get<kDppXor1>(x1) * qp);
+}
+// The rest of the row partial, from the pair sums a = (kind 0 slot 0, kind 0
+// slot 1, kind 1 slot 0, kind 1 slot 1): bit 3 (kind) and bit 2 (slot) as
+// bank-masked stages, and bit 1 (quad_perm [2, 3, 0, 1]) as a plain add, 7
+// instructions. Lane l returns the sum over the 16 lanes of its row of the
+// product (kind (l >> 3) & 1, slot (l >> 2) & 1, state n0 + (l & 1)); the
+// two rows of a half-wave (lane bit 4) are added later, in a fixed order.
+__device__ __forceinline__ float row_partial_pairs(const float (&a)[4]) {
   return dpp_add<kDppXor2>(rs_bits32_shift(a));
 }
 
@@ -680,16 +687,6 @@ struct RowLoader {
       dst[i] = in_tile ? (n / NPL) * bc_group_floats(NPL) + k * NPL + (n % NPL) : -1;
     }
   }
-  // The same tile with each group's NPL = 2 states of a step in swapped
-  // order (the copy that lanes holding their states swapped read).
-  __device__ __forceinline__ void store_swapped(float* tile, const float (&v)[PERS]) const {
-    static_assert(NPL == 2, "state pairs");
-#pragma unroll
-    for (int i = 0; i < PERS; ++i) {
-      if (valid(i)) tile[dst[i] ^ 1] = v[i];
-      asm volatile("" ::"v"(v[i]));
-    }
-  }
   __device__ __forceinline__ void load(float (&v)[PERS], const GBuf& g) const {
 #pragma unroll
     for (int i = 0; i < PERS; ++i) v[i] = ld_elem<ES>(g, src[i]);
@@ -710,6 +707,107 @@ struct RowLoader {
     return dst[i] >= 0;
   }
 };
+
+// Broadcast tiles of B and C for two states per lane: per state group q
+// and quad m, 16 floats (the group's 2 states x 4 steps x {B, C}); groups
+// kBCGroup2 floats apart (16 banks), so that the two half-waves' groups
+// fall on disjoint banks. Two layouts of the 16:
+// * kRow (the forward's row broadcasts): [kind][k % 4][n % 2], one float
+//   per lane of a 16-lane row;
+// * kQuad (the backward's quad broadcasts): [(k % 2) * 2 + n % 2][kind * 2 +
+//   (k % 4) / 2], so that lane p of a quad reads its 4 floats with one
+//   128-bit load and holds B of steps 4m + (p >> 1) and 4m + 2 + (p >> 1),
+//   then C of the same two steps, each of state n0 + (p & 1) (qp_get).
+constexpr int kBCGroup2 = kQuads * 16 + 16;
+enum class BCLayout { kRow, kQuad };
+
+// Staging of 16 rows of B and C (fp32 or bf16, rows ld apart) into such a
+// tile: thread tid moves tile elements tid, tid + nthreads, ... (PERS of
+// them), state fastest, of both B and C. Padded states and steps past T are
+// zero.
+template <int PERS, int ES = 4, BCLayout L = BCLayout::kRow>
+struct BCRowLoader {
+  unsigned src[PERS];  // byte offset in the sub-chunk's global [16][ld] block, or kOOB
+  int dst[PERS];       // B's slot in the tile (C's is kKind further), or -1
+  int tid, nthreads, ntile;
+  int w0;
+  static constexpr int kKind = L == BCLayout::kRow ? 8 : 2;
+  __device__ __forceinline__ BCRowLoader(int tid_, int nthreads_, int N, int NP, int ld)
+      : tid(tid_), nthreads(nthreads_), ntile(kSteps * NP),
+        w0(__builtin_amdgcn_readfirstlane(tid_) & ~63) {
+#pragma unroll
+    for (int i = 0; i < PERS; ++i) {
+      const int e = tid + i * nthreads;       // tile element (k, n), n fastest
+      const int k = e / NP, n = e % NP;
+      const bool in_tile = e < kSteps * NP;
+      src[i] = (in_tile && n < N) ? (unsigned)ES * (unsigned)(k * ld + n) : kOOB;
+      const int in_quad = L == BCLayout::kRow ? (k % 4) * 2 + (n % 2)
+                                              : ((k % 2) * 2 + (n % 2)) * 4 + (k % 4) / 2;
+      dst[i] = in_tile ? (n / 2) * kBCGroup2 + (k / 4) * 16 + in_quad : -1;
+    }
+  }
+  __device__ __forceinline__ void load(float (&v)[PERS], const GBuf& g) const {
+#pragma unroll
+    for (int i = 0; i < PERS; ++i) v[i] = ld_elem<ES>(g, src[i]);
+  }
+  __device__ __forceinline__ bool valid(int i) const {
+    if ((i + 1) * nthreads <= ntile) return true;
+    if (ntile % 64 == 0) return w0 + i * nthreads < ntile;
+    return dst[i] >= 0;
+  }
+  // kind 0 (B) or 1 (C)
+  __device__ __forceinline__ void store(float* tile, const float (&v)[PERS], int kind) const {
+#pragma unroll
+    for (int i = 0; i < PERS; ++i) {
+      if (valid(i)) tile[dst[i] + kKind * kind] = v[i];
+      asm volatile("" ::"v"(v[i]));
+    }
+  }
+};
+
+// Quad broadcasts from a kQuad tile. Lane p of a quad holding its two states
+// in swapped order when p is odd (register j: state n0 + (j ^ (p & 1))), the
+// value of step 4m + s, register j, is in the quad's register (s >> 1) (B;
+// C: 2 + (s >> 1)) of lane ((s & 1) << 1) | (j ^ (p & 1)): sel = (s & 1) * 2
+// + j picks one of four quad_perm patterns, [0,1,0,1], [1,0,1,0], [2,3,2,3]
+// and [3,2,3,2]. With sel a constant after unrolling, each switch below
+// folds to one case.
+__host__ __device__ constexpr int qp_sel(int s, int j) { return (s & 1) * 2 + j; }
+// The broadcast value itself (the compiler folds the DPP read into the
+// multiply or add that uses it).
+__device__ __forceinline__ float qp_get(float r, int sel) {
+  switch (sel) {
+    case 0: return dpp_get<0x44>(r);
+    case 1: return dpp_get<0x11>(r);
+    case 2: return dpp_get<0xEE>(r);
+    default: return dpp_get<0xBB>(r);
+  }
+}
+// acc += (the broadcast value of r) * x, one v_fmac_f32_dpp (the compiler
+// does not fold a DPP read into v_fmac). r must come from an LDS load, not
+// from a VALU instruction: a DPP read of a VGPR needs 2 wait states after a
+// VALU write of it, which the compiler does not check inside the asm (the
+// ISA check of the build keeps it so).
+__device__ __forceinline__ void qp_fmac(float& acc, float r, float x, int sel) {
+  switch (sel) {
+    case 0:
+      asm("v_fmac_f32_dpp %0, %1, %2 quad_perm:[0,1,0,1] row_mask:0xf bank_mask:0xf"
+          : "+v"(acc) : "v"(r), "v"(x));
+      break;
+    case 1:
+      asm("v_fmac_f32_dpp %0, %1, %2 quad_perm:[1,0,1,0] row_mask:0xf bank_mask:0xf"
+          : "+v"(acc) : "v"(r), "v"(x));
+      break;
+    case 2:
+      asm("v_fmac_f32_dpp %0, %1, %2 quad_perm:[2,3,2,3] row_mask:0xf bank_mask:0xf"
+          : "+v"(acc) : "v"(r), "v"(x));
+      break;
+    default:
+      asm("v_fmac_f32_dpp %0, %1, %2 quad_perm:[3,2,3,2] row_mask:0xf bank_mask:0xf"
+          : "+v"(acc) : "v"(r), "v"(x));
+      break;
+  }
+}
 
 // NPL states x 4 steps of a group's B or C tile: v[s][j] = tile[(4m+s)*NPL + j].
 template <int NPL>

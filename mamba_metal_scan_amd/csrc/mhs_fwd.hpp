@@ -77,14 +77,11 @@ struct FwdArgs {
 
 constexpr int kCH = 32;   // channels per block
 
-// Two states per lane (NPL 2): B and C reach the lanes by DPP row broadcasts.
-// Per state group q and quad m the tile holds the 16 values [kind][step][j]
-// (kind 0: B, 1: C; 4 steps; the group's 2 states), one per lane of a 16-lane
-// row: each lane reads one float per quad, and the multiply (B) and the fma
-// (C) that use a value broadcast it from its lane with row_newbcast. Groups
-// are kBCGroup2 floats apart (16 banks): the two half-waves' groups fall on
-// disjoint banks, and the two rows of a half-wave read the same 16 floats.
-constexpr int kBCGroup2 = kQuads * 16 + 16;
+// Two states per lane (NPL 2): B and C reach the lanes by DPP row broadcasts
+// from a broadcast tile in the row layout (BCLayout::kRow): each lane of a
+// 16-lane row reads one float per quad, and the multiply (B) and the fma (C)
+// that use a value broadcast it from its lane with row_newbcast. The two
+// rows of a half-wave read the same 16 floats.
 __host__ __device__ constexpr int fwd_bc_floats(int G, int NPL) {
   return NPL == 2 ? 2 * G * kBCGroup2 : 2 * bc_tile_floats(2 * G, NPL);
 }
@@ -95,47 +92,6 @@ __host__ __device__ constexpr int fwd_buf_floats(int G, int NPL) {
          + fwd_bc_floats(G, NPL)        // B, C tiles
          + G * kCH * kSteps;            // per-wave y partials (both half-waves added)
 }
-
-// Staging of 16 rows of B and C (fp32 or bf16, rows ld apart) into the
-// broadcast tile of the two-state plans (see kBCGroup2): thread tid moves
-// tile elements tid, tid + nthreads, ... (PERS of them), state fastest, of
-// both B and C. Padded states and steps past T are zero.
-template <int PERS, int ES = 4>
-struct BCRowLoader {
-  unsigned src[PERS];  // byte offset in the sub-chunk's global [16][ld] block, or kOOB
-  int dst[PERS];       // B's slot in the tile (C's is 8 further), or -1
-  int tid, nthreads, ntile;
-  int w0;
-  __device__ __forceinline__ BCRowLoader(int tid_, int nthreads_, int N, int NP, int ld)
-      : tid(tid_), nthreads(nthreads_), ntile(kSteps * NP),
-        w0(__builtin_amdgcn_readfirstlane(tid_) & ~63) {
-#pragma unroll
-    for (int i = 0; i < PERS; ++i) {
-      const int e = tid + i * nthreads;       // tile element (k, n), n fastest
-      const int k = e / NP, n = e % NP;
-      const bool in_tile = e < kSteps * NP;
-      src[i] = (in_tile && n < N) ? (unsigned)ES * (unsigned)(k * ld + n) : kOOB;
-      dst[i] = in_tile ? (n / 2) * kBCGroup2 + (k / 4) * 16 + (k % 4) * 2 + (n % 2) : -1;
-    }
-  }
-  __device__ __forceinline__ void load(float (&v)[PERS], const GBuf& g) const {
-#pragma unroll
-    for (int i = 0; i < PERS; ++i) v[i] = ld_elem<ES>(g, src[i]);
-  }
-  __device__ __forceinline__ bool valid(int i) const {
-    if ((i + 1) * nthreads <= ntile) return true;
-    if (ntile % 64 == 0) return w0 + i * nthreads < ntile;
-    return dst[i] >= 0;
-  }
-  // kind 0 (B) or 1 (C)
-  __device__ __forceinline__ void store(float* tile, const float (&v)[PERS], int kind) const {
-#pragma unroll
-    for (int i = 0; i < PERS; ++i) {
-      if (valid(i)) tile[dst[i] + 8 * kind] = v[i];
-      asm volatile("" ::"v"(v[i]));
-    }
-  }
-};
 
 // u[s][j] = B * bx[s] for the quad's 4 steps and 2 states, B broadcast from
 // lane 2s + j of the row's value r (read from the broadcast tile). The
