@@ -125,8 +125,8 @@ constexpr int kSweepMax = 4;
 // odd channel hold their two states in swapped order, and the dB / dC
 // products are summed over each 16-lane row in registers (pair_sum_xor1, then
 // row_partial_pairs: each lane reads its partner channel's dt * x and dy too).
-// Such kernels stage B and C in a quad broadcast tile (BCLayout::kQuad, one
-// 128-bit read per lane and quad) and take each value from the right lane of
+// Such kernels stage B and C in a quad broadcast tile (BCLayout::kQuad, two
+// 64-bit reads per lane and quad) and take each value from the right lane of
 // the quad with quad_perm DPP (qp_get, qp_fmac), which serves both state
 // orders. The two rows of a half-wave are then added in the finishing step (RP: the
 // kernels without the in-kernel sweep, which keep two row partials per block
@@ -148,7 +148,7 @@ __host__ __device__ constexpr bool bwd_row_partial(int NPL, bool CARRY, int SWEE
 // One staging buffer (the kernel keeps two) and the single-buffered rest.
 __host__ __device__ constexpr int bwd_buf_floats(int G, int NPL, bool rl = false) {
   return 4 * kCH * kSteps               // dt, dy, x, dt*x (channel-major)
-         + (rl ? 2 * G * kBCGroup2      // B, C quad broadcast tile
+         + (rl ? 2 * G * kBCGroupQ      // B, C quad broadcast tile
                : 2 * bc_tile_floats(2 * G, NPL));   // B, C tiles
 }
 __host__ __device__ constexpr int bwd_lds_floats(int G, int NPL, bool rl = false,
@@ -298,7 +298,10 @@ bwd_kernel(BwdArgs a) {
     u[j] = opaque_copy(u[j]);
     an[j] = opaque_copy(an[j]);
   }
-  float sdt_acc = 0.f;   // CARRY: sum of dt over the segment
+  // CARRY: the sum of dt over the segment, per staging task (the dt of 4
+  // steps of one channel as staged), added over the channels' tasks at the
+  // end: a quarter of the adds that every lane summing its steps would take.
+  float sdt_part = 0.f;
 
   const size_t row0 = (size_t)b * T;
   // Only the gated kernels read dt, B, C from (and write ddt into) column
@@ -377,6 +380,10 @@ bwd_kernel(BwdArgs a) {
   auto store_sub = [&](int j, int ci) {   // staging registers (chunk ci) -> buffer j
     float* s0 = lds + j * BUF;
     if constexpr (GATED) qdt.gate(pd, in_len(ci), a.dt_lo, a.dt_span, gbias);
+    if constexpr (CARRY) {
+#pragma unroll
+      for (int f = 0; f < PER; ++f) sdt_part += (pd[f].x + pd[f].y) + (pd[f].z + pd[f].w);
+    }
     ql.store_cm(s0, pd);
     ql.store_cm(s0 + oDY, py);
     if constexpr (!CARRY) ql.store_cm(s0 + oX, px);
@@ -428,7 +435,7 @@ bwd_kernel(BwdArgs a) {
         s1a += v1.x; s1b += v1.y;
         s2a += v2.x; s2b += v2.y;
       }
-      // dx, ddt, dB/dC partials: written once, not read again here (NT).
+      // dx, ddt: written once, not read again here (NT).
       st_elem<ES, kStream>(gdx, t0v * s1a, o0);
       st_elem<ES, kStream>(gdx, t1v * s1b, o1);
       float g0 = __builtin_fmaf(x0, s1a, -s2a), g1 = __builtin_fmaf(x1, s1b, -s2b);
@@ -467,8 +474,11 @@ bwd_kernel(BwdArgs a) {
         gbs.atomic_add(vb, o);
         gcs.atomic_add(vc, o);
       } else {
-        gbs.st<kStream>(vb, o);
-        gcs.st<kStream>(vc, o);
+        // plain stores: the reduction kernel reads the partials right after
+        // this kernel, and they are then still cached (measured: 11.9 ->
+        // 11.1 us for its 50 MB at 16x512x1536x16 against non-temporal ones)
+        gbs.st(vb, o);
+        gcs.st(vc, o);
       }
     }
   };
@@ -569,7 +579,7 @@ bwd_kernel(BwdArgs a) {
       const float* s0 = lds + (k & 1) * BUF;
       const float* gB = s0 + oB + q * bc_group_floats(NPL);
       const float* gC = s0 + oC + q * bc_group_floats(NPL);
-      const float* gQ = s0 + oB + q * kBCGroup2 + (lane & 3) * 4;   // RL
+      const float* gQ = s0 + oB + q * kBCGroupQ + (lane & 3) * 2;   // RL
       if (it.first) {
         float h0[NPL];
 #pragma unroll
@@ -639,9 +649,10 @@ bwd_kernel(BwdArgs a) {
           f4_to(dysp, lds4(s0 + oDY + cm_quad(cp, m)));
           f4_to(dtxsp, lds4(s0 + oDTX + cm_quad(cp, m)));
         }
-        float4 qbc;   // RL: B and C of the quad broadcast tile
+        float2 qb, qc;   // RL: B and C of the quad broadcast tile
         if constexpr (RL) {
-          qbc = lds4(gQ + 16 * m);
+          qb = lds2(gQ + 16 * m);
+          qc = lds2(gQ + 16 * m + 8);
         } else {
           load_quad_rows<NPL>(Bq, gB, m);
           load_quad_rows<NPL>(Cq, gC, m);
@@ -656,14 +667,14 @@ bwd_kernel(BwdArgs a) {
           for (int j = 0; j < NPL; ++j) {
             if constexpr (RL) {
               gk[j] = u[j];
-              qp_fmac(gk[j], (s >> 1) ? qbc.w : qbc.z, dys[s], qp_sel(s, j));
+              qp_fmac(gk[j], (s >> 1) ? qc.y : qc.x, dys[s], qp_sel(s, j));
             } else {
               gk[j] = __builtin_fmaf(dys[s], Cq[s][j], u[j]);
             }
             u[j] = da[kk][j] * gk[j];
             const float qv = u[j] * (kk == 0 ? hc[j] : hs[kk - 1][j]);
             if constexpr (RL) {
-              const float br = (s >> 1) ? qbc.y : qbc.x;
+              const float br = (s >> 1) ? qb.y : qb.x;
               if (j == 0) s1 = qp_get(br, qp_sel(s, 0)) * gk[0];
               else qp_fmac(s1, br, gk[j], qp_sel(s, j));
             } else {
@@ -726,8 +737,9 @@ bwd_kernel(BwdArgs a) {
       const float* s0 = lds + (i & 1) * BUF;
       const float* gB = s0 + oB + q * bc_group_floats(NPL);
       const float* gC = s0 + oC + q * bc_group_floats(NPL);
-      // RL: this lane's 4 floats of each quad of the quad broadcast tile
-      const float* gQ = s0 + oB + q * kBCGroup2 + (lane & 3) * 4;
+      // RL: this lane's floats of each quad of the quad broadcast tile (B;
+      // C 8 further)
+      const float* gQ = s0 + oB + q * kBCGroupQ + (lane & 3) * 2;
 
       if constexpr (CARRY) {
         // The adjoint alone: G_t = dy_t C_t + dA_{t+1} G_{t+1}, dA formed on
@@ -740,7 +752,6 @@ bwd_kernel(BwdArgs a) {
           load_quad_rows<NPL>(Cq, gC, m);
 #pragma unroll
           for (int s = 3; s >= 0; --s) {
-            sdt_acc += dts[s];
 #pragma unroll
             for (int j = 0; j < NPL; ++j)
               u[j] = exp2_hw(dts[s] * a2[j]) * __builtin_fmaf(dys[s], Cq[s][j], u[j]);
@@ -798,9 +809,10 @@ bwd_kernel(BwdArgs a) {
           f4_to(dysp, lds4(s0 + oDY + cm_quad(cp, m)));
           f4_to(dtxsp, lds4(s0 + oDTX + cm_quad(cp, m)));
         }
-        float4 qbc;   // RL: B and C of the quad broadcast tile
+        float2 qb, qc;   // RL: B and C of the quad broadcast tile
         if constexpr (RL) {
-          qbc = lds4(gQ + 16 * m);
+          qb = lds2(gQ + 16 * m);
+          qc = lds2(gQ + 16 * m + 8);
         } else {
           load_quad_rows<NPL>(Bq, gB, m);
           load_quad_rows<NPL>(Cq, gC, m);
@@ -817,7 +829,7 @@ bwd_kernel(BwdArgs a) {
           for (int j = 0; j < NPL; ++j) {
             if constexpr (RL) {
               gk[j] = u[j];                                            // G_k
-              qp_fmac(gk[j], (s >> 1) ? qbc.w : qbc.z, dys[s], qp_sel(s, j));
+              qp_fmac(gk[j], (s >> 1) ? qc.y : qc.x, dys[s], qp_sel(s, j));
             } else {
               gk[j] = __builtin_fmaf(dys[s], Cq[s][j], u[j]);          // G_k
             }
@@ -826,7 +838,7 @@ bwd_kernel(BwdArgs a) {
             if constexpr (RL) {
               // G_k . B_k: the first product a DPP multiply, as the fma
               // into 0 of the other plans rounds it
-              const float br = (s >> 1) ? qbc.y : qbc.x;
+              const float br = (s >> 1) ? qb.y : qb.x;
               if (j == 0) s1 = qp_get(br, qp_sel(s, 0)) * gk[0];
               else qp_fmac(s1, br, gk[j], qp_sel(s, j));
             } else {
@@ -890,7 +902,18 @@ bwd_kernel(BwdArgs a) {
   if constexpr (CARRY) {
     // L_s = dA_a * G_a, a the segment's first step: u after the walk.
     store_states<NPL>(GBuf(a.carryL + slot * slice, slice_bytes), st_lane, nvalid, u, sw);
-    if (q == 0 && act) a.carrySdt[slot * D + d] = sdt_acc;
+    // The staging tasks' sums of dt, channel tid % 32 each (NT a multiple of
+    // 32; threads without a task hold 0), added per channel in a fixed
+    // order. The loop ended on a barrier: LDS is free.
+    static_assert(NT % kCH == 0, "staging tasks keep their channel");
+    lds[tid] = sdt_part;
+    __syncthreads();
+    if (q == 0 && act) {
+      float sdt = 0.f;
+#pragma unroll
+      for (int r = 0; r < NT / kCH; ++r) sdt += lds[r * kCH + c];
+      a.carrySdt[slot * D + d] = sdt;
+    }
     return;
   }
   finalize(last_par, chunk_len(c_lo), sdx.at(c_lo), sddt.at(c_lo), sBsum.at(c_lo),

@@ -37,7 +37,7 @@ MHS_FOR_PLANS(MHS_BWD_ATOM_INST, extern, 2)
 
 namespace {
 
-constexpr int kVersion = (0 << 16) | (6 << 8) | 0;   // 0.6: relabelled channel sums, DPP-broadcast B/C
+constexpr int kVersion = (0 << 16) | (7 << 8) | 0;   // 0.7: quad-broadcast B/C and DPP partner products in the backward
 
 thread_local char g_err[512] = "";
 

@@ -709,16 +709,20 @@ struct RowLoader {
 };
 
 // Broadcast tiles of B and C for two states per lane: per state group q
-// and quad m, 16 floats (the group's 2 states x 4 steps x {B, C}); groups
-// kBCGroup2 floats apart (16 banks), so that the two half-waves' groups
-// fall on disjoint banks. Two layouts of the 16:
+// and quad m, 16 floats (the group's 2 states x 4 steps x {B, C}). Two
+// layouts:
 // * kRow (the forward's row broadcasts): [kind][k % 4][n % 2], one float
-//   per lane of a 16-lane row;
-// * kQuad (the backward's quad broadcasts): [(k % 2) * 2 + n % 2][kind * 2 +
-//   (k % 4) / 2], so that lane p of a quad reads its 4 floats with one
-//   128-bit load and holds B of steps 4m + (p >> 1) and 4m + 2 + (p >> 1),
-//   then C of the same two steps, each of state n0 + (p & 1) (qp_get).
+//   per lane of a 16-lane row; groups kBCGroup2 floats apart (16 banks),
+//   so that the two half-waves' groups fall on disjoint banks;
+// * kQuad (the backward's quad broadcasts): [kind][(k % 2) * 2 + n % 2][(k
+//   % 4) / 2], so that lane p of a quad reads 2 floats of B and 2 of C with
+//   two 64-bit loads and holds B (then C) of steps 4m + (p >> 1) and 4m + 2
+//   + (p >> 1), each of state n0 + (p & 1) (qp_get); groups kBCGroupQ
+//   floats apart (8 banks): the staging writes of a wave (8 groups x 8
+//   contiguous floats) then hit 64 distinct banks and the half-waves' reads
+//   disjoint ones.
 constexpr int kBCGroup2 = kQuads * 16 + 16;
+constexpr int kBCGroupQ = kQuads * 16 + 8;
 enum class BCLayout { kRow, kQuad };
 
 // Staging of 16 rows of B and C (fp32 or bf16, rows ld apart) into such a
@@ -728,10 +732,10 @@ enum class BCLayout { kRow, kQuad };
 template <int PERS, int ES = 4, BCLayout L = BCLayout::kRow>
 struct BCRowLoader {
   unsigned src[PERS];  // byte offset in the sub-chunk's global [16][ld] block, or kOOB
-  int dst[PERS];       // B's slot in the tile (C's is kKind further), or -1
+  int dst[PERS];       // B's slot in the tile (C's is 8 further), or -1
   int tid, nthreads, ntile;
   int w0;
-  static constexpr int kKind = L == BCLayout::kRow ? 8 : 2;
+  static constexpr int kGroup = L == BCLayout::kRow ? kBCGroup2 : kBCGroupQ;
   __device__ __forceinline__ BCRowLoader(int tid_, int nthreads_, int N, int NP, int ld)
       : tid(tid_), nthreads(nthreads_), ntile(kSteps * NP),
         w0(__builtin_amdgcn_readfirstlane(tid_) & ~63) {
@@ -742,8 +746,8 @@ struct BCRowLoader {
       const bool in_tile = e < kSteps * NP;
       src[i] = (in_tile && n < N) ? (unsigned)ES * (unsigned)(k * ld + n) : kOOB;
       const int in_quad = L == BCLayout::kRow ? (k % 4) * 2 + (n % 2)
-                                              : ((k % 2) * 2 + (n % 2)) * 4 + (k % 4) / 2;
-      dst[i] = in_tile ? (n / 2) * kBCGroup2 + (k / 4) * 16 + in_quad : -1;
+                                              : ((k % 2) * 2 + (n % 2)) * 2 + (k % 4) / 2;
+      dst[i] = in_tile ? (n / 2) * kGroup + (k / 4) * 16 + in_quad : -1;
     }
   }
   __device__ __forceinline__ void load(float (&v)[PERS], const GBuf& g) const {
@@ -759,7 +763,7 @@ struct BCRowLoader {
   __device__ __forceinline__ void store(float* tile, const float (&v)[PERS], int kind) const {
 #pragma unroll
     for (int i = 0; i < PERS; ++i) {
-      if (valid(i)) tile[dst[i] + kKind * kind] = v[i];
+      if (valid(i)) tile[dst[i] + 8 * kind] = v[i];
       asm volatile("" ::"v"(v[i]));
     }
   }
@@ -767,8 +771,8 @@ struct BCRowLoader {
 
 // Quad broadcasts from a kQuad tile. Lane p of a quad holding its two states
 // in swapped order when p is odd (register j: state n0 + (j ^ (p & 1))), the
-// value of step 4m + s, register j, is in the quad's register (s >> 1) (B;
-// C: 2 + (s >> 1)) of lane ((s & 1) << 1) | (j ^ (p & 1)): sel = (s & 1) * 2
+// value of step 4m + s, register j, is in the quad's B (or C) register
+// (s >> 1) of lane ((s & 1) << 1) | (j ^ (p & 1)): sel = (s & 1) * 2
 // + j picks one of four quad_perm patterns, [0,1,0,1], [1,0,1,0], [2,3,2,3]
 // and [3,2,3,2]. With sel a constant after unrolling, each switch below
 // folds to one case.

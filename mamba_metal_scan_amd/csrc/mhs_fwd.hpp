@@ -219,9 +219,17 @@ fwd_kernel(FwdArgs a) {
     rl.load(pb, sB.at(i));
     if constexpr (!NOY) rl.load(pc, sC.at(i));
   };
+  // FCARRY: the sum of dt over the segment, per staging task (the dt of 4
+  // steps of one channel as staged), added over the channels' tasks at the
+  // end: a quarter of the adds that every lane summing its steps would take.
+  float sdt_part = 0.f;
   auto store_sub = [&](int i) {           // staging registers -> LDS buffer i&1
     float* buf = lds + (i & 1) * BUF;
     if constexpr (GATED) qdt.gate(pd, sub_len(i), a.dt_lo, a.dt_span, gbias);
+    if constexpr (FCARRY) {
+#pragma unroll
+      for (int f = 0; f < PER; ++f) sdt_part += (pd[f].x + pd[f].y) + (pd[f].z + pd[f].w);
+    }
     ql.store_cm(buf, pd);
     ql.store_cm_product(buf + kCH * kSteps, pd, px);
     if constexpr (BCAST) {
@@ -305,7 +313,6 @@ fwd_kernel(FwdArgs a) {
   }
 #pragma unroll
   for (int j = 0; j < NPL; ++j) h[j] = opaque_copy(h[j]);   // h may come from a load
-  float sdt_acc = 0.f;   // FCARRY: sum of dt over the segment
   constexpr int kDone = 0x7FFFFFFF;
   // Step count after the next checkpoint, and its slot.
   int next_ck = a.ckpt != nullptr ? min((t_beg / a.K + 1) * a.K, T) : kDone;
@@ -365,7 +372,6 @@ fwd_kernel(FwdArgs a) {
       float da[4][NPL], u[4][NPL];
 #pragma unroll
       for (int s = 0; s < 4; ++s) {
-        if constexpr (FCARRY) sdt_acc += dts[s];
 #pragma unroll
         for (int j = 0; j < NPL; ++j) {
           da[s][j] = exp2_hw(dts[s] * a2[j]);
@@ -433,7 +439,18 @@ fwd_kernel(FwdArgs a) {
   if constexpr (FCARRY) {
     const size_t slot = (size_t)seg * a.batch + b;
     store_states<NPL>(GBuf(a.carryH + slot * ck_stride, slice_bytes), ck_lane, nvalid, h);
-    if (q == 0 && act) a.carrySdt[slot * D + d] = sdt_acc;
+    // The staging tasks' sums of dt, channel tid % 32 each (NT a multiple of
+    // 32; threads without a task hold 0), added per channel in a fixed
+    // order. The loop ended on a barrier: LDS is free.
+    static_assert(NT % kCH == 0, "staging tasks keep their channel");
+    lds[tid] = sdt_part;
+    __syncthreads();
+    if (q == 0 && act) {
+      float sdt = 0.f;
+#pragma unroll
+      for (int r = 0; r < NT / kCH; ++r) sdt += lds[r * kCH + c];
+      a.carrySdt[slot * D + d] = sdt;
+    }
     return;
   }
   // KALIGNED: the last checkpoint (slot nchunk-1) is the state after step T-1,
