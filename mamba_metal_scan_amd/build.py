@@ -166,7 +166,8 @@ def emit_assembly(out_dir: Path) -> Path:
 # bwd_sweep_lds_floats in mhs_bwd.hpp) with the header constants below, which
 # tests/test_build.py reads back from the headers.
 K_CH, K_STEPS, K_BC_PAD, K_SWEEP_MAX = 32, 16, 4, 4
-K_BC_GROUP2 = 4 * 16 + 16        # kBCGroup2: a state group of a broadcast tile
+K_BC_GROUP2 = 4 * 16 + 16        # kBCGroup2: a state group of the row broadcast tile
+K_BC_GROUPQ = 4 * 16 + 8         # kBCGroupQ: a state group of the quad broadcast tile
 LDS_PER_CU = 160 * 1024          # gfx950
 VGPRS_PER_SIMD_LANE = 512        # wave64 VGPR file per SIMD lane (gfx950, no AGPR split used)
 
@@ -188,7 +189,7 @@ def scan_lds_bytes(kind: str, g: int, npl: int) -> int:
     rp = kind == "bwd" and npl == 2         # row-partial channel sums (bwd_row_partial)
     np_ = 2 * g * npl
     # B and C: the quad broadcast tile (rl) or the per-group tiles
-    bc = 2 * g * K_BC_GROUP2 if rl else 2 * _bc_tile_floats(2 * g, npl)
+    bc = 2 * g * K_BC_GROUPQ if rl else 2 * _bc_tile_floats(2 * g, npl)
     buf = 4 * K_CH * K_STEPS + bc
     sums = 4 * (K_STEPS * (16 if np_ <= 16 else 48) + 4) if rp else 2 * K_STEPS * np_
     floats = 2 * buf + g * 64 * K_STEPS + sums
