@@ -507,6 +507,42 @@ def traced_step_us(out_dir: str):
     return None
 
 
+def trace_spans(trace: str, n_steps: int):
+    """From a rocprofv3 kernel trace (run_kernel_trace.csv) of `bench.py
+    --steps n_steps --no-extra --no-train`: the timed steps' per-kernel
+    durations (us) and their launch spans (`spans`, None where the trace
+    does not have that shape). The timed steps are the last n_steps
+    (forward, backward, reduction) dispatch triples."""
+    import csv
+    durs: dict = {}
+    spans = None
+    if os.path.exists(trace):
+        rows = sorted(csv.DictReader(open(trace)), key=lambda r: int(r["Start_Timestamp"]))
+        # The timed steps' launches as the bench's events bracket them: the
+        # backward launch from bwd_kernel's start to bwd_reduce_kernel's end,
+        # and the idle gaps before each forward and each backward (markers).
+        scan = [(_short_kernel(r["Kernel_Name"]), int(r["Start_Timestamp"]),
+                 int(r["End_Timestamp"])) for r in rows
+                if _short_kernel(r["Kernel_Name"]) in ("fwd_kernel", "bwd_kernel",
+                                                       "bwd_reduce_kernel")]
+        end = len(scan)
+        steps = [scan[i:i + 3] for i in range(end - 3 * n_steps, end, 3)] if end > 0 else []
+        if steps and all([k[0] for k in st] == ["fwd_kernel", "bwd_kernel", "bwd_reduce_kernel"]
+                         for st in steps):
+            n = len(steps)
+            for st in steps:
+                for name, t0, t1 in st:
+                    durs.setdefault(name, []).append((t1 - t0) / 1e3)
+            spans = {"steps": n,
+                     "fwd_us": sum(st[0][2] - st[0][1] for st in steps) / n / 1e3,
+                     "bwd_launch_us": sum(st[2][2] - st[1][1] for st in steps) / n / 1e3,
+                     "gap_before_bwd_us": sum(st[1][1] - st[0][2] for st in steps) / n / 1e3,
+                     "gap_before_fwd_us": sum(b[0][1] - a[2][2] for a, b in zip(steps, steps[1:]))
+                     / max(n - 1, 1) / 1e3,
+                     "steps_with_gaps": sum(1 for st in steps if st[1][1] - st[0][2] > 1000)}
+    return durs, spans
+
+
 def pmc_summary(args) -> None:
     """Per-launch HBM traffic from two rocprofv3 --pmc passes (FETCH_SIZE, then
     WRITE_SIZE, KiB per dispatch), each scaled by what the counter reads for
@@ -522,34 +558,8 @@ def pmc_summary(args) -> None:
     shape = (args.batch, args.seqlen, args.d_inner, args.d_state)
     tag = shape_tag(*shape)
     nbytes = scan_bytes(*shape)
-    # Kernel-trace durations: the last `steps` dispatches of each kernel are
-    # those of bench.py's timed steps.
-    durs: dict = {}
-    spans = None
-    trace = os.path.join(args.pmc_summary, "kt", "run_kernel_trace.csv")
-    if os.path.exists(trace):
-        rows = sorted(csv.DictReader(open(trace)), key=lambda r: int(r["Start_Timestamp"]))
-        for r in rows:
-            durs.setdefault(_short_kernel(r["Kernel_Name"]), []).append(
-                (int(r["End_Timestamp"]) - int(r["Start_Timestamp"])) / 1e3)
-        # The timed steps' launches as the bench's events bracket them: the
-        # backward launch from bwd_kernel's start to bwd_reduce_kernel's end,
-        # and the idle gaps before each forward and each backward (markers).
-        scan = [(_short_kernel(r["Kernel_Name"]), int(r["Start_Timestamp"]),
-                 int(r["End_Timestamp"])) for r in rows
-                if _short_kernel(r["Kernel_Name"]) in ("fwd_kernel", "bwd_kernel",
-                                                       "bwd_reduce_kernel")]
-        steps = [scan[i:i + 3] for i in range(len(scan) - 3 * args.steps, len(scan), 3)]
-        if steps and all([k[0] for k in st] == ["fwd_kernel", "bwd_kernel", "bwd_reduce_kernel"]
-                         for st in steps):
-            n = len(steps)
-            spans = {"steps": n,
-                     "fwd_us": sum(st[0][2] - st[0][1] for st in steps) / n / 1e3,
-                     "bwd_launch_us": sum(st[2][2] - st[1][1] for st in steps) / n / 1e3,
-                     "gap_before_bwd_us": sum(st[1][1] - st[0][2] for st in steps) / n / 1e3,
-                     "gap_before_fwd_us": sum(b[0][1] - a[2][2] for a, b in zip(steps, steps[1:]))
-                     / max(n - 1, 1) / 1e3,
-                     "steps_with_gaps": sum(1 for st in steps if st[1][1] - st[0][2] > 1000)}
+    durs, spans = trace_spans(os.path.join(args.pmc_summary, "kt", "run_kernel_trace.csv"),
+                              args.steps)
     kernels = {}
     for kern in ("fwd_kernel", "bwd_kernel", "bwd_reduce_kernel"):
         if (kern, "FETCH_SIZE") not in mean:

@@ -69,3 +69,36 @@ def test_kernel_labels_name_each_pass():
         "backward reduction"
     assert bench.kernel_label("void mhs::zero_grads_kernel<0>(float*)") == "zero fill"
     assert bench.kernel_label("__amd_rocclr_copyBuffer") == "copy"
+
+
+def test_trace_spans_of_the_timed_steps(tmp_path):
+    """bench.py's kernel-trace summary: the timed steps' launch spans are
+    those of the last (forward, backward, reduction) dispatch triples (a
+    synthetic trace: 2 warm-up steps, then 3 timed steps of fwd 50 us, bwd
+    100 + reduce 12 us with 1 us between them and a 4 us marker gap before
+    each backward)."""
+    names = {"fwd": "void mhs::fwd_kernel<2, 4, 3, true, false, 0, 4>(mhs::FwdArgs)",
+             "bwd": "void mhs::bwd_kernel<2, 4, 3, false, false, 4, false, 0>(mhs::BwdArgs)",
+             "red": "void mhs::bwd_reduce_kernel<4>(float const*, float const*)"}
+    rows, t = [], 0
+
+    def launch(kind, us, gap=1.0):
+        nonlocal t
+        t += int(gap * 1000)
+        rows.append((names[kind], t, t + int(us * 1000)))
+        t += int(us * 1000)
+    for _ in range(2):                 # warm-up steps (not counted)
+        launch("fwd", 60); launch("bwd", 130); launch("red", 15)
+    for _ in range(3):                 # timed steps
+        launch("fwd", 50, gap=2); launch("bwd", 100, gap=4); launch("red", 12)
+    path = tmp_path / "run_kernel_trace.csv"
+    with open(path, "w") as f:
+        f.write("Kernel_Name,Start_Timestamp,End_Timestamp\n")
+        for name, t0, t1 in rows:
+            f.write(f'"{name}",{t0},{t1}\n')
+    durs, spans = bench.trace_spans(str(path), 3)
+    assert spans["steps"] == 3 and spans["fwd_us"] == 50 and spans["bwd_launch_us"] == 113
+    assert spans["gap_before_bwd_us"] == 4 and spans["gap_before_fwd_us"] == 2
+    assert spans["steps_with_gaps"] == 3
+    assert durs["bwd_kernel"] == [100.0] * 3 and durs["fwd_kernel"] == [50.0] * 3
+    assert bench.trace_spans(str(path), 6)[1] is None   # not 6 timed steps
