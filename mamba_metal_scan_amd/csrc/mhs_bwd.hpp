@@ -427,13 +427,20 @@ bwd_kernel(BwdArgs a) {
       const unsigned od1 = okc ? od0 + (unsigned)ES * (unsigned)ld_ddt : kOOB;
       const float2 xv = lds2(tx + cm_elem(cc, k)), dtv = lds2(tdt + cm_elem(cc, k));
       const float x0 = xv.x, x1 = xv.y, t0v = dtv.x, t1v = dtv.y;
+      // The waves' partials summed in order from wave 0's (not from 0.f:
+      // an add of zero that the compiler keeps, for the sign of zero).
       float s1a = 0.f, s1b = 0.f, s2a = 0.f, s2b = 0.f;
 #pragma unroll
       for (int w = 0; w < G; ++w) {
         const float2 v1 = lds2(tS + w * 64 * kSteps + ((k / 2) * 64 + cc) * 2);
         const float2 v2 = lds2(tS + w * 64 * kSteps + ((k / 2) * 64 + kCH + cc) * 2);
-        s1a += v1.x; s1b += v1.y;
-        s2a += v2.x; s2b += v2.y;
+        if (w == 0) {
+          s1a = v1.x; s1b = v1.y;
+          s2a = v2.x; s2b = v2.y;
+        } else {
+          s1a += v1.x; s1b += v1.y;
+          s2a += v2.x; s2b += v2.y;
+        }
       }
       // dx, ddt: written once, not read again here (NT).
       st_elem<ES, kStream>(gdx, t0v * s1a, o0);
