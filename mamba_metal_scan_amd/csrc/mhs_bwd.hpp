@@ -128,8 +128,8 @@ constexpr int kSweepMax = 4;
 // Such kernels stage B and C in a quad broadcast tile (BCLayout::kQuad, two
 // 64-bit reads per lane and quad) and take each value from the right lane of
 // the quad with quad_perm DPP (qp_get, qp_fmac), which serves both state
-// orders. The two rows of a half-wave are then added in the finishing step (RP: the
-// kernels without the in-kernel sweep, which keep two row partials per block
+// orders. The two rows of a half-wave are then added in the finishing step
+// (RP: the kernels without the in-kernel sweep, which keep two row partials per block
 // sum: tile [row][kind][16 steps][rp_step_floats], the kinds rp_kind_floats
 // apart and the rows twice that, so that the 32 lanes of a half-wave that
 // write one step pair's partials hit 32 distinct banks), or in registers by one more

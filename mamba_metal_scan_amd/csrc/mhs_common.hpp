@@ -778,7 +778,7 @@ struct BCRowLoader {
 // folds to one case.
 __host__ __device__ constexpr int qp_sel(int s, int j) { return (s & 1) * 2 + j; }
 // The broadcast value itself (the compiler folds the DPP read into the
-// multiply or add that uses it).
+// multiply that uses it: v_mul_f32_dpp).
 __device__ __forceinline__ float qp_get(float r, int sel) {
   switch (sel) {
     case 0: return dpp_get<0x44>(r);
@@ -790,8 +790,8 @@ __device__ __forceinline__ float qp_get(float r, int sel) {
 // acc += (the broadcast value of r) * x, one v_fmac_f32_dpp (the compiler
 // does not fold a DPP read into v_fmac). r must come from an LDS load, not
 // from a VALU instruction: a DPP read of a VGPR needs 2 wait states after a
-// VALU write of it, which the compiler does not check inside the asm (the
-// ISA check of the build keeps it so).
+// VALU write of it, which the compiler does not check inside the asm
+// (build.py's dpp_hazards rejects compiled assembly where it fails).
 __device__ __forceinline__ void qp_fmac(float& acc, float r, float x, int sel) {
   switch (sel) {
     case 0:
