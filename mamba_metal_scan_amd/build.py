@@ -166,6 +166,7 @@ def emit_assembly(out_dir: Path) -> Path:
 # bwd_sweep_lds_floats in mhs_bwd.hpp) with the header constants below, which
 # tests/test_build.py reads back from the headers.
 K_CH, K_STEPS, K_BC_PAD, K_SWEEP_MAX = 32, 16, 4, 4
+K_CM_ROW = 20                    # kCmRow: a row of the backward's padded channel-major tiles
 K_BC_GROUP2 = 4 * 16 + 16        # kBCGroup2: a state group of the row broadcast tile
 K_BC_GROUPQ = 4 * 16 + 8         # kBCGroupQ: a state group of the quad broadcast tile
 LDS_PER_CU = 160 * 1024          # gfx950
@@ -190,7 +191,8 @@ def scan_lds_bytes(kind: str, g: int, npl: int) -> int:
     np_ = 2 * g * npl
     # B and C: the quad broadcast tile (rl) or the per-group tiles
     bc = 2 * g * K_BC_GROUPQ if rl else 2 * _bc_tile_floats(2 * g, npl)
-    buf = 4 * K_CH * K_STEPS + bc
+    # dt, dy, x, dt*x: padded channel-major tiles, swizzled in the carry pass
+    buf = 4 * K_CH * (K_STEPS if kind == "bwd_carry" else K_CM_ROW) + bc
     sums = 4 * (K_STEPS * (16 if np_ <= 16 else 48) + 4) if rp else 2 * K_STEPS * np_
     floats = 2 * buf + g * 64 * K_STEPS + sums
     if kind == "bwd_sweep":

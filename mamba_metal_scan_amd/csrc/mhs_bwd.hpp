@@ -145,15 +145,24 @@ __host__ __device__ constexpr bool bwd_row_partial(int NPL, bool CARRY, int SWEE
   return bwd_relabel(NPL, CARRY) && SWEEP == 0;
 }
 
+// The layout of the backward's channel-major tiles (dt, dy, x, dt*x): padded
+// in the gradient kernels, whose walk switches staging buffers every chunk
+// (one address add per tile row and switch, not per quad); swizzled in the
+// adjoint-carry pass, whose occupancy its LDS sets (4 blocks per CU at d_state
+// 16, 3 with the padding).
+__host__ __device__ constexpr CmLayout bwd_cm(bool carry) {
+  return carry ? CmLayout::kSwizzled : CmLayout::kPadded;
+}
+
 // One staging buffer (the kernel keeps two) and the single-buffered rest.
-__host__ __device__ constexpr int bwd_buf_floats(int G, int NPL, bool rl = false) {
-  return 4 * kCH * kSteps               // dt, dy, x, dt*x (channel-major)
+__host__ __device__ constexpr int bwd_buf_floats(int G, int NPL, bool rl, bool carry) {
+  return 4 * (carry ? cml_tile_floats<CmLayout::kSwizzled>(kCH)
+                    : cml_tile_floats<CmLayout::kPadded>(kCH))   // dt, dy, x, dt*x
          + (rl ? 2 * G * kBCGroupQ      // B, C quad broadcast tile
                : 2 * bc_tile_floats(2 * G, NPL));   // B, C tiles
 }
-__host__ __device__ constexpr int bwd_lds_floats(int G, int NPL, bool rl = false,
-                                                 bool rp = false) {
-  return 2 * bwd_buf_floats(G, NPL, rl)
+__host__ __device__ constexpr int bwd_lds_floats(int G, int NPL, bool rl, bool rp, bool carry) {
+  return 2 * bwd_buf_floats(G, NPL, rl, carry)
          + G * 64 * kSteps                       // (s1, s2) per wave
          + (rp ? 4 * rp_kind_floats(2 * G * NPL)  // dB, dC row partials of a chunk
                : 2 * kSteps * 2 * G * NPL);      // dB, dC block sums of a chunk
@@ -161,7 +170,7 @@ __host__ __device__ constexpr int bwd_lds_floats(int G, int NPL, bool rl = false
 // The swept kernels (SWEEP > 0) keep each lane's swept states in LDS after
 // that: kSweepMax slots of NPL floats per thread, [slot][thread][NPL].
 __host__ __device__ constexpr int bwd_sweep_lds_floats(int G, int NPL) {
-  return bwd_lds_floats(G, NPL, bwd_relabel(NPL, false), false) + kSweepMax * 64 * G * NPL;
+  return bwd_lds_floats(G, NPL, bwd_relabel(NPL, false), false, false) + kSweepMax * 64 * G * NPL;
 }
 
 // GATED: see BwdArgs. The staging threads gate each dt once per block as they
@@ -185,7 +194,9 @@ bwd_kernel(BwdArgs a) {
   constexpr int NP = 2 * G * NPL;
   constexpr bool RL = bwd_relabel(NPL, CARRY);
   constexpr bool RP = bwd_row_partial(NPL, CARRY, SWEEP);
-  constexpr int BUF = bwd_buf_floats(G, NPL, RL);
+  constexpr int BUF = bwd_buf_floats(G, NPL, RL, CARRY);
+  constexpr CmLayout kBwdCm = bwd_cm(CARRY);
+  constexpr int kBwdCmTile = cml_tile_floats<kBwdCm>(kCH);
   constexpr int PER = (kCH * kQuads + NT - 1) / NT;
   constexpr int PERS = (kSteps * NP + NT - 1) / NT;
   constexpr int FT = (kSteps / 2 * kCH + NT - 1) / NT;      // dx/ddt tasks per thread
@@ -220,13 +231,18 @@ bwd_kernel(BwdArgs a) {
   const int c_lo = seg * a.cps;                      // this block's chunks [c_lo, c_hi)
   const int c_hi = min(c_lo + a.cps, nch);
 
-  float* tS = lds + 2 * BUF;                          // [G][64][16]
+  constexpr int RPS = rp_step_floats(NP), RPK = rp_kind_floats(NP);
+  // LDS: the (s1, s2) tile tS at 0 (its finishing-step reads then take their
+  // offsets from one loop-invariant register: read2's 8-bit fields reach the
+  // four waves' partials), the dB / dC tile tDBC, then the two staging
+  // buffers (sbuf).
+  float* tS = lds;                                    // [8 pairs][G][64][2]
   float* tDBC = tS + G * 64 * kSteps;                 // [2][16][NP], RP: [2][2][16][RPS]
+  float* sbuf = tDBC + (RP ? 4 * RPK : 2 * kSteps * NP);
   // Staging buffer j: dt, dy, x (channel-major), B, C (per lane group; with
   // RL one quad broadcast tile of both, at oB).
-  constexpr int oDY = kCH * kSteps, oX = 2 * kCH * kSteps, oDTX = 3 * kCH * kSteps,
-                oB = 4 * kCH * kSteps, oC = oB + bc_tile_floats(2 * G, NPL);
-  constexpr int RPS = rp_step_floats(NP), RPK = rp_kind_floats(NP);
+  constexpr int oDY = kBwdCmTile, oX = 2 * kBwdCmTile, oDTX = 3 * kBwdCmTile,
+                oB = 4 * kBwdCmTile, oC = oB + bc_tile_floats(2 * G, NPL);
   // The reduce-scatter leaves lane `lane` with the total of product rs_index:
   // products are numbered kind * 2NPL + slot * NPL + j (kind 0: dB, 1: dC;
   // slot: step k + slot; j: state n0 + j of this half-wave's group). With RL
@@ -378,16 +394,17 @@ bwd_kernel(BwdArgs a) {
   const float* ck_next = ck_row + (ptrdiff_t)(c_hi - 3) * (ptrdiff_t)slice;
   int ck_i = c_hi - 3;
   auto store_sub = [&](int j, int ci) {   // staging registers (chunk ci) -> buffer j
-    float* s0 = lds + j * BUF;
+    float* s0 = sbuf + j * BUF;
     if constexpr (GATED) qdt.gate(pd, in_len(ci), a.dt_lo, a.dt_span, gbias);
     if constexpr (CARRY) {
 #pragma unroll
       for (int f = 0; f < PER; ++f) sdt_part += (pd[f].x + pd[f].y) + (pd[f].z + pd[f].w);
     }
-    ql.store_cm(s0, pd);
-    ql.store_cm(s0 + oDY, py);
-    if constexpr (!CARRY) ql.store_cm(s0 + oX, px);
-    if constexpr (!CARRY) ql.store_cm_product(s0 + oDTX, pd, px);   // dt * x, once per block
+    ql.template store_cm<kBwdCm>(s0, pd);
+    ql.template store_cm<kBwdCm>(s0 + oDY, py);
+    if constexpr (!CARRY) ql.template store_cm<kBwdCm>(s0 + oX, px);
+    if constexpr (!CARRY)   // dt * x, once per block
+      ql.template store_cm_product<kBwdCm>(s0 + oDTX, pd, px);
     if constexpr (RL) {
       rlq.store(s0 + oB, pb, 0);
       rlq.store(s0 + oB, pc, 1);
@@ -412,8 +429,8 @@ bwd_kernel(BwdArgs a) {
   // tiles.
   auto finalize = [&](int j, int len, const GBuf& gdx, const GBuf& gddt, const GBuf& gbs,
                       const GBuf& gcs) {
-    const float* tx = lds + j * BUF + oX;
-    const float* tdt = lds + j * BUF;
+    const float* tx = sbuf + j * BUF + oX;
+    const float* tdt = sbuf + j * BUF;
 #pragma unroll
     for (int f = 0; f < FT; ++f) {
       const int task0 = tid + f * NT;
@@ -425,15 +442,16 @@ bwd_kernel(BwdArgs a) {
       const unsigned o1 = okc ? o0 + (unsigned)ES * (unsigned)D : kOOB;
       const unsigned od0 = okc ? (unsigned)ES * ((unsigned)k * (unsigned)ld_ddt + cc) : kOOB;
       const unsigned od1 = okc ? od0 + (unsigned)ES * (unsigned)ld_ddt : kOOB;
-      const float2 xv = lds2(tx + cm_elem(cc, k)), dtv = lds2(tdt + cm_elem(cc, k));
+      const float2 xv = lds2(tx + cml_elem<kBwdCm>(cc, k));
+      const float2 dtv = lds2(tdt + cml_elem<kBwdCm>(cc, k));
       const float x0 = xv.x, x1 = xv.y, t0v = dtv.x, t1v = dtv.y;
       // The waves' partials summed in order from wave 0's (not from 0.f:
       // an add of zero that the compiler keeps, for the sign of zero).
       float s1a = 0.f, s1b = 0.f, s2a = 0.f, s2b = 0.f;
 #pragma unroll
       for (int w = 0; w < G; ++w) {
-        const float2 v1 = lds2(tS + w * 64 * kSteps + ((k / 2) * 64 + cc) * 2);
-        const float2 v2 = lds2(tS + w * 64 * kSteps + ((k / 2) * 64 + kCH + cc) * 2);
+        const float2 v1 = lds2(tS + ((k / 2) * G + w) * 128 + cc * 2);
+        const float2 v2 = lds2(tS + ((k / 2) * G + w) * 128 + (kCH + cc) * 2);
         if (w == 0) {
           s1a = v1.x; s1b = v1.y;
           s2a = v2.x; s2b = v2.y;
@@ -566,7 +584,7 @@ bwd_kernel(BwdArgs a) {
     // this thread's LDS slot l (lanes contiguous: conflict-free 32 / 64 /
     // 128-bit accesses); registers are what the walk is short of.
     static_assert(SWEEP <= kSweepMax, "LDS slots for the swept states");
-    float* const tH = lds + bwd_lds_floats(G, NPL, RL, RP) + tid * NPL;
+    float* const tH = lds + bwd_lds_floats(G, NPL, RL, RP, false) + tid * NPL;
     auto h_slot = [&](int l) { return tH + l * NT * NPL; };
     Pos pos{cc_top, 0, n_top, cc_top == cc_lo ? lo_first : 0};
     const Item it0 = item_at(pos);
@@ -583,7 +601,7 @@ bwd_kernel(BwdArgs a) {
       const Item it = item_at(pos);
       const Pos pos1 = advance(pos);
       const Item it1 = item_at(pos1), it2 = item_at(advance(pos1));
-      const float* s0 = lds + (k & 1) * BUF;
+      const float* s0 = sbuf + (k & 1) * BUF;
       const float* gB = s0 + oB + q * bc_group_floats(NPL);
       const float* gC = s0 + oC + q * bc_group_floats(NPL);
       const float* gQ = s0 + oB + q * kBCGroupQ + (lane & 3) * 2;   // RL
@@ -607,8 +625,8 @@ bwd_kernel(BwdArgs a) {
       for (int m = 0; m < kQuads; ++m) {
         float dts[4], dtxs[4], Bq[4][NPL];
         float2 qb;   // RL: B of the quad broadcast tile
-        f4_to(dts, lds4(s0 + cm_quad(c, m)));
-        f4_to(dtxs, lds4(s0 + oDTX + cm_quad(c, m)));
+        f4_to(dts, lds4(s0 + cml_quad<kBwdCm>(c, m)));
+        f4_to(dtxs, lds4(s0 + oDTX + cml_quad<kBwdCm>(c, m)));
         if constexpr (RL) {
           qb = lds2(gQ + 16 * m);
         } else {
@@ -649,12 +667,12 @@ bwd_kernel(BwdArgs a) {
       for (int m = kQuads - 1; m >= 0; --m) {
         float dts[4], dys[4], dtxs[4], Bq[4][NPL], Cq[4][NPL], s1q[4], s2q[4];
         float dysp[4], dtxsp[4];   // RL: the partner channel's
-        f4_to(dts, lds4(s0 + cm_quad(c, m)));
-        f4_to(dys, lds4(s0 + oDY + cm_quad(c, m)));
-        f4_to(dtxs, lds4(s0 + oDTX + cm_quad(c, m)));
+        f4_to(dts, lds4(s0 + cml_quad<kBwdCm>(c, m)));
+        f4_to(dys, lds4(s0 + oDY + cml_quad<kBwdCm>(c, m)));
+        f4_to(dtxs, lds4(s0 + oDTX + cml_quad<kBwdCm>(c, m)));
         if constexpr (RL) {
-          f4_to(dysp, lds4(s0 + oDY + cm_quad(cp, m)));
-          f4_to(dtxsp, lds4(s0 + oDTX + cm_quad(cp, m)));
+          f4_to(dysp, lds4(s0 + oDY + cml_quad<kBwdCm>(cp, m)));
+          f4_to(dtxsp, lds4(s0 + oDTX + cml_quad<kBwdCm>(cp, m)));
         }
         float2 qb, qc;   // RL: B and C of the quad broadcast tile
         if constexpr (RL) {
@@ -711,9 +729,9 @@ bwd_kernel(BwdArgs a) {
                                                           __float_as_uint(s2q[s]), false, false);
           o[s] = __uint_as_float(sw[0]) + __uint_as_float(sw[1]);
         }
-        float* const ts = tS + wave * 64 * kSteps;
-        *reinterpret_cast<float2*>(ts + (2 * m * 64 + lane) * 2) = make_float2(o[0], o[1]);
-        *reinterpret_cast<float2*>(ts + ((2 * m + 1) * 64 + lane) * 2) = make_float2(o[2], o[3]);
+        float* const ts = tS + wave * 128 + lane * 2;
+        *reinterpret_cast<float2*>(ts + 2 * m * G * 128) = make_float2(o[0], o[1]);
+        *reinterpret_cast<float2*>(ts + (2 * m + 1) * G * 128) = make_float2(o[2], o[3]);
         if (m == 2) store_sub((k + 1) & 1, it1.ci);
         if (m == 1) load_item(it2);
       }
@@ -741,7 +759,7 @@ bwd_kernel(BwdArgs a) {
     for (int i = 0; i < nit; ++i) {
       prio.step(i);
       const int ci = c_hi - 1 - i;
-      const float* s0 = lds + (i & 1) * BUF;
+      const float* s0 = sbuf + (i & 1) * BUF;
       const float* gB = s0 + oB + q * bc_group_floats(NPL);
       const float* gC = s0 + oC + q * bc_group_floats(NPL);
       // RL: this lane's floats of each quad of the quad broadcast tile (B;
@@ -754,8 +772,8 @@ bwd_kernel(BwdArgs a) {
 #pragma unroll
         for (int m = kQuads - 1; m >= 0; --m) {
           float dts[4], dys[4], Cq[4][NPL];
-          f4_to(dts, lds4(s0 + cm_quad(c, m)));
-          f4_to(dys, lds4(s0 + oDY + cm_quad(c, m)));
+          f4_to(dts, lds4(s0 + cml_quad<kBwdCm>(c, m)));
+          f4_to(dys, lds4(s0 + oDY + cml_quad<kBwdCm>(c, m)));
           load_quad_rows<NPL>(Cq, gC, m);
 #pragma unroll
           for (int s = 3; s >= 0; --s) {
@@ -777,8 +795,8 @@ bwd_kernel(BwdArgs a) {
       for (int m = 0; m < kQuads; ++m) {
         float dts[4], dtxs[4], Bq[4][NPL];
         float2 qb;   // RL: B of the quad broadcast tile
-        f4_to(dts, lds4(s0 + cm_quad(c, m)));
-        f4_to(dtxs, lds4(s0 + oDTX + cm_quad(c, m)));
+        f4_to(dts, lds4(s0 + cml_quad<kBwdCm>(c, m)));
+        f4_to(dtxs, lds4(s0 + oDTX + cml_quad<kBwdCm>(c, m)));
         if constexpr (RL) {
           qb = lds2(gQ + 16 * m);
         } else {
@@ -809,12 +827,12 @@ bwd_kernel(BwdArgs a) {
       for (int m = kQuads - 1; m >= 0; --m) {
         float dts[4], dys[4], dtxs[4], Bq[4][NPL], Cq[4][NPL], s1q[4], s2q[4];
         float dysp[4], dtxsp[4];   // RL: the partner channel's
-        f4_to(dts, lds4(s0 + cm_quad(c, m)));
-        f4_to(dys, lds4(s0 + oDY + cm_quad(c, m)));
-        f4_to(dtxs, lds4(s0 + oDTX + cm_quad(c, m)));
+        f4_to(dts, lds4(s0 + cml_quad<kBwdCm>(c, m)));
+        f4_to(dys, lds4(s0 + oDY + cml_quad<kBwdCm>(c, m)));
+        f4_to(dtxs, lds4(s0 + oDTX + cml_quad<kBwdCm>(c, m)));
         if constexpr (RL) {
-          f4_to(dysp, lds4(s0 + oDY + cm_quad(cp, m)));
-          f4_to(dtxsp, lds4(s0 + oDTX + cm_quad(cp, m)));
+          f4_to(dysp, lds4(s0 + oDY + cml_quad<kBwdCm>(cp, m)));
+          f4_to(dtxsp, lds4(s0 + oDTX + cml_quad<kBwdCm>(cp, m)));
         }
         float2 qb, qc;   // RL: B and C of the quad broadcast tile
         if constexpr (RL) {
@@ -876,12 +894,13 @@ bwd_kernel(BwdArgs a) {
                                                           __float_as_uint(s2q[s]), false, false);
           o[s] = __uint_as_float(sw[0]) + __uint_as_float(sw[1]);
         }
-        // tS: per wave a step-pair-major tile [8 pairs][64 rows][2] (rows 0-31:
-        // s1 of the channels, 32-63: s2), so that finalize's 64-bit reads of
-        // one pair over 32 rows are contiguous (no bank conflicts).
-        float* const ts = tS + wave * 64 * kSteps;
-        *reinterpret_cast<float2*>(ts + (2 * m * 64 + lane) * 2) = make_float2(o[0], o[1]);
-        *reinterpret_cast<float2*>(ts + ((2 * m + 1) * 64 + lane) * 2) = make_float2(o[2], o[3]);
+        // tS: [8 step pairs][G waves][64 rows][2] (rows 0-31: s1 of the
+        // channels, 32-63: s2): a wave's 64-bit writes of one pair are
+        // contiguous (no bank conflicts), and finalize's reads of a pair's
+        // partials over the waves lie within 2 KB of one address (read2).
+        float* const ts = tS + wave * 128 + lane * 2;
+        *reinterpret_cast<float2*>(ts + 2 * m * G * 128) = make_float2(o[0], o[1]);
+        *reinterpret_cast<float2*>(ts + (2 * m + 1) * G * 128) = make_float2(o[2], o[3]);
         if (m == 2) store_sub((i + 1) & 1, ci - 1);  // unused when ci == 0
         if (m == 1) load_next();             // chunk ci - 2: loads nothing when ci < 2
       }

@@ -253,9 +253,9 @@ void fill(Plan& p) {
   fill_elem<NPL, G, MINW, 2>(p.k[kBF16]);
   p.fwd_lds = mhs::fwd_lds_floats(G, NPL) * 4;
   p.bwd_lds = mhs::bwd_lds_floats(G, NPL, mhs::bwd_relabel(NPL, false),
-                                   mhs::bwd_row_partial(NPL, false, 0)) * 4;
+                                   mhs::bwd_row_partial(NPL, false, 0), false) * 4;
   p.bwd_carry_lds = mhs::bwd_lds_floats(G, NPL, mhs::bwd_relabel(NPL, true),
-                                         mhs::bwd_row_partial(NPL, true, 0)) * 4;
+                                         mhs::bwd_row_partial(NPL, true, 0), true) * 4;
   p.bwd_sw_lds = mhs::bwd_sweep_lds_floats(G, NPL) * 4;
 }
 

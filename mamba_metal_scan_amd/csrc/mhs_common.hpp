@@ -352,9 +352,31 @@ __device__ __forceinline__ int cm_quad(int row, int m) {
   return row * kSteps + (((m ^ row ^ (row >> 2)) & 3) << 2);
 }
 __device__ __forceinline__ int cm_elem(int row, int k) { return cm_quad(row, k >> 2) + (k & 3); }
+// The padded channel-major layout: rows kCmRow = 20 floats apart (80 bytes:
+// the 16 rows of any 16 consecutive lanes start on 16 distinct 4-bank
+// groups), quads in order. A lane's four quads are then one base register
+// plus immediates 0, 16, 32, 48 bytes, where the swizzle needs a register per
+// quad (an address add per quad for each buffer switch).
+constexpr int kCmRow = 20;
+enum class CmLayout { kSwizzled, kPadded };
+template <CmLayout L>
+__device__ __forceinline__ int cml_quad(int row, int m) {
+  if constexpr (L == CmLayout::kPadded) return row * kCmRow + 4 * m;
+  else return cm_quad(row, m);
+}
+template <CmLayout L>
+__device__ __forceinline__ int cml_elem(int row, int k) {
+  if constexpr (L == CmLayout::kPadded) return row * kCmRow + k;
+  else return cm_elem(row, k);
+}
+template <CmLayout L>
+__host__ __device__ constexpr int cml_tile_floats(int ch) {
+  return L == CmLayout::kPadded ? ch * kCmRow : ch * kSteps;
+}
 
 __device__ __forceinline__ float4 lds4(const float* p) { return *reinterpret_cast<const float4*>(p); }
 __device__ __forceinline__ float2 lds2(const float* p) { return *reinterpret_cast<const float2*>(p); }
+
 
 // ------------------------------------------------------------- buffer I/O
 //
@@ -601,20 +623,22 @@ struct QuadLoader {
       v[i].w = s0 + 3 < len ? gate_dt(v[i].w + bias[i], lo, span) : 0.f;
     }
   }
-  // Channel-major swizzled tile [CH][16].
+  // Channel-major tile [CH][16] (swizzled) or [CH][kCmRow] (padded).
+  template <CmLayout L = CmLayout::kSwizzled>
   __device__ __forceinline__ void store_cm(float* tile, const float4 (&v)[PER]) const {
 #pragma unroll
     for (int i = 0; i < PER; ++i) {
-      if (valid(i)) sts4(tile + cm_quad(chan(i), quad(i)), v[i]);
+      if (valid(i)) sts4(tile + cml_quad<L>(chan(i), quad(i)), v[i]);
       consume(v[i]);
     }
   }
+  template <CmLayout L = CmLayout::kSwizzled>
   __device__ __forceinline__ void store_cm_product(float* tile, const float4 (&a)[PER],
                                                    const float4 (&b)[PER]) const {
 #pragma unroll
     for (int i = 0; i < PER; ++i) {
       if (valid(i))
-        sts4(tile + cm_quad(chan(i), quad(i)),
+        sts4(tile + cml_quad<L>(chan(i), quad(i)),
              make_float4(a[i].x * b[i].x, a[i].y * b[i].y, a[i].z * b[i].z, a[i].w * b[i].w));
       consume(a[i]);
       consume(b[i]);

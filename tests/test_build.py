@@ -25,6 +25,9 @@ def test_audit_constants_match_the_headers():
     assert build.K_STEPS == _constant("mhs_common.hpp", "kSteps")
     assert build.K_BC_PAD == _constant("mhs_common.hpp", "kBCPad")
     assert build.K_SWEEP_MAX == _constant("mhs_bwd.hpp", "kSweepMax")
+    assert build.K_CM_ROW == _constant("mhs_common.hpp", "kCmRow")
+    assert "return carry ? CmLayout::kSwizzled : CmLayout::kPadded;" in (
+        CSRC / "mhs_bwd.hpp").read_text()
     m = re.search(r"constexpr int kBCGroup2 = kQuads \* 16 \+ 16;", (CSRC / "mhs_common.hpp").read_text())
     assert m and _constant("mhs_common.hpp", "kQuads") * 16 + 16 == build.K_BC_GROUP2 == 80
     m = re.search(r"constexpr int kBCGroupQ = kQuads \* 16 \+ 8;", (CSRC / "mhs_common.hpp").read_text())
@@ -33,16 +36,18 @@ def test_audit_constants_match_the_headers():
 
 def test_lds_sizes_of_the_training_plan():
     """d_state 16 (NPL 2, G 4): forward 29,696 B (B and C in the row
-    broadcast tile); backward 41,536 B with the row-partial sums and B / C in
-    the quad broadcast tile (3 blocks per CU fit the 160 KiB of gfx950);
-    carry pass 39,424 B (per-group B / C tiles); swept backward 47,616 B (the
-    quad broadcast tile and the sweep's state slots, no row partials)."""
+    broadcast tile); backward 45,632 B with the row-partial sums, the padded
+    channel-major tiles (4 x 32 rows of 20 floats per staging buffer) and B /
+    C in the quad broadcast tile (3 blocks per CU fit the 160 KiB of gfx950);
+    carry pass 39,424 B (swizzled channel-major tiles, per-group B / C tiles:
+    4 blocks per CU); swept backward 51,712 B (the quad broadcast tile and
+    the sweep's state slots, no row partials)."""
     assert build.scan_lds_bytes("fwd", 4, 2) == 4 * 2 * (1024 + 8 * 80 + 4 * 512) == 29696
     assert build.scan_lds_bytes("bwd_carry", 4, 2) == 4 * (2 * (2048 + 2 * 288) + 4096 + 512) == 39424
     sweep = build.scan_lds_bytes("bwd_sweep", 4, 2)
-    assert sweep == 4 * (2 * (2048 + 8 * 72) + 4096 + 512 + 4 * 64 * 4 * 2) == 47616
+    assert sweep == 4 * (2 * (2560 + 8 * 72) + 4096 + 512 + 4 * 64 * 4 * 2) == 51712
     rp = build.scan_lds_bytes("bwd", 4, 2)
-    assert rp == 4 * (2 * (2048 + 8 * 72) + 4096 + 4 * (16 * 16 + 4)) == 41536
+    assert rp == 4 * (2 * (2560 + 8 * 72) + 4096 + 4 * (16 * 16 + 4)) == 45632
     assert 3 * rp <= build.LDS_PER_CU and 3 * sweep <= 160 * 1024
 
 
