@@ -185,7 +185,7 @@ def scan_lds_bytes(kind: str, g: int, npl: int) -> int:
         # two states per lane: the broadcast tile (fwd_bc_floats)
         bc = 2 * g * K_BC_GROUP2 if npl == 2 else 2 * _bc_tile_floats(2 * g, npl)
         buf = 2 * K_CH * K_STEPS + bc + g * K_CH * K_STEPS
-        ck = 2 * K_CH * 2 * g * npl if npl == 2 else 0   # the staged checkpoint tiles
+        ck = 2 * K_CH * (2 * g * npl + 2) if npl == 2 else 0   # the staged checkpoint tiles
         return 4 * (2 * buf + ck)
     rl = kind != "bwd_carry" and npl == 2   # swapped state pairs (bwd_relabel)
     rp = kind == "bwd" and npl == 2         # row-partial channel sums (bwd_row_partial)

@@ -136,9 +136,12 @@ __device__ __forceinline__ void bcast_dot_c(float (&y)[4], float r, const float 
         "v"(h[2][1]), "v"(h[3][0]), "v"(h[3][1]));
 }
 // The two pipeline buffers, then (two states per lane) the checkpoint tiles
-// of the two sub-chunk parities, [32 channels][NP] each.
+// of the two sub-chunk parities, [32 channels][NP + 2] each (rows of an odd
+// number of float pairs: the 32 lanes' 64-bit writes of a column hit 64
+// distinct banks).
+__host__ __device__ constexpr int fwd_ck_row(int G, int NPL) { return 2 * G * NPL + 2; }
 __host__ __device__ constexpr int fwd_lds_floats(int G, int NPL) {
-  return 2 * fwd_buf_floats(G, NPL) + (NPL == 2 ? 2 * kCH * 2 * G * NPL : 0);
+  return 2 * fwd_buf_floats(G, NPL) + (NPL == 2 ? 2 * kCH * fwd_ck_row(G, NPL) : 0);
 }
 
 // KALIGNED: the checkpoint stride K is a multiple of 16, so checkpoints fall
@@ -340,23 +343,26 @@ fwd_kernel(FwdArgs a) {
   // Staged checkpoints (two states per lane, strides that are multiples of
   // 16): at the end of a sub-chunk each lane writes its states to the LDS
   // tile of the sub-chunk's parity, [32 channels][NP] (the (D, N) slice's
-  // layout), and after the barrier thread t stores floats 2t and 2t + 1 of it
-  // to the checkpoint: each wave writes 512 contiguous bytes, whole lines,
+  // layout, rows CKR floats apart), and after the barrier thread t stores
+  // floats 2t and 2t + 1 of it to the checkpoint: each wave writes 512
+  // contiguous bytes, whole lines,
   // where the lanes' own stores (8 bytes every N floats) leave lines for the
   // caches to assemble from the 2G lane groups (measured at 16x512x1536x16:
   // forward 50.5 -> 49.9 us; 4x16384x2048x16 forward 824 -> 797 us).
   constexpr bool CKL = KALIGNED && NPL == 2 && PASS != kPassCarry;
+  constexpr int CKR = fwd_ck_row(G, NPL);
   float* const ckt = lds + 2 * BUF;
   const float* ck_pend = nullptr;   // the checkpoint staged, not yet stored
   unsigned ck_off0 = kOOB, ck_off1 = kOOB;
+  const int ck_rd = (2 * tid) / NP * CKR + (2 * tid) % NP;   // 2 * NT == kCH * NP
   {
-    const int cc = (2 * tid) / NP, nn = (2 * tid) % NP;   // 2 * NT == kCH * NP
+    const int cc = (2 * tid) / NP, nn = (2 * tid) % NP;
     const bool okc = d0 + cc < D;
     ck_off0 = (okc && nn < N) ? 4u * (unsigned)((d0 + cc) * N + nn) : kOOB;
     ck_off1 = (okc && nn + 1 < N) ? 4u * (unsigned)((d0 + cc) * N + nn + 1) : kOOB;
   }
   auto flush_ck = [&](int par) {   // the staged checkpoint of parity par
-    const float2 v = lds2(ckt + par * kCH * NP + 2 * tid);
+    const float2 v = lds2(ckt + par * kCH * CKR + ck_rd);
     const GBuf g(ck_pend, slice_bytes);
     g.st(v.x, ck_off0);
     g.st(v.y, ck_off1);
@@ -479,7 +485,7 @@ fwd_kernel(FwdArgs a) {
       // A checkpoint at the end of this sub-chunk (uniform test).
       if (next_ck == t0 + kSteps && next_ck < T) {
         if constexpr (CKL) {
-          *reinterpret_cast<float2*>(ckt + P * kCH * NP + c * NP + n0) = make_float2(h[0], h[1]);
+          *reinterpret_cast<float2*>(ckt + P * kCH * CKR + c * CKR + n0) = make_float2(h[0], h[1]);
           ck_pend = ck_ptr;
         } else {
           store_states<NPL>(GBuf(ck_ptr, slice_bytes), ck_lane, nvalid, h);

@@ -35,14 +35,15 @@ def test_audit_constants_match_the_headers():
 
 
 def test_lds_sizes_of_the_training_plan():
-    """d_state 16 (NPL 2, G 4): forward 33,792 B (B and C in the row
-    broadcast tile, the two staged checkpoint tiles); backward 45,632 B with the row-partial sums, the padded
+    """d_state 16 (NPL 2, G 4): forward 34,304 B (B and C in the row
+    broadcast tile, the two staged checkpoint tiles of 32 rows of 18 floats);
+    backward 45,632 B with the row-partial sums, the padded
     channel-major tiles (4 x 32 rows of 20 floats per staging buffer) and B /
     C in the quad broadcast tile (3 blocks per CU fit the 160 KiB of gfx950);
     carry pass 39,424 B (swizzled channel-major tiles, per-group B / C tiles:
     4 blocks per CU); swept backward 51,712 B (the quad broadcast tile and
     the sweep's state slots, no row partials)."""
-    assert build.scan_lds_bytes("fwd", 4, 2) == 4 * (2 * (1024 + 8 * 80 + 4 * 512) + 2 * 512) == 33792
+    assert build.scan_lds_bytes("fwd", 4, 2) == 4 * (2 * (1024 + 8 * 80 + 4 * 512) + 2 * 576) == 34304
     assert build.scan_lds_bytes("bwd_carry", 4, 2) == 4 * (2 * (2048 + 2 * 288) + 4096 + 512) == 39424
     sweep = build.scan_lds_bytes("bwd_sweep", 4, 2)
     assert sweep == 4 * (2 * (2560 + 8 * 72) + 4096 + 512 + 4 * 64 * 4 * 2) == 51712
