@@ -212,7 +212,8 @@ struct Plan {
   int npl = 0;      // states per lane
   int G = 0;        // waves per block (d_state padded to 2*G*npl)
   Kernels k[2];     // by Elem
-  int fwd_lds = 0;  // bytes
+  int fwd_lds = 0;       // bytes, a launch that writes checkpoints
+  int fwd_lds_nock = 0;  // bytes, one that does not (no checkpoint tiles)
   int bwd_ki = 0;   // largest chunk the backward walks directly
   int bwd_lds = 0;  // bytes, the gradient kernels
   int bwd_carry_lds = 0;  // bytes, the adjoint-carry kernels
@@ -252,6 +253,7 @@ void fill(Plan& p) {
   fill_elem<NPL, G, MINW, 4>(p.k[kF32]);
   fill_elem<NPL, G, MINW, 2>(p.k[kBF16]);
   p.fwd_lds = mhs::fwd_lds_floats(G, NPL) * 4;
+  p.fwd_lds_nock = mhs::fwd_lds_floats(G, NPL, false) * 4;
   p.bwd_lds = mhs::bwd_lds_floats(G, NPL, mhs::bwd_relabel(NPL, false),
                                    mhs::bwd_row_partial(NPL, false, 0), false) * 4;
   p.bwd_carry_lds = mhs::bwd_lds_floats(G, NPL, mhs::bwd_relabel(NPL, true),
@@ -447,7 +449,8 @@ int launch_fwd(const Plan& p, mhs::FwdArgs a, int batch, hipStream_t s, const Ga
   int rc = ensure_lds(reinterpret_cast<const void*>(fn), p.fwd_lds);
   if (rc) return rc;
   const dim3 grid((unsigned)((a.D + mhs::kCH - 1) / mhs::kCH), (unsigned)(batch * nseg));
-  hipLaunchKernelGGL(fn, grid, dim3(64 * p.G), p.fwd_lds, s, a);
+  hipLaunchKernelGGL(fn, grid, dim3(64 * p.G), a.ckpt != nullptr ? p.fwd_lds : p.fwd_lds_nock, s,
+                     a);
   return check_launch("forward scan kernel");
 }
 
@@ -544,15 +547,15 @@ int scan_fwd(const void* x, const void* dt, const float* aneg, const void* B, co
   rc = ensure_lds(reinterpret_cast<const void*>(cfn), p.fwd_lds);
   if (rc) return rc;
   hipLaunchKernelGGL(cfn, dim3(nblk, (unsigned)(batch * (w.sg.nseg - 1) * w.sg.cunits)),
-                     dim3(64 * p.G), p.fwd_lds, s, c);
+                     dim3(64 * p.G), p.fwd_lds_nock, s, c);
   rc = check_launch("forward carry kernel");
   if (rc) return rc;
   const bool aligned = a.K % mhs::kSteps == 0 || a.K >= a.T;
   const FwdFn fn = aligned ? (g.on ? kk.fwd_g : kk.fwd) : (g.on ? kk.fwd_any_g : kk.fwd_any);
   rc = ensure_lds(reinterpret_cast<const void*>(fn), p.fwd_lds);
   if (rc) return rc;
-  hipLaunchKernelGGL(fn, dim3(nblk, (unsigned)(batch * w.sg.nseg)), dim3(64 * p.G), p.fwd_lds, s,
-                     a);
+  hipLaunchKernelGGL(fn, dim3(nblk, (unsigned)(batch * w.sg.nseg)), dim3(64 * p.G),
+                     a.ckpt != nullptr ? p.fwd_lds : p.fwd_lds_nock, s, a);
   return check_launch("forward scan kernel");
 }
 

@@ -135,13 +135,15 @@ __device__ __forceinline__ void bcast_dot_c(float (&y)[4], float r, const float 
       : "v"(r), "v"(h[0][0]), "v"(h[0][1]), "v"(h[1][0]), "v"(h[1][1]), "v"(h[2][0]),
         "v"(h[2][1]), "v"(h[3][0]), "v"(h[3][1]));
 }
-// The two pipeline buffers, then (two states per lane) the checkpoint tiles
-// of the two sub-chunk parities, [32 channels][NP + 2] each (rows of an odd
-// number of float pairs: the 32 lanes' 64-bit writes of a column hit 64
-// distinct banks).
+// The two pipeline buffers, then (two states per lane, ck: a launch that
+// writes checkpoints) the checkpoint tiles of the two sub-chunk parities,
+// [32 channels][NP + 2] each (rows of an odd number of float pairs: the 32
+// lanes' 64-bit writes of a column hit 64 distinct banks). A launch without
+// checkpoints never touches the tiles and is launched without them (the
+// prefill: 5 blocks per CU at d_state 16 instead of 4).
 __host__ __device__ constexpr int fwd_ck_row(int G, int NPL) { return 2 * G * NPL + 2; }
-__host__ __device__ constexpr int fwd_lds_floats(int G, int NPL) {
-  return 2 * fwd_buf_floats(G, NPL) + (NPL == 2 ? 2 * kCH * fwd_ck_row(G, NPL) : 0);
+__host__ __device__ constexpr int fwd_lds_floats(int G, int NPL, bool ck = true) {
+  return 2 * fwd_buf_floats(G, NPL) + (ck && NPL == 2 ? 2 * kCH * fwd_ck_row(G, NPL) : 0);
 }
 
 // KALIGNED: the checkpoint stride K is a multiple of 16, so checkpoints fall
