@@ -1124,7 +1124,8 @@ def bench_scan(args) -> dict:
     elapsed = time.perf_counter() - t0
     ms = elapsed * 1e3 / args.steps
     fwd_ms = sum(e[0].elapsed_time(e[1]) for e in events) / len(events)
-    bwd_ms = sum(e[1].elapsed_time(e[2]) for e in events) / len(events)
+    bwd_each = [e[1].elapsed_time(e[2]) for e in events]
+    bwd_ms = sum(bwd_each) / len(events)
     nbytes = scan_bytes(bt, t_len, d, n)
     bwd_gbs = nbytes["bwd"] / (bwd_ms * 1e-3) / 1e9
     fwd_gbs = nbytes["fwd"] / (fwd_ms * 1e-3) / 1e9
@@ -1157,7 +1158,9 @@ def bench_scan(args) -> dict:
                                         if counters else None),
                      "kernel": "scan backward launch (bwd_kernel + bwd_reduce_kernel)",
                      "avg_ms": bwd_ms, "algorithmic_bytes": nbytes["bwd"],
-                     "timed_launches": len(events), "events": event_kind()},
+                     "timed_launches": len(events), "events": event_kind(),
+                     "launch_ms_min": min(bwd_each),
+                     "launch_ms_median": sorted(bwd_each)[len(bwd_each) // 2]},
         "valu": valu_block(counters),
         "scan_fwd": {"avg_ms": fwd_ms, "achieved_GBs": fwd_gbs,
                      "algorithmic_bytes": nbytes["fwd"]},
