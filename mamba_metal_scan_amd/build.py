@@ -178,14 +178,17 @@ def _bc_tile_floats(nq: int, npl: int) -> int:
 
 
 def scan_lds_bytes(kind: str, g: int, npl: int) -> int:
-    """Dynamic LDS per block of the scan kernels of plan (NPL, G): "fwd",
-    "bwd" (the gradient kernels), "bwd_carry" (the adjoint-carry pass) or
-    "bwd_sweep" (the swept backward, checkpoint strides 32-64)."""
-    if kind == "fwd":
+    """Dynamic LDS per block of the scan kernels of plan (NPL, G): "fwd" (a
+    forward launch that writes checkpoints), "fwd_nock" (one that does not:
+    the prefill, the carry pass), "bwd" (the gradient kernels), "bwd_carry"
+    (the adjoint-carry pass) or "bwd_sweep" (the swept backward, checkpoint
+    strides 32-64)."""
+    if kind in ("fwd", "fwd_nock"):
         # two states per lane: the broadcast tile (fwd_bc_floats)
         bc = 2 * g * K_BC_GROUP2 if npl == 2 else 2 * _bc_tile_floats(2 * g, npl)
         buf = 2 * K_CH * K_STEPS + bc + g * K_CH * K_STEPS
-        ck = 2 * K_CH * (2 * g * npl + 2) if npl == 2 else 0   # the staged checkpoint tiles
+        # the staged checkpoint tiles
+        ck = 2 * K_CH * (2 * g * npl + 2) if npl == 2 and kind == "fwd" else 0
         return 4 * (2 * buf + ck)
     rl = kind != "bwd_carry" and npl == 2   # swapped state pairs (bwd_relabel)
     rp = kind == "bwd" and npl == 2         # row-partial channel sums (bwd_row_partial)
@@ -236,7 +239,8 @@ def resource_usage(verbose: bool = False) -> dict:
 AUDIT = [
     ("fwd_kernel<2, 4, 3, true, false, 0, 4>", "forward, checkpoint stride a multiple of 16",
      "fwd", 4, 2),
-    ("fwd_kernel<2, 4, 3, true, false, 1, 4>", "forward carry pass (time segments)", "fwd", 4, 2),
+    ("fwd_kernel<2, 4, 3, true, false, 1, 4>", "forward carry pass (time segments)", "fwd_nock",
+     4, 2),
     ("fwd_kernel<2, 4, 3, true, true, 0, 4>", "gated forward (TinyMamba block)", "fwd", 4, 2),
     ("bwd_kernel<2, 4, 3, false, false, 4, false, 0>", "backward, fixed-order partials",
      "bwd", 4, 2),
@@ -288,7 +292,10 @@ def write_resource_profile(path: Path) -> Path:
              "device-only build of the library's sources (the flags of `build.py`). "
              "`waves/SIMD (registers)` is the compiler's occupancy from VGPRs, SGPRs and the "
              "launch bounds; `LDS B/block` is the dynamic LDS the host launches each scan "
-             f"kernel with, and `waves/SIMD (LDS)` what {LDS_PER_CU // 1024} KiB of LDS per CU "
+             "kernel with (a forward that writes checkpoints; one that does not, as the "
+             f"prefill, leaves out the {scan_lds_bytes('fwd', 4, 2) - scan_lds_bytes('fwd_nock', 4, 2)} "
+             "B of checkpoint tiles at d_state 16), and `waves/SIMD (LDS)` what "
+             f"{LDS_PER_CU // 1024} KiB of LDS per CU "
              "allows for that block size (blocks per CU x waves per block / 4 SIMDs). A kernel "
              "runs at the smaller of the two, or fewer when its grid is smaller than the GPU: "
              "at 16x512x1536x16 the forward and backward grids are 768 blocks of 4 waves, 3 per "

@@ -44,6 +44,7 @@ def test_lds_sizes_of_the_training_plan():
     4 blocks per CU); swept backward 51,712 B (the quad broadcast tile and
     the sweep's state slots, no row partials)."""
     assert build.scan_lds_bytes("fwd", 4, 2) == 4 * (2 * (1024 + 8 * 80 + 4 * 512) + 2 * 576) == 34304
+    assert build.scan_lds_bytes("fwd_nock", 4, 2) == 4 * 2 * (1024 + 8 * 80 + 4 * 512) == 29696
     assert build.scan_lds_bytes("bwd_carry", 4, 2) == 4 * (2 * (2048 + 2 * 288) + 4096 + 512) == 39424
     sweep = build.scan_lds_bytes("bwd_sweep", 4, 2)
     assert sweep == 4 * (2 * (2560 + 8 * 72) + 4096 + 512 + 4 * 64 * 4 * 2) == 51712
