@@ -345,9 +345,10 @@ fwd_kernel(FwdArgs a) {
   // Staged checkpoints (two states per lane, strides that are multiples of
   // 16): at the end of a sub-chunk each lane writes its states to the LDS
   // tile of the sub-chunk's parity, [32 channels][NP] (the (D, N) slice's
-  // layout, rows CKR floats apart), and after the barrier thread t stores
-  // floats 2t and 2t + 1 of it to the checkpoint: each wave writes 512
-  // contiguous bytes, whole lines,
+  // layout, rows CKR floats apart), and after the barrier (in quad 2 of the
+  // next sub-chunk, away from quad 1's y stores: 49.6 -> 48.8 us at
+  // 16x512x1536x16) thread t stores floats 2t and 2t + 1 of it to the
+  // checkpoint: each wave writes 512 contiguous bytes, whole lines,
   // where the lanes' own stores (8 bytes every N floats) leave lines for the
   // caches to assemble from the 2G lane groups (measured at 16x512x1536x16:
   // forward 50.5 -> 49.9 us; 4x16384x2048x16 forward 824 -> 797 us).
@@ -464,7 +465,7 @@ fwd_kernel(FwdArgs a) {
       // buffer written is not read again.
       if (!NOY && m == 0) y_read(P ^ 1);
       if constexpr (CKL) {
-        if (m == 0 && ck_pend != nullptr) flush_ck(P ^ 1);
+        if (m == 2 && ck_pend != nullptr) flush_ck(P ^ 1);
       }
       if (!NOY && m == 1) y_write(i - 1);
       if (m == 1) store_sub(i + 1, std::integral_constant<int, P ^ 1>{});
