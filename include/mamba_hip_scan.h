@@ -55,11 +55,11 @@ int64_t mhs_num_chunks(int64_t seqlen, int64_t chunk);
 
 /* The largest checkpoint stride the backward walks directly (its register
  * window, 16 steps); 0 if d_state is unsupported. Any chunk >= 1 is correct.
- * Strides of 2, 3 or 4 windows (32, 48, 64: the reference's own 64 among
- * them) are swept inside the backward kernel: it rebuilds the states between
- * the caller's checkpoints itself, with no extra workspace. Other strides
- * above the window cost one extra forward pass inside mhs_scan_bwd_f32 and
- * stride-16 checkpoints in its workspace. No counterpart in the reference
+ * A stride of 2 windows (32) is swept inside the backward kernel: it
+ * rebuilds the states between the caller's checkpoints itself, with no extra
+ * workspace. Other strides above the window (the reference's own 64 among
+ * them) cost one extra forward pass inside mhs_scan_bwd_f32 and stride-16
+ * checkpoints in its workspace (the faster choice from 3 windows on). No counterpart in the reference
  * (its stride is the module constant SSM_CHUNK, mamba_metal/scan.py:58). */
 int64_t mhs_preferred_chunk(int64_t d_state);
 

@@ -165,7 +165,7 @@ def emit_assembly(out_dir: Path) -> Path:
 # headers (fwd_lds_floats in mhs_fwd.hpp, bwd_lds_floats and
 # bwd_sweep_lds_floats in mhs_bwd.hpp) with the header constants below, which
 # tests/test_build.py reads back from the headers.
-K_CH, K_STEPS, K_BC_PAD, K_SWEEP_MAX = 32, 16, 4, 4
+K_CH, K_STEPS, K_BC_PAD, K_SWEEP_MAX = 32, 16, 4, 2
 K_CM_ROW = 20                    # kCmRow: a row of the backward's padded channel-major tiles
 K_BC_GROUP2 = 4 * 16 + 16        # kBCGroup2: a state group of the row broadcast tile
 K_BC_GROUPQ = 4 * 16 + 8         # kBCGroupQ: a state group of the quad broadcast tile
@@ -182,7 +182,7 @@ def scan_lds_bytes(kind: str, g: int, npl: int) -> int:
     forward launch that writes checkpoints), "fwd_nock" (one that does not:
     the prefill, the carry pass), "bwd" (the gradient kernels), "bwd_carry"
     (the adjoint-carry pass) or "bwd_sweep" (the swept backward, checkpoint
-    strides 32-64)."""
+    stride 32)."""
     if kind in ("fwd", "fwd_nock"):
         # two states per lane: the broadcast tile (fwd_bc_floats)
         bc = 2 * g * K_BC_GROUP2 if npl == 2 else 2 * _bc_tile_floats(2 * g, npl)
@@ -245,9 +245,9 @@ AUDIT = [
     ("bwd_kernel<2, 4, 3, false, false, 4, false, 0>", "backward, fixed-order partials",
      "bwd", 4, 2),
     ("bwd_kernel<2, 4, 3, false, false, 4, true, 0>", "backward, fp32 atomics", "bwd", 4, 2),
-    ("bwd_kernel<2, 4, 3, false, false, 4, false, 4>", "backward, swept strides 32-64",
+    ("bwd_kernel<2, 4, 3, false, false, 4, false, 2>", "backward, swept stride 32",
      "bwd_sweep", 4, 2),
-    ("bwd_kernel<2, 4, 3, false, false, 4, true, 4>", "backward, swept strides, atomics",
+    ("bwd_kernel<2, 4, 3, false, false, 4, true, 2>", "backward, swept stride, atomics",
      "bwd_sweep", 4, 2),
     ("bwd_kernel<2, 4, 3, false, true, 4, false, 0>", "backward carry pass (time segments)",
      "bwd_carry", 4, 2),

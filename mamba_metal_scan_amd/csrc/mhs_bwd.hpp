@@ -117,9 +117,13 @@ struct BwdArgs {
 };
 
 // Largest number of 16-step chunks per caller checkpoint that the backward
-// sweeps inside the kernel (checkpoint strides 32, 48 and 64 steps); larger
-// strides recompute stride-16 checkpoints in a separate pass.
-constexpr int kSweepMax = 4;
+// sweeps inside the kernel (checkpoint stride 32 steps); larger strides
+// recompute stride-16 checkpoints in a separate pass. From three windows on
+// the separate pass is the faster (backward launch at 16x512x1536x16, chunk
+// 48: 153.2 against 155.0 us, chunk 64: 154.2 against 158.7 us; at
+// 4x16384x2048x16 1793 against 1827 and 1800 against 1881 us), at two the
+// sweep (149.9 against 154.0 us, 1763 against 1797 us).
+constexpr int kSweepMax = 2;
 
 // Channel sums of the two-state plans' gradient kernels (RL): the lanes of
 // odd channel hold their two states in swapped order, and the dB / dC

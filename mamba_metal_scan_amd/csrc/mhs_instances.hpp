@@ -33,7 +33,7 @@
   PREFIX template __global__ void fwd_kernel<NPL, G, MINW, true, true, kPassCkpt, ES>(FwdArgs);
 
 // Backward: ungated / gated, gradient pass / adjoint-carry pass; the
-// gradient pass with the in-kernel sweep of the checkpoint strides 32..64
+// gradient pass with the in-kernel sweep of the checkpoint stride 32
 // (kSweepMax 16-step chunks per caller checkpoint), ungated / gated.
 #define MHS_BWD_INST(PREFIX, NPL, G, MINW, ES)                                    \
   PREFIX template __global__ void bwd_kernel<NPL, G, MINW, false, false, ES>(BwdArgs); \

@@ -41,13 +41,13 @@ def test_lds_sizes_of_the_training_plan():
     channel-major tiles (4 x 32 rows of 20 floats per staging buffer) and B /
     C in the quad broadcast tile (3 blocks per CU fit the 160 KiB of gfx950);
     carry pass 39,424 B (swizzled channel-major tiles, per-group B / C tiles:
-    4 blocks per CU); swept backward 51,712 B (the quad broadcast tile and
-    the sweep's state slots, no row partials)."""
+    4 blocks per CU); swept backward 47,616 B (the quad broadcast tile and
+    the sweep's two state slots, no row partials)."""
     assert build.scan_lds_bytes("fwd", 4, 2) == 4 * (2 * (1024 + 8 * 80 + 4 * 512) + 2 * 576) == 34304
     assert build.scan_lds_bytes("fwd_nock", 4, 2) == 4 * 2 * (1024 + 8 * 80 + 4 * 512) == 29696
     assert build.scan_lds_bytes("bwd_carry", 4, 2) == 4 * (2 * (2048 + 2 * 288) + 4096 + 512) == 39424
     sweep = build.scan_lds_bytes("bwd_sweep", 4, 2)
-    assert sweep == 4 * (2 * (2560 + 8 * 72) + 4096 + 512 + 4 * 64 * 4 * 2) == 51712
+    assert sweep == 4 * (2 * (2560 + 8 * 72) + 4096 + 512 + 2 * 64 * 4 * 2) == 47616
     rp = build.scan_lds_bytes("bwd", 4, 2)
     assert rp == 4 * (2 * (2560 + 8 * 72) + 4096 + 4 * (16 * 16 + 4)) == 45632
     assert 3 * rp <= build.LDS_PER_CU and 3 * sweep <= 160 * 1024

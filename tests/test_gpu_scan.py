@@ -325,10 +325,10 @@ def test_empty_sequence():
 # blocks per CU): segment counts above the chunk count, uneven last segments,
 # chunk strides off the 16-step window, the fine-checkpoint recompute path and
 # the state gradient entering the last segment.
-# Strides 32, 48 and 64 are swept inside the backward kernel, from the
-# caller's checkpoints, also in segments that start inside a caller chunk;
-# other strides above 16 first recompute stride-16 checkpoints, in segments
-# that start on the caller's checkpoints (lcm(16, chunk) steps).
+# Stride 32 is swept inside the backward kernel, from the caller's
+# checkpoints, also in segments that start inside a caller chunk; other
+# strides above 16 first recompute stride-16 checkpoints, in segments that
+# start on the caller's checkpoints (lcm(16, chunk) steps).
 SEGMENT_CASES = [(2, 100, 64, 16, 16, 2), (1, 300, 96, 16, 16, 3), (2, 257, 40, 8, 7, 5),
                  (1, 64, 64, 16, 16, 8), (3, 200, 130, 5, 64, 3), (1, 20, 32, 16, 16, 4),
                  (2, 513, 64, 32, 16, 8), (1, 1000, 64, 16, 48, 4), (2, 777, 96, 16, 20, 6),
@@ -351,11 +351,11 @@ def _run_hip_split(inp, dy, chunk, fwd_segs, bwd_segs):
 
 
 @pytest.mark.parametrize("segs", [1, 3, 5])
-def test_swept_strides_equal_stride_16_bit_for_bit(segs):
-    """The swept backward (strides 32, 48, 64) keeps the stride-16 time
-    segments; with 3 or 5 of them over 1000 steps (63 chunks of 16) some
-    segments start inside a caller chunk, and the last caller chunk is
-    partial. With the forward unsegmented (every checkpoint a sequential
+def test_strides_32_48_64_equal_stride_16_bit_for_bit(segs):
+    """The backward at strides 32 (swept), 48 and 64 (stride-16 checkpoints
+    recomputed) keeps the stride-16 time segments; with 3 or 5 of them over
+    1000 steps (63 chunks of 16) some segments start inside a caller chunk,
+    and the last caller chunk is partial. With the forward unsegmented (every checkpoint a sequential
     state) every gradient equals stride 16's bit for bit (fixed order).
     A segmented forward starts each segment from its combined carry, and
     stride 16 then checkpoints states that derive from it where a sweep
@@ -368,7 +368,7 @@ def test_swept_strides_equal_stride_16_bit_for_bit(segs):
     with reduction(_native.REDUCTION_FIXED):
         base = _run_hip_split(_to_dev(arrs), dy, 16, 1, segs)
         for chunk in (32, 48, 64):
-            print(f"[case] swept stride {chunk} vs 16, {segs} backward segments", flush=True)
+            print(f"[case] stride {chunk} vs 16, {segs} backward segments", flush=True)
             other = _run_hip_split(_to_dev(arrs), dy, chunk, 1, segs)
             assert torch.equal(base[0], other[0]) and torch.equal(base[1], other[1])
             for name, a, b in zip(("dx", "ddt", "dAneg", "dB", "dC"), base[2], other[2]):

@@ -63,7 +63,7 @@ def test_workspace_size_formula():
     + dAneg batch partials + the gated dt-bias batch partials. Atomic
     reduction: only the fp32 dB/dC sums a bf16 backward rounds from. Either
     way + fine checkpoints when the stride exceeds the 16-step window and is
-    not swept in the kernel (strides 32, 48 and 64 are)."""
+    not swept in the kernel (stride 32 is)."""
     lib = _native.library()
     nblk, s, a = 48, 16 * 512 * 16, 16 * 1536 * 16
     try:
@@ -71,14 +71,16 @@ def test_workspace_size_formula():
         assert lib.mhs_deterministic() == 1
         base = 2 * nblk * s * 4 + a * 4 + 16 * 1536 * 4
         assert lib.mhs_scan_bwd_workspace_bytes(16, 512, 1536, 16, 16) == base
-        assert lib.mhs_scan_bwd_workspace_bytes(16, 512, 1536, 16, 64) == base
+        assert lib.mhs_scan_bwd_workspace_bytes(16, 512, 1536, 16, 32) == base
+        assert lib.mhs_scan_bwd_workspace_bytes(16, 512, 1536, 16, 64) == base + 32 * a * 4
         assert lib.mhs_scan_bwd_workspace_bytes(16, 512, 1536, 16, 128) == base + 32 * a * 4
         assert lib.mhs_scan_bwd_workspace_bytes(16, 512, 1536, 16, 40) == base + 32 * a * 4
         assert lib.mhs_scan_bwd_workspace_bytes(16, 512, 1536, 0, 16) == 0
         _native.set_reduction(_native.REDUCTION_ATOMIC)
         assert lib.mhs_deterministic() == 0
         assert lib.mhs_scan_bwd_workspace_bytes(16, 512, 1536, 16, 16) == 2 * s * 4
-        assert lib.mhs_scan_bwd_workspace_bytes(16, 512, 1536, 16, 64) == 2 * s * 4
+        assert lib.mhs_scan_bwd_workspace_bytes(16, 512, 1536, 16, 32) == 2 * s * 4
+        assert lib.mhs_scan_bwd_workspace_bytes(16, 512, 1536, 16, 64) == 2 * s * 4 + 32 * a * 4
         assert lib.mhs_scan_bwd_workspace_bytes(16, 512, 1536, 16, 128) == 2 * s * 4 + 32 * a * 4
     finally:
         _native.set_reduction(_native.REDUCTION_AUTO)
