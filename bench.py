@@ -688,7 +688,7 @@ def kernel_label(name: str) -> str:
     if m:
         a = [v.strip() for v in m.group(2).split(",")]
         if m.group(1) == "fwd_kernel":
-            return {"0": "forward", "1": "forward carry pass", "2": "forward checkpoint pass"}[a[5]]
+            return {"0": "forward", "1": "forward carry pass", "2": "backward checkpoint recompute"}[a[5]]
         if a[4] == "true":
             return "backward carry pass"
         red = "atomics" if len(a) > 6 and a[6] == "true" else "fixed order"
@@ -758,7 +758,7 @@ def kernel_counters(args) -> None:
         "| kernel | dispatches per launch | avg us | read MB | write MB | HBM MB | achieved GB/s "
         "| cycles | VALU busy | waves / CU | VALU / wave | LDS conflict |",
         "|---|---|---|---|---|---|---|---|---|---|---|---|"]
-    order = ["forward carry pass", "forward", "forward checkpoint pass", "zero fill",
+    order = ["forward carry pass", "forward", "backward checkpoint recompute", "zero fill",
              "backward carry pass"]
     labels = sorted({k for k, _ in vals} - {"copy"},
                     key=lambda k: (order.index(k) if k in order else len(order), k))

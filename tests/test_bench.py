@@ -60,7 +60,7 @@ def test_kernel_labels_name_each_pass():
     b = "void mhs::bwd_kernel<2, 4, 3, false, {}, 4, {}, {}>(mhs::BwdArgs)"
     assert bench.kernel_label(f.format(0)) == "forward"
     assert bench.kernel_label(f.format(1)) == "forward carry pass"
-    assert bench.kernel_label(f.format(2)) == "forward checkpoint pass"
+    assert bench.kernel_label(f.format(2)) == "backward checkpoint recompute"
     assert bench.kernel_label(b.format("true", "false", 0)) == "backward carry pass"
     assert bench.kernel_label(b.format("false", "false", 0)) == "backward (fixed order)"
     assert bench.kernel_label(b.format("false", "true", 0)) == "backward (atomics)"
