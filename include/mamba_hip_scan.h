@@ -59,8 +59,9 @@ int64_t mhs_num_chunks(int64_t seqlen, int64_t chunk);
  * rebuilds the states between the caller's checkpoints itself, with no extra
  * workspace. Other strides above the window (the reference's own 64 among
  * them) cost one extra forward pass inside mhs_scan_bwd_f32 and stride-16
- * checkpoints in its workspace (the faster choice from 3 windows on). No counterpart in the reference
- * (its stride is the module constant SSM_CHUNK, mamba_metal/scan.py:58). */
+ * checkpoints in its workspace (the faster choice from 3 windows on). No
+ * counterpart in the reference (its stride is the module constant
+ * SSM_CHUNK, mamba_metal/scan.py:58). */
 int64_t mhs_preferred_chunk(int64_t d_state);
 
 /* Tuning knob, process-wide: force the number of d_state entries each GPU
