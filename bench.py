@@ -368,6 +368,10 @@ def run_launches(args) -> None:
     dev = torch.device("cuda", 0)
     x, dt, aneg, b_in, c_in, dy = (t.to(dev) for t in make_inputs(bt, t_len, d, n))
     for i in range(args.launches):
+        if args.forward_only:
+            # the inference forward: y and the final state, no checkpoints
+            torch.ops.mamba_hip.scan_fwd(x, dt, aneg, b_in, c_in, args.chunk, False)
+            continue
         _, ckpt, _ = torch.ops.mamba_hip.scan_fwd(x, dt, aneg, b_in, c_in, args.chunk, True)
         torch.ops.mamba_hip.scan_bwd(x, dt, aneg, b_in, c_in, dy, None, ckpt, args.chunk)
     src = torch.empty(COPY_BYTES // 4, device=dev)
@@ -375,7 +379,8 @@ def run_launches(args) -> None:
     for _ in range(args.launches):
         dst.copy_(src)
     torch.cuda.synchronize()
-    print(f"launches done: {args.launches} x (scan_fwd, scan_bwd) at {bt}x{t_len}x{d}x{n} "
+    ops = "scan_fwd without checkpoints" if args.forward_only else "scan_fwd, scan_bwd"
+    print(f"launches done: {args.launches} x ({ops}) at {bt}x{t_len}x{d}x{n} "
           f"chunk {args.chunk}, {args.launches} x copy of {COPY_BYTES} B", flush=True)
 
 
@@ -732,7 +737,8 @@ def kernel_counters(args) -> None:
     nbytes = scan_bytes(*shape)
     extra = (f"--batch {args.batch} --seqlen {args.seqlen} --d-inner {args.d_inner} "
              f"--d-state {args.d_state} --chunk {args.chunk}"
-             + (f" --reduction {args.reduction}" if args.reduction != "auto" else ""))
+             + (f" --reduction {args.reduction}" if args.reduction != "auto" else "")
+             + (" --forward-only" if args.forward_only else ""))
     # One --pmc pass per sub-folder, with the counters its CSV holds.
     cmds = [f"rocprofv3 --kernel-trace --stats -d OUT/kt -o run --output-format csv -- "
             f"python3 bench.py --launches {args.launches} {extra}"]
@@ -744,10 +750,13 @@ def kernel_counters(args) -> None:
         cmds.append(f"rocprofv3 --pmc {' '.join(names)} -d OUT/{sub} -o run --output-format csv "
                     f"-- python3 bench.py --launches {args.launches} {extra}")
     cmds.append(f"python3 bench.py --kernel-counters OUT --launches {args.launches} {extra}")
-    lines = [f"# Scan kernels at {tag}, chunk {args.chunk} (fp32, "
-             f"{reduction_name(*shape, args.chunk)} reduction): per-kernel time, HBM traffic, "
-             "VALU issue", "", PROFILE_RUN_NOTE, ""] + ["    " + c for c in cmds] + [
-        "", f"{args.launches} launches of the forward and the backward. Durations: kernel-trace "
+    what = ("the forward without checkpoints" if args.forward_only
+            else f"{reduction_name(*shape, args.chunk)} reduction")
+    lines = [f"# Scan kernels at {tag}, chunk {args.chunk} (fp32, {what}): per-kernel time, "
+             "HBM traffic, VALU issue", "", PROFILE_RUN_NOTE, ""] + ["    " + c for c in cmds] + [
+        "", f"{args.launches} launches of the forward"
+        + (" without checkpoints (y and the final state)" if args.forward_only
+           else " and the backward") + ". Durations: kernel-trace "
         "average over all dispatches (the first launch included). HBM traffic per launch: the "
         f"counters summed over a launch's dispatches of the kernel, scaled by what a "
         f"{COPY_BYTES} B device copy reads (FETCH_SIZE x{fetch_factor:.3f}, WRITE_SIZE "
@@ -789,6 +798,8 @@ def kernel_counters(args) -> None:
     for side, name in (("fwd", "forward"), ("bwd", "backward")):
         alg = nbytes[side]
         us = tot[side + "_us"]
+        if not us:
+            continue
         lines.append(f"| {name} | {us:.1f} | {tot[side] / 1e6:.1f} | {alg / 1e6:.1f} | "
                      f"{tot[side] / alg:.2f} | {alg / (us * 1e-6) / 1e9 if us else 0:.0f} |")
     known = {"FETCH_SIZE", "WRITE_SIZE"} | set(ISSUE_COUNTERS.split())
@@ -803,7 +814,8 @@ def kernel_counters(args) -> None:
                 f"{per_launch[(lab, c)]:.4g}" if (lab, c) in per_launch else ""
                 for c in other) + " |")
     red = "" if args.reduction == "auto" else f"_{args.reduction}"
-    md = ROOT / "profiles" / f"scan_{tag}_chunk{args.chunk}{red}_kernels.md"
+    fo = "_forward" if args.forward_only else ""
+    md = ROOT / "profiles" / f"scan_{tag}_chunk{args.chunk}{red}{fo}_kernels.md"
     md.write_text("\n".join(lines) + "\n")
     print("\n".join(lines))
     print(f"\nwrote {md.relative_to(ROOT)}")
@@ -1249,6 +1261,9 @@ def main() -> int:
                     help="the backward's reduction of dB, dC, dAneg (default: the library's)")
     ap.add_argument("--launches", type=int, default=0,
                     help="profiling driver: only N scan_fwd/scan_bwd launches + N copies")
+    ap.add_argument("--forward-only", action="store_true",
+                    help="with --launches / --kernel-counters: the forward alone, without "
+                         "checkpoints (the prefill's launch; pass --chunk = --seqlen)")
     ap.add_argument("--pmc-summary", default=None, metavar="DIR",
                     help="summarise rocprofv3 FETCH_SIZE / WRITE_SIZE passes under DIR")
     ap.add_argument("--strides", default="16,32,64,128",
