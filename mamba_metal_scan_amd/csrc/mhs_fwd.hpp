@@ -475,7 +475,7 @@ fwd_kernel(FwdArgs a) {
         // Checkpoints inside this quad (any stride; uniform tests per step).
 #pragma unroll
         for (int s = 0; s < 4; ++s) {
-          if (t0 + 4 * m + s + 1 == next_ck) {
+          if (i < nsub && t0 + 4 * m + s + 1 == next_ck) {
             store_states<NPL>(GBuf(ck_ptr, slice_bytes), ck_lane, nvalid, hq[s]);
             ck_ptr += ck_stride;
             next_ck = next_ck == T ? kDone : min(next_ck + a.K, T);
@@ -485,8 +485,10 @@ fwd_kernel(FwdArgs a) {
       step_fence();
     }
     if constexpr (KALIGNED) {
-      // A checkpoint at the end of this sub-chunk (uniform test).
-      if (next_ck == t0 + kSteps && next_ck < T) {
+      // A checkpoint at the end of this sub-chunk (uniform test; none in the
+      // padding sub-chunk past the segment, whose end may be the position of
+      // a checkpoint of the next segment).
+      if (next_ck == t0 + kSteps && next_ck < T && i < nsub) {
         if constexpr (CKL) {
           *reinterpret_cast<float2*>(ckt + P * kCH * CKR + c * CKR + n0) = make_float2(h[0], h[1]);
           ck_pend = ck_ptr;
@@ -499,12 +501,15 @@ fwd_kernel(FwdArgs a) {
     }
     __syncthreads();
   };
-  int i = 0;
-  for (; i + 1 < nsub; i += 2) {
+  // Pairs of sub-chunks; an odd count is padded with sub-chunk nsub, whose
+  // inputs are empty (identity steps: h passes through, nothing is stored).
+  // A separate last iteration instead made the compiler copy the staging
+  // registers of one set into another at every turn of the loop (10 VALU
+  // per pair, and a wait for the loads that fill them).
+  for (int i = 0; i < nsub; i += 2) {
     iter(i, I0{});
     iter(i + 1, I1{});
   }
-  if (i < nsub) iter(i, I0{});
   if constexpr (FCARRY) {
     const size_t slot = (size_t)seg * a.batch + b;
     store_states<NPL>(GBuf(a.carryH + slot * ck_stride, slice_bytes), ck_lane, nvalid, h);
@@ -531,7 +536,7 @@ fwd_kernel(FwdArgs a) {
   if (KALIGNED && a.ckpt != nullptr && last_seg)
     store_states<NPL>(GBuf(ck_base + (size_t)(a.nchunk - 1) * ck_stride, slice_bytes), ck_lane,
                       nvalid, h);
-  if constexpr (!NOY) {
+  if (!NOY && (nsub & 1) == 0) {   // else the padding sub-chunk wrote it
     y_read((nsub - 1) & 1);
     y_write(nsub - 1);
   }
