@@ -6,6 +6,7 @@
 // (the Python layer takes it from torch's caching allocator).
 #include <hip/hip_runtime.h>
 
+#include <algorithm>
 #include <atomic>
 #include <cmath>
 #include <cstdarg>
@@ -329,6 +330,64 @@ int ensure_lds(const void* fn, int bytes) {
   return MHS_OK;
 }
 
+// Dynamic LDS of a forward launch of nblocks blocks of `waves` waves that
+// needs lds bytes. A block runs its whole sequence (or time segment), so the
+// last round of a grid larger than the blocks the GPU holds at once lasts
+// about as long as a full round however few blocks it has. Where the grid
+// takes several rounds, the LDS is raised (never lowered) so that the blocks
+// per CU minimise rounds x the waves per SIMD a round keeps busy, counted as
+// at least 3 (below that one wave's issue latency, not the SIMD's VALU, sets
+// a round's length). 32x2048x4096x16 prefill, 4096 blocks: 4 per CU in 4
+// rounds instead of 5 per CU in 3.2, 891 against 925 us.
+constexpr int kCuLdsBytes = 160 * 1024;   // gfx950 LDS per CU
+int fwd_round_lds(const void* fn, int lds, long long nblocks, int waves) {
+  struct Entry { const void* fn; int lds; long long nblocks; int waves, cus, out; };
+  static Entry cache[32];
+  static int ncache = 0, next = 0;
+  static std::mutex mu;
+  const int cus = device_cus();
+  std::lock_guard<std::mutex> lk(mu);
+  for (int i = 0; i < ncache; ++i) {
+    const Entry& c = cache[i];
+    if (c.fn == fn && c.lds == lds && c.nblocks == nblocks && c.waves == waves && c.cus == cus)
+      return c.out;
+  }
+  auto occupancy = [&](int bytes) {
+    int b = 0;
+    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&b, fn, 64 * waves, bytes) != hipSuccess) {
+      (void)hipGetLastError();
+      return 0;
+    }
+    return b;
+  };
+  int out = lds;
+  const int bmax = occupancy(lds);
+  if (bmax > 1 && nblocks > (long long)cus * bmax) {
+    auto cost = [&](int b) {
+      const long long per_round = (long long)cus * b;
+      return (double)((nblocks + per_round - 1) / per_round) * std::max(b * waves / 4.0, 3.0);
+    };
+    int best = bmax;
+    for (int b = bmax - 1; b >= 1; --b)
+      if (cost(b) < cost(best)) best = b;
+    // The smallest size, from just above the limit of best + 1 blocks, at
+    // which the device holds best blocks per CU.
+    for (int bytes = (std::max(lds, kCuLdsBytes / (best + 1) + 1) + 15) & ~15;
+         best < bmax && bytes <= kCuLdsBytes / best; bytes += 256) {
+      const int b = occupancy(bytes);
+      if (b == best) {
+        out = bytes;
+        break;
+      }
+      if (b < best) break;
+    }
+  }
+  cache[next] = Entry{fn, lds, nblocks, waves, cus, out};
+  next = (next + 1) % 32;
+  ncache = std::min(ncache + 1, 32);
+  return out;
+}
+
 int check_shape(int64_t batch, int64_t seqlen, int64_t d_inner, int64_t d_state, int64_t chunk) {
   if (batch < 1 || seqlen < 1 || d_inner < 1 || d_state < 1)
     return fail(MHS_EINVAL, "sizes must be positive: batch %lld seqlen %lld d_inner %lld d_state %lld",
@@ -446,11 +505,13 @@ int launch_fwd(const Plan& p, mhs::FwdArgs a, int batch, hipStream_t s, const Ga
     a.seg_len = a.T;
     a.h_init = nullptr;
   }
-  int rc = ensure_lds(reinterpret_cast<const void*>(fn), p.fwd_lds);
-  if (rc) return rc;
   const dim3 grid((unsigned)((a.D + mhs::kCH - 1) / mhs::kCH), (unsigned)(batch * nseg));
-  hipLaunchKernelGGL(fn, grid, dim3(64 * p.G), a.ckpt != nullptr ? p.fwd_lds : p.fwd_lds_nock, s,
-                     a);
+  const int lds = fwd_round_lds(reinterpret_cast<const void*>(fn),
+                                a.ckpt != nullptr ? p.fwd_lds : p.fwd_lds_nock,
+                                (long long)grid.x * grid.y, p.G);
+  int rc = ensure_lds(reinterpret_cast<const void*>(fn), std::max(lds, p.fwd_lds));
+  if (rc) return rc;
+  hipLaunchKernelGGL(fn, grid, dim3(64 * p.G), lds, s, a);
   return check_launch("forward scan kernel");
 }
 
@@ -544,18 +605,23 @@ int scan_fwd(const void* x, const void* dt, const float* aneg, const void* B, co
   c.seg_len = w.sg.ups * mhs::kSteps;
   const Kernels& kk = p.k[e];
   const FwdFn cfn = g.on ? kk.fcarry_g : kk.fcarry;
-  rc = ensure_lds(reinterpret_cast<const void*>(cfn), p.fwd_lds);
+  const dim3 cgrid(nblk, (unsigned)(batch * (w.sg.nseg - 1) * w.sg.cunits));
+  const int clds = fwd_round_lds(reinterpret_cast<const void*>(cfn), p.fwd_lds_nock,
+                                 (long long)cgrid.x * cgrid.y, p.G);
+  rc = ensure_lds(reinterpret_cast<const void*>(cfn), std::max(clds, p.fwd_lds));
   if (rc) return rc;
-  hipLaunchKernelGGL(cfn, dim3(nblk, (unsigned)(batch * (w.sg.nseg - 1) * w.sg.cunits)),
-                     dim3(64 * p.G), p.fwd_lds_nock, s, c);
+  hipLaunchKernelGGL(cfn, cgrid, dim3(64 * p.G), clds, s, c);
   rc = check_launch("forward carry kernel");
   if (rc) return rc;
   const bool aligned = a.K % mhs::kSteps == 0 || a.K >= a.T;
   const FwdFn fn = aligned ? (g.on ? kk.fwd_g : kk.fwd) : (g.on ? kk.fwd_any_g : kk.fwd_any);
-  rc = ensure_lds(reinterpret_cast<const void*>(fn), p.fwd_lds);
+  const dim3 grid(nblk, (unsigned)(batch * w.sg.nseg));
+  const int lds = fwd_round_lds(reinterpret_cast<const void*>(fn),
+                                a.ckpt != nullptr ? p.fwd_lds : p.fwd_lds_nock,
+                                (long long)grid.x * grid.y, p.G);
+  rc = ensure_lds(reinterpret_cast<const void*>(fn), std::max(lds, p.fwd_lds));
   if (rc) return rc;
-  hipLaunchKernelGGL(fn, dim3(nblk, (unsigned)(batch * w.sg.nseg)), dim3(64 * p.G),
-                     a.ckpt != nullptr ? p.fwd_lds : p.fwd_lds_nock, s, a);
+  hipLaunchKernelGGL(fn, grid, dim3(64 * p.G), lds, s, a);
   return check_launch("forward scan kernel");
 }
 
